@@ -1,0 +1,185 @@
+"""Pins the cache oracle (oracle/cache_oracle.c) with a from-scratch pure-Python brute force on tiny configurations,
+and checks the cache invariants over a long Zipf trace."""
+import numpy as np
+import pytest
+
+from oracle import cache, synth
+
+
+class Brute:
+    """Direct restatement of the device ensure (a8:864-1039) and the admission host step (nvtier.py:708-806), written
+    with explicit sorts and Python sets instead of selection/compaction."""
+
+    def __init__(self, L, E, S, R, budget, age, qmax, latency, tier=True):
+        self.L, self.E, self.S, self.R = L, E, S, R
+        self.budget, self.agemin, self.qmax, self.lat, self.tier = budget, age, qmax, latency, tier
+        n = L * E
+        self.slot_of = [-1] * n
+        self.slot_key = [-1] * S
+        self.slot_last = [-1] * S
+        self.tick = 0
+        self.ram = [0] * n
+        self.ring = [0] * (1 + R)
+        self.res = [0] * n
+        self.pin = set()
+        if tier:
+            for li in range(L):
+                self.res[li * E] = self.ram[li * E] = 1
+                self.pin.add(li * E)
+        self.age = [0] * n
+        self.inflight = set()
+        self.htick = 1
+        self.snaps = []
+        self.last = {}
+        self.seen = 0
+        self.pending = {}
+        self.hstep = 0
+
+    def ensure(self, li, ids, w):
+        E = self.E
+        self.tick += 1
+        T = self.tick
+        if self.tier:
+            for i in range(len(ids)):
+                key = li * E + ids[i]
+                if self.slot_of[key] < 0 and not self.ram[key]:
+                    c = self.ring[0]
+                    self.ring[0] += 1
+                    self.ring[1 + c % self.R] = key
+                    ids[i], w[i] = 0, 0.0
+        need = sorted(set(ids))
+        miss = []
+        for e in need:
+            s = self.slot_of[li * E + e]
+            if s >= 0:
+                if self.slot_last[s] != 0x7FFFFFFF:
+                    self.slot_last[s] = T
+            else:
+                miss.append(e)
+        elig = [(self.slot_last[s] + 1, s) for s in range(self.S) if self.slot_last[s] < T]
+        nm = min(len(miss), len(elig)) if self.S else 0
+        chosen = sorted(elig)[:nm]                        # exact LRU, ties by slot
+        tau = chosen[-1][0] if nm else None
+        V = sorted(s for u, s in chosen if u < tau) + [s for u, s in chosen if u == tau]
+        vict = []
+        for mi in range(nm):
+            s, e = V[mi], miss[mi]
+            old = self.slot_key[s]
+            wb = -1 if (self.tier and old >= 0 and self.ram[old]) else old
+            if old >= 0:
+                self.slot_of[old] = -1
+            key = li * E + e
+            self.slot_key[s], self.slot_of[key], self.slot_last[s] = key, s, T
+            vict.append((wb, s))
+            if self.tier and wb >= 0:
+                self.ram[wb] = 1
+        return T, list(ids), nm, miss[:nm], vict
+
+    def host_step(self):
+        n = self.L * self.E
+        self.htick += 1
+        snap = (list(self.ram), list(self.ring), [s >= 0 for s in self.slot_of])
+        self.snaps.append(snap)
+        hs = self.hstep
+        self.hstep += 1
+        if len(self.snaps) < 2:
+            return [], []
+        prev = self.snaps[-2]
+        view = list(prev[0])
+        for k, v in self.last.items():
+            view[k] = v
+        ring, vram = prev[1], prev[2]
+        res = list(self.res)
+        for k in range(n):
+            if view[k] == 1 and self.res[k] == 0:
+                self.age[k] = self.htick
+                res[k] = 1
+        for k in self.pending.pop(hs, []):
+            res[k] = 1
+            self.age[k] = self.htick
+            self.inflight.discard(k)
+        cnt = ring[0]
+        newm = min(cnt - self.seen, self.R)
+        keys = [ring[1 + (p % self.R)] for p in range(cnt - newm, cnt)] if newm > 0 else []
+        counts = {}
+        for k in keys:
+            counts[k] = counts.get(k, 0) + 1
+        want = [k for k in sorted(counts) if res[k] == 0 and k not in self.inflight]
+        want.sort(key=lambda k: -counts[k])               # Python sort is stable
+        self.seen = cnt
+        inflight_n = len(self.inflight)
+        over = sum(res) + inflight_n + len(want) - self.budget
+        ev = []
+        if over > 0:
+            c1 = sorted((k for k in range(n) if res[k] and vram[k] and k not in self.pin), key=lambda k: (self.age[k], k))
+            ev = c1[:over]
+            over -= len(ev)
+            if over > 0:
+                c2 = sorted((k for k in range(n) if res[k] and k not in self.pin and self.age[k] <= self.htick - self.agemin
+                             and k not in ev), key=lambda k: (self.age[k], k))
+                ev += c2[:over]
+            for k in ev:
+                res[k] = 0
+        free = max(0, min(self.budget - sum(res) - inflight_n, self.qmax - inflight_n))
+        adm = want[:free]
+        for k in adm:
+            self.inflight.add(k)
+        self.pending.setdefault(hs + self.lat, []).extend(adm)
+        self.last = {k: res[k] for k in range(n) if res[k] != view[k]}
+        for k, v in self.last.items():
+            self.ram[k] = v
+        self.res = res
+        return adm, ev
+
+
+@pytest.mark.parametrize("seed,tier", [(1, True), (2, True), (3, False), (4, True)])
+def test_cache_oracle_vs_bruteforce(seed, tier):
+    L, E, S, R, P = 3, 8, 5, 16, 3
+    budget, age, qmax, lat = 7, 2, 3, 2
+    rng = np.random.default_rng(seed)
+    steps = 120
+    ids = np.stack([np.stack([rng.choice(E, P, replace=False) for _ in range(L)]) for _ in range(steps)]).astype(np.int32)
+    w = rng.random((steps, L, P)).astype(np.float32)
+    co = cache.CacheOracle(L, E, S, ring_cap=R, tier=tier, budget=budget, age=age, qmax=qmax, latency=lat)
+    br = Brute(L, E, S, R, budget, age, qmax, lat, tier=tier)
+    for n in range(steps):
+        for li in range(L):
+            a_ids, a_w = ids[n, li].copy(), w[n, li].copy()
+            rec = co.ensure(li, a_ids, a_w)
+            T, post, nm, miss, vict = br.ensure(li, list(ids[n, li]), list(w[n, li]))
+            assert rec[0] == T and list(rec[2:2 + P]) == post and rec[2 + P] == nm
+            assert list(rec[3 + P:3 + P + nm]) == miss
+            assert [tuple(rec[3 + 2 * P + 2 * i:5 + 2 * P + 2 * i]) for i in range(nm)] == vict
+            assert np.array_equal(a_ids, np.array(post, np.int32))
+        if tier:
+            adm, ev = co.host_step()
+            badm, bev = br.host_step()
+            assert adm.tolist() == badm and ev.tolist() == bev, n
+            assert co.ram_res.tolist() == br.ram
+        assert co.slot_of.tolist() == br.slot_of and co.slot_last.tolist() == br.slot_last
+
+
+def test_cache_invariants_zipf():
+    L, E, S = 8, 64, 120
+    steps, P = 600, 6
+    ids, w = synth.zipf_trace(99, steps, L, E, P)
+    co = cache.CacheOracle(L, E, S, budget=60, qmax=16, latency=3)
+    qmax = 16
+    for n in range(steps):
+        for li in range(L):
+            a, b = ids[n, li, 0].copy(), w[n, li, 0].copy()
+            rec = co.ensure(li, a, b)
+            T, nm = rec[0], rec[2 + P]
+            slots = rec[3 + 2 * P + 1:3 + 4 * P:2][:nm]
+            assert len(set(slots.tolist())) == nm
+            # every assigned slot is now stamped T and owned by a key of this layer
+            assert all(co.slot_last[s] == T and co.slot_key[s] // E == li for s in slots)
+        adm, ev = co.host_step()
+        assert len(adm) <= qmax and int(co.inflight.sum()) <= qmax
+        sk = co.slot_key
+        own = sk[sk >= 0]
+        assert len(set(own.tolist())) == own.size                          # one slot per key
+        assert all(co.slot_of[k] == s for s, k in enumerate(sk) if k >= 0)  # slot_of / slot_key bijection
+        assert int((co.slot_of >= 0).sum()) == own.size <= S
+        # budget holds after eviction, except for device write-backs flagged during the step
+        assert int(co.res.sum()) + int(co.inflight.sum()) <= 60 + 2 * L * P

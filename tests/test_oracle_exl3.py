@@ -1,0 +1,188 @@
+"""Pins the EXL3 oracle (oracle/exl3.py) against independent checks: closed forms computed another way, brute force,
+invariants and a float64 dense reconstruction. A plausible slip (wrong byte, wrong shift, transposed tile, dropped
+rounding) fails at least one of these."""
+import hashlib
+import json
+import os
+import struct
+
+import numpy as np
+import pytest
+
+from oracle import exl3, synth
+
+GOLD = os.path.join(os.path.dirname(__file__), "golden")
+
+
+def _half_bits(v: float) -> int:
+    return struct.unpack("<H", struct.pack("<e", v))[0]
+
+
+def test_codebook_exhaustive_vs_python_ints():
+    """Every state: pure-Python integer arithmetic + IEEE half rounding from the struct module (independent of numpy's
+    float16 cast)."""
+    tab = exl3.codebook_table().view(np.uint16)
+    c1 = struct.unpack("<e", struct.pack("<H", 0x1EEE))[0]
+    c2 = struct.unpack("<e", struct.pack("<H", 0xC931))[0]
+    assert (c1, c2) == (exl3.C1, exl3.C2)
+    for s in range(65536):
+        x = (s * 0x83DCD12D) & 0xFFFFFFFF
+        h = 1024 + sum((x >> (8 * i)) & 0xFF for i in range(4))
+        assert 1024 <= h <= 2044
+        assert tab[s] == _half_bits(h * c1 + c2), s
+
+
+def test_codebook_known_answers_and_range():
+    cb = exl3.codebook_table().astype(np.float64)
+    assert cb[0] == -3.453125                       # x = 0: h = 1024, 1024*c1 + c2 exactly
+    # state 1: x = 0x83DCD12D, bytes 0x83+0xDC+0xD1+0x2D = 131+220+209+45 = 605 -> h = 1629
+    assert exl3.codebook_raw_h(np.array([1]))[0] == 1629
+    assert cb[1] == float(np.float16(1629 * exl3.C1 + exl3.C2))
+    assert cb.min() >= -3.4532 and cb.max() <= 3.4532     # exl3_ops.sycl:522 range
+    assert abs(cb.mean()) < 0.05 and 0.9 < cb.std() < 1.1
+    h = json.load(open(os.path.join(GOLD, "codebook.json")))
+    assert hashlib.sha256(exl3.codebook_table().tobytes()).hexdigest() == h["sha256"]
+    assert [int(v) for v in exl3.codebook_table().view(np.uint16)[h["probe_states"]]] == h["probe_bits"]
+
+
+def _brute_states(words, K):
+    """Bit-by-bit: bit b of the tile stream is bit 31 - b%32 of word b//32 (MSB first); state t = the 16 bits
+    ending (exclusive) at (t+1)K, circular."""
+    nb = 32 * words.size
+    bits = [(int(words[b // 32]) >> (31 - b % 32)) & 1 for b in range(nb)]
+    out = []
+    for t in range(256):
+        e = (t + 1) * K
+        v = 0
+        for b in range(e - 16, e):
+            v = (v << 1) | bits[b % nb]
+        out.append(v)
+    return np.array(out)
+
+
+@pytest.mark.parametrize("K", [2, 3, 4])
+def test_tile_states_bruteforce(K):
+    rng = np.random.default_rng(K)
+    for _ in range(3):
+        w = rng.integers(0, 1 << 32, size=8 * K, dtype=np.uint64).astype(np.uint32)
+        assert np.array_equal(exl3.tile_states(w[None], K)[0], _brute_states(w, K))
+
+
+@pytest.mark.parametrize("K", [2, 3, 4])
+def test_trellis_symbol_invariants(K):
+    """Encode 256 random K-bit symbols MSB-first: state t's low K bits are symbol t and state t >> K equals the low
+    16-K bits of state t-1 (the trellis shift)."""
+    rng = np.random.default_rng(10 + K)
+    sym = rng.integers(0, 1 << K, size=256)
+    bits = []
+    for s in sym:
+        bits += [(int(s) >> (K - 1 - i)) & 1 for i in range(K)]
+    words = np.array([int("".join(map(str, bits[32 * i:32 * i + 32])), 2) for i in range(8 * K)], dtype=np.uint32)
+    st = exl3.tile_states(words[None], K)[0].astype(np.int64)
+    assert np.array_equal(st & ((1 << K) - 1), sym)
+    mask = (1 << (16 - K)) - 1
+    assert np.array_equal(st >> K, np.roll(st, 1) & mask)
+
+
+def test_tile_pos_bijection():
+    r, c = exl3.tile_pos(np.arange(256))
+    assert len(set(zip(r.tolist(), c.tolist()))) == 256 and r.max() == 15 and c.max() == 15
+    assert (r[0], c[0]) == (0, 0) and (r[1], c[1]) == (1, 0) and (r[4], c[4]) == (0, 8) and (r[32], c[32]) == (0, 1)
+
+
+def test_planar4_index_map():
+    K, G, D = 3, 8, 3
+    rows, n = 2, 8
+    nat = np.arange(rows * n * 24, dtype=np.uint32).reshape(rows, n, 24)
+    pl = exl3.planar4(nat, K)
+    for r in range(rows):
+        flat_in, flat_out = nat[r].reshape(-1), pl[r].reshape(-1)
+        for q in range(n // 4):
+            for t in range(4):
+                for g in range(G):
+                    for i in range(D):
+                        assert flat_out[q * 96 + i * 32 + t * 8 + g] == flat_in[(q * 4 + t) * 24 + 3 * g + i]
+    assert np.array_equal(exl3.unplanar4(pl, K), nat)
+    nat2 = np.arange(64, dtype=np.uint32).reshape(1, 4, 16)
+    assert np.array_equal(exl3.planar4(nat2, 2), nat2)
+
+
+def test_trellis_words_little_endian():
+    tr = np.array([[[0x1234, 0x5678, -1, 0]]], dtype=np.int16)
+    assert exl3.trellis_words(tr).tolist() == [[[0x56781234, 0x0000FFFF]]]
+
+
+def test_fwht128_vs_scipy():
+    from scipy.linalg import hadamard
+    Hm = hadamard(128)
+    v = np.random.default_rng(0).standard_normal((5, 128)).astype(np.float32)
+    ref = v.astype(np.float64) @ Hm.T
+    assert np.allclose(exl3.fwht128(v), ref, rtol=1e-5, atol=1e-4)
+    assert np.array_equal(Hm @ Hm, 128 * np.eye(128, dtype=Hm.dtype))
+    e = np.zeros(128, np.float32)
+    e[5] = 1.0
+    assert np.array_equal(exl3.fwht128(e), Hm[:, 5].astype(np.float32))
+
+
+def test_blob_layout():
+    o = exl3.blob_layout(2048, 512, 3)
+    assert o["blob"] == 1_195_008 and o["d"] == 786_432 and o["suh_g"] == 786_432 + 393_216
+    assert exl3.blob_bytes(2560, 640, 3) == 1_862_400           # reference value (moe_offload.py:8)
+    assert [exl3.blob_bytes(4096, 1536, k) for k in (2, 3, 4)] == [4_752_384, 7_111_680, 9_470_976]
+
+
+def test_pack_unpack_roundtrip():
+    H, I, K = 256, 128, 3
+    g, u, d = synth.expert_checkpoint(np.random.default_rng(1), H, I, K)
+    blob = exl3.pack_expert(g, u, d, K)
+    assert blob.size == exl3.blob_bytes(H, I, K)
+    up = exl3.unpack_blob(blob, H, I, K)
+    gu = exl3.trellis_words(np.concatenate([g["trellis"], u["trellis"]], axis=1))
+    assert np.array_equal(up["gu"], gu) and np.array_equal(up["d"], exl3.trellis_words(d["trellis"]))
+    assert np.array_equal(up["svh_d"], d["svh"]) and np.array_equal(up["suh_u"], u["suh"])
+
+
+@pytest.mark.parametrize("K", [2, 3, 4])
+def test_expert_forward_vs_dense_float64(K):
+    """The rounded oracle pipeline stays close to an independent float64 dense computation; a dropped scale, a
+    transposed tile or a sign error would move it by O(1)."""
+    H, I = 256, 256
+    blob = synth.expert_blob(7, K, H, I, K)
+    ew = exl3.ExpertWeights(blob, H, I, K)
+    x = exl3.bf16_to_f32(synth.activations(7, 3, H))
+    for m in range(3):
+        y = exl3.expert_pair(x[m], ew, 0.37)
+        ref = exl3.dense_reference(x[m], ew, 0.37)
+        assert np.linalg.norm(y - ref) / np.linalg.norm(ref) < 3e-3
+        yp = exl3.expert_pair(x[m], ew, 0.37, "prefill")
+        assert np.linalg.norm(yp - ref) / np.linalg.norm(ref) < 3e-3
+
+
+def test_moe_forward_combine_order():
+    H, I, K = 256, 128, 3
+    ews = {e: exl3.ExpertWeights(synth.expert_blob(3, e, H, I, K), H, I, K) for e in range(4)}
+    x = synth.activations(3, 2, H)
+    ids = np.array([[0, 2], [3, 1]], np.int32)
+    w = np.array([[0.6, 0.4], [0.5, 0.5]], np.float32)
+    out, of = exl3.moe_forward(x, ids, w, ews)
+    y = exl3.expert_pair(exl3.bf16_to_f32(x[1]), ews[3], 0.5) + exl3.expert_pair(exl3.bf16_to_f32(x[1]), ews[1], 0.5)
+    assert np.allclose(of[1], y, rtol=0, atol=1e-7)
+    assert np.array_equal(out, exl3.f32_to_bf16(of))
+
+
+def test_bf16_rne():
+    f = np.array([1.0, 1.00390625, 1.01171875, -2.5, 3.0e-3], np.float32)    # 1 + 2^-8 ties to even (1.0)
+    b = exl3.f32_to_bf16(f)
+    assert b[0] == 0x3F80 and b[1] == 0x3F80 and b[2] == 0x3F82 and exl3.bf16_to_f32(b)[3] == -2.5
+
+
+def test_align_stable_counting_sort():
+    rng = np.random.default_rng(5)
+    ids = rng.integers(0, 16, size=(37, 4)).astype(np.int32)
+    w = rng.random((37, 4)).astype(np.float32)
+    a = exl3.align(ids, w, 16, pad=8)
+    order = np.argsort(ids.reshape(-1), kind="stable")
+    assert np.array_equal(a["pair_tok"], order // 4)
+    assert np.array_equal(np.sort(a["act_expert"]), np.unique(ids))
+    assert np.array_equal(ids.reshape(-1)[order][a["pair_of"]], ids.reshape(-1))
+    assert a["n_blk"] == sum(-(-c // 8) for c in np.bincount(ids.reshape(-1)) if c)
