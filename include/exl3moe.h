@@ -1,0 +1,112 @@
+/* C-ABI of the MI355X EXL3 expert-offload hot path (libexl3moe.so).
+ *
+ * Plain pointers, sizes and a hipStream_t (passed as void*); every entry point returns 0 on success or an EXL3_E*
+ * code, with a message available from exl3_last_error() (thread-local). Device pointers are HIP device (or pinned,
+ * device-mapped host) addresses. Work is enqueued on `stream`; nothing synchronises the host except where noted.
+ *
+ * Each function replaces one op of the reference's torch library TORCH_LIBRARY(exl3xpu_moe)
+ * (kernels/moe-a8/exl3_moe.a8.sycl:1555-1592); the reference file:line of the implementation it replaces is given on
+ * every declaration. The torch custom-op library _moe.so registers the same schemas and calls these functions.
+ *
+ * Process-wide configuration (tier flags, victim list, host stride, thresholds) mirrors the reference's moe_set_*
+ * globals (a8:682-789): it is read when a call is enqueued, so a captured HIP graph keeps the pointers it saw.
+ * Calls that use the expert cache on one device must be stream-ordered: the device-side cache state and the
+ * reduction counters of the decode kernels are shared by all calls on that device.
+ */
+#ifndef EXL3MOE_H
+#define EXL3MOE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+    EXL3_OK = 0,
+    EXL3_EINVAL = 1,        /* bad argument / shape / dtype (the reference's TORCH_CHECK failures) */
+    EXL3_EUNSUPPORTED = 2,  /* geometry outside what the kernels implement */
+    EXL3_EHIP = 3,          /* HIP runtime error */
+    EXL3_EWORKSPACE = 4,    /* workspace smaller than exl3_*_workspace() */
+    EXL3_ENOMEM = 5
+};
+
+/* activation / output dtypes (the reference accepts fp16 and bf16; fp32 is an extension for exact checks) */
+enum { EXL3_DT_F16 = 0, EXL3_DT_BF16 = 1, EXL3_DT_F32 = 2 };
+
+/* last error message of the calling thread ("" if none) */
+const char* exl3_last_error(void);
+
+/* bytes of one expert blob. Replaces blob_bytes (a8:1551; Geom a8:42-54). */
+int64_t exl3_blob_bytes(int H, int I, int K);
+
+/* ---- process-wide configuration (a8:682-789) ---------------------------------------------------------------------- */
+
+/* moe_set_tier (a8:768-774): ram_res uint8 [L*E] (1 = RAM-tier copy valid), miss ring int32 [1 + cap]
+ * ([0] = monotonic count), safe int32 [L]. ram_res == NULL turns the tier (masking) off. */
+int exl3_set_tier(uint8_t* ram_res, int32_t* miss_ring, int64_t ring_numel, const int32_t* safe);
+/* moe_set_victims (a8:757): device int32 [1 + 2E] victim list, NULL = no victim write-back */
+int exl3_set_victims(int32_t* vict);
+/* moe_set_host_stride (a8:765): stride of a key's RAM-tier address, 0 = the blob size */
+int exl3_set_host_stride(int64_t stride);
+/* moe_set_prefill_min_m (a8:775), moe_set_pair_max_m (a8:727), moe_set_splits (a8:685), moe_set_mr (a8:729) */
+int exl3_set_prefill_min_m(int64_t m);
+int exl3_set_pair_max_m(int64_t m);
+int exl3_set_splits(int64_t gu_p, int64_t dn_p);
+int exl3_set_mr(int64_t mr);
+/* moe_set_debug (a8:728): accepted for API compatibility; kernel skipping for timing probes is not provided */
+int exl3_set_debug(int64_t v);
+/* Decision log of the device cache (no reference counterpart; test hook): int32 buffer [1 + cap * (3 + 4P)],
+ * buf[0] = records written; one record per ensure call, layout of the oracle's (see DESIGN). NULL = off. */
+int exl3_set_decision_log(int32_t* buf, int64_t cap_records);
+
+/* ---- routed-expert MoE --------------------------------------------------------------------------------------------- */
+
+/* workspace bytes for a decode call of M rows (pair mode) */
+size_t exl3_moe_forward_workspace(int M, int H, int I, int topk);
+
+/* moe_forward (a8:1221-1225 -> moe_forward_impl a8:1263-1314): out[m] = sum_k w[m,k] * expert(ids[m,k])(x[m]).
+ * x, out: [M, H] with row strides, dtype EXL3_DT_*; ids int32 / w fp32 [M, topk] contiguous; ptrs int64 [n_experts]
+ * blob addresses (device slots or device-mapped pinned host memory). M <= pair_max_m runs the decode GEMV kernels,
+ * larger M the grouped prefill path. */
+int exl3_moe_forward(const void* x, int x_dtype, int64_t x_stride, int M, int H, const int32_t* topk_ids,
+                     const float* topk_w, int topk, const int64_t* ptrs, int I, int K, int n_experts, void* out,
+                     int64_t out_stride, void* workspace, size_t workspace_bytes, void* stream);
+
+/* moe_forward_cached (a8:1229-1261): the same through the device-managed expert cache of layer `layer`:
+ * ensure (tier mask, hits, exact-LRU victims, assignment) -> victim write-back -> GEMVs with write-through of misses
+ * -> combine + commit. topk_ids / topk_w are rewritten in place by the tier mask (the reference does the same).
+ * M == 0, M >= prefill_min_m or n_slots == 0 fall back to exl3_moe_forward on the layer's pointer table. */
+int exl3_moe_forward_cached(const void* x, int x_dtype, int64_t x_stride, int M, int H, int32_t* topk_ids,
+                            float* topk_w, int topk, int64_t* ptrs_all, int layer, int32_t* slot_of, int32_t* slot_key,
+                            int32_t* slot_last, int32_t* tick, int n_slots, const int64_t* host_base,
+                            int64_t slot_base, int64_t* fill_all, int32_t* fill_list, int max_fill, int I, int K,
+                            int n_experts, void* out, int64_t out_stride, void* workspace, size_t workspace_bytes,
+                            void* stream);
+
+/* moe_align (a8:1316-1323 -> launch_align a8:639-680): token sort by expert into the reference's packed buffers:
+ * ib int32 [4A + 1 + 2*npairs + 16] = act_expert[A] act_start[A] act_cnt[A] act_pstart[A] n_act pair_tok[npairs]
+ * pair_of[npairs] ..., fb fp32 [npairs] = pair_w, A = min(npairs, n_experts). Canonical order: pairs of an expert in
+ * ascending pair index. */
+int exl3_moe_align(const int32_t* topk_ids, const float* topk_w, int M, int topk, int n_experts, int pad, int32_t* ib,
+                   float* fb, void* stream);
+
+/* Bit-exact dequantization (ReconstructKernel, exl3_esimd.h:869-936): PLANAR4 trellis words
+ * [k_tiles][n_tiles][8K] -> fp16 bits [16 k_tiles][16 n_tiles] (W_inner, Hadamard domain). */
+int exl3_dequant(const uint32_t* trellis, int k_tiles, int n_tiles, int K, uint16_t* out, void* stream);
+
+/* ---- host memory and copies (a8:1527-1549) --------------------------------------------------------------------------- */
+
+/* host_alloc (a8:1529-1537): pinned, device-mapped host memory (hipHostMalloc); NULL on failure */
+void* exl3_host_alloc(int64_t nbytes);
+int exl3_host_free(void* p);
+/* usm_kind (a8:1540-1544): 0 unknown/pageable, 1 pinned host, 2 device, 3 managed */
+int exl3_usm_kind(const void* p);
+/* memcpy_async (a8:1546-1549): async copy of raw bytes on `stream` */
+int exl3_memcpy_async(void* dst, const void* src, int64_t nbytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* EXL3MOE_H */

@@ -1,0 +1,153 @@
+// Device building blocks for EXL3 (mul1 trellis) experts on CDNA4 (gfx950, wave64).
+//
+// Trellis tile: 16x16 weights of K bits = 8K uint32 words, MSB-first bit stream. Value t (0..255) is the 16-bit window
+// ending at bit (t+1)K of the tile stream (circular) and lands at
+//     row = 8((t>>1)&1) + 2((t>>3)&3) + (t&1)   (input / k)      col = (t>>5) + 8((t>>2)&1)   (output / n)
+// (reference: kernels/moe-a8/exl3_esimd.h:4-14). A "period" is D = K/gcd(K,32) words holding V = 32/gcd(K,32)
+// values; a tile has G = 256/V periods. Lanes of a wave own one period each, so every lane decodes the same value
+// positions u = 0..V-1 with compile-time shifts.
+//
+// Codebook mul1 (exl3_esimd.h:40-68): x = s * 0x83DCD12D mod 2^32, h = 1024 + bytesum(x) (its bit pattern is
+// 0x6400 + bytesum as fp16, exact), w = RNE_fp16(h * c1 + c2). On gfx950 v_mul_lo_u32 is full rate, so the decode is
+// bfe + mul + sad (+ the consumer's FMA).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace exl3 {
+
+typedef _Float16 half_t;
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+typedef uint16_t bf16_bits;
+
+constexpr float kC1 = 0.00676727294921875f;   // fp16 0x1eee
+constexpr float kC2 = -10.3828125f;           // fp16 0xc931
+constexpr float kRsqrt128 = 0.08838834764831845f;
+constexpr uint32_t kMul1 = 0x83DCD12Du;
+
+constexpr int cgcd(int a, int b) { return b == 0 ? a : cgcd(b, a % b); }
+
+template <int K>
+struct Geo {
+    static constexpr int g = cgcd(K, 32);
+    static constexpr int D = K / g;          // words per period
+    static constexpr int V = 32 / g;         // values per period
+    static constexpr int G = 256 / V;        // periods per tile
+    static constexpr int W = 8 * K;          // words per tile
+    static constexpr int NTW = 64 / G;       // tiles covered by one wave (one period per lane)
+    static_assert(G <= 64, "K too large for one period per lane");
+};
+
+// ---- codebook -------------------------------------------------------------------------------------------------------
+
+// raw fp16 bit pattern of h = 1024 + bytesum(s * mul1) in the low 16 bits (s may carry garbage above bit 15 only if
+// the caller masks; all callers pass clean 16-bit states)
+__device__ __forceinline__ uint32_t cb_raw(uint32_t s) {
+    return __builtin_amdgcn_sad_u8(s * kMul1, 0u, 0x6400u);
+}
+__device__ __forceinline__ half_t cb_h(uint32_t s) {
+    return __builtin_bit_cast(half_t, (uint16_t)cb_raw(s));
+}
+// bit-exact codebook value: h * c1 + c2 is exact in fp32 (22 significant bits), one rounding to fp16 (RNE)
+__device__ __forceinline__ half_t cb_w(uint32_t s) {
+    return (half_t)__builtin_fmaf((float)cb_h(s), kC1, kC2);
+}
+
+// ---- trellis state extraction -----------------------------------------------------------------------------------------
+// Period-relative stream bits: [-32, 0) = previous period's last word, [32j, 32j+32) = word j of the period.
+// Every 16-bit window lies either inside one word or inside a funnel F_m = stream bits [32m-16, 32m+16) around a word
+// boundary, so after D funnel alignbits every state is one v_bfe_u32 (a clean 16-bit value).
+
+template <int K>
+struct Period {
+    static constexpr int D = Geo<K>::D;
+    uint32_t w[D];       // words of the period
+    uint32_t f[D];       // f[m] = stream bits [32m - 16, 32m + 16)
+    __device__ __forceinline__ void set(const uint32_t* words, uint32_t prev) {
+#pragma unroll
+        for (int j = 0; j < D; ++j) w[j] = words[j];
+        f[0] = __builtin_amdgcn_alignbit(prev, w[0], 16);
+#pragma unroll
+        for (int m = 1; m < D; ++m) f[m] = __builtin_amdgcn_alignbit(w[m - 1], w[m], 16);
+    }
+    // state of value u (compile-time)
+    template <int u>
+    __device__ __forceinline__ uint32_t state() const {
+        constexpr int e = K * (u + 1);                 // window = stream bits [e-16, e)
+        constexpr int j = (e - 16) >= 0 ? (e - 16) / 32 : -1;
+        constexpr bool in_word = j >= 0 && e <= 32 * j + 32;
+        if constexpr (in_word) {
+            return __builtin_amdgcn_ubfe(w[j], (uint32_t)(32 * j + 32 - e), 16u);
+        } else {
+            constexpr int m = (e - 1) / 32;            // boundary 32m lies inside the window
+            return __builtin_amdgcn_ubfe(f[m], (uint32_t)(32 * m + 16 - e), 16u);
+        }
+    }
+};
+
+// position of value u of period p inside the 16x16 tile
+template <int K>
+__host__ __device__ constexpr int val_row(int p, int u) {
+    int t = Geo<K>::V * p + u;
+    return 8 * ((t >> 1) & 1) + 2 * ((t >> 3) & 3) + (t & 1);
+}
+template <int K>
+__host__ __device__ constexpr int val_col(int p, int u) {
+    int t = Geo<K>::V * p + u;
+    return (t >> 5) + 8 * ((t >> 2) & 1);
+}
+
+// ---- wave helpers -----------------------------------------------------------------------------------------------------
+
+__device__ __forceinline__ int lane_id() { return __lane_id(); }
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
+    return v;
+}
+
+// In-wave unnormalised Sylvester Walsh-Hadamard of 128 values, lane l holding x[2l] (v0) and x[2l+1] (v1).
+// Butterflies in the order of exl3_esimd.h:210-220 (h = 1, 2, ..., 64), lower element a + b, upper a - b: the fp32
+// results are identical to the sequential restatement.
+__device__ __forceinline__ void wave_fwht128(float& v0, float& v1) {
+    {
+        float a = v0 + v1, b = v0 - v1;
+        v0 = a;
+        v1 = b;
+    }
+    const int l = lane_id();
+#pragma unroll
+    for (int m = 1; m < 64; m <<= 1) {
+        float p0 = __shfl_xor(v0, m, 64), p1 = __shfl_xor(v1, m, 64);
+        bool up = (l & m) != 0;
+        v0 = up ? p0 - v0 : v0 + p0;
+        v1 = up ? p1 - v1 : v1 + p1;
+    }
+}
+
+__device__ __forceinline__ float bf16_to_f32(bf16_bits b) { return __uint_as_float((uint32_t)b << 16); }
+__device__ __forceinline__ bf16_bits f32_to_bf16(float f) {
+    uint32_t u = __float_as_uint(f);
+    u += 0x7FFFu + ((u >> 16) & 1u);      // round to nearest even (finite inputs)
+    return (bf16_bits)(u >> 16);
+}
+// activation dtypes: 0 fp16, 1 bf16, 2 fp32
+__device__ __forceinline__ float ld_act(const void* x, int dt, size_t i) {
+    if (dt == 1) return bf16_to_f32(((const bf16_bits*)x)[i]);
+    if (dt == 2) return ((const float*)x)[i];
+    return (float)((const half_t*)x)[i];
+}
+__device__ __forceinline__ void st_act(void* y, int dt, size_t i, float v) {
+    if (dt == 1) ((bf16_bits*)y)[i] = f32_to_bf16(v);
+    else if (dt == 2) ((float*)y)[i] = v;
+    else ((half_t*)y)[i] = (half_t)v;
+}
+
+// release/acquire around a last-arriver counter (device scope: the L2 of each XCD is private)
+__device__ __forceinline__ int arrive(int* counter) {
+    __threadfence();
+    return atomicAdd(counter, 1);
+}
+
+}  // namespace exl3

@@ -1,0 +1,326 @@
+// Device-managed expert slot cache for CDNA4: one 1024-thread workgroup per MoE layer call.
+//
+// ensure_kernel, decode mode (reference kernels/moe-a8/exl3_moe.a8.sycl:831-1040, canonical order):
+//   1. T = ++tick
+//   2. tier mask: picks whose expert is in neither VRAM (slot_of < 0) nor RAM (ram_res == 0) are logged to the miss
+//      ring in ascending pick order (wave ballot + prefix popcount) and replaced in place by (safe expert, weight 0)
+//   3. need = set of post-mask picks; hits (ascending expert) stamp slot_last = T unless pinned; misses are compacted in
+//      ascending expert id (block exclusive scan)
+//   4. nm = min(misses, max_fill, slots with slot_last < T); tau = nm-th smallest u = slot_last + 1 among those slots,
+//      found by 8-bit radix passes over LDS histograms starting at the highest byte where the keys differ
+//   5. victims = ascending-slot({u < tau}) ++ first `want` of ascending-slot({u == tau}) (ordered compaction over
+//      per-thread contiguous slot chunks), paired with misses in order; the old owner is repointed to its host copy,
+//      the miss gets the slot and a write-through target fill_all[key]
+// The reference builds the miss and victim lists with SLM fetch_add, so its pairing is not deterministic; here every
+// list is produced by prefix sums in work-item order, which defines the canonical decisions the oracle restates.
+//
+// victim_copy_kernel (reference a8:1168-1189): copies each victim slot whose old owner is not RAM-resident back to the
+// owner's RAM-tier page and flags it resident.
+#include <climits>
+
+#include "exl3_common.cuh"
+#include "exl3_kernels.h"
+
+namespace exl3 {
+
+constexpr int kEnsureThreads = 1024;
+constexpr int kEnsureLdsSlots = 24576;     // slot_last is staged in LDS up to this many slots
+
+// exclusive scan over the 1024 threads of the block; `total` = block sum. Contains barriers: call uniformly.
+__device__ __forceinline__ int block_excl_scan(int v, int* sw, int& total) {
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    int incl = v;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const int t = __shfl_up(incl, o, 64);
+        if (lane >= o) incl += t;
+    }
+    if (lane == 63) sw[wv] = incl;
+    __syncthreads();
+    int wbase = 0, tot = 0;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const int t = sw[i];
+        wbase += i < wv ? t : 0;
+        tot += t;
+    }
+    __syncthreads();
+    total = tot;
+    return wbase + incl - v;
+}
+
+__device__ __forceinline__ int block_sum(int v, int* sw) {
+    int t;
+    block_excl_scan(v, sw, t);
+    return t;
+}
+
+__device__ __forceinline__ uint32_t block_min_u32(uint32_t v, uint32_t* su) {
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) v = min(v, (uint32_t)__shfl_xor((int)v, o, 64));
+    if (lane == 0) su[wv] = v;
+    __syncthreads();
+    uint32_t r = su[0];
+#pragma unroll
+    for (int i = 1; i < 16; ++i) r = min(r, su[i]);
+    __syncthreads();
+    return r;
+}
+
+__device__ __forceinline__ uint32_t block_max_u32(uint32_t v, uint32_t* su) {
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) v = max(v, (uint32_t)__shfl_xor((int)v, o, 64));
+    if (lane == 0) su[wv] = v;
+    __syncthreads();
+    uint32_t r = su[0];
+#pragma unroll
+    for (int i = 1; i < 16; ++i) r = max(r, su[i]);
+    __syncthreads();
+    return r;
+}
+
+__global__ void __launch_bounds__(kEnsureThreads) ensure_kernel(EnsureArgs A) {
+    extern __shared__ int dyn[];
+    __shared__ int sw[16];
+    __shared__ uint32_t su[16];
+    __shared__ int sh[8];
+    __shared__ int hist[256];
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int E = A.E, S = A.S, P = A.P;
+    int* need = dyn;                  // [E]
+    int* miss = need + E;             // [E]
+    int* vslot = miss + E;            // [E]
+    int* vwb = vslot + E;             // [E]
+    int* pid = vwb + E;               // [P]
+    int* sl = pid + P;                // [S] when staged
+    const bool sl_lds = S <= kEnsureLdsSlots;
+    const int32_t* slg = A.slot_last;
+
+    if (tid == 0) sh[0] = ++A.tick[0];
+    if (wv == 0) {                                            // tier mask, ascending pick order
+        int cnt = A.ram_res ? A.ring[0] : 0;
+        for (int b = 0; b < P; b += 64) {
+            const int i = b + lane;
+            int id = i < P ? min(max(A.ids[i], 0), E - 1) : 0;
+            bool msk = false;
+            if (A.ram_res && i < P) {
+                const int key = A.layer * E + id;
+                msk = A.slot_of[key] < 0 && !A.ram_res[key];
+            }
+            const uint64_t bal = __ballot(msk);
+            if (msk) {
+                const int pos = cnt + __popcll(bal & ((1ull << lane) - 1ull));
+                A.ring[1 + (int)((uint32_t)pos % (uint32_t)A.ring_cap)] = A.layer * E + id;
+                id = A.safe[A.layer];
+                A.ids[i] = id;
+                A.w[i] = 0.0f;
+            }
+            if (i < P) pid[i] = id;
+            cnt += __popcll(bal);
+        }
+        if (A.ram_res && lane == 0) A.ring[0] = cnt;
+        if (lane == 0) sh[5] = cnt;
+    }
+    for (int e = tid; e < E; e += kEnsureThreads) need[e] = 0;
+    if (sl_lds)
+        for (int s = tid; s < S; s += kEnsureThreads) sl[s] = slg[s];
+    __syncthreads();
+    const int T = sh[0];
+    for (int i = tid; i < P; i += kEnsureThreads) need[pid[i]] = 1;
+    __syncthreads();
+    // hits and misses: work-item e = expert e (E <= 1024)
+    bool is_miss = false;
+    if (tid < E && need[tid]) {
+        const int s = A.slot_of[A.layer * E + tid];
+        if (s >= 0) {
+            const int la = sl_lds ? sl[s] : slg[s];
+            if (la != INT_MAX) {
+                A.slot_last[s] = T;
+                if (sl_lds) sl[s] = T;
+            }
+        } else {
+            is_miss = true;
+        }
+    }
+    int nmiss;
+    const int mpos = block_excl_scan(is_miss ? 1 : 0, sw, nmiss);
+    if (is_miss) miss[mpos] = tid;
+    int nm = S > 0 ? min(nmiss, A.max_fill) : 0;
+    __syncthreads();
+
+    if (nm > 0) {
+        const int C = (S + kEnsureThreads - 1) / kEnsureThreads;
+        const int s0 = min(S, tid * C), s1 = min(S, s0 + C);
+        int elig = 0, empty = 0;
+        uint32_t umin = 0xFFFFFFFFu, umax = 0u;
+        for (int s = s0; s < s1; ++s) {
+            const int la = sl_lds ? sl[s] : slg[s];
+            if (la >= T) continue;
+            const uint32_t u = (uint32_t)(la + 1);
+            ++elig;
+            empty += la == -1;
+            umin = min(umin, u);
+            umax = max(umax, u);
+        }
+        elig = block_sum(elig, sw);
+        empty = block_sum(empty, sw);
+        umin = block_min_u32(umin, su);
+        umax = block_max_u32(umax, su);
+        nm = min(nm, elig);
+        if (nm > 0) {
+            int top = 24;
+            while (top > 0 && ((umin ^ umax) >> top) == 0) top -= 8;
+            uint32_t prefix = top == 24 ? 0u : (umin & (0xFFFFFFFFu << (top + 8)));
+            int want = nm;
+            if (empty >= nm) {
+                prefix = 0u;
+                top = -8;
+            }
+            for (int shift = top; shift >= 0; shift -= 8) {
+                if (tid < 256) hist[tid] = 0;
+                __syncthreads();
+                const uint32_t hmask = shift == 24 ? 0u : (0xFFFFFFFFu << (shift + 8));
+                for (int s = s0; s < s1; ++s) {
+                    const int la = sl_lds ? sl[s] : slg[s];
+                    if (la >= T) continue;
+                    const uint32_t u = (uint32_t)(la + 1);
+                    if ((u & hmask) != (prefix & hmask)) continue;
+                    atomicAdd(&hist[(u >> shift) & 255u], 1);
+                }
+                __syncthreads();
+                if (wv == 0) {
+                    int c[4], loc = 0;
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) {
+                        c[k] = hist[lane * 4 + k];
+                        loc += c[k];
+                    }
+                    int incl = loc;
+#pragma unroll
+                    for (int o = 1; o < 64; o <<= 1) {
+                        const int t = __shfl_up(incl, o, 64);
+                        if (lane >= o) incl += t;
+                    }
+                    int cum = incl - loc;
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) {
+                        if (cum < want && want <= cum + c[k]) {
+                            sh[2] = lane * 4 + k;
+                            sh[3] = want - cum;
+                        }
+                        cum += c[k];
+                    }
+                }
+                __syncthreads();
+                prefix |= (uint32_t)sh[2] << shift;
+                want = sh[3];
+                __syncthreads();
+            }
+            const uint32_t tau = prefix;
+            int n_lt = 0, n_eq = 0;
+            for (int s = s0; s < s1; ++s) {
+                const int la = sl_lds ? sl[s] : slg[s];
+                if (la >= T) continue;
+                const uint32_t u = (uint32_t)(la + 1);
+                n_lt += u < tau;
+                n_eq += u == tau;
+            }
+            int tot_lt, tot_eq;
+            int blt = block_excl_scan(n_lt, sw, tot_lt);
+            const int beq = block_excl_scan(n_eq, sw, tot_eq);
+            const int take_eq = max(0, min(n_eq, want - beq));
+            int ieq = 0;
+            for (int s = s0; s < s1; ++s) {
+                const int la = sl_lds ? sl[s] : slg[s];
+                if (la >= T) continue;
+                const uint32_t u = (uint32_t)(la + 1);
+                if (u < tau) vslot[blt++] = s;
+                else if (u == tau && ieq < take_eq) vslot[tot_lt + beq + ieq++] = s;
+            }
+            __syncthreads();
+            for (int mi = tid; mi < nm; mi += kEnsureThreads) {
+                const int s = vslot[mi], e = miss[mi];
+                const int old = A.slot_key[s];
+                const int wb = (old >= 0 && A.ram_res && A.ram_res[old]) ? -1 : old;
+                vwb[mi] = wb;
+                if (A.vict) {
+                    A.vict[1 + 2 * mi] = wb;
+                    A.vict[2 + 2 * mi] = s;
+                }
+                if (old >= 0) {
+                    A.slot_of[old] = -1;
+                    A.ptrs_all[old] = A.host_base[old / E] + (int64_t)(old % E) * A.hstride;
+                }
+                const int key = A.layer * E + e;
+                A.slot_key[s] = key;
+                A.slot_of[key] = s;
+                A.slot_last[s] = T;
+                A.fill_all[key] = A.slot_base + (int64_t)s * A.blob;
+                A.fill_list[1 + mi] = e;
+            }
+        }
+    }
+    __syncthreads();
+    if (tid == 0) {
+        A.fill_list[0] = nm;
+        if (A.vict) A.vict[0] = nm;
+    }
+    if (A.log && wv == 0) {                                   // decision record, same layout as the oracle's
+        const int idx = A.log[0];
+        if (idx < A.log_cap) {
+            int32_t* r = A.log + 1 + (int64_t)idx * (3 + 4 * P);
+            if (lane == 0) {
+                r[0] = T;
+                r[1] = sh[5];
+                r[2 + P] = nm;
+            }
+            for (int i = lane; i < P; i += 64) {
+                r[2 + i] = pid[i];
+                r[3 + P + i] = i < nm ? miss[i] : -1;
+                r[3 + 2 * P + 2 * i] = i < nm ? vwb[i] : -2;
+                r[4 + 2 * P + 2 * i] = i < nm ? vslot[i] : -2;
+            }
+        }
+        if (lane == 0) A.log[0] = idx + 1;
+    }
+}
+
+__global__ void __launch_bounds__(256) victim_copy_kernel(VictimArgs A, int chunks) {
+    const int i = blockIdx.x / chunks, c = blockIdx.x % chunks;
+    if (i >= A.vict[0]) return;
+    const int old = A.vict[1 + 2 * i], s = A.vict[2 + 2 * i];
+    if (old < 0) return;
+    if (A.ram_res && c == 0 && threadIdx.x == 0) A.ram_res[old] = 1;
+    const uint4* src = (const uint4*)(A.slot_base + (int64_t)s * A.blob);
+    uint4* dst = (uint4*)(A.host_base[old / A.E] + (int64_t)(old % A.E) * A.hstride);
+    const int64_t n16 = A.blob >> 4, per = A.chunk_bytes >> 4;
+    const int64_t b0 = (int64_t)c * per, b1 = min(n16, b0 + per);
+    for (int64_t q = b0 + threadIdx.x; q < b1; q += 256) dst[q] = src[q];
+}
+
+// ---- host launchers ------------------------------------------------------------------------------------------------
+
+hipError_t launch_ensure(const EnsureArgs& a, hipStream_t s) {
+    const size_t lds = (size_t)(4 * a.E + a.P + (a.S <= kEnsureLdsSlots ? a.S : 0)) * sizeof(int);
+    static bool attr = false;
+    if (!attr) {
+        hipError_t e = hipFuncSetAttribute((const void*)ensure_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                           120 * 1024);
+        if (e != hipSuccess) return e;
+        attr = true;
+    }
+    if (lds > 120 * 1024) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(ensure_kernel, dim3(1), dim3(kEnsureThreads), lds, s, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_victim_copy(const VictimArgs& a, int max_victims, hipStream_t s) {
+    const int chunks = (int)((a.blob + a.chunk_bytes - 1) / a.chunk_bytes);
+    if (max_victims <= 0) return hipSuccess;
+    hipLaunchKernelGGL(victim_copy_kernel, dim3((unsigned)(max_victims * chunks)), dim3(256), 0, s, a, chunks);
+    return hipGetLastError();
+}
+
+}  // namespace exl3

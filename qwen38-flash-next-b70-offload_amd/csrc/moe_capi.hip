@@ -1,0 +1,308 @@
+// C-ABI entry points of libexl3moe.so (declarations and reference citations: include/exl3moe.h).
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdarg>
+#include <cstdio>
+#include <string>
+
+#include "../../include/exl3moe.h"
+#include "exl3_kernels.h"
+
+using namespace exl3;
+
+namespace {
+
+thread_local std::string g_err;
+
+struct Config {
+    uint8_t* ram_res = nullptr;
+    int32_t* ring = nullptr;
+    int ring_cap = 0;
+    const int32_t* safe = nullptr;
+    int32_t* vict = nullptr;
+    int64_t host_stride = 0;
+    int prefill_min_m = 256;
+    int pair_max_m = 4;
+    int gu_p = 0, dn_p = 0, mr = 0, debug = 0;
+    int32_t* log = nullptr;
+    int64_t log_cap = 0;
+};
+Config g_cfg;
+
+int fail(int code, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_err = buf;
+    return code;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+    return fail(EXL3_EHIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+int check_geometry(int H, int I, int K, int E) {
+    if (H <= 0 || I <= 0 || H % 128 || I % 128) return fail(EXL3_EINVAL, "moe: H (%d) and I (%d) must be multiples of 128", H, I);
+    if (K < 2 || K > 4) return fail(EXL3_EUNSUPPORTED, "moe: K=%d not supported (K in 2..4)", K);
+    if (E <= 0 || E > kMaxExperts) return fail(EXL3_EINVAL, "moe: n_experts=%d must be in 1..%d", E, kMaxExperts);
+    if (H > 64 * 128 || I > 64 * 128) return fail(EXL3_EUNSUPPORTED, "moe: H and I up to 8192 (got %d, %d)", H, I);
+    return EXL3_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* exl3_last_error(void) { return g_err.c_str(); }
+
+int64_t exl3_blob_bytes(int H, int I, int K) { return blob_geom(H, I, K).blob; }
+
+int exl3_set_tier(uint8_t* ram_res, int32_t* miss_ring, int64_t ring_numel, const int32_t* safe) {
+    if (!ram_res) {
+        g_cfg.ram_res = nullptr;
+        g_cfg.ring = nullptr;
+        g_cfg.ring_cap = 0;
+        g_cfg.safe = nullptr;
+        return EXL3_OK;
+    }
+    if (!miss_ring || ring_numel < 2 || !safe) return fail(EXL3_EINVAL, "moe_set_tier: ring [1 + cap] and safe [L] required");
+    g_cfg.ram_res = ram_res;
+    g_cfg.ring = miss_ring;
+    g_cfg.ring_cap = (int)(ring_numel - 1);
+    g_cfg.safe = safe;
+    return EXL3_OK;
+}
+
+int exl3_set_victims(int32_t* vict) {
+    g_cfg.vict = vict;
+    return EXL3_OK;
+}
+
+int exl3_set_host_stride(int64_t stride) {
+    if (stride < 0 || stride % 16) return fail(EXL3_EINVAL, "moe_set_host_stride: stride must be a non-negative multiple of 16");
+    g_cfg.host_stride = stride;
+    return EXL3_OK;
+}
+
+int exl3_set_prefill_min_m(int64_t m) {
+    g_cfg.prefill_min_m = (int)std::max<int64_t>(1, m);
+    return EXL3_OK;
+}
+
+int exl3_set_pair_max_m(int64_t m) {
+    g_cfg.pair_max_m = (int)std::max<int64_t>(0, m);
+    return EXL3_OK;
+}
+
+int exl3_set_splits(int64_t gu_p, int64_t dn_p) {
+    g_cfg.gu_p = (int)gu_p;
+    g_cfg.dn_p = (int)dn_p;
+    return EXL3_OK;
+}
+
+int exl3_set_mr(int64_t mr) {
+    g_cfg.mr = (int)mr;
+    return EXL3_OK;
+}
+
+int exl3_set_debug(int64_t v) {
+    g_cfg.debug = (int)v;
+    return EXL3_OK;
+}
+
+int exl3_set_decision_log(int32_t* buf, int64_t cap_records) {
+    g_cfg.log = buf;
+    g_cfg.log_cap = buf ? cap_records : 0;
+    return EXL3_OK;
+}
+
+size_t exl3_moe_forward_workspace(int M, int H, int I, int topk) {
+    return decode_workspace_bytes(M * topk, H, I);
+}
+
+static int forward_impl(const void* x, int x_dtype, int64_t x_stride, int M, int H, const int32_t* ids, const float* w,
+                        int topk, const int64_t* ptrs, int I, int K, int E, void* out, int64_t out_stride, void* ws,
+                        size_t ws_bytes, hipStream_t st, const int64_t* fill, int64_t* commit_ptrs, int64_t* commit_fill,
+                        const int32_t* fill_list) {
+    const int npairs = M * topk;
+    if (npairs > kMaxPairs || M > kMaxRows)
+        return fail(EXL3_EUNSUPPORTED, "moe_forward: M=%d x topk=%d exceeds the decode kernels (%d pairs, %d rows)", M,
+                    topk, kMaxPairs, kMaxRows);
+    const size_t need = decode_workspace_bytes(npairs, H, I);
+    if (!ws || ws_bytes < need) return fail(EXL3_EWORKSPACE, "moe_forward: workspace %zu < %zu bytes", ws_bytes, need);
+    DecodeArgs a{};
+    a.x = x;
+    a.x_dt = x_dtype;
+    a.x_stride = x_stride;
+    a.ids = ids;
+    a.w = w;
+    a.M = M;
+    a.topk = topk;
+    a.npairs = npairs;
+    a.E = E;
+    a.ptrs = ptrs;
+    a.fill = fill;
+    a.commit_ptrs = commit_ptrs;
+    a.commit_fill = commit_fill;
+    a.fill_list = fill_list;
+    uint8_t* p = (uint8_t*)ws;
+    a.abuf = (_Float16*)p;
+    p += align256((size_t)npairs * I * 2);
+    a.ybuf = (float*)p;
+    p += align256((size_t)npairs * H * 4);
+    a.part_gu = (float*)p;
+    p += align256((size_t)npairs * (I / 128) * (H / 128) * 256 * 4);
+    a.part_d = (float*)p;
+    a.out = out;
+    a.out_stride = out_stride;
+    a.g = blob_geom(H, I, K);
+    hipError_t e = launch_gateup(K, a, st);
+    if (e != hipSuccess) return hip_fail(e, "gateup launch");
+    e = launch_down(K, a, st);
+    if (e != hipSuccess) return hip_fail(e, "down launch");
+    return EXL3_OK;
+}
+
+int exl3_moe_forward(const void* x, int x_dtype, int64_t x_stride, int M, int H, const int32_t* topk_ids,
+                     const float* topk_w, int topk, const int64_t* ptrs, int I, int K, int n_experts, void* out,
+                     int64_t out_stride, void* workspace, size_t workspace_bytes, void* stream) {
+    if (M < 0 || topk <= 0) return fail(EXL3_EINVAL, "moe_forward: M=%d topk=%d", M, topk);
+    if (x_dtype < EXL3_DT_F16 || x_dtype > EXL3_DT_F32) return fail(EXL3_EINVAL, "moe_forward: x dtype");
+    int r = check_geometry(H, I, K, n_experts);
+    if (r) return r;
+    if (M == 0) return EXL3_OK;
+    if (!x || !topk_ids || !topk_w || !ptrs || !out) return fail(EXL3_EINVAL, "moe_forward: null pointer");
+    return forward_impl(x, x_dtype, x_stride, M, H, topk_ids, topk_w, topk, ptrs, I, K, n_experts, out, out_stride,
+                        workspace, workspace_bytes, (hipStream_t)stream, nullptr, nullptr, nullptr, nullptr);
+}
+
+int exl3_moe_forward_cached(const void* x, int x_dtype, int64_t x_stride, int M, int H, int32_t* topk_ids,
+                            float* topk_w, int topk, int64_t* ptrs_all, int layer, int32_t* slot_of, int32_t* slot_key,
+                            int32_t* slot_last, int32_t* tick, int n_slots, const int64_t* host_base,
+                            int64_t slot_base, int64_t* fill_all, int32_t* fill_list, int max_fill, int I, int K,
+                            int n_experts, void* out, int64_t out_stride, void* workspace, size_t workspace_bytes,
+                            void* stream) {
+    const int E = n_experts;
+    if (M < 0 || topk <= 0 || layer < 0) return fail(EXL3_EINVAL, "moe_forward_cached: M=%d topk=%d layer=%d", M, topk, layer);
+    if (x_dtype < EXL3_DT_F16 || x_dtype > EXL3_DT_F32) return fail(EXL3_EINVAL, "moe_forward_cached: x dtype");
+    int r = check_geometry(H, I, K, E);
+    if (r) return r;
+    if (M == 0) return EXL3_OK;
+    hipStream_t st = (hipStream_t)stream;
+    if (!ptrs_all) return fail(EXL3_EINVAL, "moe_forward_cached: null ptrs_all");
+    if (M >= g_cfg.prefill_min_m || n_slots == 0)
+        return exl3_moe_forward(x, x_dtype, x_stride, M, H, topk_ids, topk_w, topk, ptrs_all + (int64_t)layer * E, I, K,
+                                E, out, out_stride, workspace, workspace_bytes, stream);
+    if (!slot_of || !slot_key || !slot_last || !tick || !host_base || !fill_all || !fill_list)
+        return fail(EXL3_EINVAL, "moe_forward_cached: null cache state");
+    const BlobGeom g = blob_geom(H, I, K);
+    const int P = M * topk;
+    if (P > kMaxPairs) return fail(EXL3_EUNSUPPORTED, "moe_forward_cached: %d picks > %d", P, kMaxPairs);
+    EnsureArgs ea{};
+    ea.ids = topk_ids;
+    ea.w = topk_w;
+    ea.P = P;
+    ea.layer = layer;
+    ea.E = E;
+    ea.S = n_slots;
+    ea.ptrs_all = ptrs_all;
+    ea.slot_of = slot_of;
+    ea.slot_key = slot_key;
+    ea.slot_last = slot_last;
+    ea.tick = tick;
+    ea.host_base = host_base;
+    ea.slot_base = slot_base;
+    ea.blob = g.blob;
+    ea.hstride = g_cfg.host_stride ? g_cfg.host_stride : g.blob;
+    ea.fill_all = fill_all;
+    ea.fill_list = fill_list;
+    ea.max_fill = std::min(max_fill, E);
+    ea.ram_res = g_cfg.ram_res;
+    ea.ring = g_cfg.ring;
+    ea.ring_cap = g_cfg.ring_cap;
+    ea.safe = g_cfg.safe;
+    ea.vict = g_cfg.vict;
+    ea.log = g_cfg.log;
+    ea.log_cap = g_cfg.log_cap;
+    hipError_t e = launch_ensure(ea, st);
+    if (e != hipSuccess) return hip_fail(e, "ensure launch");
+    if (g_cfg.vict) {
+        VictimArgs va{};
+        va.vict = g_cfg.vict;
+        va.host_base = host_base;
+        va.slot_base = slot_base;
+        va.blob = g.blob;
+        va.hstride = ea.hstride;
+        va.E = E;
+        va.ram_res = g_cfg.ram_res;
+        va.chunk_bytes = 64 * 1024;
+        const int mv = std::min(std::min(ea.max_fill, E), P);
+        e = launch_victim_copy(va, mv, st);
+        if (e != hipSuccess) return hip_fail(e, "victim copy launch");
+    }
+    int64_t* pl = ptrs_all + (int64_t)layer * E;
+    int64_t* fl = fill_all + (int64_t)layer * E;
+    return forward_impl(x, x_dtype, x_stride, M, H, topk_ids, topk_w, topk, pl, I, K, E, out, out_stride, workspace,
+                        workspace_bytes, st, fl, pl, fl, fill_list);
+}
+
+int exl3_moe_align(const int32_t* topk_ids, const float* topk_w, int M, int topk, int n_experts, int pad, int32_t* ib,
+                   float* fb, void* stream) {
+    (void)topk_ids; (void)topk_w; (void)M; (void)topk; (void)n_experts; (void)pad; (void)ib; (void)fb; (void)stream;
+    return fail(EXL3_EUNSUPPORTED, "moe_align: not built yet");
+}
+
+int exl3_dequant(const uint32_t* trellis, int k_tiles, int n_tiles, int K, uint16_t* out, void* stream) {
+    if (K < 2 || K > 4) return fail(EXL3_EUNSUPPORTED, "dequant: K=%d", K);
+    if (!trellis || !out || k_tiles <= 0 || n_tiles <= 0) return fail(EXL3_EINVAL, "dequant: bad arguments");
+    if ((K & 1) && n_tiles % 4) return fail(EXL3_EINVAL, "dequant: PLANAR4 needs n_tiles %% 4 == 0");
+    hipError_t e = launch_dequant(K, trellis, (_Float16*)out, k_tiles, n_tiles, (hipStream_t)stream);
+    if (e != hipSuccess) return hip_fail(e, "dequant launch");
+    return EXL3_OK;
+}
+
+void* exl3_host_alloc(int64_t nbytes) {
+    void* p = nullptr;
+    if (nbytes <= 0) {
+        fail(EXL3_EINVAL, "host_alloc: %lld bytes", (long long)nbytes);
+        return nullptr;
+    }
+    hipError_t e = hipHostMalloc(&p, (size_t)nbytes, hipHostMallocDefault);
+    if (e != hipSuccess) {
+        hip_fail(e, "hipHostMalloc");
+        return nullptr;
+    }
+    return p;
+}
+
+int exl3_host_free(void* p) {
+    if (!p) return EXL3_OK;
+    hipError_t e = hipHostFree(p);
+    return e == hipSuccess ? EXL3_OK : hip_fail(e, "hipHostFree");
+}
+
+int exl3_usm_kind(const void* p) {
+    hipPointerAttribute_t at;
+    if (hipPointerGetAttributes(&at, p) != hipSuccess) {
+        (void)hipGetLastError();
+        return 0;
+    }
+    switch (at.type) {
+        case hipMemoryTypeHost: return 1;
+        case hipMemoryTypeDevice: return 2;
+        case hipMemoryTypeManaged: return 3;
+        default: return 0;
+    }
+}
+
+int exl3_memcpy_async(void* dst, const void* src, int64_t nbytes, void* stream) {
+    if (nbytes < 0 || (nbytes && (!dst || !src))) return fail(EXL3_EINVAL, "memcpy_async: bad arguments");
+    if (!nbytes) return EXL3_OK;
+    hipError_t e = hipMemcpyAsync(dst, src, (size_t)nbytes, hipMemcpyDefault, (hipStream_t)stream);
+    return e == hipSuccess ? EXL3_OK : hip_fail(e, "hipMemcpyAsync");
+}
+
+}  // extern "C"

@@ -1,0 +1,176 @@
+// torch.ops.exl3xpu_moe: the reference's op schemas (kernels/moe-a8/exl3_moe.a8.sycl:1555-1592) implemented on the HIP
+// dispatch key (DispatchKey::CUDA under PyTorch-ROCm) as thin wrappers over the C-ABI of libexl3moe.so.
+// Shape/dtype checks raise RuntimeError like the reference's TORCH_CHECKs (a8:1266-1271).
+#include <ATen/hip/HIPContext.h>
+#include <c10/hip/HIPStream.h>
+#include <torch/all.h>
+#include <torch/library.h>
+
+#include "../../include/exl3moe.h"
+
+namespace {
+
+void* cur_stream(const at::Tensor& like) {
+    return (void*)c10::hip::getCurrentHIPStream(like.device().index()).stream();
+}
+
+void check(int rc, const char* what) { TORCH_CHECK(rc == EXL3_OK, what, ": ", exl3_last_error()); }
+
+int dtype_code(const at::Tensor& x) {
+    if (x.scalar_type() == at::kBFloat16) return EXL3_DT_BF16;
+    if (x.scalar_type() == at::kHalf) return EXL3_DT_F16;
+    if (x.scalar_type() == at::kFloat) return EXL3_DT_F32;
+    TORCH_CHECK(false, "x dtype: bf16, fp16 or fp32 expected, got ", x.scalar_type());
+}
+
+at::Tensor moe_forward(at::Tensor x, at::Tensor topk_ids, at::Tensor topk_w, at::Tensor ptrs, int64_t I, int64_t K,
+                       int64_t n_experts) {
+    TORCH_CHECK(x.dim() == 2 && x.stride(1) == 1, "moe_forward: x must be [M, H] with unit column stride");
+    TORCH_CHECK(topk_ids.scalar_type() == at::kInt && topk_ids.is_contiguous(), "moe_forward: topk_ids int32 contiguous");
+    TORCH_CHECK(topk_w.scalar_type() == at::kFloat && topk_w.is_contiguous(), "moe_forward: topk_w fp32 contiguous");
+    TORCH_CHECK(ptrs.scalar_type() == at::kLong && ptrs.is_contiguous(), "moe_forward: ptrs int64 contiguous");
+    const int M = (int)x.size(0), H = (int)x.size(1), topk = (int)topk_ids.size(-1);
+    TORCH_CHECK(topk_ids.numel() == (int64_t)M * topk && topk_w.numel() == topk_ids.numel(), "moe_forward: ids/w [M, topk]");
+    TORCH_CHECK(ptrs.numel() >= n_experts, "moe_forward: ptrs [n_experts]");
+    auto out = at::empty_like(x);
+    if (M == 0) return out;
+    const size_t ws = exl3_moe_forward_workspace(M, H, (int)I, topk);
+    auto w = at::empty({(int64_t)ws}, x.options().dtype(at::kByte));
+    check(exl3_moe_forward(x.data_ptr(), dtype_code(x), x.stride(0), M, H, topk_ids.data_ptr<int>(),
+                           topk_w.data_ptr<float>(), topk, ptrs.data_ptr<int64_t>(), (int)I, (int)K, (int)n_experts,
+                           out.data_ptr(), out.stride(0), w.data_ptr(), ws, cur_stream(x)),
+          "moe_forward");
+    return out;
+}
+
+at::Tensor moe_forward_cached(at::Tensor x, at::Tensor topk_ids, at::Tensor topk_w, at::Tensor ptrs_all, int64_t layer,
+                              at::Tensor slot_of, at::Tensor slot_key, at::Tensor slot_last, at::Tensor tick,
+                              at::Tensor host_base, int64_t slot_base, at::Tensor fill_all, at::Tensor fill_list,
+                              int64_t max_fill, int64_t I, int64_t K, int64_t n_experts, at::Tensor pend,
+                              at::Tensor done_seq) {
+    (void)pend;
+    (void)done_seq;     // copy-engine prefetch commits are not built (the prefetch worker is not part of this library)
+    TORCH_CHECK(x.dim() == 2 && x.stride(1) == 1, "moe_forward_cached: x must be [M, H] with unit column stride");
+    TORCH_CHECK(ptrs_all.scalar_type() == at::kLong && fill_all.scalar_type() == at::kLong &&
+                    slot_of.scalar_type() == at::kInt,
+                "moe_forward_cached: ptrs_all/fill_all int64, slot_of int32");
+    TORCH_CHECK(topk_ids.scalar_type() == at::kInt && topk_ids.is_contiguous() && topk_w.scalar_type() == at::kFloat &&
+                    topk_w.is_contiguous(),
+                "tier mask: int32 ids, fp32 w");
+    const int M = (int)x.size(0), H = (int)x.size(1), topk = (int)topk_ids.size(-1);
+    TORCH_CHECK(topk_ids.numel() == (int64_t)M * topk && topk_w.numel() == topk_ids.numel(), "moe_forward_cached: ids/w [M, topk]");
+    TORCH_CHECK(ptrs_all.numel() >= (layer + 1) * n_experts && slot_of.numel() == ptrs_all.numel() &&
+                    fill_all.numel() == ptrs_all.numel() && host_base.numel() > layer &&
+                    fill_list.numel() >= 1 + n_experts && slot_last.numel() == slot_key.numel(),
+                "moe_forward_cached: cache state sizes");
+    auto out = at::empty_like(x);
+    if (M == 0) return out;
+    const size_t ws = exl3_moe_forward_workspace(M, H, (int)I, topk);
+    auto w = at::empty({(int64_t)ws}, x.options().dtype(at::kByte));
+    check(exl3_moe_forward_cached(x.data_ptr(), dtype_code(x), x.stride(0), M, H, topk_ids.data_ptr<int>(),
+                                  topk_w.data_ptr<float>(), topk, ptrs_all.data_ptr<int64_t>(), (int)layer,
+                                  slot_of.data_ptr<int>(), slot_key.data_ptr<int>(), slot_last.data_ptr<int>(),
+                                  tick.data_ptr<int>(), (int)slot_key.numel(), host_base.data_ptr<int64_t>(), slot_base,
+                                  fill_all.data_ptr<int64_t>(), fill_list.data_ptr<int>(), (int)max_fill, (int)I,
+                                  (int)K, (int)n_experts, out.data_ptr(), out.stride(0), w.data_ptr(), ws,
+                                  cur_stream(x)),
+          "moe_forward_cached");
+    return out;
+}
+
+std::vector<at::Tensor> moe_align(at::Tensor topk_ids, at::Tensor topk_w, int64_t n_experts, int64_t pad) {
+    TORCH_CHECK(topk_ids.scalar_type() == at::kInt && topk_ids.is_contiguous() && topk_ids.dim() == 2, "moe_align: ids");
+    TORCH_CHECK(topk_w.scalar_type() == at::kFloat && topk_w.is_contiguous(), "moe_align: w");
+    const int M = (int)topk_ids.size(0), topk = (int)topk_ids.size(1), npairs = M * topk;
+    const int A = std::min(npairs, (int)n_experts);
+    auto ib = at::empty({4 * A + 1 + 2 * npairs + 16}, topk_ids.options());
+    auto fb = at::empty({npairs}, topk_w.options());
+    check(exl3_moe_align(topk_ids.data_ptr<int>(), topk_w.data_ptr<float>(), M, topk, (int)n_experts, (int)pad,
+                         ib.data_ptr<int>(), fb.data_ptr<float>(), cur_stream(topk_ids)),
+          "moe_align");
+    return {ib, fb};
+}
+
+at::Tensor host_alloc(int64_t nbytes) {
+    void* p = exl3_host_alloc(nbytes);
+    TORCH_CHECK(p, "host_alloc failed for ", nbytes, " bytes: ", exl3_last_error());
+    return at::from_blob(p, {nbytes}, [](void* q) { exl3_host_free(q); },
+                         at::TensorOptions().dtype(at::kByte).device(at::kCPU));
+}
+
+int64_t usm_kind(int64_t ptr) { return exl3_usm_kind(reinterpret_cast<const void*>(ptr)); }
+
+void memcpy_async(int64_t dst, int64_t src, int64_t nbytes) {
+    void* s = (void*)c10::hip::getCurrentHIPStream().stream();
+    check(exl3_memcpy_async(reinterpret_cast<void*>(dst), reinterpret_cast<const void*>(src), nbytes, s), "memcpy_async");
+}
+
+int64_t blob_bytes(int64_t H, int64_t I, int64_t K) { return exl3_blob_bytes((int)H, (int)I, (int)K); }
+
+void moe_set_splits(int64_t gu_p, int64_t dn_p) { check(exl3_set_splits(gu_p, dn_p), "moe_set_splits"); }
+void moe_set_mr(int64_t mr) { check(exl3_set_mr(mr), "moe_set_mr"); }
+void moe_set_debug(int64_t v) { check(exl3_set_debug(v), "moe_set_debug"); }
+void moe_set_pair_max_m(int64_t v) { check(exl3_set_pair_max_m(v), "moe_set_pair_max_m"); }
+void moe_set_prefill_min_m(int64_t v) { check(exl3_set_prefill_min_m(v), "moe_set_prefill_min_m"); }
+void moe_set_victims(at::Tensor v) {
+    if (!v.numel()) return check(exl3_set_victims(nullptr), "moe_set_victims");
+    TORCH_CHECK(v.scalar_type() == at::kInt && v.is_cuda(), "moe_set_victims: device int32 tensor");
+    check(exl3_set_victims(v.data_ptr<int>()), "moe_set_victims");
+}
+void moe_set_tier(at::Tensor ram_res, at::Tensor miss, at::Tensor safe) {
+    if (!ram_res.numel()) return check(exl3_set_tier(nullptr, nullptr, 0, nullptr), "moe_set_tier");
+    TORCH_CHECK(ram_res.scalar_type() == at::kByte && miss.scalar_type() == at::kInt && safe.scalar_type() == at::kInt,
+                "moe_set_tier: uint8 ram_res, int32 miss ring, int32 safe");
+    check(exl3_set_tier(ram_res.data_ptr<uint8_t>(), miss.data_ptr<int>(), miss.numel(), safe.data_ptr<int>()),
+          "moe_set_tier");
+}
+void moe_set_host_stride(int64_t s) { check(exl3_set_host_stride(s), "moe_set_host_stride"); }
+// pinned host memory is device-mapped on MI355X: nothing to prefetch (the reference maps xe-SVM pages, a8:777-781)
+void moe_svm_prefetch(at::Tensor ptrs, int64_t nbytes, at::Tensor like) {
+    (void)ptrs;
+    (void)nbytes;
+    (void)like;
+}
+void moe_set_decision_log(at::Tensor buf) {
+    if (!buf.numel()) return check(exl3_set_decision_log(nullptr, 0), "moe_set_decision_log");
+    TORCH_CHECK(buf.scalar_type() == at::kInt && buf.is_cuda() && buf.is_contiguous(), "decision log: device int32");
+    check(exl3_set_decision_log(buf.data_ptr<int>(), 1 << 30), "moe_set_decision_log");
+}
+at::Tensor dequant(at::Tensor trellis, int64_t k_tiles, int64_t n_tiles, int64_t K) {
+    TORCH_CHECK(trellis.is_cuda() && trellis.is_contiguous(), "dequant: contiguous device words");
+    auto out = at::empty({16 * k_tiles, 16 * n_tiles}, trellis.options().dtype(at::kHalf));
+    check(exl3_dequant(reinterpret_cast<const uint32_t*>(trellis.data_ptr()), (int)k_tiles, (int)n_tiles, (int)K,
+                       reinterpret_cast<uint16_t*>(out.data_ptr()), cur_stream(trellis)),
+          "dequant");
+    return out;
+}
+
+}  // namespace
+
+TORCH_LIBRARY(exl3xpu_moe, m) {
+    m.def("moe_forward(Tensor x, Tensor topk_ids, Tensor topk_w, Tensor ptrs, int I, int K, int n_experts) -> Tensor");
+    m.impl("moe_forward", c10::DispatchKey::CUDA, &moe_forward);
+    m.def("moe_forward_cached(Tensor x, Tensor(i!) topk_ids, Tensor(j!) topk_w, Tensor(a!) ptrs_all, int layer, "
+          "Tensor(b!) slot_of, Tensor(c!) slot_key, Tensor(d!) slot_last, Tensor(e!) tick, Tensor host_base, "
+          "int slot_base, Tensor(f!) fill_all, Tensor(g!) fill_list, int max_fill, int I, int K, int n_experts, "
+          "Tensor(h!) pend, Tensor done_seq) -> Tensor");
+    m.impl("moe_forward_cached", c10::DispatchKey::CUDA, &moe_forward_cached);
+    m.def("moe_align(Tensor topk_ids, Tensor topk_w, int n_experts, int pad) -> Tensor[]");
+    m.impl("moe_align", c10::DispatchKey::CUDA, &moe_align);
+    m.def("host_alloc(int nbytes) -> Tensor", &host_alloc);
+    m.def("usm_kind(int ptr) -> int", &usm_kind);
+    m.def("memcpy_async(int dst, int src, int nbytes) -> ()", &memcpy_async);
+    m.def("blob_bytes(int H, int I, int K) -> int", &blob_bytes);
+    m.def("moe_set_splits(int gu_p, int dn_p) -> ()", &moe_set_splits);
+    m.def("moe_set_mr(int mr) -> ()", &moe_set_mr);
+    m.def("moe_set_debug(int v) -> ()", &moe_set_debug);
+    m.def("moe_set_pair_max_m(int v) -> ()", &moe_set_pair_max_m);
+    m.def("moe_set_prefill_min_m(int v) -> ()", &moe_set_prefill_min_m);
+    m.def("moe_set_victims(Tensor v) -> ()", &moe_set_victims);
+    m.def("moe_set_tier(Tensor ram_res, Tensor miss, Tensor safe) -> ()", &moe_set_tier);
+    m.def("moe_set_host_stride(int s) -> ()", &moe_set_host_stride);
+    m.def("moe_svm_prefetch(Tensor ptrs, int nbytes, Tensor like) -> ()", &moe_svm_prefetch);
+    m.def("moe_set_decision_log(Tensor buf) -> ()", &moe_set_decision_log);
+    m.def("dequant(Tensor trellis, int k_tiles, int n_tiles, int K) -> Tensor");
+    m.impl("dequant", c10::DispatchKey::CUDA, &dequant);
+}

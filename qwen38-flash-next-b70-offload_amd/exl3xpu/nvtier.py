@@ -1,0 +1,427 @@
+"""RAM expert tier for the MI355X device-managed expert cache (reference plugin/exl3xpu/nvtier.py).
+
+Tiers: HBM slots (device LRU, write-through on miss) -> RAM tier (one pinned, device-mapped host arena with a fixed
+address per expert, read zero-copy by the kernels) -> expert store (all experts; a pluggable fill source with a
+deterministic completion latency in host steps, standing in for the reference's O_DIRECT NVMe reads).
+
+Device side (csrc/moe_cache.hip): picks whose expert is in neither HBM nor RAM are masked to (safe expert, weight 0) and
+logged to a miss ring; HBM victims whose RAM copy is not valid are written back to their RAM address and flagged.
+Host side (call step() after every decode step): consume the previous step's device snapshot, complete fills, admit the
+most-missed keys into free budget, evict RAM copies of HBM-resident experts first and then keys older than AGE steps,
+and upload the changed flags. The RAM arena is never unmapped, so an evicted key's bytes stay readable: the reference's
+punch/write-back race (its docs/results.md:164-172) cannot corrupt data here; "punch" is bookkeeping only.
+"""
+from __future__ import annotations
+
+import ctypes
+import logging
+import os
+import time
+from concurrent.futures import ThreadPoolExecutor
+
+import numpy as np
+import torch
+
+from .moe_offload import ExpertStore, s64
+
+MiB2 = 2 << 20
+log = logging.getLogger("exl3xpu")
+
+
+class TierStore(ExpertStore):
+    """ExpertStore whose host copies live at fixed-stride addresses of one pinned arena (the reference uses a sparse
+    2 MiB-stride memfd, nvtier.py:22-53). stride defaults to the blob size rounded up to 4 KiB."""
+
+    def __init__(self, H, I, K, E, n_slots, n_layers, stride=None, device=None):
+        super().__init__(H, I, K, E, n_slots, device=device, max_layers=n_layers)
+        self.stride = int(stride) if stride else (self.blob + 4095) // 4096 * 4096
+        assert self.blob <= self.stride and self.stride % 16 == 0
+        self.L = n_layers
+        self.size = n_layers * E * self.stride
+        self.arena = self.X.host_alloc(self.size)
+        self.base = s64(self.arena.data_ptr())
+        self.X.moe_set_host_stride(self.stride)
+
+    def add_layer(self, key, blobs=None):
+        li = len(self.layer_index)
+        if li >= self.L:
+            raise RuntimeError(f"TierStore: more than n_layers={self.L} MoE layers")
+        self.layer_index[key] = li
+        base = self.base + li * self.E * self.stride
+        self._host_ptr[key] = base + torch.arange(self.E, dtype=torch.int64) * self.stride
+        self.ptrs_all[li * self.E:(li + 1) * self.E].copy_(self._host_ptr[key])
+        self.host_base[li] = base
+        self.slot_of[key] = torch.full((self.E,), -1, dtype=torch.int32)
+        if blobs is not None:
+            for e in range(self.E):
+                self.arena[(li * self.E + e) * self.stride:(li * self.E + e) * self.stride + self.blob].copy_(blobs[e])
+        return None
+
+    def addr(self, key: int) -> int:                       # key = li * E + e
+        return self.base + key * self.stride
+
+    def host_view(self, key):
+        li = self.layer_index[key]
+        return self.arena[li * self.E * self.stride:(li + 1) * self.E * self.stride].view(self.E, self.stride)[:, :self.blob]
+
+
+class SyntheticExpertSource:
+    """Deterministic stand-in for the packed NVMe store (serve/pack_store.py): record r holds the blob of synthetic
+    expert r % n_distinct of workload `seed`; `read(r, dst)` copies it to a host address."""
+
+    def __init__(self, H, I, K, seed: int, n_distinct: int = 64):
+        from .synth import expert_blob
+        self.blob = int(expert_blob(seed, 0, H, I, K).numel())
+        self.n = n_distinct
+        self.buf = np.stack([expert_blob(seed, i, H, I, K).numpy() for i in range(n_distinct)])
+        self.rec = self.blob
+
+    def read(self, rec_index: int, dst: int) -> None:
+        src = self.buf[rec_index % self.n]
+        ctypes.memmove(dst, src.ctypes.data, self.blob)
+
+    def blob_of(self, rec_index: int) -> np.ndarray:
+        return self.buf[rec_index % self.n]
+
+
+class NvTier:
+    """Tier base: flags, miss ring, pinned safe expert per layer (nvtier.py:56-87).
+    source: object with read(rec_index, dst_addr) (an NVMe store reader or SyntheticExpertSource).
+    ram_budget: bytes (records = bytes // stride, like the reference) or, with budget_records, a record count."""
+
+    def __init__(self, store: TierStore, source, meta=None, ram_budget_bytes=2 << 30, ring_cap=1 << 16, safe=0,
+                 dev=None, ckpt_layer=None, budget_records: int | None = None, latency: int = 8):
+        self.st, self.E = store, store.E
+        self.src = source
+        self.L = len(ckpt_layer) if ckpt_layer is not None else store.L
+        self.ckpt = np.asarray(ckpt_layer if ckpt_layer is not None else range(self.L), dtype=np.int64)
+        self.dev = dev or store.dev
+        self.blob = store.blob
+        self.budget = int(budget_records) if budget_records else max(1, int(ram_budget_bytes // store.stride))
+        self.latency = max(1, int(latency))
+        n = self.L * self.E
+        self.res_dev = torch.zeros(n, dtype=torch.uint8, device=self.dev)
+        self.ring = torch.zeros(1 + ring_cap, dtype=torch.int32, device=self.dev)
+        self.safe = torch.full((self.L,), safe, dtype=torch.int32, device=self.dev)
+        self.vict = torch.zeros(1 + 2 * self.E, dtype=torch.int32, device=self.dev)
+        self.res = np.zeros(n, dtype=np.uint8)
+        self.pinned = set(li * self.E + safe for li in range(self.L))
+        self.ring_seen = 0
+        self.stats = dict(nvme_reads=0, nvme_ms=0.0, evicts=0, masked=0, steps=0, fill_ms=0.0, ring_overflow=0)
+        for k in sorted(self.pinned):
+            self._fill(k)
+        self.res_dev.copy_(torch.from_numpy(self.res))
+        X = store.X
+        X.moe_set_tier(self.res_dev, self.ring, self.safe)
+        if os.environ.get("EXL3_NVTIER_NO_VICTIM", "0") != "1":
+            X.moe_set_victims(self.vict)
+        else:
+            X.moe_set_victims(torch.zeros(0, dtype=torch.int32, device=self.dev))
+
+    def close(self):
+        X = self.st.X
+        X.moe_set_tier(torch.zeros(0, dtype=torch.uint8, device=self.dev), torch.zeros(0, dtype=torch.int32, device=self.dev),
+                       torch.zeros(0, dtype=torch.int32, device=self.dev))
+        X.moe_set_victims(torch.zeros(0, dtype=torch.int32, device=self.dev))
+        X.moe_set_host_stride(0)
+
+    def rec_index(self, key: int) -> int:
+        return int(self.ckpt[key // self.E]) * self.E + key % self.E
+
+    def _fill(self, key: int) -> None:
+        t = time.perf_counter()
+        self.src.read(self.rec_index(key), self.st.addr(key))
+        self.res[key] = 1
+        self.stats["nvme_reads"] += 1
+        self.stats["nvme_ms"] += (time.perf_counter() - t) * 1e3
+
+    def fill_many(self, keys) -> None:
+        keys = [int(k) for k in keys]
+        if not keys:
+            return
+        if not hasattr(self, "_pool"):
+            self._pool = ThreadPoolExecutor(int(os.environ.get("EXL3_NVTIER_FILL_THREADS", "16")))
+        t = time.perf_counter()
+        list(self._pool.map(lambda k: self.src.read(self.rec_index(k), self.st.addr(k)), keys))
+        for k in keys:
+            self.res[k] = 1
+        self.stats["nvme_reads"] += len(keys)
+        self.stats["nvme_ms"] += (time.perf_counter() - t) * 1e3
+
+    def ram_bytes(self) -> int:
+        return int(self.res.sum()) * self.st.stride
+
+    def warm(self, keys_ckpt, max_bytes):
+        """Fill the RAM tier with the hottest experts (checkpoint keys, hottest first) up to max_bytes
+        (nvtier.py:492-509)."""
+        inv = {int(c): li for li, c in enumerate(self.ckpt)}
+        t = time.perf_counter()
+        cap = int(max_bytes // self.st.stride)
+        have = int(self.res.sum())
+        todo, seen = [], set()
+        for kc in keys_ckpt:
+            if have + len(todo) >= cap:
+                break
+            li = inv.get(int(kc) // self.E)
+            if li is None:
+                continue
+            k = li * self.E + int(kc) % self.E
+            if not self.res[k] and k not in seen:
+                todo.append(k)
+                seen.add(k)
+        self.fill_many(todo)
+        if hasattr(self, "age"):
+            self.age[todo] = 0
+        self.res_dev.copy_(torch.from_numpy(self.res))
+        return len(todo), time.perf_counter() - t
+
+    def log_stats(self, logger=None, every=200):
+        logger = logger or log
+        if self.stats["steps"] % every or not self.stats["steps"]:
+            return
+        b = getattr(self, "_last", None) or {k: 0 for k in self.stats}
+        d = {k: self.stats.get(k, 0) - b.get(k, 0) for k in self.stats}
+        n = max(1, d.get("steps", 0))
+        logger.info("exl3xpu: nvtier last %d steps: masked/step %.2f fills/step %.2f evicts/step %.1f host ms/step %.2f "
+                    "admit_dropped %d ram %.2f GB", n, d.get("masked", 0) / n, d.get("nvme_reads", 0) / n,
+                    d.get("evicts", 0) / n, d.get("fill_ms", 0) / n, d.get("admit_dropped", 0), self.ram_bytes() / 2 ** 30)
+        self._last = dict(self.stats)
+
+
+class NvTierFast(NvTier):
+    """Vectorised bookkeeping + background fills (nvtier.py:175-278): age, in-flight set, pinned mask; fills complete
+    `latency` host steps after admission (deterministic)."""
+
+    def __init__(self, *a, **k):
+        super().__init__(*a, **k)
+        n = self.L * self.E
+        self.age = np.zeros(n, dtype=np.int64)
+        self.tick = 1
+        self.pin_mask = np.zeros(n, dtype=bool)
+        self.pin_mask[list(self.pinned)] = True
+        self.inflight = np.zeros(n, dtype=bool)
+        self._pending = {}                 # host step -> [(key, future)]
+        self._hstep = 0
+        self._pool = ThreadPoolExecutor(int(os.environ.get("EXL3_NVTIER_FILL_THREADS", "16")))
+
+    def _queue_fill(self, key: int, hs: int) -> None:
+        """fill admitted at host step hs: copied by a worker, flagged resident at host step hs + latency"""
+        fut = self._pool.submit(self.src.read, self.rec_index(key), self.st.addr(key))
+        self._pending.setdefault(hs + self.latency, []).append((key, fut))
+        self.stats["nvme_reads"] += 1
+
+    def _completed(self, hs: int):
+        done = []
+        for key, fut in self._pending.pop(hs, []):
+            fut.result()
+            done.append(key)
+        return done
+
+    def close(self):
+        self._pool.shutdown(wait=True)
+        super().close()
+
+
+class AdmissionPolicy:
+    """Host bookkeeping of the admission-controlled tier step (_async_step_admit, nvtier.py:708-806), pure numpy.
+
+    decide() consumes the device state of the PREVIOUS step (flags with the previous upload overlaid, miss ring, HBM
+    residency) plus the keys whose fills completed now, and returns (admitted keys, evicted keys, flag diff keys, flag
+    diff values). Ordering contract: misses by descending count, ties by ascending key; evictions by ascending age,
+    ties by ascending key (the reference's numpy argsort default is not stable)."""
+
+    def __init__(self, n, pinned, budget, age=4, qmax=256, ring_cap=1 << 16):
+        self.n, self.budget, self.admit_age, self.admit_qmax, self.cap = n, int(budget), int(age), int(qmax), int(ring_cap)
+        self.res = np.zeros(n, dtype=np.uint8)
+        self.age = np.zeros(n, dtype=np.int64)
+        self.inflight = np.zeros(n, dtype=bool)
+        self.pin_mask = np.zeros(n, dtype=bool)
+        self.pin_mask[list(pinned)] = True
+        self.res[list(pinned)] = 1
+        self.tick = 1
+        self.ring_seen = 0
+        self.stats = dict(masked=0, evicts=0, admit_dropped=0, ring_overflow=0)
+
+    def decide(self, view, ring, vram, done_keys):
+        newly = (view == 1) & (self.res == 0)        # victims written back by the device: newest RAM entries
+        self.age[newly] = self.tick
+        res = self.res.copy()
+        res[newly] = 1
+        for kk in done_keys:
+            res[kk] = 1
+            self.age[kk] = self.tick
+            self.inflight[kk] = False
+        cnt = int(ring[0])
+        newm = cnt - self.ring_seen
+        if newm > self.cap:
+            self.stats["ring_overflow"] += newm - self.cap
+            newm = self.cap
+        want = np.zeros(0, dtype=np.int64)
+        if newm > 0:
+            lo, hi = (cnt - newm) % self.cap, cnt % self.cap
+            r = ring[1:]
+            keys = np.concatenate([r[lo:], r[:hi]]) if hi <= lo else r[lo:hi]
+            u, c = np.unique(keys[:newm].astype(np.int64), return_counts=True)
+            ok = (res[u] == 0) & (~self.inflight[u])
+            u, c = u[ok], c[ok]
+            want = u[np.argsort(-c, kind="stable")]
+        self.ring_seen = cnt
+        self.stats["masked"] += max(0, newm)
+        inflight_n = int(self.inflight.sum())
+        over = int(res.sum()) + inflight_n + len(want) - self.budget
+        ev_keys = np.zeros(0, dtype=np.int64)
+        if over > 0:
+            cand1 = np.nonzero((res == 1) & vram & ~self.pin_mask)[0]
+            take1 = cand1[np.argsort(self.age[cand1], kind="stable")[:over]]
+            over -= len(take1)
+            take2 = np.zeros(0, dtype=np.int64)
+            if over > 0:
+                m = (res == 1) & ~self.pin_mask & (self.age <= self.tick - self.admit_age)
+                m[take1] = False
+                cand2 = np.nonzero(m)[0]
+                take2 = cand2[np.argsort(self.age[cand2], kind="stable")[:over]]
+            ev_keys = np.concatenate([take1, take2]).astype(np.int64)
+            res[ev_keys] = 0
+            self.stats["evicts"] += len(ev_keys)
+        free = min(self.budget - int(res.sum()) - inflight_n, self.admit_qmax - inflight_n)
+        adm = want[:max(0, free)].astype(np.int64)
+        self.stats["admit_dropped"] += len(want) - len(adm)
+        self.inflight[adm] = True
+        diff = np.nonzero(res != view)[0].astype(np.int64)
+        self.res = res
+        return adm, ev_keys, diff, res[diff].copy()
+
+
+class NvTierAsync(NvTierFast):
+    """One-step-lagged, event-ordered bookkeeping without a per-step device sync (nvtier.py:282-386) with the
+    admission policy (AdmissionPolicy): AGE = EXL3_NVTIER_ADMIT_AGE (default 4), QMAX = EXL3_NVTIER_ADMIT_QMAX
+    (default 256). Host step n snapshots the device state after decode step n and acts on the snapshot of step n-1."""
+
+    def __init__(self, *a, **k):
+        super().__init__(*a, **k)
+        n = self.L * self.E
+        self._n = n
+        self._h_res = [torch.empty(n, dtype=torch.uint8).pin_memory() for _ in range(2)]
+        self._h_ring = [torch.empty(self.ring.numel(), dtype=torch.int32).pin_memory() for _ in range(2)]
+        self._h_slot = [torch.empty(n, dtype=torch.int32).pin_memory() for _ in range(2)]
+        self._snap_ev = [None, None]
+        self._k = 0
+        self._last_diff = None
+        self.policy = AdmissionPolicy(n, self.pinned, self.budget, int(os.environ.get("EXL3_NVTIER_ADMIT_AGE", "4")),
+                                      int(os.environ.get("EXL3_NVTIER_ADMIT_QMAX", "256")), self.ring.numel() - 1)
+        self.policy.res[:] = self.res
+        self.res = self.policy.res
+        self.log_decisions = False
+        self.decisions = []                # (admitted keys, evicted keys) per step when log_decisions
+
+    @property
+    def inflight_keys(self):
+        return np.nonzero(self.policy.inflight)[0]
+
+    def step(self) -> int:
+        t0 = time.perf_counter()
+        pol = self.policy
+        pol.tick += 1
+        self.tick = pol.tick
+        hs = self._hstep
+        self._hstep += 1
+        n = self._n
+        cur = torch.cuda.current_stream(self.dev)
+        k = self._k
+        self._k ^= 1
+        self._h_res[k].copy_(self.res_dev[:n], non_blocking=True)
+        self._h_ring[k].copy_(self.ring, non_blocking=True)
+        self._h_slot[k].copy_(self.st.slot_of_dev[:n], non_blocking=True)
+        ev = torch.cuda.Event()
+        ev.record(cur)
+        self._snap_ev[k] = ev
+        j = k ^ 1
+        if self._snap_ev[j] is None:
+            self.stats["steps"] += 1
+            if self.log_decisions:
+                self.decisions.append((np.zeros(0, np.int64), np.zeros(0, np.int64)))
+            return 0
+        self._snap_ev[j].synchronize()
+        view = self._h_res[j].numpy().copy()
+        if self._last_diff is not None:
+            dk, dv = self._last_diff
+            view[dk] = dv
+        ring = self._h_ring[j].numpy()
+        vram = self._h_slot[j].numpy() >= 0
+        seen0 = pol.ring_seen
+        adm, ev_keys, diff, vals = pol.decide(view, ring, vram, self._completed(hs))
+        for kk in adm.tolist():
+            self._queue_fill(kk, hs)
+        if len(diff):
+            idx = torch.from_numpy(diff).pin_memory().to(self.dev, non_blocking=True)
+            val = torch.from_numpy(vals).pin_memory().to(self.dev, non_blocking=True)
+            self.res_dev.index_copy_(0, idx, val)
+            self._last_diff = (diff, vals)
+        else:
+            self._last_diff = None
+        self.res = pol.res
+        self.age, self.inflight, self.ring_seen = pol.age, pol.inflight, pol.ring_seen
+        if self.log_decisions:
+            self.decisions.append((adm.copy(), ev_keys.copy()))
+        for key in ("masked", "evicts", "admit_dropped", "ring_overflow"):
+            self.stats[key] = pol.stats[key]
+        self.stats["steps"] += 1
+        self.stats["fill_ms"] += (time.perf_counter() - t0) * 1e3
+        return int(max(0, pol.ring_seen - seen0))
+
+
+def _ensure_for_prefill(self, li, ids):
+    """Prefill: synchronously make every expert this layer's batch uses RAM-resident and flag it on the device, so
+    the prefill kernel can read it zero-copy (nvtier.py:389-457). Evicts, in order: prefill-only fills of other
+    layers, RAM copies of HBM-resident experts, the oldest; never this layer's keys, pinned keys or in-flight fills.
+    Ties by ascending key (stable sort)."""
+    n = self.L * self.E
+    if not hasattr(self, "transient"):
+        self.transient = np.zeros(n, dtype=bool)
+    keys = np.unique(ids.reshape(-1).to("cpu", torch.int64).numpy()) + li * self.E
+    miss = keys[self.res[keys] == 0]
+    if len(miss):
+        inflight = getattr(self, "inflight", np.zeros(n, dtype=bool))
+        over = int(self.res.sum()) + int(inflight.sum()) + len(miss) - self.budget
+        if over > 0:
+            torch.cuda.synchronize(self.dev)
+            res_d = self.res_dev.cpu().numpy()
+            newly = (res_d == 1) & (self.res == 0)
+            self.res[newly] = 1
+            if hasattr(self, "age"):
+                self.age[newly] = self.tick
+            age = getattr(self, "age", np.zeros(n, dtype=np.int64))
+            ok = (self.res == 1) & ~inflight
+            ok[list(self.pinned)] = False
+            ok[keys] = False
+            vram = self.st.slot_of_dev[:n].cpu().numpy() >= 0
+            ev = []
+            for m in (ok & self.transient, ok & ~self.transient & vram, ok & ~self.transient & ~vram):
+                if over <= 0:
+                    break
+                c = np.nonzero(m)[0]
+                c = c[np.argsort(age[c], kind="stable")[:over]]
+                ev.append(c)
+                over -= len(c)
+            ev = np.concatenate(ev) if ev else np.zeros(0, dtype=np.int64)
+            if len(ev):
+                self.res[ev] = 0
+                self.transient[ev] = False
+                self.res_dev.index_fill_(0, torch.from_numpy(ev.astype(np.int64)).to(self.dev), 0)
+            self.stats["prefill_evicts"] = self.stats.get("prefill_evicts", 0) + len(ev)
+    miss = [int(k) for k in miss]
+    self.fill_many(miss)
+    for k in miss:
+        if hasattr(self, "inflight"):
+            self.inflight[k] = False
+        if hasattr(self, "age"):
+            self.age[k] = self.tick
+        self.transient[k] = True
+    if miss:
+        idx = torch.tensor(miss, dtype=torch.int64).to(self.dev, non_blocking=True)
+        self.res_dev.index_fill_(0, idx, 1)
+    self.stats["prefill_fills"] = self.stats.get("prefill_fills", 0) + len(miss)
+    return len(miss)
+
+
+NvTier.ensure_for_prefill = _ensure_for_prefill

@@ -1,0 +1,47 @@
+"""C-ABI library: loads, exports every function include/exl3moe.h declares, validates arguments on the host (no
+compute calls: this runs without a GPU)."""
+import ctypes
+
+import pytest
+
+from exl3xpu import capi
+
+
+def test_exports_every_declared_symbol():
+    names = capi.declared_functions()
+    assert len(names) >= 20
+    L = ctypes.CDLL(capi.LIB_PATH)
+    missing = [n for n in names if not hasattr(L, n)]
+    assert not missing, missing
+    assert set(names) == set(capi.SIGNATURES), set(names) ^ set(capi.SIGNATURES)
+
+
+def test_blob_bytes():
+    L = capi.lib()
+    assert L.exl3_blob_bytes(2048, 512, 3) == 1_195_008
+    assert L.exl3_blob_bytes(2560, 640, 3) == 1_862_400
+    assert [L.exl3_blob_bytes(4096, 1536, k) for k in (2, 3, 4)] == [4_752_384, 7_111_680, 9_470_976]
+
+
+@pytest.mark.parametrize("H,I,K,E,code", [(100, 512, 3, 512, 1), (2048, 500, 3, 512, 1), (2048, 512, 5, 512, 2),
+                                          (2048, 512, 3, 2048, 1)])
+def test_forward_rejects_bad_geometry(H, I, K, E, code):
+    L = capi.lib()
+    rc = L.exl3_moe_forward(None, 0, 0, 1, H, None, None, 10, None, I, K, E, None, 0, None, 0, None)
+    assert rc == code
+    assert L.exl3_last_error()
+
+
+def test_forward_rejects_bad_dtype_and_workspace():
+    L = capi.lib()
+    assert L.exl3_moe_forward(None, 7, 0, 1, 2048, None, None, 10, None, 512, 3, 512, None, 0, None, 0, None) == 1
+    assert L.exl3_moe_forward(None, 1, 0, 0, 2048, None, None, 10, None, 512, 3, 512, None, 0, None, 0, None) == 0
+    assert L.exl3_moe_forward_workspace(1, 2048, 512, 10) > 0
+
+
+def test_setters():
+    L = capi.lib()
+    assert L.exl3_set_host_stride(7) == 1
+    assert L.exl3_set_host_stride(0) == 0
+    assert L.exl3_set_tier(None, None, 0, None) == 0
+    assert L.exl3_set_pair_max_m(4) == 0 and L.exl3_set_prefill_min_m(256) == 0

@@ -1,0 +1,100 @@
+"""GPU parity of the device expert cache and the RAM tier: every ensure decision (mask set, miss list, victims with
+write-back flags, slot ids, ring count) and every host admission/eviction decision must equal the oracle's, bit for
+bit; outputs through the cache must equal outputs of the plain forward on the post-mask picks, bit for bit."""
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import cache, synth
+
+pytestmark = pytest.mark.gpu
+GOLD = os.path.join(os.path.dirname(__file__), "golden")
+
+
+def _setup(L, E, S, H, I, K, budget, qmax, age, latency, ring_cap, seed):
+    from exl3xpu import nvtier
+    store = nvtier.TierStore(H, I, K, E, S, n_layers=L)
+    for li in range(L):
+        store.add_layer(f"model.layers.{li}.mlp")
+    src = nvtier.SyntheticExpertSource(H, I, K, seed, n_distinct=16)
+    tier = nvtier.NvTierAsync(store, src, ring_cap=ring_cap, budget_records=budget, latency=latency)
+    tier.policy.admit_age, tier.policy.admit_qmax = age, qmax
+    tier.log_decisions = True
+    # reference table: every expert's true blob in HBM (independent of the cache)
+    blobs = torch.from_numpy(src.buf).cuda()
+    ref_ptr = torch.tensor([blobs[r % src.n].data_ptr() for r in range(L * E)], dtype=torch.int64, device="cuda")
+    return store, tier, blobs, ref_ptr
+
+
+def _run(store, tier, ids, w, H, check_out_every=0, ref_ptr=None):
+    """ids/w [steps, L, P]: 48-layer decode steps through forward_cached + the host step; returns the device
+    decision log (records) and optionally checks outputs against the plain forward."""
+    X = store.X
+    steps, L, P = ids.shape
+    rl = cache.rec_len(P)
+    logbuf = torch.zeros(1 + steps * L * rl, dtype=torch.int32, device="cuda")
+    X.moe_set_decision_log(logbuf)
+    x = torch.randn(1, H, generator=torch.Generator().manual_seed(0)).to(torch.bfloat16).cuda()
+    ids_d = torch.from_numpy(ids).cuda()
+    w_d = torch.from_numpy(w).cuda()
+    keys = list(store.layer_index)
+    bad = 0
+    try:
+        for n in range(steps):
+            for li in range(L):
+                it = ids_d[n, li].view(1, P).clone()
+                wt = w_d[n, li].view(1, P).clone()
+                out = store.forward_cached(keys[li], x, it, wt)
+                if check_out_every and n % check_out_every == 0:
+                    E = store.E
+                    ref = X.moe_forward(x, it, wt, ref_ptr[li * E:(li + 1) * E], store.I, store.K, E)
+                    bad += int(not torch.equal(out, ref))
+            tier.step()
+        torch.cuda.synchronize()
+    finally:
+        X.moe_set_decision_log(torch.zeros(0, dtype=torch.int32, device="cuda"))
+    lg = logbuf.cpu().numpy()
+    assert lg[0] == steps * L
+    return lg[1:].reshape(steps, L, rl), bad
+
+
+def test_cache_golden_small():
+    g = np.load(os.path.join(GOLD, "cache_small.npz"))
+    L, E, S, P = int(g["L"]), int(g["E"]), int(g["S"]), int(g["P"])
+    print(f"case cache golden L={L} E={E} S={S}", flush=True)
+    H = I = 128
+    store, tier, blobs, ref_ptr = _setup(L, E, S, H, I, 3, int(g["budget"]), int(g["qmax"]), int(g["age"]),
+                                         int(g["latency"]), int(g["ring_cap"]), 3)
+    recs, bad = _run(store, tier, g["ids"], g["w"], H, check_out_every=1, ref_ptr=ref_ptr)
+    assert np.array_equal(recs, g["recs"])
+    flat, pos = g["host_log"], 0
+    for n, (adm, ev) in enumerate(tier.decisions):
+        na, ne = int(flat[pos]), int(flat[pos + 1])
+        pos += 2
+        assert adm.tolist() == flat[pos:pos + na].tolist(), n
+        assert ev.tolist() == flat[pos + na:pos + na + ne].tolist(), n
+        pos += na + ne
+    assert bad == 0
+    tier.close()
+
+
+def test_cache_config1_trace_bitexact():
+    """48 layers x 512 experts, 8,000 slots, RAM budget 1,075 records, 4,000-step Zipf(1.1) trace of 10 picks per
+    layer, 8-step fill latency, AGE 4, QMAX 256: every device and host decision equals the oracle's. Experts are tiny
+    (H = I = 128): the decisions do not depend on the expert shape."""
+    L, E, S, P, steps = 48, 512, 8000, 10, int(os.environ.get("EXL3_TEST_C1_STEPS", "4000"))
+    print(f"case cache config1 steps={steps}", flush=True)
+    ids, w = synth.zipf_trace(20261202, steps, L, E, P)
+    ids, w = ids[:, :, 0], w[:, :, 0]
+    co = cache.CacheOracle(L, E, S, budget=1075, age=4, qmax=256, latency=8)
+    orecs, olog = co.run(ids, w)
+    store, tier, blobs, ref_ptr = _setup(L, E, S, 128, 128, 3, 1075, 256, 4, 8, 1 << 16, 7)
+    recs, bad = _run(store, tier, ids, w, 128, check_out_every=97, ref_ptr=ref_ptr)
+    mism = np.nonzero((recs != orecs).any(axis=-1))
+    assert mism[0].size == 0, f"first mismatch at step/layer {mism[0][0]}/{mism[1][0]}"
+    for n, ((a1, e1), (a2, e2)) in enumerate(zip(tier.decisions, olog)):
+        assert a1.tolist() == a2.tolist() and e1.tolist() == e2.tolist(), n
+    assert bad == 0
+    tier.close()
