@@ -58,7 +58,8 @@ int exl3_set_mr(int64_t mr);
 /* moe_set_debug (a8:728): accepted for API compatibility; kernel skipping for timing probes is not provided */
 int exl3_set_debug(int64_t v);
 /* Decision log of the device cache (no reference counterpart; test hook): int32 buffer [1 + cap * (3 + 4P)],
- * buf[0] = records written; one record per ensure call, layout of the oracle's (see DESIGN). NULL = off. */
+ * buf[0] = records written; one record per ensure call of 3 + 4P int32: [T, ring count, P post-mask ids, misses nm,
+ * P filled experts (-1 pad), P (write-back key or -1, slot) pairs (-2 pad)]. NULL = off. */
 int exl3_set_decision_log(int32_t* buf, int64_t cap_records);
 
 /* ---- routed-expert MoE --------------------------------------------------------------------------------------------- */
@@ -92,9 +93,45 @@ int exl3_moe_forward_cached(const void* x, int x_dtype, int64_t x_stride, int M,
 int exl3_moe_align(const int32_t* topk_ids, const float* topk_w, int M, int topk, int n_experts, int pad, int32_t* ib,
                    float* fb, void* stream);
 
+/* Flag upload of the host tier step (replaces the index_copy_ of plugin/exl3xpu/nvtier.py:791-793):
+ * flags[packed[i] >> 1] = packed[i] & 1 for i < n. `packed` may be pinned, device-mapped host memory (read in place,
+ * no staging copy): the caller keeps it unchanged until the work queued on `stream` so far has run. Keys outside
+ * [0, n_flags) are skipped. */
+int exl3_scatter_flags(uint8_t* flags, int64_t n_flags, const int32_t* packed, int64_t n, void* stream);
+
+/* Device health flags (no reference counterpart): flags4[0] = bounded waits of the fused decode kernel that timed
+ * out since load (0 in a healthy run; a timeout means an output was computed from an incomplete intermediate).
+ * Synchronises `stream`. */
+int exl3_device_status(int32_t* flags4, void* stream);
+
 /* Bit-exact dequantization (ReconstructKernel, exl3_esimd.h:869-936): PLANAR4 trellis words
  * [k_tiles][n_tiles][8K] -> fp16 bits [16 k_tiles][16 n_tiles] (W_inner, Hadamard domain). */
 int exl3_dequant(const uint32_t* trellis, int k_tiles, int n_tiles, int K, uint16_t* out, void* stream);
+
+/* ---- RAM-tier admission (host) ---------------------------------------------------------------------------------- */
+
+/* Books of the admission step besides the per-key arrays; the counters accumulate over calls. */
+typedef struct {
+    int64_t n;              /* keys (layers x experts) */
+    int64_t budget;         /* RAM records */
+    int64_t admit_age;      /* evict non-HBM RAM copies only when older than this many steps (AGE) */
+    int64_t admit_qmax;     /* at most this many fills in flight (QMAX) */
+    int64_t ring_cap;       /* capacity of the device miss ring */
+    int64_t tick;           /* current host step (set by the caller) */
+    int64_t ring_seen;      /* miss-ring count consumed so far */
+    int64_t masked, evicts, admit_dropped, ring_overflow;
+} exl3_admit_state;
+
+/* One admission decision (_async_step_admit, plugin/exl3xpu/nvtier.py:708-806), host only, no allocation after the
+ * first call of a thread. res u8 [n] / age i64 [n] / inflight u8 [n]: the host's books, updated in place; pin u8 [n];
+ * view u8 [n]: previous step's device flags with the previous upload overlaid; ring i32 [1 + ring_cap] and slot_of
+ * i32 [n]: previous step's snapshots; done [n_done]: fills completed now. Outputs (capacity n each): admitted keys
+ * (misses by descending count, ties ascending key), evicted keys (HBM-duplicated RAM copies first, then entries older
+ * than admit_age, each by ascending age, ties ascending key), and the flag diff (keys ascending, new values). */
+int exl3_admit_decide(exl3_admit_state* st, uint8_t* res, int64_t* age, uint8_t* inflight, const uint8_t* pin,
+                      const uint8_t* view, const int32_t* ring, const int32_t* slot_of, const int64_t* done,
+                      int64_t n_done, int64_t* adm, int64_t* n_adm, int64_t* ev, int64_t* n_ev, int64_t* diff,
+                      uint8_t* vals, int64_t* n_diff);
 
 /* ---- host memory and copies (a8:1527-1549) --------------------------------------------------------------------------- */
 

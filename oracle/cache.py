@@ -8,7 +8,7 @@ Parity pinning (tests/test_oracle_cache.py): a from-scratch pure-Python brute fo
 (u, slot) pairs; host step by direct set arithmetic) on tiny L/E/S; invariants on the full config-1 trace
 (slot_of/slot_key bijection, victims never touched this tick, at most S assigned, RAM budget respected after
 eviction, at most QMAX in flight). Age-tie order of the reference (numpy default argsort) is NOT pinned: the contract
-is the stable order (ascending key), stated in DESIGN.md.
+is the stable order (ascending key): equal ages are admitted/evicted in ascending key order.
 """
 from __future__ import annotations
 

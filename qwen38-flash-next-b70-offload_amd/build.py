@@ -21,6 +21,7 @@ ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 ARCH = "gfx950"
 
 HIP_SOURCES = ["moe_decode.hip", "moe_cache.hip", "moe_prefill.hip", "moe_capi.hip"]
+HOST_SOURCES = ["tier_host.cpp"]          # host-only C++ (g++)
 HIPCC_FLAGS = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}", "-Xclang", "-target-feature", "-Xclang",
                "-packed-fp32-ops", "-Wno-unused-command-line-argument"]
 
@@ -39,10 +40,18 @@ def build_hip(jobs: int = 8) -> str:
     srcs = [s for s in HIP_SOURCES if os.path.exists(os.path.join(CSRC, s))]
     objs = [os.path.join(BUILD, s.replace(".hip", ".o")) for s in srcs]
 
+    hsrcs = [s for s in HOST_SOURCES if os.path.exists(os.path.join(CSRC, s))]
+    hobjs = [os.path.join(BUILD, s.replace(".cpp", ".o")) for s in hsrcs]
+
     def comp(i):
-        _run([hipcc, *HIPCC_FLAGS, "-c", os.path.join(CSRC, srcs[i]), "-o", objs[i]])
+        if i < len(srcs):
+            _run([hipcc, *HIPCC_FLAGS, "-c", os.path.join(CSRC, srcs[i]), "-o", objs[i]])
+        else:
+            j = i - len(srcs)
+            _run(["g++", "-O3", "-std=c++17", "-fPIC", "-Wall", "-c", os.path.join(CSRC, hsrcs[j]), "-o", hobjs[j]])
     with ThreadPoolExecutor(max(1, jobs)) as ex:
-        list(ex.map(comp, range(len(srcs))))
+        list(ex.map(comp, range(len(srcs) + len(hsrcs))))
+    objs = objs + hobjs
     lib = os.path.join(OUT, "libexl3moe.so")
     tmp = lib + ".tmp"
     _run([hipcc, "-shared", f"--offload-arch={ARCH}", "-fPIC", *objs, "-o", tmp])

@@ -144,10 +144,46 @@ __device__ __forceinline__ void st_act(void* y, int dt, size_t i, float v) {
     else ((half_t*)y)[i] = (half_t)v;
 }
 
-// release/acquire around a last-arriver counter (device scope: the L2 of each XCD is private)
-__device__ __forceinline__ int arrive(int* counter) {
-    __threadfence();
-    return atomicAdd(counter, 1);
+// ---- cross-workgroup exchange ------------------------------------------------------------------------------------------
+// Each XCD has a private L2, and an agent-scope fence (__threadfence) writes back and invalidates the whole L2
+// (buffer_wbl2 / buffer_inv). Data exchanged between workgroups of one kernel therefore uses agent-scope atomic stores
+// and loads (global_store/load ... sc1: written through to / read from the device coherence point) and the producer
+// waits for its stores (vmcnt(0)) before the workgroup barrier that precedes the counter increment.
+__device__ __forceinline__ void st_agent(float* p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+__device__ __forceinline__ float ld_agent(const float* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// sum_i p[i * stride] for i = 0..n-1 in index order, loads issued 16 at a time (one round trip per 16 values)
+__device__ __forceinline__ float sum_agent(const float* p, int n, int stride) {
+    float acc = 0.f;
+    int i = 0;
+    for (; i + 16 <= n; i += 16) {
+        float v[16];
+#pragma unroll
+        for (int j = 0; j < 16; ++j) v[j] = ld_agent(p + (size_t)(i + j) * stride);
+#pragma unroll
+        for (int j = 0; j < 16; ++j) acc += v[j];
+    }
+    if (i < n) {
+        float v[16];
+#pragma unroll
+        for (int j = 0; j < 16; ++j) v[j] = i + j < n ? ld_agent(p + (size_t)(i + j) * stride) : 0.f;
+#pragma unroll
+        for (int j = 0; j < 16; ++j)
+            if (i + j < n) acc += v[j];
+    }
+    return acc;
+}
+__device__ __forceinline__ void wait_stores() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+__device__ __forceinline__ int counter_add(int* c, int v) {
+    return __hip_atomic_fetch_add(c, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void counter_reset(int* c) { __hip_atomic_store(c, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+
+// global-address-space view of a generic pointer (global_load instead of flat_load)
+typedef const __attribute__((address_space(1))) uint32_t gu32_t;
+__device__ __forceinline__ gu32_t* as_global(const uint32_t* p) { return (gu32_t*)p; }
 
 }  // namespace exl3

@@ -10,12 +10,14 @@ namespace exl3 {
 constexpr int kMaxPairs = 1024;     // pairs (rows x top-k) of one decode call
 constexpr int kMaxRows = 256;       // rows of one decode call
 constexpr int kMaxExperts = 1024;   // experts per layer (one ensure work-item per expert)
+constexpr int kMaxI = 4096;         // intermediate size of the decode kernels (abuf staged in LDS)
 
 struct DecodeArgs {
     const void* x; int x_dt; int64_t x_stride;     // activations [M, H], dt 0 = fp16, 1 = bf16
     const int32_t* ids; const float* w;            // [M * topk] (post-mask when cached)
     int M, topk, npairs, E;
     const int64_t* ptrs;                           // per-layer blob pointer table [E]
+    const int64_t* pair_ptr;                       // blob pointer per pair (written by ensure) or null
     const int64_t* fill;                           // per-layer write-through targets [E] (0 = none) or null
     int64_t* commit_ptrs;                          // cache commit: ptrs[e] = fill[e] for e in fill_list
     int64_t* commit_fill;
@@ -23,7 +25,6 @@ struct DecodeArgs {
     _Float16* abuf;                                // [npairs, I]
     float* ybuf;                                   // [npairs, H]
     float* part_gu;                                // [npairs, I/128, H/128, 256]
-    float* part_d;                                 // [npairs, H/128, I/128, 128]
     void* out; int64_t out_stride;                 // [M, H], same dtype as x
     BlobGeom g;
 };
@@ -37,6 +38,7 @@ struct EnsureArgs {
     const uint8_t* ram_res; int32_t* ring; int ring_cap; const int32_t* safe;   // tier (null ram_res: off)
     int32_t* vict;                                 // victim list [1 + 2E] or null
     int32_t* log; int64_t log_cap;                 // decision log (debug) or null: [count, records...]
+    int64_t* pair_ptr;                             // out: blob pointer of every post-mask pick [P] (or null)
 };
 
 struct VictimArgs {
@@ -45,19 +47,22 @@ struct VictimArgs {
 };
 
 // decode.hip
-hipError_t launch_gateup(int K, const DecodeArgs& a, hipStream_t s);
-hipError_t launch_down(int K, const DecodeArgs& a, hipStream_t s);
+hipError_t launch_moe_layer(int K, const DecodeArgs& a, hipStream_t s);
+int read_status(int* out, hipStream_t s);
 hipError_t launch_dequant(int K, const uint32_t* tr, _Float16* out, int k_tiles, int n_tiles, hipStream_t s);
 // cache.hip
 hipError_t launch_ensure(const EnsureArgs& a, hipStream_t s);
 hipError_t launch_victim_copy(const VictimArgs& a, int max_victims, hipStream_t s);
+hipError_t launch_scatter_flags(uint8_t* flags, int64_t n_flags, const int32_t* packed, int64_t n, hipStream_t s);
+
+// 256-row slices of H handled by the split-K gate/up workgroups (H is a multiple of 128)
+__host__ __device__ static inline int gu_slices(int H) { return (H + 255) / 256; }
 
 // workspace of a decode call (bytes, 256-aligned parts)
 static inline size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
 static inline size_t decode_workspace_bytes(int npairs, int H, int I) {
     return align256((size_t)npairs * I * 2) + align256((size_t)npairs * H * 4) +
-           align256((size_t)npairs * (I / 128) * (H / 128) * 256 * 4) +
-           align256((size_t)npairs * (H / 128) * (I / 128) * 128 * 4);
+           align256((size_t)npairs * (I / 128) * gu_slices(H) * 256 * 4) + align256((size_t)npairs * 8);
 }
 
 }  // namespace exl3

@@ -267,6 +267,10 @@ __global__ void __launch_bounds__(kEnsureThreads) ensure_kernel(EnsureArgs A) {
         A.fill_list[0] = nm;
         if (A.vict) A.vict[0] = nm;
     }
+    // blob pointer of every post-mask pick (read by the GEMV workgroups; the slots of hits and the host copies of
+    // misses stay valid for the whole call, fills are committed at its end)
+    if (A.pair_ptr)
+        for (int i = tid; i < P; i += kEnsureThreads) A.pair_ptr[i] = A.ptrs_all[A.layer * E + pid[i]];
     if (A.log && wv == 0) {                                   // decision record, same layout as the oracle's
         const int idx = A.log[0];
         if (idx < A.log_cap) {
@@ -320,6 +324,21 @@ hipError_t launch_victim_copy(const VictimArgs& a, int max_victims, hipStream_t 
     const int chunks = (int)((a.blob + a.chunk_bytes - 1) / a.chunk_bytes);
     if (max_victims <= 0) return hipSuccess;
     hipLaunchKernelGGL(victim_copy_kernel, dim3((unsigned)(max_victims * chunks)), dim3(256), 0, s, a, chunks);
+    return hipGetLastError();
+}
+
+// flag upload of the host tier step: packed[i] = key << 1 | value, read in place (pinned host memory is device-mapped)
+__global__ void scatter_flags_kernel(uint8_t* flags, int64_t n_flags, const int32_t* packed, int64_t n) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const int32_t p = packed[i];
+    const int64_t key = p >> 1;
+    if (p >= 0 && key < n_flags) flags[key] = (uint8_t)(p & 1);
+}
+
+hipError_t launch_scatter_flags(uint8_t* flags, int64_t n_flags, const int32_t* packed, int64_t n, hipStream_t s) {
+    if (n <= 0) return hipSuccess;
+    hipLaunchKernelGGL(scatter_flags_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, flags, n_flags, packed, n);
     return hipGetLastError();
 }
 

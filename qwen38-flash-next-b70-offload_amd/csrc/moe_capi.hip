@@ -48,7 +48,7 @@ int check_geometry(int H, int I, int K, int E) {
     if (H <= 0 || I <= 0 || H % 128 || I % 128) return fail(EXL3_EINVAL, "moe: H (%d) and I (%d) must be multiples of 128", H, I);
     if (K < 2 || K > 4) return fail(EXL3_EUNSUPPORTED, "moe: K=%d not supported (K in 2..4)", K);
     if (E <= 0 || E > kMaxExperts) return fail(EXL3_EINVAL, "moe: n_experts=%d must be in 1..%d", E, kMaxExperts);
-    if (H > 64 * 128 || I > 64 * 128) return fail(EXL3_EUNSUPPORTED, "moe: H and I up to 8192 (got %d, %d)", H, I);
+    if (H > 64 * 128 || I > kMaxI) return fail(EXL3_EUNSUPPORTED, "moe: H up to 8192, I up to %d (got %d, %d)", kMaxI, H, I);
     return EXL3_OK;
 }
 
@@ -123,10 +123,15 @@ size_t exl3_moe_forward_workspace(int M, int H, int I, int topk) {
     return decode_workspace_bytes(M * topk, H, I);
 }
 
+static int64_t* pair_ptr_area(void* ws, int npairs, int H, int I) {
+    return (int64_t*)((uint8_t*)ws + align256((size_t)npairs * I * 2) + align256((size_t)npairs * H * 4) +
+                      align256((size_t)npairs * (I / 128) * gu_slices(H) * 256 * 4));
+}
+
 static int forward_impl(const void* x, int x_dtype, int64_t x_stride, int M, int H, const int32_t* ids, const float* w,
                         int topk, const int64_t* ptrs, int I, int K, int E, void* out, int64_t out_stride, void* ws,
                         size_t ws_bytes, hipStream_t st, const int64_t* fill, int64_t* commit_ptrs, int64_t* commit_fill,
-                        const int32_t* fill_list) {
+                        const int32_t* fill_list, const int64_t* pair_ptr) {
     const int npairs = M * topk;
     if (npairs > kMaxPairs || M > kMaxRows)
         return fail(EXL3_EUNSUPPORTED, "moe_forward: M=%d x topk=%d exceeds the decode kernels (%d pairs, %d rows)", M,
@@ -144,6 +149,7 @@ static int forward_impl(const void* x, int x_dtype, int64_t x_stride, int M, int
     a.npairs = npairs;
     a.E = E;
     a.ptrs = ptrs;
+    a.pair_ptr = pair_ptr;
     a.fill = fill;
     a.commit_ptrs = commit_ptrs;
     a.commit_fill = commit_fill;
@@ -154,15 +160,11 @@ static int forward_impl(const void* x, int x_dtype, int64_t x_stride, int M, int
     a.ybuf = (float*)p;
     p += align256((size_t)npairs * H * 4);
     a.part_gu = (float*)p;
-    p += align256((size_t)npairs * (I / 128) * (H / 128) * 256 * 4);
-    a.part_d = (float*)p;
     a.out = out;
     a.out_stride = out_stride;
     a.g = blob_geom(H, I, K);
-    hipError_t e = launch_gateup(K, a, st);
-    if (e != hipSuccess) return hip_fail(e, "gateup launch");
-    e = launch_down(K, a, st);
-    if (e != hipSuccess) return hip_fail(e, "down launch");
+    hipError_t e = launch_moe_layer(K, a, st);
+    if (e != hipSuccess) return hip_fail(e, "moe layer launch");
     return EXL3_OK;
 }
 
@@ -176,7 +178,7 @@ int exl3_moe_forward(const void* x, int x_dtype, int64_t x_stride, int M, int H,
     if (M == 0) return EXL3_OK;
     if (!x || !topk_ids || !topk_w || !ptrs || !out) return fail(EXL3_EINVAL, "moe_forward: null pointer");
     return forward_impl(x, x_dtype, x_stride, M, H, topk_ids, topk_w, topk, ptrs, I, K, n_experts, out, out_stride,
-                        workspace, workspace_bytes, (hipStream_t)stream, nullptr, nullptr, nullptr, nullptr);
+                        workspace, workspace_bytes, (hipStream_t)stream, nullptr, nullptr, nullptr, nullptr, nullptr);
 }
 
 int exl3_moe_forward_cached(const void* x, int x_dtype, int64_t x_stride, int M, int H, int32_t* topk_ids,
@@ -227,6 +229,10 @@ int exl3_moe_forward_cached(const void* x, int x_dtype, int64_t x_stride, int M,
     ea.vict = g_cfg.vict;
     ea.log = g_cfg.log;
     ea.log_cap = g_cfg.log_cap;
+    const size_t need = decode_workspace_bytes(P, H, I);
+    if (!workspace || workspace_bytes < need)
+        return fail(EXL3_EWORKSPACE, "moe_forward_cached: workspace %zu < %zu bytes", workspace_bytes, need);
+    ea.pair_ptr = pair_ptr_area(workspace, P, H, I);
     hipError_t e = launch_ensure(ea, st);
     if (e != hipSuccess) return hip_fail(e, "ensure launch");
     if (g_cfg.vict) {
@@ -246,13 +252,29 @@ int exl3_moe_forward_cached(const void* x, int x_dtype, int64_t x_stride, int M,
     int64_t* pl = ptrs_all + (int64_t)layer * E;
     int64_t* fl = fill_all + (int64_t)layer * E;
     return forward_impl(x, x_dtype, x_stride, M, H, topk_ids, topk_w, topk, pl, I, K, E, out, out_stride, workspace,
-                        workspace_bytes, st, fl, pl, fl, fill_list);
+                        workspace_bytes, st, fl, pl, fl, fill_list, ea.pair_ptr);
 }
 
 int exl3_moe_align(const int32_t* topk_ids, const float* topk_w, int M, int topk, int n_experts, int pad, int32_t* ib,
                    float* fb, void* stream) {
     (void)topk_ids; (void)topk_w; (void)M; (void)topk; (void)n_experts; (void)pad; (void)ib; (void)fb; (void)stream;
     return fail(EXL3_EUNSUPPORTED, "moe_align: not built yet");
+}
+
+int exl3_scatter_flags(uint8_t* flags, int64_t n_flags, const int32_t* packed, int64_t n, void* stream) {
+    if (n < 0 || n_flags < 0 || n > (int64_t)1 << 31) return fail(EXL3_EINVAL, "scatter_flags: n=%lld", (long long)n);
+    if (n == 0) return EXL3_OK;
+    if (!flags || !packed) return fail(EXL3_EINVAL, "scatter_flags: null pointer");
+    hipError_t e = launch_scatter_flags(flags, n_flags, packed, n, (hipStream_t)stream);
+    return e == hipSuccess ? EXL3_OK : hip_fail(e, "scatter_flags");
+}
+
+int exl3_device_status(int32_t* flags4, void* stream) {
+    if (!flags4) return fail(EXL3_EINVAL, "device_status: null output");
+    hipError_t e = (hipError_t)read_status(flags4, (hipStream_t)stream);
+    if (e != hipSuccess) return hip_fail(e, "device_status");
+    e = hipStreamSynchronize((hipStream_t)stream);
+    return e == hipSuccess ? EXL3_OK : hip_fail(e, "device_status sync");
 }
 
 int exl3_dequant(const uint32_t* trellis, int k_tiles, int n_tiles, int K, uint16_t* out, void* stream) {

@@ -1,15 +1,17 @@
 // Decode-size routed-expert MoE (pair mode: one row per (token, expert) pair), EXL3 trellis dequantization fused into
-// the expert GEMVs, for CDNA4.
+// the expert GEMVs, for CDNA4. One launch per MoE layer (moe_layer_kernel), two kinds of workgroups:
 //
-//   gateup_kernel : WG per (pair, 128-column block of I, 128-row block of H). Fused input Hadamard of x*suh for gate
-//                   and up, trellis GEMV (one period per lane, bfe + mul + sad + fma_mix per weight), split-K partials;
-//                   the last-arriving WG of a (pair, block) reduces the partials in fixed order and runs the epilogue
-//                   (output Hadamards * svh, SiLU(g)*u, *suh_d, down-input Hadamard) -> abuf (fp16).
-//   down_kernel   : WG per (pair, 128-column block of H, 128-row block of I): GEMV of abuf against the down trellis,
-//                   last-arriver epilogue (output Hadamard * w * svh_d) -> y (fp32); the last pair of a (row, block)
-//                   sums the top-k y's in k order into out (the combine), and the last (row, block) commits the
-//                   expert-cache fills (ptrs[e] = fill[e]; fill[e] = 0).
-//   dequant_kernel: bit-exact fp16 W_inner of one trellis matrix.
+//   gate/up WGs (ids 0 .. n_gu-1), one per (pair, 128-column block of I, 256-row slice of H): issue their trellis-word
+//     loads first, then the input Hadamard of x*suh for gate and up, the trellis GEMV (one period per lane: bfe + mul
+//     + sad + fma_mix per weight) and split-K partials; the last-arriving WG of a (pair, block) reduces the partials in
+//     fixed order and runs the epilogue (output Hadamards * svh, SiLU(g)*u, *suh_d, down-input Hadamard) -> abuf
+//     (fp16) and counts the block as ready for the pair.
+//   down WGs (ids n_gu ..), one per (pair, 128-column block of H) over the whole K = I: issue their word loads, wait
+//     (bounded) until the pair's abuf is complete, GEMV with an in-WG reduction, epilogue (output Hadamard * w *
+//     svh_d) -> y (fp32); the last pair of a (row, block) sums the top-k y's in k order into out (the combine); the
+//     last (row, block) commits the expert-cache fills (ptrs[e] = fill[e]; fill[e] = 0) and clears the ready counts.
+// Gate/up WGs have lower ids, so on every XCD they are dispatched before any down WG and never wait: the down WGs'
+// wait always ends (it is also bounded, with an error flag, so a broken assumption cannot hang the GPU).
 //
 // Reference semantics: kernels/moe-a8/exl3_moe.a8.sycl GateUpKernel (121-260), DownKernel (264-368), CombineKernel
 // (371-395); kernels/moe-a8/exl3_esimd.h ReconstructKernel (869-936). Accumulation is fp32 throughout (the reference
@@ -26,7 +28,11 @@ namespace exl3 {
 __device__ int g_cnt_gu[kMaxPairs * 64];
 __device__ int g_cnt_d[kMaxPairs * 64];
 __device__ int g_cnt_c[kMaxRows * 64];
+__device__ int g_ready[kMaxPairs];
 __device__ int g_cnt_all[4];
+__device__ int g_status[4];          // [0]: spin timeouts (should stay 0)
+
+constexpr int kSpinMax = 1 << 22;
 
 // word offset of (tile-row r, tile-col `tile`, period p, plane i) in a PLANAR4 matrix with tiles_n tile-columns
 template <int K>
@@ -60,8 +66,8 @@ __device__ __forceinline__ void dequant_store(const Period<K>& P, int p, _Float1
     }
 }
 
-// GEMV over `nrows` (compile-time 4) tile-rows of 8 tile-columns (one 128-column block): per lane accumulators for its
-// column pair, for every column pass. Optional write-through of the words it reads.
+// GEMV of 4 tile-rows x 8 tile-columns (one 128-column block) per wave: load() issues the word loads (and the
+// optional write-through stores), compute() decodes and accumulates each lane's column pair for every column pass.
 template <int K>
 struct Gemv8 {
     using GM = Geo<K>;
@@ -69,9 +75,34 @@ struct Gemv8 {
     static constexpr int NQ = V / 8;
     static_assert(NQ >= 1, "one value octet per period at least");
 
-    // xh: 16 half2 per tile-row... laid out [tile-row][8] half2 (128-row block = 8 tile-rows)
-    __device__ __forceinline__ static void run(const uint32_t* tr, uint32_t* trd, int tiles_n, int r0, int xrow0,
-                                               int col_tile0, const half2_t* xh, float (&acc)[NCP][2]) {
+    uint32_t wd[NCP][4][D];
+
+    __device__ __forceinline__ void load(const uint32_t* tr, int tiles_n, int r0, int col_tile0) {
+        const int l = lane_id();
+        const int p = l % G, j = l / G;
+#pragma unroll
+        for (int cp = 0; cp < NCP; ++cp)
+#pragma unroll
+            for (int rr = 0; rr < 4; ++rr)
+#pragma unroll
+                for (int i = 0; i < D; ++i)
+                    wd[cp][rr][i] = __builtin_nontemporal_load(as_global(tr) +
+                                                               word_off<K>(r0 + rr, tiles_n, col_tile0 + cp * NTW + j, p, i));
+    }
+
+    __device__ __forceinline__ void write_through(uint32_t* trd, int tiles_n, int r0, int col_tile0) const {
+        const int l = lane_id();
+        const int p = l % G, j = l / G;
+#pragma unroll
+        for (int cp = 0; cp < NCP; ++cp)
+#pragma unroll
+            for (int rr = 0; rr < 4; ++rr)
+#pragma unroll
+                for (int i = 0; i < D; ++i) trd[word_off<K>(r0 + rr, tiles_n, col_tile0 + cp * NTW + j, p, i)] = wd[cp][rr][i];
+    }
+
+    // xh: activations of the 128-row block, [tile-row][8] half2; xrow0 = first tile-row of this wave in the block
+    __device__ __forceinline__ void compute(int xrow0, const half2_t* xh, float (&acc)[NCP][2]) const {
         const int l = lane_id();
         const int p = l % G, j = l / G;
         const int src_lane = j * G + ((p + G - 1) % G);
@@ -80,23 +111,11 @@ struct Gemv8 {
         for (int cp = 0; cp < NCP; ++cp) {
             acc[cp][0] = 0.f;
             acc[cp][1] = 0.f;
-            const int tile = col_tile0 + cp * NTW + j;
-            uint32_t wd[4][D];
-#pragma unroll
-            for (int rr = 0; rr < 4; ++rr)
-#pragma unroll
-                for (int i = 0; i < D; ++i) wd[rr][i] = __builtin_nontemporal_load(tr + word_off<K>(r0 + rr, tiles_n, tile, p, i));
-            if (trd) {
-#pragma unroll
-                for (int rr = 0; rr < 4; ++rr)
-#pragma unroll
-                    for (int i = 0; i < D; ++i) trd[word_off<K>(r0 + rr, tiles_n, tile, p, i)] = wd[rr][i];
-            }
 #pragma unroll
             for (int rr = 0; rr < 4; ++rr) {
-                const uint32_t prev = (uint32_t)__shfl((int)wd[rr][D - 1], src_lane, 64);
+                const uint32_t prev = (uint32_t)__shfl((int)wd[cp][rr][D - 1], src_lane, 64);
                 Period<K> P;
-                P.set(wd[rr], prev);
+                P.set(wd[cp][rr], prev);
                 const half2_t* xr = xh + (xrow0 + rr) * 8;
                 half2_t xv[2][NQ];
 #pragma unroll
@@ -123,90 +142,103 @@ struct Gemv8 {
     }
 };
 
+constexpr int kWaves = 8;                    // waves per workgroup (both kinds)
+constexpr int kThreads = 64 * kWaves;
+
+struct LayerShared {
+    half2_t xh[2][2][64];    // gate/up WG: activations of its two 128-row blocks, [proj][block][64] half2
+    float ssum[2][2];
+    float red[kWaves][128];  // per-wave column sums
+    float tot[256];          // reduced split-K partials of the last-arriving gate/up WG
+    half2_t xd[kMaxI / 2];   // down WG: the pair's abuf
+    int last;
+};
+
+// pointer of the blob of pair a: precomputed by the cache's ensure (pair_ptr) or looked up through ids/ptrs
+__device__ __forceinline__ const uint8_t* pair_base(const DecodeArgs& A, int a, int& e) {
+    e = min(max(A.ids[a], 0), A.E - 1);          // out-of-range ids are clamped, never dereferenced
+    return A.pair_ptr ? (const uint8_t*)A.pair_ptr[a] : (const uint8_t*)A.ptrs[e];
+}
+
+// gate/up WG per (pair, 128-column block of I, 256-row slice of H): waves (proj = w & 1, quarter = w >> 1) each cover
+// 4 tile-rows x 8 tile-columns.
 template <int K>
-__global__ void __launch_bounds__(256) gateup_kernel(DecodeArgs A) {
+__device__ __forceinline__ void gateup_wg(const DecodeArgs& A, int blk, LayerShared& S) {
     using GV = Gemv8<K>;
     const int H = A.g.H, I = A.g.I;
-    const int nbn = I / 128, ksn = H / 128;
-    int blk = blockIdx.x;
+    const int nbn = I / 128, ksn = gu_slices(H);
     const int ks = blk % ksn;
     blk /= ksn;
     const int nb = blk % nbn, a = blk / nbn;
     const int tid = threadIdx.x, wv = tid >> 6, l = tid & 63;
-    const int e = min(max(A.ids[a], 0), A.E - 1);      // out-of-range ids are clamped, never dereferenced
+    int e;
+    const uint8_t* base = pair_base(A, a, e);
     const int m = a / A.topk;
-    const uint8_t* base = (const uint8_t*)A.ptrs[e];
     uint8_t* dst = A.fill ? (uint8_t*)A.fill[e] : nullptr;
+    const int proj = wv & 1, qt = wv >> 1;
+    const int tiles_n = 2 * I / 16, r0 = ks * 16 + qt * 4, ct0 = proj * (I / 16) + nb * 8;
 
-    __shared__ half2_t xh_s[2][64];
-    __shared__ float ssum[2];
-    __shared__ float red[2][128];
-    __shared__ int last;
-
-    if (dst && nb == 0 && ks == 0) {            // write-through of the vector tail (suh/svh)
-        const uint32_t* s = (const uint32_t*)(base + A.g.off_suh_g);
-        uint32_t* d = (uint32_t*)(dst + A.g.off_suh_g);
-        const int n = (int)((A.g.blob - A.g.off_suh_g) >> 2);
-        for (int i = tid; i < n; i += 256) d[i] = s[i];
-    }
-    if (wv < 2) {                                // input Hadamard of x * suh for this 128-row block
-        const half_t* suh = (const half_t*)(base + (wv ? A.g.off_suh_u : A.g.off_suh_g));
-        const int k0 = ks * 128 + 2 * l;
+    // the last slice of an H that is an odd multiple of 128 has one 128-row block: its second-block waves only add 0
+    const bool live = ks * 256 + (qt >> 1) * 128 < H;
+    GV g;
+    if (live) g.load((const uint32_t*)base, tiles_n, r0, ct0);
+    if (wv < 4 && ks * 256 + (wv >> 1) * 128 >= H) {
+        if (l == 0) S.ssum[wv & 1][wv >> 1] = 0.f;
+    } else if (wv < 4) {                         // input Hadamards of x * suh: (proj, 128-row block) per wave
+        const int pj = wv & 1, hb = wv >> 1;
+        const half_t* suh = (const half_t*)(base + (pj ? A.g.off_suh_u : A.g.off_suh_g));
+        const int k0 = ks * 256 + hb * 128 + 2 * l;
         const size_t xo = (size_t)m * A.x_stride + k0;
         float v0 = (float)(half_t)(ld_act(A.x, A.x_dt, xo) * (float)suh[k0]);
         float v1 = (float)(half_t)(ld_act(A.x, A.x_dt, xo + 1) * (float)suh[k0 + 1]);
         wave_fwht128(v0, v1);
         const half_t h0 = (half_t)(v0 * kRsqrt128), h1 = (half_t)(v1 * kRsqrt128);
-        xh_s[wv][l] = half2_t{h0, h1};
+        S.xh[pj][hb][l] = half2_t{h0, h1};
         const float s = wave_sum((float)h0 + (float)h1);
-        if (l == 0) ssum[wv] = s;
+        if (l == 0) S.ssum[pj][hb] = s;
+    }
+    if (dst) {                                   // write-through of a cache miss into its HBM slot
+        if (live) g.write_through((uint32_t*)dst, tiles_n, r0, ct0);
+        if (nb == 0 && ks == 0) {
+            const uint32_t* sv = (const uint32_t*)(base + A.g.off_suh_g);
+            uint32_t* dv = (uint32_t*)(dst + A.g.off_suh_g);
+            const int n = (int)((A.g.blob - A.g.off_suh_g) >> 2);
+            for (int i = tid; i < n; i += kThreads) dv[i] = sv[i];
+        }
     }
     __syncthreads();
-
-    const int proj = wv & 1, hf = wv >> 1;
     float acc[GV::NCP][2];
-    const uint32_t* tr = (const uint32_t*)base;
-    uint32_t* trd = dst ? (uint32_t*)dst : nullptr;
-    GV::run(tr, trd, 2 * I / 16, ks * 8 + hf * 4, hf * 4, proj * (I / 16) + nb * 8, xh_s[proj], acc);
-    int col[GV::NCP];
-    bool own[GV::NCP];
+    if (live) {
+        g.compute((qt & 1) * 4, &S.xh[proj][qt >> 1][0], acc);
+    } else {
+#pragma unroll
+        for (int cp = 0; cp < GV::NCP; ++cp) acc[cp][0] = acc[cp][1] = 0.f;
+    }
 #pragma unroll
     for (int cp = 0; cp < GV::NCP; ++cp) {
-        own[cp] = GV::reduce(acc[cp], cp, col[cp]);
-        if (hf == 1 && own[cp]) {
-            red[proj][col[cp]] = acc[cp][0];
-            red[proj][col[cp] + 8] = acc[cp][1];
+        int c0;
+        if (GV::reduce(acc[cp], cp, c0)) {
+            S.red[wv][c0] = acc[cp][0];
+            S.red[wv][c0 + 8] = acc[cp][1];
         }
     }
     __syncthreads();
-    if (hf == 0) {
-        float* part = A.part_gu + ((size_t)(a * nbn + nb) * ksn + ks) * 256 + proj * 128;
-#pragma unroll
-        for (int cp = 0; cp < GV::NCP; ++cp) {
-            if (own[cp]) {
-                const int c0 = col[cp];
-                part[c0] = kC1 * (acc[cp][0] + red[proj][c0]) + kC2 * ssum[proj];
-                part[c0 + 8] = kC1 * (acc[cp][1] + red[proj][c0 + 8]) + kC2 * ssum[proj];
-            }
-        }
+    if (tid < 256) {                             // column tid of [gate 128 | up 128]: sum the 4 quarters in order
+        const int pj = tid >> 7, c = tid & 127;
+        const float t = S.red[pj][c] + S.red[pj + 2][c] + S.red[pj + 4][c] + S.red[pj + 6][c];
+        st_agent(A.part_gu + ((size_t)(a * nbn + nb) * ksn + ks) * 256 + tid,
+                 kC1 * t + kC2 * (S.ssum[pj][0] + S.ssum[pj][1]));
     }
-    __threadfence();
+    wait_stores();
     __syncthreads();
-    if (tid == 0) last = atomicAdd(&g_cnt_gu[a * nbn + nb], 1) == ksn - 1;
+    if (tid == 0) S.last = counter_add(&g_cnt_gu[a * nbn + nb], 1) == ksn - 1;
     __syncthreads();
-    if (!last) return;
-    __threadfence();
+    if (!S.last) return;
+    if (tid == 0) counter_reset(&g_cnt_gu[a * nbn + nb]);
+    if (tid < 256) S.tot[tid] = sum_agent(A.part_gu + (size_t)(a * nbn + nb) * ksn * 256 + tid, ksn, 256);
+    __syncthreads();
     if (wv != 0) return;
-    if (l == 0) g_cnt_gu[a * nbn + nb] = 0;
-    const float* pp = A.part_gu + (size_t)(a * nbn + nb) * ksn * 256;
-    float g0 = 0.f, g1 = 0.f, u0 = 0.f, u1 = 0.f;
-    for (int s = 0; s < ksn; ++s) {
-        const float* q = pp + s * 256;
-        g0 += __builtin_nontemporal_load(q + 2 * l);
-        g1 += __builtin_nontemporal_load(q + 2 * l + 1);
-        u0 += __builtin_nontemporal_load(q + 128 + 2 * l);
-        u1 += __builtin_nontemporal_load(q + 129 + 2 * l);
-    }
+    float g0 = S.tot[2 * l], g1 = S.tot[2 * l + 1], u0 = S.tot[128 + 2 * l], u1 = S.tot[129 + 2 * l];
     wave_fwht128(g0, g1);
     wave_fwht128(u0, u1);
     const int c = nb * 128 + 2 * l;
@@ -222,113 +254,143 @@ __global__ void __launch_bounds__(256) gateup_kernel(DecodeArgs A) {
     a0 = (float)(half_t)(a0 * (float)sud[0]);
     a1 = (float)(half_t)(a1 * (float)sud[1]);
     wave_fwht128(a0, a1);
-    *(half2_t*)(A.abuf + (size_t)a * I + c) = half2_t{(half_t)(a0 * kRsqrt128), (half_t)(a1 * kRsqrt128)};
+    const half2_t hv = half2_t{(half_t)(a0 * kRsqrt128), (half_t)(a1 * kRsqrt128)};
+    __hip_atomic_store((uint32_t*)(A.abuf + (size_t)a * I + c), __builtin_bit_cast(uint32_t, hv), __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+    wait_stores();
+    if (l == 0) counter_add(&g_ready[a], 1);
 }
 
+// down WG per (pair, 128-column block of H) over the full K = I: the 4-row chunks of the I/16 tile-rows go round-robin
+// to the eight waves, the per-wave column sums are reduced in LDS in wave order (no cross-WG exchange), then the output
+// Hadamard * w * svh_d -> y, and the combine.
 template <int K>
-__global__ void __launch_bounds__(128) down_kernel(DecodeArgs A) {
+__device__ __forceinline__ void down_wg(const DecodeArgs& A, int blk, LayerShared& S) {
     using GV = Gemv8<K>;
     const int H = A.g.H, I = A.g.I;
-    const int nbn = H / 128, ksn = I / 128;
-    int blk = blockIdx.x;
-    const int ks = blk % ksn;
-    blk /= ksn;
+    const int nbn = H / 128, kt = I / 16;
     const int nb = blk % nbn, a = blk / nbn;
     const int tid = threadIdx.x, wv = tid >> 6, l = tid & 63;
-    const int e = min(max(A.ids[a], 0), A.E - 1);      // out-of-range ids are clamped, never dereferenced
+    int e;
+    const uint8_t* base = pair_base(A, a, e);
     const int m = a / A.topk;
-    const uint8_t* base = (const uint8_t*)A.ptrs[e];
     uint8_t* dst = A.fill ? (uint8_t*)A.fill[e] : nullptr;
-
-    __shared__ half2_t xh_s[64];
-    __shared__ float ssum;
-    __shared__ float red[128];
-    __shared__ int last;
-
-    if (wv == 0) {
-        const half2_t v = *(const half2_t*)(A.abuf + (size_t)a * I + ks * 128 + 2 * l);
-        xh_s[l] = v;
-        const float s = wave_sum((float)v.x + (float)v.y);
-        if (l == 0) ssum = s;
-    }
-    __syncthreads();
-    float acc[GV::NCP][2];
+    const int tiles_n = H / 16, ct0 = nb * 8;
     const uint32_t* tr = (const uint32_t*)(base + A.g.gu_bytes);
     uint32_t* trd = dst ? (uint32_t*)(dst + A.g.gu_bytes) : nullptr;
-    GV::run(tr, trd, H / 16, ks * 8 + wv * 4, wv * 4, nb * 8, xh_s, acc);
-    int col[GV::NCP];
-    bool own[GV::NCP];
-#pragma unroll
-    for (int cp = 0; cp < GV::NCP; ++cp) {
-        own[cp] = GV::reduce(acc[cp], cp, col[cp]);
-        if (wv == 1 && own[cp]) {
-            red[col[cp]] = acc[cp][0];
-            red[col[cp] + 8] = acc[cp][1];
-        }
-    }
-    __syncthreads();
-    if (wv == 0) {
-        float* part = A.part_d + ((size_t)(a * nbn + nb) * ksn + ks) * 128;
-#pragma unroll
-        for (int cp = 0; cp < GV::NCP; ++cp) {
-            if (own[cp]) {
-                const int c0 = col[cp];
-                part[c0] = kC1 * (acc[cp][0] + red[c0]) + kC2 * ssum;
-                part[c0 + 8] = kC1 * (acc[cp][1] + red[c0 + 8]) + kC2 * ssum;
+    const int nch = (kt / 4 + kWaves - 1 - wv) / kWaves;      // 4-row chunks of this wave: q = wv + kWaves * c
+    GV g0, g1;
+    if (nch > 0) g0.load(tr, tiles_n, wv * 4, ct0);
+    if (nch > 1) g1.load(tr, tiles_n, (wv + kWaves) * 4, ct0);
+    if (tid == 0) {                              // wait for the pair's whole abuf (all I/128 gate/up epilogues)
+        int it = 0;
+        while (__hip_atomic_load(&g_ready[a], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < I / 128) {
+            __builtin_amdgcn_s_sleep(1);
+            if (++it > kSpinMax) {
+                atomicAdd(&g_status[0], 1);
+                break;
             }
         }
     }
-    __threadfence();
     __syncthreads();
-    if (tid == 0) last = atomicAdd(&g_cnt_d[a * nbn + nb], 1) == ksn - 1;
+    half2_t* xs = S.xd;                          // abuf of the pair, [I/2] half2
+    for (int i = tid; i < I / 2; i += kThreads)
+        xs[i] = __builtin_bit_cast(half2_t, __hip_atomic_load((const uint32_t*)(A.abuf + (size_t)a * I) + i,
+                                                              __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
     __syncthreads();
-    if (!last) return;
-    __threadfence();
+    float acc[GV::NCP][2], tacc[GV::NCP][2];
+    float xsum = 0.f;
+#pragma unroll
+    for (int cp = 0; cp < GV::NCP; ++cp) acc[cp][0] = acc[cp][1] = 0.f;
+    for (int c = 0; c < nch; ++c) {
+        const int r0 = (wv + kWaves * c) * 4;
+        GV& gc = (c & 1) ? g1 : g0;
+        if (trd) gc.write_through(trd, tiles_n, r0, ct0);
+        gc.compute(0, xs + r0 * 8, tacc);
+        if (c + 2 < nch) gc.load(tr, tiles_n, r0 + 8 * kWaves, ct0);
+#pragma unroll
+        for (int cp = 0; cp < GV::NCP; ++cp) {
+            acc[cp][0] += tacc[cp][0];
+            acc[cp][1] += tacc[cp][1];
+        }
+        {   // sum of the 64 activations of these 4 tile-rows (raw-h correction)
+            const half2_t v = xs[r0 * 8 + (l & 31)];
+            xsum += (l < 32) ? (float)v.x + (float)v.y : 0.f;
+        }
+    }
+    xsum = wave_sum(xsum);
+#pragma unroll
+    for (int cp = 0; cp < GV::NCP; ++cp) {
+        int c0;
+        const bool own = GV::reduce(acc[cp], cp, c0);
+        if (own) {
+            S.red[wv][c0] = kC1 * acc[cp][0] + kC2 * xsum;
+            S.red[wv][c0 + 8] = kC1 * acc[cp][1] + kC2 * xsum;
+        }
+    }
+    __syncthreads();
     if (wv != 0) return;
-    if (l == 0) g_cnt_d[a * nbn + nb] = 0;
-    const float* pp = A.part_d + (size_t)(a * nbn + nb) * ksn * 128;
     float v0 = 0.f, v1 = 0.f;
-    for (int s = 0; s < ksn; ++s) {
-        v0 += __builtin_nontemporal_load(pp + s * 128 + 2 * l);
-        v1 += __builtin_nontemporal_load(pp + s * 128 + 2 * l + 1);
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+        v0 += S.red[w][2 * l];
+        v1 += S.red[w][2 * l + 1];
     }
     wave_fwht128(v0, v1);
     const int c = nb * 128 + 2 * l;
     const half_t* svd = (const half_t*)(base + A.g.off_svh_d) + c;
     const float sc = kRsqrt128 * A.w[a];
     float* y = A.ybuf + (size_t)a * H + c;
-    y[0] = v0 * sc * (float)svd[0];
-    y[1] = v1 * sc * (float)svd[1];
+    st_agent(y, v0 * sc * (float)svd[0]);
+    st_agent(y + 1, v1 * sc * (float)svd[1]);
     // combine: the last pair of row m to finish this 128-column block sums the top-k outputs in k order
-    __threadfence();
+    wait_stores();
     int old = 0;
-    if (l == 0) old = atomicAdd(&g_cnt_c[m * nbn + nb], 1);
+    if (l == 0) old = counter_add(&g_cnt_c[m * nbn + nb], 1);
     old = __shfl(old, 0, 64);
     if (old != A.topk - 1) return;
-    __threadfence();
-    if (l == 0) g_cnt_c[m * nbn + nb] = 0;
+    if (l == 0) counter_reset(&g_cnt_c[m * nbn + nb]);
+    const float* yb = A.ybuf + (size_t)(m * A.topk) * H + c;
     float o0 = 0.f, o1 = 0.f;
-    for (int k = 0; k < A.topk; ++k) {
-        const float* yk = A.ybuf + (size_t)(m * A.topk + k) * H + c;
-        o0 += __builtin_nontemporal_load(yk);
-        o1 += __builtin_nontemporal_load(yk + 1);
+    for (int k0 = 0; k0 < A.topk; k0 += 8) {     // 16 loads in flight per round
+        float v[8][2];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const bool ok = k0 + j < A.topk;
+            v[j][0] = ok ? ld_agent(yb + (size_t)(k0 + j) * H) : 0.f;
+            v[j][1] = ok ? ld_agent(yb + (size_t)(k0 + j) * H + 1) : 0.f;
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+            if (k0 + j < A.topk) {
+                o0 += v[j][0];
+                o1 += v[j][1];
+            }
     }
     const size_t oo = (size_t)m * A.out_stride + c;
     st_act(A.out, A.x_dt, oo, o0);
     st_act(A.out, A.x_dt, oo + 1, o1);
-    if (!A.commit_ptrs) return;
-    __threadfence();
-    if (l == 0) old = atomicAdd(&g_cnt_all[0], 1);
+    // the last (row, block) of the layer: clear the ready counts and commit the cache fills
+    if (l == 0) old = counter_add(&g_cnt_all[0], 1);
     old = __shfl(old, 0, 64);
     if (old != A.M * nbn - 1) return;
-    __threadfence();
-    if (l == 0) g_cnt_all[0] = 0;
+    if (l == 0) counter_reset(&g_cnt_all[0]);
+    for (int i = l; i < A.npairs; i += 64) counter_reset(&g_ready[i]);
+    if (!A.commit_ptrs) return;
     const int nf = A.fill_list[0];
     for (int i = l; i < nf; i += 64) {
         const int ef = A.fill_list[1 + i];
         A.commit_ptrs[ef] = A.commit_fill[ef];
         A.commit_fill[ef] = 0;
     }
+}
+
+template <int K>
+__global__ void __launch_bounds__(kThreads) moe_layer_kernel(DecodeArgs A) {
+    __shared__ LayerShared S;
+    const int n_gu = A.npairs * (A.g.I / 128) * gu_slices(A.g.H);
+    if ((int)blockIdx.x < n_gu) gateup_wg<K>(A, blockIdx.x, S);
+    else down_wg<K>(A, blockIdx.x - n_gu, S);
 }
 
 // bit-exact dequantization of one trellis matrix (PLANAR4 words [k_tiles][n_tiles][8K]) -> fp16 [16 k_tiles][16 n_tiles]
@@ -358,22 +420,19 @@ __global__ void __launch_bounds__(256) dequant_kernel(const uint32_t* __restrict
 
 // ---- host launchers ------------------------------------------------------------------------------------------------
 
-hipError_t launch_gateup(int K, const DecodeArgs& a, hipStream_t s) {
-    dim3 grid((unsigned)(a.npairs * (a.g.I / 128) * (a.g.H / 128)));
-    if (K == 2) hipLaunchKernelGGL(gateup_kernel<2>, grid, dim3(256), 0, s, a);
-    else if (K == 3) hipLaunchKernelGGL(gateup_kernel<3>, grid, dim3(256), 0, s, a);
-    else if (K == 4) hipLaunchKernelGGL(gateup_kernel<4>, grid, dim3(256), 0, s, a);
+hipError_t launch_moe_layer(int K, const DecodeArgs& a, hipStream_t s) {
+    const int n_gu = a.npairs * (a.g.I / 128) * gu_slices(a.g.H);
+    const int n_dn = a.npairs * (a.g.H / 128);
+    dim3 grid((unsigned)(n_gu + n_dn));
+    if (K == 2) hipLaunchKernelGGL(moe_layer_kernel<2>, grid, dim3(kThreads), 0, s, a);
+    else if (K == 3) hipLaunchKernelGGL(moe_layer_kernel<3>, grid, dim3(kThreads), 0, s, a);
+    else if (K == 4) hipLaunchKernelGGL(moe_layer_kernel<4>, grid, dim3(kThreads), 0, s, a);
     else return hipErrorInvalidValue;
     return hipGetLastError();
 }
 
-hipError_t launch_down(int K, const DecodeArgs& a, hipStream_t s) {
-    dim3 grid((unsigned)(a.npairs * (a.g.H / 128) * (a.g.I / 128)));
-    if (K == 2) hipLaunchKernelGGL(down_kernel<2>, grid, dim3(128), 0, s, a);
-    else if (K == 3) hipLaunchKernelGGL(down_kernel<3>, grid, dim3(128), 0, s, a);
-    else if (K == 4) hipLaunchKernelGGL(down_kernel<4>, grid, dim3(128), 0, s, a);
-    else return hipErrorInvalidValue;
-    return hipGetLastError();
+int read_status(int* out, hipStream_t s) {
+    return (int)hipMemcpyFromSymbolAsync(out, HIP_SYMBOL(g_status), sizeof(int) * 4, 0, hipMemcpyDeviceToHost, s);
 }
 
 hipError_t launch_dequant(int K, const uint32_t* tr, _Float16* out, int k_tiles, int n_tiles, hipStream_t s) {

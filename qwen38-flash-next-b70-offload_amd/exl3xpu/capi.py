@@ -37,6 +37,9 @@ SIGNATURES = {
                                         c_p]),
     "exl3_moe_align": (c_i32, [c_p, c_p, c_i32, c_i32, c_i32, c_i32, c_p, c_p, c_p]),
     "exl3_dequant": (c_i32, [c_p, c_i32, c_i32, c_i32, c_p, c_p]),
+    "exl3_device_status": (c_i32, [c_p, c_p]),
+    "exl3_scatter_flags": (c_i32, [c_p, c_i64, c_p, c_i64, c_p]),
+    "exl3_admit_decide": (c_i32, [c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_i64, c_p, c_p, c_p, c_p, c_p, c_p, c_p]),
     "exl3_host_alloc": (c_p, [c_i64]),
     "exl3_host_free": (c_i32, [c_p]),
     "exl3_usm_kind": (c_i32, [c_p]),

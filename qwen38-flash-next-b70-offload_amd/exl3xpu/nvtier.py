@@ -190,7 +190,10 @@ class NvTier:
 
 class NvTierFast(NvTier):
     """Vectorised bookkeeping + background fills (nvtier.py:175-278): age, in-flight set, pinned mask; fills complete
-    `latency` host steps after admission (deterministic)."""
+    `latency` host steps after admission (deterministic). The fills admitted by one host step are copied by a few
+    worker tasks (one future per chunk of keys), since each completes as a group."""
+
+    FILL_CHUNKS = 4
 
     def __init__(self, *a, **k):
         super().__init__(*a, **k)
@@ -200,21 +203,34 @@ class NvTierFast(NvTier):
         self.pin_mask = np.zeros(n, dtype=bool)
         self.pin_mask[list(self.pinned)] = True
         self.inflight = np.zeros(n, dtype=bool)
-        self._pending = {}                 # host step -> [(key, future)]
+        self._pending = {}                 # host step -> [(keys, future)]
         self._hstep = 0
         self._pool = ThreadPoolExecutor(int(os.environ.get("EXL3_NVTIER_FILL_THREADS", "16")))
 
+    def _read_keys(self, keys) -> None:
+        for key in keys:
+            self.src.read(self.rec_index(key), self.st.addr(key))
+
+    def _queue_fills(self, keys, hs: int) -> None:
+        """fills admitted at host step hs: copied by workers, flagged resident at host step hs + latency"""
+        keys = [int(k) for k in keys]
+        if not keys:
+            return
+        per = -(-len(keys) // self.FILL_CHUNKS)
+        lst = self._pending.setdefault(hs + self.latency, [])
+        for i in range(0, len(keys), per):
+            part = keys[i:i + per]
+            lst.append((part, self._pool.submit(self._read_keys, part)))
+        self.stats["nvme_reads"] += len(keys)
+
     def _queue_fill(self, key: int, hs: int) -> None:
-        """fill admitted at host step hs: copied by a worker, flagged resident at host step hs + latency"""
-        fut = self._pool.submit(self.src.read, self.rec_index(key), self.st.addr(key))
-        self._pending.setdefault(hs + self.latency, []).append((key, fut))
-        self.stats["nvme_reads"] += 1
+        self._queue_fills([key], hs)
 
     def _completed(self, hs: int):
         done = []
-        for key, fut in self._pending.pop(hs, []):
+        for keys, fut in self._pending.pop(hs, []):
             fut.result()
-            done.append(key)
+            done.extend(keys)
         return done
 
     def close(self):
@@ -222,91 +238,106 @@ class NvTierFast(NvTier):
         super().close()
 
 
+class _AdmitState(ctypes.Structure):
+    _fields_ = [(f, ctypes.c_int64) for f in ("n", "budget", "admit_age", "admit_qmax", "ring_cap", "tick",
+                                               "ring_seen", "masked", "evicts", "admit_dropped", "ring_overflow")]
+
+
+def _ptr(a: np.ndarray) -> int:
+    assert a.flags.c_contiguous
+    return a.ctypes.data
+
+
 class AdmissionPolicy:
-    """Host bookkeeping of the admission-controlled tier step (_async_step_admit, nvtier.py:708-806), pure numpy.
+    """Host bookkeeping of the admission-controlled tier step (_async_step_admit, nvtier.py:708-806); the decision
+    runs natively (exl3_admit_decide in libexl3moe.so) over the numpy books held here.
 
     decide() consumes the device state of the PREVIOUS step (flags with the previous upload overlaid, miss ring, HBM
-    residency) plus the keys whose fills completed now, and returns (admitted keys, evicted keys, flag diff keys, flag
+    slot map) plus the keys whose fills completed now, and returns (admitted keys, evicted keys, flag diff keys, flag
     diff values). Ordering contract: misses by descending count, ties by ascending key; evictions by ascending age,
     ties by ascending key (the reference's numpy argsort default is not stable)."""
 
     def __init__(self, n, pinned, budget, age=4, qmax=256, ring_cap=1 << 16):
-        self.n, self.budget, self.admit_age, self.admit_qmax, self.cap = n, int(budget), int(age), int(qmax), int(ring_cap)
+        from . import capi
+        self._lib = capi.lib()
+        self.n = int(n)
         self.res = np.zeros(n, dtype=np.uint8)
         self.age = np.zeros(n, dtype=np.int64)
         self.inflight = np.zeros(n, dtype=bool)
         self.pin_mask = np.zeros(n, dtype=bool)
         self.pin_mask[list(pinned)] = True
         self.res[list(pinned)] = 1
-        self.tick = 1
-        self.ring_seen = 0
-        self.stats = dict(masked=0, evicts=0, admit_dropped=0, ring_overflow=0)
+        self._st = _AdmitState(n=self.n, budget=int(budget), admit_age=int(age), admit_qmax=int(qmax),
+                               ring_cap=int(ring_cap), tick=1)
+        self._out = np.empty((3, self.n), dtype=np.int64)
+        self._vals = np.empty(self.n, dtype=np.uint8)
+        self._cnt = np.zeros(3, dtype=np.int64)
 
-    def decide(self, view, ring, vram, done_keys):
-        newly = (view == 1) & (self.res == 0)        # victims written back by the device: newest RAM entries
-        self.age[newly] = self.tick
-        res = self.res.copy()
-        res[newly] = 1
-        for kk in done_keys:
-            res[kk] = 1
-            self.age[kk] = self.tick
-            self.inflight[kk] = False
-        cnt = int(ring[0])
-        newm = cnt - self.ring_seen
-        if newm > self.cap:
-            self.stats["ring_overflow"] += newm - self.cap
-            newm = self.cap
-        want = np.zeros(0, dtype=np.int64)
-        if newm > 0:
-            lo, hi = (cnt - newm) % self.cap, cnt % self.cap
-            r = ring[1:]
-            keys = np.concatenate([r[lo:], r[:hi]]) if hi <= lo else r[lo:hi]
-            u, c = np.unique(keys[:newm].astype(np.int64), return_counts=True)
-            ok = (res[u] == 0) & (~self.inflight[u])
-            u, c = u[ok], c[ok]
-            want = u[np.argsort(-c, kind="stable")]
-        self.ring_seen = cnt
-        self.stats["masked"] += max(0, newm)
-        inflight_n = int(self.inflight.sum())
-        over = int(res.sum()) + inflight_n + len(want) - self.budget
-        ev_keys = np.zeros(0, dtype=np.int64)
-        if over > 0:
-            cand1 = np.nonzero((res == 1) & vram & ~self.pin_mask)[0]
-            take1 = cand1[np.argsort(self.age[cand1], kind="stable")[:over]]
-            over -= len(take1)
-            take2 = np.zeros(0, dtype=np.int64)
-            if over > 0:
-                m = (res == 1) & ~self.pin_mask & (self.age <= self.tick - self.admit_age)
-                m[take1] = False
-                cand2 = np.nonzero(m)[0]
-                take2 = cand2[np.argsort(self.age[cand2], kind="stable")[:over]]
-            ev_keys = np.concatenate([take1, take2]).astype(np.int64)
-            res[ev_keys] = 0
-            self.stats["evicts"] += len(ev_keys)
-        free = min(self.budget - int(res.sum()) - inflight_n, self.admit_qmax - inflight_n)
-        adm = want[:max(0, free)].astype(np.int64)
-        self.stats["admit_dropped"] += len(want) - len(adm)
-        self.inflight[adm] = True
-        diff = np.nonzero(res != view)[0].astype(np.int64)
-        self.res = res
-        return adm, ev_keys, diff, res[diff].copy()
+    def _field(name):
+        return property(lambda self: int(getattr(self._st, name)),
+                        lambda self, v: setattr(self._st, name, int(v)))
+
+    budget = _field("budget")
+    admit_age = _field("admit_age")
+    admit_qmax = _field("admit_qmax")
+    cap = _field("ring_cap")
+    tick = _field("tick")
+    ring_seen = _field("ring_seen")
+    del _field
+
+    @property
+    def stats(self):
+        st = self._st
+        return dict(masked=st.masked, evicts=st.evicts, admit_dropped=st.admit_dropped, ring_overflow=st.ring_overflow)
+
+    def decide(self, view, ring, slot_of, done_keys):
+        """view u8 [n], ring i32 [1 + cap], slot_of i32 [n] (>= 0: resident in HBM), done_keys: completed fills."""
+        view = np.ascontiguousarray(view, dtype=np.uint8)
+        ring = np.ascontiguousarray(ring, dtype=np.int32)
+        slot_of = np.ascontiguousarray(slot_of, dtype=np.int32)
+        done = np.ascontiguousarray(np.asarray(done_keys, dtype=np.int64).reshape(-1))
+        assert view.size == self.n and slot_of.size == self.n and ring.size == self.cap + 1
+        c = self._cnt
+        cp = _ptr(c)
+        rc = self._lib.exl3_admit_decide(ctypes.byref(self._st), _ptr(self.res), _ptr(self.age), _ptr(self.inflight),
+                                         _ptr(self.pin_mask), _ptr(view), _ptr(ring), _ptr(slot_of), _ptr(done),
+                                         done.size, _ptr(self._out[0]), cp, _ptr(self._out[1]), cp + 8,
+                                         _ptr(self._out[2]), _ptr(self._vals), cp + 16)
+        if rc != 0:
+            raise RuntimeError(f"exl3_admit_decide: error {rc} (corrupt snapshot or bad done key)")
+        na, ne, nd = int(c[0]), int(c[1]), int(c[2])
+        return (self._out[0, :na].copy(), self._out[1, :ne].copy(), self._out[2, :nd].copy(),
+                self._vals[:nd].copy())
 
 
 class NvTierAsync(NvTierFast):
     """One-step-lagged, event-ordered bookkeeping without a per-step device sync (nvtier.py:282-386) with the
     admission policy (AdmissionPolicy): AGE = EXL3_NVTIER_ADMIT_AGE (default 4), QMAX = EXL3_NVTIER_ADMIT_QMAX
-    (default 256). Host step n snapshots the device state after decode step n and acts on the snapshot of step n-1."""
+    (default 256). Host step n snapshots the device state after decode step n and acts on the snapshot of step n-1.
+
+    Per step on the stream: three snapshot copies into pinned double buffers and one flag-scatter kernel that reads
+    the (key, value) diff in place from a pinned double buffer; no host allocation, no extra synchronisation."""
 
     def __init__(self, *a, **k):
         super().__init__(*a, **k)
+        from . import capi
+        self._capi = capi
         n = self.L * self.E
         self._n = n
+        X = self.st.X
         self._h_res = [torch.empty(n, dtype=torch.uint8).pin_memory() for _ in range(2)]
         self._h_ring = [torch.empty(self.ring.numel(), dtype=torch.int32).pin_memory() for _ in range(2)]
         self._h_slot = [torch.empty(n, dtype=torch.int32).pin_memory() for _ in range(2)]
-        self._snap_ev = [None, None]
+        self._np_res = [t.numpy() for t in self._h_res]
+        self._np_ring = [t.numpy() for t in self._h_ring]
+        self._np_slot = [t.numpy() for t in self._h_slot]
+        self._h_diff = [X.host_alloc(4 * n).view(torch.int32) for _ in range(2)]   # device-mapped pinned
+        self._np_diff = [t.numpy() for t in self._h_diff]
+        self._snap_ev = [torch.cuda.Event(), torch.cuda.Event()]
+        self._have = [False, False]
         self._k = 0
         self._last_diff = None
+        self._view = np.empty(n, dtype=np.uint8)
         self.policy = AdmissionPolicy(n, self.pinned, self.budget, int(os.environ.get("EXL3_NVTIER_ADMIT_AGE", "4")),
                                       int(os.environ.get("EXL3_NVTIER_ADMIT_QMAX", "256")), self.ring.numel() - 1)
         self.policy.res[:] = self.res
@@ -327,35 +358,37 @@ class NvTierAsync(NvTierFast):
         self._hstep += 1
         n = self._n
         cur = torch.cuda.current_stream(self.dev)
+        L, sh = self._capi.lib(), cur.cuda_stream
         k = self._k
         self._k ^= 1
-        self._h_res[k].copy_(self.res_dev[:n], non_blocking=True)
-        self._h_ring[k].copy_(self.ring, non_blocking=True)
-        self._h_slot[k].copy_(self.st.slot_of_dev[:n], non_blocking=True)
-        ev = torch.cuda.Event()
-        ev.record(cur)
-        self._snap_ev[k] = ev
+        for dst, src, nb in ((self._h_res[k], self.res_dev, n), (self._h_ring[k], self.ring, 4 * self.ring.numel()),
+                             (self._h_slot[k], self.st.slot_of_dev, 4 * n)):
+            rc = L.exl3_memcpy_async(dst.data_ptr(), src.data_ptr(), nb, sh)
+            if rc:
+                self._capi.check(rc, "nvtier snapshot")
+        self._snap_ev[k].record(cur)
+        self._have[k] = True
         j = k ^ 1
-        if self._snap_ev[j] is None:
+        if not self._have[j]:
             self.stats["steps"] += 1
             if self.log_decisions:
                 self.decisions.append((np.zeros(0, np.int64), np.zeros(0, np.int64)))
             return 0
         self._snap_ev[j].synchronize()
-        view = self._h_res[j].numpy().copy()
+        view = self._view
+        np.copyto(view, self._np_res[j])
         if self._last_diff is not None:
             dk, dv = self._last_diff
             view[dk] = dv
-        ring = self._h_ring[j].numpy()
-        vram = self._h_slot[j].numpy() >= 0
         seen0 = pol.ring_seen
-        adm, ev_keys, diff, vals = pol.decide(view, ring, vram, self._completed(hs))
-        for kk in adm.tolist():
-            self._queue_fill(kk, hs)
+        adm, ev_keys, diff, vals = pol.decide(view, self._np_ring[j], self._np_slot[j], self._completed(hs))
+        self._queue_fills(adm, hs)
         if len(diff):
-            idx = torch.from_numpy(diff).pin_memory().to(self.dev, non_blocking=True)
-            val = torch.from_numpy(vals).pin_memory().to(self.dev, non_blocking=True)
-            self.res_dev.index_copy_(0, idx, val)
+            # buffer k was last read by the scatter of step n-2, which ran before the snapshot just waited for
+            buf = self._np_diff[k]
+            buf[:len(diff)] = (diff << 1) | vals
+            self._capi.check(L.exl3_scatter_flags(self.res_dev.data_ptr(), n, self._h_diff[k].data_ptr(), len(diff),
+                                                  sh), "nvtier flag upload")
             self._last_diff = (diff, vals)
         else:
             self._last_diff = None
@@ -363,8 +396,8 @@ class NvTierAsync(NvTierFast):
         self.age, self.inflight, self.ring_seen = pol.age, pol.inflight, pol.ring_seen
         if self.log_decisions:
             self.decisions.append((adm.copy(), ev_keys.copy()))
-        for key in ("masked", "evicts", "admit_dropped", "ring_overflow"):
-            self.stats[key] = pol.stats[key]
+        for key, v in pol.stats.items():
+            self.stats[key] = v
         self.stats["steps"] += 1
         self.stats["fill_ms"] += (time.perf_counter() - t0) * 1e3
         return int(max(0, pol.ring_seen - seen0))
