@@ -9,8 +9,9 @@ calls, replays it and runs the host tier step (the way a serving engine replays 
 by one instead); `value` is tokens per second over the timed steps.
 
 roofline: the fused dequant-GEMV layer kernel (moe_layer_kernel, one moe_forward call per layer) on HBM-resident experts,
-timed with HIP events on the launch stream: algorithmic bytes per call = distinct experts x blob bytes (every byte of
-each routed expert blob is read once) / average call duration, against the MI355X HBM3E peak of 8 TB/s.
+R x 48 calls captured in one HIP graph and timed with HIP events around its replay on the launch stream: algorithmic
+bytes per call = distinct experts x blob bytes (every byte of each routed expert blob is read once) / average call
+duration, against the MI355X HBM3E peak of 8 TB/s.
 cpu_baseline: the PyTorch CPU restatement of the same layer math (oracle/cpu_path.py), one config-0 layer timed and
 scaled to 48 layers.
 """
@@ -31,6 +32,11 @@ H, I, K, E, L, TOPK = 2048, 512, 3, 512, 48, 10
 SLOTS, BUDGET = 8000, 1075
 SEED = 20261203
 HBM_PEAK = 8000.0   # GB/s, MI355X HBM3E
+# HBM counters of one resident moe_layer_kernel<3> call at this workload (KiB per dispatch, rocprofv3 --pmc FETCH_SIZE
+# and --pmc WRITE_SIZE over bench.py --roofline-only) and the factor that maps each counter to the bytes of a plain
+# 256 MiB device copy in the same runs; re-measured whenever the kernel changes.
+PMC_KIB = {"fetch": 6268.1, "write": 512.6}
+PMC_SCALE = {"fetch": 262144 / 131083.5, "write": 1.0}
 
 
 def log(*a):
@@ -68,13 +74,17 @@ def cpu_baseline(samples: int = 10):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=200)
-    ap.add_argument("--warmup", type=int, default=100)
+    ap.add_argument("--steps", type=int, default=500)
+    ap.add_argument("--warmup", type=int, default=1000, help="untimed steps: the cache and RAM tier start empty and "
+                    "reach their steady state after about 1,000 steps of the Zipf trace")
     ap.add_argument("--bs", type=int, default=1)
     ap.add_argument("--roofline-steps", type=int, default=20)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--budget-records", type=int, default=BUDGET)
     ap.add_argument("--eager", action="store_true", help="launch the 48 layer calls eagerly instead of a HIP graph")
+    ap.add_argument("--roofline-only", action="store_true",
+                    help="counter runs: only the HBM-resident layer calls, after 3 device copies of 256 MiB (the "
+                         "known-size calibration kernel for FETCH_SIZE / WRITE_SIZE)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: the expert-offload path is single-GPU (the reference has no multi-GPU "
@@ -97,7 +107,9 @@ def main():
     tier = nvtier.NvTierAsync(store, src, budget_records=args.budget_records, latency=8)
     log(f"setup {time.perf_counter() - t0:.1f} s: slots {SLOTS} x {store.blob} B, pinned arena {store.size / 2**30:.1f} GiB")
     steps, warm, bs = args.steps, args.warmup, args.bs
-    ids_np, w_np = synth.zipf_trace(SEED, warm + steps, L, E, TOPK, M=bs)
+    if args.roofline_only:
+        steps, warm = 0, 0
+    ids_np, w_np = synth.zipf_trace(SEED, max(warm + steps, args.roofline_steps), L, E, TOPK, M=bs)
     ids_all = torch.from_numpy(ids_np).to(dev)
     w_all = torch.from_numpy(w_np).to(dev)
     xs = torch.randn(L, bs, H, generator=torch.Generator().manual_seed(SEED)).to(torch.bfloat16).to(dev)
@@ -124,10 +136,17 @@ def main():
         host_s["launch"] += t2 - t
         host_s["tier_step"] += time.perf_counter() - t2
 
+    if args.roofline_only:
+        a = torch.empty(256 << 20, dtype=torch.uint8, device=dev)
+        b = torch.empty_like(a)
+        for _ in range(3):
+            b.copy_(a)
+        torch.cuda.synchronize()
+        del a, b
     for n in range(min(warm, 2)):
         decode_step(n)
     torch.cuda.synchronize()
-    if not args.eager:
+    if not args.eager and not args.roofline_only:
         graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(graph, capture_error_mode="thread_local"):
             layers()
@@ -141,11 +160,12 @@ def main():
         decode_step(n)
     torch.cuda.synchronize()
     el = time.perf_counter() - t1
-    tok_s = steps * bs / el
+    tok_s = steps * bs / el if steps else 0.0
     d = {k: tier.stats.get(k, 0) - st0.get(k, 0) for k in ("masked", "evicts", "nvme_reads", "admit_dropped")}
-    host_ms = {k: round(v / steps * 1e3, 4) for k, v in host_s.items()}
-    log(f"decode ({'eager' if graph is None else 'graph'}) {steps} steps in {el:.3f} s: {tok_s:.1f} tok/s; per step masked {d['masked'] / steps:.1f} "
-        f"fills {d['nvme_reads'] / steps:.2f} evicts {d['evicts'] / steps:.2f}; host ms per step {host_ms}")
+    host_ms = {k: round(v / max(steps, 1) * 1e3, 4) for k, v in host_s.items()}
+    sd = max(steps, 1)
+    log(f"decode ({'eager' if graph is None else 'graph'}) {steps} steps in {el:.3f} s: {tok_s:.1f} tok/s; per step masked {d['masked'] / sd:.1f} "
+        f"fills {d['nvme_reads'] / sd:.2f} evicts {d['evicts'] / sd:.2f}; host ms per step {host_ms}")
 
     # ---- roofline: dequant-GEMV on HBM-resident experts, distinct slots per (step, layer) call
     X = store.X
@@ -166,29 +186,35 @@ def main():
     ids_r = torch.from_numpy(ids_np[:R]).to(dev)
     w_r = torch.from_numpy(w_np[:R]).to(dev)
     stream = torch.cuda.current_stream()
-    for r in range(min(2, R)):            # warm-up
+    for r in range(min(2, R)):            # eager warm-up
         for li in range(L):
             X.moe_forward(xs[li], ids_r[r, li], w_r[r, li], tbl[r, li], I, K, E)
-    evs = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(L)] for _ in range(R)]
     torch.cuda.synchronize()
-    t2 = time.perf_counter()
-    for r in range(R):
-        for li in range(L):
-            a, b = evs[r][li]
-            a.record(stream)
-            X.moe_forward(xs[li], ids_r[r, li], w_r[r, li], tbl[r, li], I, K, E)
-            b.record(stream)
+    # the R x 48 calls as one HIP graph, timed with events around its replay on the launch stream: the kernels run
+    # back to back, so the per-call time is the kernel's duration (plus the small dispatch gap between graph nodes)
+    rgraph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(rgraph, capture_error_mode="thread_local"):
+        for r in range(R):
+            for li in range(L):
+                X.moe_forward(xs[li], ids_r[r, li], w_r[r, li], tbl[r, li], I, K, E)
+    rgraph.replay()
     torch.cuda.synchronize()
-    el2 = time.perf_counter() - t2
-    ms = np.array([[evs[r][li][0].elapsed_time(evs[r][li][1]) for li in range(L)] for r in range(R)])
-    achieved = float(nbytes.sum() / (ms.sum() * 1e-3) / 1e9)
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    ev0.record(stream)
+    rgraph.replay()
+    ev1.record(stream)
+    torch.cuda.synchronize()
+    us_call = ev0.elapsed_time(ev1) * 1e3 / (R * L)
+    achieved = float(nbytes.mean() / (us_call * 1e-6) / 1e9)
     per_call_bytes = float(nbytes.mean())
-    log(f"roofline: {R * L} calls, mean {ms.mean() * 1e3:.1f} us per call, {per_call_bytes / 1e6:.2f} MB per call -> "
-        f"{achieved:.0f} GB/s; resident decode {R * bs / el2:.0f} tok/s (host-timed, with launch gaps)")
+    resident_tok_s = 1e6 / (us_call * L) * bs
+    log(f"roofline: {R * L} calls in one graph, {us_call:.2f} us per call, {per_call_bytes / 1e6:.2f} MB per call -> "
+        f"{achieved:.0f} GB/s; all-resident decode {resident_tok_s:.0f} tok/s")
+    traffic = (PMC_KIB["fetch"] * PMC_SCALE["fetch"] + PMC_KIB["write"] * PMC_SCALE["write"]) * 1024
 
     out = {
         "metric": METRIC, "value": round(tok_s, 2), "unit": "tok/s", "n_gpus": 1, "steps": steps, "warmup": warm,
-        "ms_per_step": round(el / steps * 1e3, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "ms_per_step": round(el / sd * 1e3, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "bf16", "data": "synthetic: seeded EXL3 3bpw experts (64 distinct blobs), seeded Zipf(1.1) routing trace",
         "config": {"workload": "decode bs=%d through 48 MoE layers x 512 experts (H 2048, I 512), top-10, EXL3 K=3; "
                                "8,000 HBM slots + pinned RAM tier (%d records), admission AGE 4 / QMAX 256, "
@@ -196,16 +222,19 @@ def main():
                    "layers": L, "experts": E, "topk": TOPK, "hidden": H, "intermediate": I, "K": K, "batch": bs,
                    "hbm_slots": SLOTS, "ram_budget_records": args.budget_records},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK, 4), "traffic": None,
+                     "frac": round(achieved / HBM_PEAK, 4), "traffic": round(traffic),
+                     "traffic_note": "FETCH_SIZE + WRITE_SIZE per call from rocprofv3 --pmc runs of --roofline-only, "
+                                     "scaled by a 256 MiB copy (x%.2f / x%.2f): profiles/moe_layer_kernel_h2048_i512_top10_k3_resident_pmc.md"
+                                     % (PMC_SCALE["fetch"], PMC_SCALE["write"]),
                      "kernel": "moe_layer_kernel<3> (one moe_forward call per layer, HBM-resident experts)",
-                     "bytes_per_call": per_call_bytes, "us_per_call": round(float(ms.mean()) * 1e3, 2)},
+                     "bytes_per_call": per_call_bytes, "us_per_call": round(us_call, 2)},
         "launch": "eager" if graph is None else "hip graph of the 48 layer calls per step",
         "host_ms_per_step": host_ms,
-        "resident_decode_tok_s": round(R * bs / el2, 1),
-        "per_step": {"masked": d["masked"] / steps, "fills": d["nvme_reads"] / steps, "evicts": d["evicts"] / steps,
-                     "admit_dropped": d["admit_dropped"] / steps},
+        "resident_decode_tok_s": round(resident_tok_s, 1),
+        "per_step": {"masked": d["masked"] / sd, "fills": d["nvme_reads"] / sd, "evicts": d["evicts"] / sd,
+                     "admit_dropped": d["admit_dropped"] / sd},
     }
-    if not args.no_cpu_baseline:
+    if not args.no_cpu_baseline and not args.roofline_only:
         out["cpu_baseline"] = cpu_baseline()
         log(f"cpu baseline {out['cpu_baseline']['value']:.4f} tok/s on {out['cpu_baseline']['cores']} threads")
     tier.close()
