@@ -64,13 +64,15 @@ int exl3_set_decision_log(int32_t* buf, int64_t cap_records);
 
 /* ---- routed-expert MoE --------------------------------------------------------------------------------------------- */
 
-/* workspace bytes for a decode call of M rows (pair mode) */
-size_t exl3_moe_forward_workspace(int M, int H, int I, int topk);
+/* workspace bytes of an exl3_moe_forward call with these sizes (decode kernels for M < prefill_min_m, the prefill
+ * path otherwise: sorted routing, input Hadamards [M topk][2][H] fp16, abuf [M topk][I] fp16, y [M topk][H] fp16) */
+size_t exl3_moe_forward_workspace(int M, int H, int I, int topk, int n_experts);
 
 /* moe_forward (a8:1221-1225 -> moe_forward_impl a8:1263-1314): out[m] = sum_k w[m,k] * expert(ids[m,k])(x[m]).
  * x, out: [M, H] with row strides, dtype EXL3_DT_*; ids int32 / w fp32 [M, topk] contiguous; ptrs int64 [n_experts]
- * blob addresses (device slots or device-mapped pinned host memory). M <= pair_max_m runs the decode GEMV kernels,
- * larger M the grouped prefill path. */
+ * blob addresses (device slots or device-mapped pinned host memory). M < prefill_min_m runs the fused decode kernel
+ * (M <= 256 rows, M * topk <= 1024 pairs); M >= prefill_min_m the prefill path (moe_prefill a8:792-828): token sort,
+ * grouped MFMA GEMMs with the trellis decoded into LDS, y in fp16, combine (needs H % 256 == 0). */
 int exl3_moe_forward(const void* x, int x_dtype, int64_t x_stride, int M, int H, const int32_t* topk_ids,
                      const float* topk_w, int topk, const int64_t* ptrs, int I, int K, int n_experts, void* out,
                      int64_t out_stride, void* workspace, size_t workspace_bytes, void* stream);
@@ -88,10 +90,13 @@ int exl3_moe_forward_cached(const void* x, int x_dtype, int64_t x_stride, int M,
 
 /* moe_align (a8:1316-1323 -> launch_align a8:639-680): token sort by expert into the reference's packed buffers:
  * ib int32 [4A + 1 + 2*npairs + 16] = act_expert[A] act_start[A] act_cnt[A] act_pstart[A] n_act pair_tok[npairs]
- * pair_of[npairs] ..., fb fp32 [npairs] = pair_w, A = min(npairs, n_experts). Canonical order: pairs of an expert in
- * ascending pair index. */
+ * pair_of[npairs] ..., fb fp32 [npairs] = pair_w, A = min(npairs, n_experts); active experts ascending, act_pstart the
+ * starts padded to multiples of `pad`. Canonical order: pairs of an expert in ascending pair index (the reference's
+ * order inside an expert depends on atomics). Ids outside [0, n_experts) are clamped. The workspace (device,
+ * exl3_moe_align_workspace bytes) holds per-chunk counts. */
+size_t exl3_moe_align_workspace(int M, int topk, int n_experts);
 int exl3_moe_align(const int32_t* topk_ids, const float* topk_w, int M, int topk, int n_experts, int pad, int32_t* ib,
-                   float* fb, void* stream);
+                   float* fb, void* workspace, size_t workspace_bytes, void* stream);
 
 /* Flag upload of the host tier step (replaces the index_copy_ of plugin/exl3xpu/nvtier.py:791-793):
  * flags[packed[i] >> 1] = packed[i] & 1 for i < n. `packed` may be pinned, device-mapped host memory (read in place,

@@ -85,6 +85,17 @@ struct Period {
     }
 };
 
+// word offset of (tile-row r, tile-col `tile`, period p, plane i) in a PLANAR4 matrix with tiles_n tile-columns
+template <int K>
+__device__ __forceinline__ size_t word_off(int r, int tiles_n, int tile, int p, int i) {
+    using GM = Geo<K>;
+    if constexpr (GM::D > 1) {
+        return (size_t)r * tiles_n * GM::W + (size_t)(tile >> 2) * 4 * GM::W + i * 4 * GM::G + (tile & 3) * GM::G + p;
+    } else {
+        return (size_t)r * tiles_n * GM::W + (size_t)tile * GM::W + p;
+    }
+}
+
 // position of value u of period p inside the 16x16 tile
 template <int K>
 __host__ __device__ constexpr int val_row(int p, int u) {

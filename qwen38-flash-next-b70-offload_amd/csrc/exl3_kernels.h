@@ -46,6 +46,27 @@ struct VictimArgs {
     uint8_t* ram_res; int chunk_bytes;
 };
 
+// token sort (reference launch_align a8:639-680): pairs sorted by expert, ascending pair index inside an expert
+struct AlignOut {
+    int* act_expert; int* act_start; int* act_cnt; int* act_pstart; int* n_act;   // [A], [A], [A], [A], [1]
+    int* pair_tok; int* pair_of; float* pair_w;                                    // [npairs] each
+    int* pair_exp;                                                                  // expert of each sorted pair or null
+};
+
+struct PrefillArgs {
+    const void* x; int x_dt; int64_t x_stride;     // activations [M, H]
+    const int32_t* ids; const float* w;            // [M * topk]
+    int M, topk, npairs;
+    const int64_t* ptrs;                           // per-layer blob pointer table [E]
+    const int* act_expert; const int* act_start; const int* act_cnt; const int* n_act;
+    const int* pair_tok; const float* pair_w; const int* pair_of; const int* pair_exp;
+    _Float16* xh;                                  // [npairs (sorted)][2][H] input Hadamards (gate, up)
+    _Float16* abuf;                                // [npairs (sorted)][I]
+    _Float16* y;                                   // [npairs (sorted)][H], routing weight applied
+    void* out; int64_t out_stride;                 // [M, H], dtype of x
+    BlobGeom g;
+};
+
 // decode.hip
 hipError_t launch_moe_layer(int K, const DecodeArgs& a, hipStream_t s);
 int read_status(int* out, hipStream_t s);
@@ -54,6 +75,12 @@ hipError_t launch_dequant(int K, const uint32_t* tr, _Float16* out, int k_tiles,
 hipError_t launch_ensure(const EnsureArgs& a, hipStream_t s);
 hipError_t launch_victim_copy(const VictimArgs& a, int max_victims, hipStream_t s);
 hipError_t launch_scatter_flags(uint8_t* flags, int64_t n_flags, const int32_t* packed, int64_t n, hipStream_t s);
+// prefill.hip
+hipError_t launch_align(const int32_t* ids, const float* w, int npairs, int topk, int E, int pad, int* chunk_scratch,
+                        const AlignOut& o, hipStream_t s);
+size_t align_scratch_bytes(int npairs, int E);
+size_t prefill_workspace_bytes(int M, int H, int I, int topk, int E);
+hipError_t launch_prefill(PrefillArgs a, int E, void* ws, hipStream_t s);
 
 // 256-row slices of H handled by the split-K gate/up workgroups (H is a multiple of 128)
 __host__ __device__ static inline int gu_slices(int H) { return (H + 255) / 256; }

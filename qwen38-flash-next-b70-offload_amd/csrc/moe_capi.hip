@@ -119,8 +119,12 @@ int exl3_set_decision_log(int32_t* buf, int64_t cap_records) {
     return EXL3_OK;
 }
 
-size_t exl3_moe_forward_workspace(int M, int H, int I, int topk) {
-    return decode_workspace_bytes(M * topk, H, I);
+static bool use_prefill(int M) { return M >= g_cfg.prefill_min_m; }
+
+size_t exl3_moe_forward_workspace(int M, int H, int I, int topk, int n_experts) {
+    if (M <= 0 || topk <= 0 || H <= 0 || I <= 0) return 0;
+    const int E = std::min(std::max(n_experts, 1), kMaxExperts);
+    return use_prefill(M) ? prefill_workspace_bytes(M, H, I, topk, E) : decode_workspace_bytes(M * topk, H, I);
 }
 
 static int64_t* pair_ptr_area(void* ws, int npairs, int H, int I) {
@@ -132,6 +136,28 @@ static int forward_impl(const void* x, int x_dtype, int64_t x_stride, int M, int
                         int topk, const int64_t* ptrs, int I, int K, int E, void* out, int64_t out_stride, void* ws,
                         size_t ws_bytes, hipStream_t st, const int64_t* fill, int64_t* commit_ptrs, int64_t* commit_fill,
                         const int32_t* fill_list, const int64_t* pair_ptr) {
+    if (!fill && use_prefill(M)) {
+        if (H % 256) return fail(EXL3_EUNSUPPORTED, "moe prefill: H %% 256 == 0 required (H=%d)", H);
+        if ((int64_t)M * topk > (1 << 28)) return fail(EXL3_EUNSUPPORTED, "moe prefill: %d x %d pairs", M, topk);
+        const size_t need = prefill_workspace_bytes(M, H, I, topk, E);
+        if (!ws || ws_bytes < need)
+            return fail(EXL3_EWORKSPACE, "moe_forward (prefill): workspace %zu < %zu bytes", ws_bytes, need);
+        PrefillArgs pa{};
+        pa.x = x;
+        pa.x_dt = x_dtype;
+        pa.x_stride = x_stride;
+        pa.ids = ids;
+        pa.w = w;
+        pa.M = M;
+        pa.topk = topk;
+        pa.npairs = M * topk;
+        pa.ptrs = ptrs;
+        pa.out = out;
+        pa.out_stride = out_stride;
+        pa.g = blob_geom(H, I, K);
+        hipError_t e = launch_prefill(pa, E, ws, st);
+        return e == hipSuccess ? EXL3_OK : hip_fail(e, "moe prefill launch");
+    }
     const int npairs = M * topk;
     if (npairs > kMaxPairs || M > kMaxRows)
         return fail(EXL3_EUNSUPPORTED, "moe_forward: M=%d x topk=%d exceeds the decode kernels (%d pairs, %d rows)", M,
@@ -255,10 +281,33 @@ int exl3_moe_forward_cached(const void* x, int x_dtype, int64_t x_stride, int M,
                         workspace_bytes, st, fl, pl, fl, fill_list, ea.pair_ptr);
 }
 
+size_t exl3_moe_align_workspace(int M, int topk, int n_experts) {
+    if (M <= 0 || topk <= 0 || n_experts <= 0) return 0;
+    return align_scratch_bytes(M * topk, std::min(n_experts, kMaxExperts));
+}
+
 int exl3_moe_align(const int32_t* topk_ids, const float* topk_w, int M, int topk, int n_experts, int pad, int32_t* ib,
-                   float* fb, void* stream) {
-    (void)topk_ids; (void)topk_w; (void)M; (void)topk; (void)n_experts; (void)pad; (void)ib; (void)fb; (void)stream;
-    return fail(EXL3_EUNSUPPORTED, "moe_align: not built yet");
+                   float* fb, void* workspace, size_t workspace_bytes, void* stream) {
+    if (M < 0 || topk <= 0 || n_experts <= 0 || n_experts > kMaxExperts || pad <= 0)
+        return fail(EXL3_EINVAL, "moe_align: M=%d topk=%d n_experts=%d pad=%d", M, topk, n_experts, pad);
+    const int npairs = M * topk, A = std::min(npairs, n_experts);
+    if (npairs > 0 && (!topk_ids || !topk_w)) return fail(EXL3_EINVAL, "moe_align: null ids / w");
+    if (!ib || (npairs > 0 && !fb)) return fail(EXL3_EINVAL, "moe_align: null outputs");
+    const size_t need = exl3_moe_align_workspace(M, topk, n_experts);
+    if (need && (!workspace || workspace_bytes < need))
+        return fail(EXL3_EWORKSPACE, "moe_align: workspace %zu < %zu bytes", workspace_bytes, need);
+    AlignOut o{};
+    o.act_expert = ib;
+    o.act_start = ib + A;
+    o.act_cnt = ib + 2 * A;
+    o.act_pstart = ib + 3 * A;
+    o.n_act = ib + 4 * A;
+    o.pair_tok = ib + 4 * A + 1;
+    o.pair_of = o.pair_tok + npairs;
+    o.pair_w = fb;
+    o.pair_exp = nullptr;
+    hipError_t e = launch_align(topk_ids, topk_w, npairs, topk, n_experts, pad, (int*)workspace, o, (hipStream_t)stream);
+    return e == hipSuccess ? EXL3_OK : hip_fail(e, "moe_align launch");
 }
 
 int exl3_scatter_flags(uint8_t* flags, int64_t n_flags, const int32_t* packed, int64_t n, void* stream) {

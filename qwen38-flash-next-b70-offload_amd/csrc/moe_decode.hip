@@ -34,17 +34,6 @@ __device__ int g_status[4];          // [0]: spin timeouts (should stay 0)
 
 constexpr int kSpinMax = 1 << 22;
 
-// word offset of (tile-row r, tile-col `tile`, period p, plane i) in a PLANAR4 matrix with tiles_n tile-columns
-template <int K>
-__device__ __forceinline__ size_t word_off(int r, int tiles_n, int tile, int p, int i) {
-    using GM = Geo<K>;
-    if constexpr (GM::D > 1) {
-        return (size_t)r * tiles_n * GM::W + (size_t)(tile >> 2) * 4 * GM::W + i * 4 * GM::G + (tile & 3) * GM::G + p;
-    } else {
-        return (size_t)r * tiles_n * GM::W + (size_t)tile * GM::W + p;
-    }
-}
-
 // one period of one tile-row: xv[a][qq] holds activation rows (8a + 2q, 8a + 2q + 1), q = (qb + qq) & 3
 template <int K, int NQ, int u>
 __device__ __forceinline__ void accum_period(const Period<K>& P, const half2_t (&xv)[2][NQ], float (&acc)[2]) {

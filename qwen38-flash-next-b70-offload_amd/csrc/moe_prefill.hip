@@ -1,0 +1,483 @@
+// Prefill MoE (M >= prefill_min_m rows): token sort by expert + grouped GEMMs on MFMA with the EXL3 trellis decoded
+// into LDS (reference: moe_prefill a8:792-828, launch_align a8:639-680, GateUpDpasKernel a8:422-545,
+// DownDpasKernel a8:548-635, CombineKernel<TO, fp16> a8:371-395).
+//
+//   align      three small kernels (count per chunk of 1,024 pairs, scan, scatter): pairs sorted by expert in
+//              ascending pair order inside an expert (deterministic; wave ballots for in-chunk ranks)
+//   xh         one wave per (sorted pair, projection, 128-row block of H): xh = fp16(H(fp16(x * suh)) / sqrt(128)),
+//              computed once per pair (the column-tile workgroups of an expert all read it)
+//   gate/up    one workgroup of 8 waves per (active expert, 128-column block of I), over the expert's rows in chunks of
+//              256: the 4 tile-rows x (8 gate + 8 up) tiles of each 64-deep K chunk are decoded once into LDS as the
+//              fp16 B operand of v_mfma_f32_32x32x16_f16 (double-buffered; one barrier per chunk), A = xh rows read
+//              from HBM, fp32 accumulation over all of H; epilogue through LDS: g/u Hadamards, SwiGLU, * suh_d,
+//              Hadamard -> abuf (fp16), with the reference's rounding points
+//   down       one workgroup per (active expert, 256 columns of H), K = I, same decode/MFMA scheme, A = abuf rows;
+//              epilogue: output Hadamard * (w * svh_d) -> y (fp16, as the reference's prefill stores it)
+//   combine    out[m] = sum_k y[pair_of[m, k]] in k order (fp32), converted to the activation dtype
+#include "exl3_common.cuh"
+#include "exl3_geom.h"
+#include "exl3_kernels.h"
+
+#include <algorithm>
+
+namespace exl3 {
+
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef float float16_t __attribute__((ext_vector_type(16)));
+
+constexpr int kAlignChunk = 1024;
+constexpr int kPfWaves = 8, kPfThreads = 64 * kPfWaves;
+constexpr int kPfRows = 256;                    // rows per pass of a GEMM workgroup (4 wave rows x 64)
+constexpr int kTileBytes = 16 * 16 * 2 + 16;    // one decoded 16x16 fp16 tile in LDS ([col][k]) + 16 B pad
+constexpr int kRowBytes = 16 * kTileBytes;      // one tile-row of the 16 tiles of a workgroup
+constexpr int kChunkBytes = 4 * kRowBytes;      // 4 tile-rows (K = 64)
+constexpr int kPfLds = 2 * kChunkBytes;         // double buffer; also holds the fp32 epilogue tile [64][256]
+static_assert(kPfLds >= 64 * 256 * 4, "epilogue tile must fit the B buffers");
+
+// ---- block scan helpers (1,024 threads) ---------------------------------------------------------------------------
+__device__ __forceinline__ int wave_incl_scan(int v) {
+    const int l = lane_id();
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const int t = __shfl_up(v, d, 64);
+        if (l >= d) v += t;
+    }
+    return v;
+}
+// exclusive scan over the block; tot = block sum. sw: LDS [16 + 1]
+__device__ __forceinline__ int block_scan_1024(int v, int* sw, int& tot) {
+    const int l = lane_id(), w = threadIdx.x >> 6;
+    const int inc = wave_incl_scan(v);
+    if (l == 63) sw[w] = inc;
+    __syncthreads();
+    if (w == 0) {
+        const int x = l < 16 ? sw[l] : 0;
+        const int xi = wave_incl_scan(x);
+        if (l < 16) sw[l] = xi - x;
+        if (l == 15) sw[16] = xi;
+    }
+    __syncthreads();
+    const int r = sw[w] + inc - v;
+    tot = sw[16];
+    __syncthreads();
+    return r;
+}
+
+// ---- align -----------------------------------------------------------------------------------------------------------
+__global__ void __launch_bounds__(1024) align_count_kernel(const int32_t* ids, int npairs, int E, int* chunk_cnt) {
+    extern __shared__ int hist[];                 // [E]
+    for (int e = threadIdx.x; e < E; e += 1024) hist[e] = 0;
+    __syncthreads();
+    const int i = blockIdx.x * kAlignChunk + threadIdx.x;
+    if (i < npairs) atomicAdd(&hist[min(max(ids[i], 0), E - 1)], 1);
+    __syncthreads();
+    for (int e = threadIdx.x; e < E; e += 1024) chunk_cnt[(size_t)blockIdx.x * E + e] = hist[e];
+}
+
+// per expert (one thread each, E <= 1024): totals, starts, active list, padded starts; chunk counts -> chunk offsets
+__global__ void __launch_bounds__(1024) align_scan_kernel(int nchunks, int E, int pad, int* chunk_cnt, AlignOut o) {
+    __shared__ int sw[17];
+    const int e = threadIdx.x;
+    int tot = 0;
+    if (e < E)
+        for (int c = 0; c < nchunks; ++c) tot += chunk_cnt[(size_t)c * E + e];
+    int all;
+    const int st = block_scan_1024(e < E ? tot : 0, sw, all);
+    const int act = (e < E && tot > 0) ? 1 : 0;
+    int nact;
+    const int ai = block_scan_1024(act, sw, nact);
+    const int pc = (tot + pad - 1) / pad * pad;
+    int ptot;
+    const int pst = block_scan_1024(e < E ? pc : 0, sw, ptot);
+    if (act) {
+        o.act_expert[ai] = e;
+        o.act_start[ai] = st;
+        o.act_cnt[ai] = tot;
+        o.act_pstart[ai] = pst;
+    }
+    if (e == 0) o.n_act[0] = nact;
+    if (e < E) {
+        int run = st;
+        for (int c = 0; c < nchunks; ++c) {
+            const int v = chunk_cnt[(size_t)c * E + e];
+            chunk_cnt[(size_t)c * E + e] = run;
+            run += v;
+        }
+    }
+}
+
+// positions: chunk offset of the expert + pairs of that expert in earlier waves of the chunk + rank inside the wave
+__global__ void __launch_bounds__(1024) align_scatter_kernel(const int32_t* ids, const float* w, int npairs, int topk,
+                                                             int E, const int* chunk_off, AlignOut o) {
+    extern __shared__ int wh[];                   // [16][E] per-wave counts, then per-wave offsets
+    for (int i = threadIdx.x; i < 16 * E; i += 1024) wh[i] = 0;
+    __syncthreads();
+    const int l = lane_id(), wv = threadIdx.x >> 6;
+    const int i = blockIdx.x * kAlignChunk + threadIdx.x;
+    const bool valid = i < npairs;
+    const int e = valid ? min(max(ids[i], 0), E - 1) : -1;
+    uint64_t todo = __ballot(valid);
+    int rank = 0;
+    while (todo) {
+        const int leader = __builtin_ctzll(todo);
+        const int ev = __shfl(e, leader, 64);
+        const uint64_t m = __ballot(valid && e == ev);
+        if (valid && e == ev) rank = __popcll(m & ((1ull << l) - 1));
+        if (l == leader) wh[wv * E + ev] = __popcll(m);
+        todo &= ~m;
+    }
+    __syncthreads();
+    for (int x = threadIdx.x; x < E; x += 1024) {
+        int run = 0;
+        for (int q = 0; q < 16; ++q) {
+            const int v = wh[q * E + x];
+            wh[q * E + x] = run;
+            run += v;
+        }
+    }
+    __syncthreads();
+    if (valid) {
+        const int pos = chunk_off[(size_t)blockIdx.x * E + e] + wh[wv * E + e] + rank;
+        o.pair_tok[pos] = i / topk;
+        o.pair_w[pos] = w[i];
+        o.pair_of[i] = pos;
+        if (o.pair_exp) o.pair_exp[pos] = e;
+    }
+}
+
+hipError_t launch_align(const int32_t* ids, const float* w, int npairs, int topk, int E, int pad, int* chunk_scratch,
+                        const AlignOut& o, hipStream_t s) {
+    const int nch = npairs > 0 ? (npairs + kAlignChunk - 1) / kAlignChunk : 0;
+    if (nch == 0) {                               // no pairs: empty lists, n_act = 0 (no memset: graph-safe)
+        hipLaunchKernelGGL(align_scan_kernel, dim3(1), dim3(1024), 0, s, 0, E, pad, chunk_scratch, o);
+        return hipGetLastError();
+    }
+    hipLaunchKernelGGL(align_count_kernel, dim3(nch), dim3(1024), E * sizeof(int), s, ids, npairs, E, chunk_scratch);
+    hipLaunchKernelGGL(align_scan_kernel, dim3(1), dim3(1024), 0, s, nch, E, pad, chunk_scratch, o);
+    hipLaunchKernelGGL(align_scatter_kernel, dim3(nch), dim3(1024), 16 * E * sizeof(int), s, ids, w, npairs, topk, E,
+                       (const int*)chunk_scratch, o);
+    return hipGetLastError();
+}
+
+// ---- xh pre-pass ---------------------------------------------------------------------------------------------------
+__global__ void __launch_bounds__(kPfThreads) prefill_xh_kernel(PrefillArgs A) {
+    const int l = lane_id();
+    const int nkb = A.g.H / 128;
+    const int64_t item = (int64_t)blockIdx.x * kPfWaves + (threadIdx.x >> 6);
+    if (item >= (int64_t)A.npairs * 2 * nkb) return;
+    const int s = (int)(item / (2 * nkb));
+    const int rem = (int)(item % (2 * nkb));
+    const int pj = rem / nkb, kb = rem % nkb;
+    const int tok = A.pair_tok[s], e = A.pair_exp[s];
+    const uint8_t* base = (const uint8_t*)A.ptrs[e];
+    const half_t* suh = (const half_t*)(base + (pj ? A.g.off_suh_u : A.g.off_suh_g));
+    const int k0 = kb * 128 + 2 * l;
+    const size_t xo = (size_t)tok * A.x_stride + k0;
+    float v0 = (float)(half_t)(ld_act(A.x, A.x_dt, xo) * (float)suh[k0]);
+    float v1 = (float)(half_t)(ld_act(A.x, A.x_dt, xo + 1) * (float)suh[k0 + 1]);
+    wave_fwht128(v0, v1);
+    half2_t* dst = (half2_t*)(A.xh + ((size_t)s * 2 + pj) * A.g.H + k0);
+    *dst = half2_t{(half_t)(v0 * kRsqrt128), (half_t)(v1 * kRsqrt128)};
+}
+
+// ---- decode of one K chunk (4 tile-rows x 16 tiles) into LDS ----------------------------------------------------------
+// The 16 tiles of a workgroup: local tile j lives at global tile column tcol(j). Period q of the chunk:
+// tile-row q / (16 G), local tile (q / G) % 16, period p = q % G; G consecutive lanes hold one tile's periods, so the
+// circular previous word of a period comes from the neighbouring lane.
+template <int K>
+struct ChunkDecoder {
+    using GM = Geo<K>;
+    static constexpr int G = GM::G, D = GM::D, V = GM::V;
+    static constexpr int PER = 4 * 16 * G / kPfThreads;     // periods per thread per chunk (1, 2 or 4)
+    static_assert(PER >= 1 && 4 * 16 * G == PER * kPfThreads, "chunk periods must split evenly");
+    uint32_t wd[PER][D];
+
+    __device__ __forceinline__ static int tile_of(int q) { return (q / G) % 16; }
+    __device__ __forceinline__ static int trow_of(int q) { return q / (16 * G); }
+
+    template <typename TCol>
+    __device__ __forceinline__ void load(const uint32_t* tr, int tiles_n, int kt0, TCol tcol) {
+#pragma unroll
+        for (int j = 0; j < PER; ++j) {
+            const int q = threadIdx.x + j * kPfThreads;
+            const int p = q % G;
+#pragma unroll
+            for (int i = 0; i < D; ++i)
+                wd[j][i] = __builtin_nontemporal_load(as_global(tr) +
+                                                      word_off<K>(kt0 + trow_of(q), tiles_n, tcol(tile_of(q)), p, i));
+        }
+    }
+
+    // decode and store: value t = V p + u of tile j at (row(t), col(t)) -> LDS [trow][j][col][k = row]
+    template <int u>
+    __device__ __forceinline__ static void put(const Period<K>& P, uint8_t* tb, int p) {
+        if constexpr (u + 1 < V) {
+            const half_t w0 = cb_w(P.template state<u>());
+            const half_t w1 = cb_w(P.template state<u + 1>());
+            const int t = V * p + u;
+            const int row = 8 * ((t >> 1) & 1) + 2 * ((t >> 3) & 3);    // t even: rows row, row + 1
+            const int col = (t >> 5) + 8 * ((t >> 2) & 1);
+            *(half2_t*)(tb + col * 32 + row * 2) = half2_t{w0, w1};
+            put<u + 2>(P, tb, p);
+        }
+    }
+
+    __device__ __forceinline__ void decode_store(uint8_t* buf) const {
+        const int l = lane_id();
+#pragma unroll
+        for (int j = 0; j < PER; ++j) {
+            const int q = threadIdx.x + j * kPfThreads;
+            const int p = q % G;
+            const int src = (l / G) * G + (p + G - 1) % G;
+            const uint32_t prev = (uint32_t)__shfl((int)wd[j][D - 1], src, 64);
+            Period<K> P;
+            P.set(wd[j], prev);
+            put<0>(P, buf + trow_of(q) * kRowBytes + tile_of(q) * kTileBytes, p);
+        }
+    }
+};
+
+// B fragment of v_mfma_f32_32x32x16_f16 for columns n0..n0+31 of tile-row kt of a chunk buffer:
+// lane l: column n0 + l % 32, k = 8 (l / 32) .. + 7
+__device__ __forceinline__ half8_t ld_bfrag(const uint8_t* buf, int kt, int n0) {
+    const int l = lane_id();
+    const int n = n0 + (l & 31);
+    return *(const half8_t*)(buf + kt * kRowBytes + (n >> 4) * kTileBytes + (n & 15) * 32 + (l >> 5) * 16);
+}
+
+// A fragments (rows r0 + 32 rb + l % 32 of a [rows][lda] fp16 matrix, k = k0 + 16 ks + 8 (l / 32) .. + 7), zero rows
+// at or beyond `rows`
+__device__ __forceinline__ void ld_afrags(const half_t* a, size_t lda, int r0, int rows, int k0, half8_t (&f)[2][4]) {
+    const int l = lane_id();
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb) {
+        const int r = r0 + rb * 32 + (l & 31);
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+            if (r < rows) f[rb][ks] = *(const half8_t*)(a + (size_t)r * lda + k0 + ks * 16 + (l >> 5) * 8);
+            else f[rb][ks] = half8_t{};
+        }
+    }
+}
+
+// the GEMM core shared by gate/up and down: acc[rb][cb] (rows 64 mw + 32 rb, columns 128 nw + 32 cb) over K chunks
+template <int K, typename TCol>
+__device__ __forceinline__ void grouped_gemm(const uint32_t* tr, int tiles_n, int nchunks, TCol tcol, const half_t* a,
+                                             size_t lda, int rows, uint8_t* lds, float16_t (&acc)[2][4]) {
+    const int wv = threadIdx.x >> 6, mw = wv >> 1, nw = wv & 1;
+    const bool active = mw * 64 < rows;
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+        for (int cb = 0; cb < 4; ++cb) acc[rb][cb] = float16_t{};
+    ChunkDecoder<K> dec;
+    dec.load(tr, tiles_n, 0, tcol);
+    half8_t af[2][4];
+    for (int c = 0; c < nchunks; ++c) {
+        uint8_t* buf = lds + (c & 1) * kChunkBytes;
+        dec.decode_store(buf);
+        if (c + 1 < nchunks) dec.load(tr, tiles_n, 4 * (c + 1), tcol);
+        if (active) ld_afrags(a, lda, mw * 64, rows, c * 64, af);
+        __syncthreads();
+        if (active) {
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks) {
+#pragma unroll
+                for (int cb = 0; cb < 4; ++cb) {
+                    const half8_t b = ld_bfrag(buf, ks, nw * 128 + cb * 32);
+#pragma unroll
+                    for (int rb = 0; rb < 2; ++rb)
+                        acc[rb][cb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[rb][ks], b, acc[rb][cb], 0, 0, 0);
+                }
+            }
+        }
+    }
+    __syncthreads();                              // every wave is done with the B buffers (epilogue reuses them)
+}
+
+// C tile of wave (mw, nw) -> LDS fp32 [64 rows][256 columns] (row = local row inside the wave row mw)
+__device__ __forceinline__ void stash_acc(const float16_t (&acc)[2][4], float* ep, int nw) {
+    const int l = lane_id();
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+        for (int cb = 0; cb < 4; ++cb)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const int row = rb * 32 + (i & 3) + 8 * (i >> 2) + 4 * (l >> 5);
+                ep[row * 256 + nw * 128 + cb * 32 + (l & 31)] = acc[rb][cb][i];
+            }
+}
+
+template <int K>
+__global__ void __launch_bounds__(kPfThreads) prefill_gateup_kernel(PrefillArgs A) {
+    __shared__ __align__(16) uint8_t lds[kPfLds];
+    const int I = A.g.I, H = A.g.H, nbn = I / 128;
+    const int a = blockIdx.x / nbn, nb = blockIdx.x % nbn;
+    if (a >= A.n_act[0]) return;
+    const int e = A.act_expert[a], s0 = A.act_start[a], cnt = A.act_cnt[a];
+    const uint8_t* base = (const uint8_t*)A.ptrs[e];
+    const int wv = threadIdx.x >> 6, mw = wv >> 1, nw = wv & 1, l = lane_id();
+    const int tiles_n = 2 * I / 16;
+    auto tcol = [nb, I](int j) { return j < 8 ? nb * 8 + j : I / 16 + nb * 8 + (j - 8); };
+    const half_t* svg = (const half_t*)(base + A.g.off_svh_g);
+    const half_t* svu = (const half_t*)(base + A.g.off_svh_u);
+    const half_t* sud = (const half_t*)(base + A.g.off_suh_d);
+    float* ep = (float*)lds;
+    for (int r0 = 0; r0 < cnt; r0 += kPfRows) {
+        const int rows = min(kPfRows, cnt - r0);
+        float16_t acc[2][4];
+        // A = xh rows of this projection: xh[(s, pj)][H] with row stride 2H
+        grouped_gemm<K>((const uint32_t*)base, tiles_n, H / 64, tcol, A.xh + ((size_t)(s0 + r0) * 2 + nw) * H,
+                        2 * (size_t)H, rows, lds, acc);
+        for (int m = 0; m < 4; ++m) {
+            if (m * 64 >= rows) break;
+            if (mw == m) stash_acc(acc, ep, nw);
+            __syncthreads();
+            for (int rr = wv; rr < 64; rr += kPfWaves) {
+                const int row = m * 64 + rr;
+                if (row >= rows) break;
+                float g0 = ep[rr * 256 + 2 * l], g1 = ep[rr * 256 + 2 * l + 1];
+                float u0 = ep[rr * 256 + 128 + 2 * l], u1 = ep[rr * 256 + 129 + 2 * l];
+                wave_fwht128(g0, g1);
+                wave_fwht128(u0, u1);
+                const int c = nb * 128 + 2 * l;
+                g0 = (float)(half_t)(g0 * kRsqrt128 * (float)svg[c]);
+                g1 = (float)(half_t)(g1 * kRsqrt128 * (float)svg[c + 1]);
+                u0 = (float)(half_t)(u0 * kRsqrt128 * (float)svu[c]);
+                u1 = (float)(half_t)(u1 * kRsqrt128 * (float)svu[c + 1]);
+                float a0 = (float)(half_t)(g0 / (1.0f + expf(-g0)) * u0);
+                float a1 = (float)(half_t)(g1 / (1.0f + expf(-g1)) * u1);
+                a0 = (float)(half_t)(a0 * (float)sud[c]);
+                a1 = (float)(half_t)(a1 * (float)sud[c + 1]);
+                wave_fwht128(a0, a1);
+                *(half2_t*)(A.abuf + (size_t)(s0 + r0 + row) * I + c) =
+                    half2_t{(half_t)(a0 * kRsqrt128), (half_t)(a1 * kRsqrt128)};
+            }
+            __syncthreads();
+        }
+    }
+}
+
+template <int K>
+__global__ void __launch_bounds__(kPfThreads) prefill_down_kernel(PrefillArgs A) {
+    __shared__ __align__(16) uint8_t lds[kPfLds];
+    const int I = A.g.I, H = A.g.H, ntn = H / 256;
+    const int a = blockIdx.x / ntn, nt = blockIdx.x % ntn;
+    if (a >= A.n_act[0]) return;
+    const int e = A.act_expert[a], s0 = A.act_start[a], cnt = A.act_cnt[a];
+    const uint8_t* base = (const uint8_t*)A.ptrs[e];
+    const int wv = threadIdx.x >> 6, mw = wv >> 1, nw = wv & 1, l = lane_id();
+    const int tiles_n = H / 16;
+    auto tcol = [nt](int j) { return nt * 16 + j; };
+    const half_t* svd = (const half_t*)(base + A.g.off_svh_d);
+    float* ep = (float*)lds;
+    for (int r0 = 0; r0 < cnt; r0 += kPfRows) {
+        const int rows = min(kPfRows, cnt - r0);
+        float16_t acc[2][4];
+        grouped_gemm<K>((const uint32_t*)(base + A.g.gu_bytes), tiles_n, I / 64, tcol, A.abuf + (size_t)(s0 + r0) * I,
+                        (size_t)I, rows, lds, acc);
+        for (int m = 0; m < 4; ++m) {
+            if (m * 64 >= rows) break;
+            if (mw == m) stash_acc(acc, ep, nw);
+            __syncthreads();
+            for (int rr = wv; rr < 64; rr += kPfWaves) {
+                const int row = m * 64 + rr;
+                if (row >= rows) break;
+                const int s = s0 + r0 + row;
+                const float sc = kRsqrt128 * A.pair_w[s];
+#pragma unroll
+                for (int hb = 0; hb < 2; ++hb) {
+                    float v0 = ep[rr * 256 + hb * 128 + 2 * l], v1 = ep[rr * 256 + hb * 128 + 2 * l + 1];
+                    wave_fwht128(v0, v1);
+                    const int c = nt * 256 + hb * 128 + 2 * l;
+                    *(half2_t*)(A.y + (size_t)s * H + c) =
+                        half2_t{(half_t)(v0 * sc * (float)svd[c]), (half_t)(v1 * sc * (float)svd[c + 1])};
+                }
+            }
+            __syncthreads();
+        }
+    }
+}
+
+// out[m][h] = sum over k (in order) of y[pair_of[m topk + k]][h]; 8 columns per thread
+__global__ void __launch_bounds__(256) prefill_combine_kernel(PrefillArgs A) {
+    const int m = blockIdx.x, H = A.g.H;
+    for (int h0 = threadIdx.x * 8; h0 < H; h0 += 256 * 8) {
+        float acc[8] = {};
+        for (int k = 0; k < A.topk; ++k) {
+            const int pos = A.pair_of[m * A.topk + k];
+            const half8_t v = *(const half8_t*)(A.y + (size_t)pos * H + h0);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) acc[j] += (float)v[j];
+        }
+        const size_t oo = (size_t)m * A.out_stride + h0;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) st_act(A.out, A.x_dt, oo + j, acc[j]);
+    }
+}
+
+size_t align_scratch_bytes(int npairs, int E) {
+    return (size_t)((npairs + kAlignChunk - 1) / kAlignChunk) * E * 4;
+}
+
+size_t prefill_workspace_bytes(int M, int H, int I, int topk, int E) {
+    const size_t np = (size_t)M * topk, A = std::min<size_t>(np, (size_t)E);
+    const size_t nch = (np + kAlignChunk - 1) / kAlignChunk;
+    return align256((4 * A + 1) * 4) + 3 * align256(np * 4) + align256(np * 4) + align256(nch * E * 4) +
+           align256(np * 2 * H * 2) + align256(np * I * 2) + align256(np * H * 2);
+}
+
+hipError_t launch_prefill(PrefillArgs a, int E, void* ws, hipStream_t s) {
+    const int np = a.npairs, H = a.g.H, I = a.g.I;
+    const size_t A = std::min(np, E);
+    uint8_t* p = (uint8_t*)ws;
+    auto take = [&p](size_t n) { uint8_t* q = p; p += align256(n); return q; };
+    AlignOut o;
+    int* act = (int*)take((4 * A + 1) * 4);
+    o.act_expert = act;
+    o.act_start = act + A;
+    o.act_cnt = act + 2 * A;
+    o.act_pstart = act + 3 * A;
+    o.n_act = act + 4 * A;
+    o.pair_tok = (int*)take((size_t)np * 4);
+    o.pair_of = (int*)take((size_t)np * 4);
+    o.pair_exp = (int*)take((size_t)np * 4);
+    o.pair_w = (float*)take((size_t)np * 4);
+    int* chunk = (int*)take((size_t)((np + kAlignChunk - 1) / kAlignChunk) * E * 4);
+    a.xh = (half_t*)take((size_t)np * 2 * H * 2);
+    a.abuf = (half_t*)take((size_t)np * I * 2);
+    a.y = (half_t*)take((size_t)np * H * 2);
+    a.act_expert = o.act_expert;
+    a.act_start = o.act_start;
+    a.act_cnt = o.act_cnt;
+    a.n_act = o.n_act;
+    a.pair_tok = o.pair_tok;
+    a.pair_w = o.pair_w;
+    a.pair_of = o.pair_of;
+    a.pair_exp = o.pair_exp;
+    hipError_t e = launch_align(a.ids, a.w, np, a.topk, E, 1, chunk, o, s);
+    if (e != hipSuccess) return e;
+    const int64_t nxh = (int64_t)np * 2 * (H / 128);
+    hipLaunchKernelGGL(prefill_xh_kernel, dim3((unsigned)((nxh + kPfWaves - 1) / kPfWaves)), dim3(kPfThreads), 0, s, a);
+    const dim3 ggu((unsigned)(A * (I / 128))), gdn((unsigned)(A * (H / 256)));
+    switch (a.g.K) {
+        case 2:
+            hipLaunchKernelGGL(prefill_gateup_kernel<2>, ggu, dim3(kPfThreads), 0, s, a);
+            hipLaunchKernelGGL(prefill_down_kernel<2>, gdn, dim3(kPfThreads), 0, s, a);
+            break;
+        case 3:
+            hipLaunchKernelGGL(prefill_gateup_kernel<3>, ggu, dim3(kPfThreads), 0, s, a);
+            hipLaunchKernelGGL(prefill_down_kernel<3>, gdn, dim3(kPfThreads), 0, s, a);
+            break;
+        case 4:
+            hipLaunchKernelGGL(prefill_gateup_kernel<4>, ggu, dim3(kPfThreads), 0, s, a);
+            hipLaunchKernelGGL(prefill_down_kernel<4>, gdn, dim3(kPfThreads), 0, s, a);
+            break;
+        default: return hipErrorInvalidValue;
+    }
+    hipLaunchKernelGGL(prefill_combine_kernel, dim3((unsigned)a.M), dim3(256), 0, s, a);
+    return hipGetLastError();
+}
+
+}  // namespace exl3

@@ -34,7 +34,7 @@ at::Tensor moe_forward(at::Tensor x, at::Tensor topk_ids, at::Tensor topk_w, at:
     TORCH_CHECK(ptrs.numel() >= n_experts, "moe_forward: ptrs [n_experts]");
     auto out = at::empty_like(x);
     if (M == 0) return out;
-    const size_t ws = exl3_moe_forward_workspace(M, H, (int)I, topk);
+    const size_t ws = exl3_moe_forward_workspace(M, H, (int)I, topk, (int)n_experts);
     auto w = at::empty({(int64_t)ws}, x.options().dtype(at::kByte));
     check(exl3_moe_forward(x.data_ptr(), dtype_code(x), x.stride(0), M, H, topk_ids.data_ptr<int>(),
                            topk_w.data_ptr<float>(), topk, ptrs.data_ptr<int64_t>(), (int)I, (int)K, (int)n_experts,
@@ -65,7 +65,7 @@ at::Tensor moe_forward_cached(at::Tensor x, at::Tensor topk_ids, at::Tensor topk
                 "moe_forward_cached: cache state sizes");
     auto out = at::empty_like(x);
     if (M == 0) return out;
-    const size_t ws = exl3_moe_forward_workspace(M, H, (int)I, topk);
+    const size_t ws = exl3_moe_forward_workspace(M, H, (int)I, topk, (int)n_experts);
     auto w = at::empty({(int64_t)ws}, x.options().dtype(at::kByte));
     check(exl3_moe_forward_cached(x.data_ptr(), dtype_code(x), x.stride(0), M, H, topk_ids.data_ptr<int>(),
                                   topk_w.data_ptr<float>(), topk, ptrs_all.data_ptr<int64_t>(), (int)layer,
@@ -85,8 +85,10 @@ std::vector<at::Tensor> moe_align(at::Tensor topk_ids, at::Tensor topk_w, int64_
     const int A = std::min(npairs, (int)n_experts);
     auto ib = at::empty({4 * A + 1 + 2 * npairs + 16}, topk_ids.options());
     auto fb = at::empty({npairs}, topk_w.options());
+    const size_t wsb = exl3_moe_align_workspace(M, topk, (int)n_experts);
+    auto ws = at::empty({(int64_t)std::max<size_t>(wsb, 1)}, topk_ids.options().dtype(at::kByte));
     check(exl3_moe_align(topk_ids.data_ptr<int>(), topk_w.data_ptr<float>(), M, topk, (int)n_experts, (int)pad,
-                         ib.data_ptr<int>(), fb.data_ptr<float>(), cur_stream(topk_ids)),
+                         ib.data_ptr<int>(), fb.data_ptr<float>(), ws.data_ptr(), wsb, cur_stream(topk_ids)),
           "moe_align");
     return {ib, fb};
 }

@@ -29,13 +29,14 @@ SIGNATURES = {
     "exl3_set_mr": (c_i32, [c_i64]),
     "exl3_set_debug": (c_i32, [c_i64]),
     "exl3_set_decision_log": (c_i32, [c_p, c_i64]),
-    "exl3_moe_forward_workspace": (c_sz, [c_i32, c_i32, c_i32, c_i32]),
+    "exl3_moe_forward_workspace": (c_sz, [c_i32, c_i32, c_i32, c_i32, c_i32]),
     "exl3_moe_forward": (c_i32, [c_p, c_i32, c_i64, c_i32, c_i32, c_p, c_p, c_i32, c_p, c_i32, c_i32, c_i32, c_p, c_i64,
                                  c_p, c_sz, c_p]),
     "exl3_moe_forward_cached": (c_i32, [c_p, c_i32, c_i64, c_i32, c_i32, c_p, c_p, c_i32, c_p, c_i32, c_p, c_p, c_p, c_p,
                                         c_i32, c_p, c_i64, c_p, c_p, c_i32, c_i32, c_i32, c_i32, c_p, c_i64, c_p, c_sz,
                                         c_p]),
-    "exl3_moe_align": (c_i32, [c_p, c_p, c_i32, c_i32, c_i32, c_i32, c_p, c_p, c_p]),
+    "exl3_moe_align_workspace": (c_sz, [c_i32, c_i32, c_i32]),
+    "exl3_moe_align": (c_i32, [c_p, c_p, c_i32, c_i32, c_i32, c_i32, c_p, c_p, c_p, c_sz, c_p]),
     "exl3_dequant": (c_i32, [c_p, c_i32, c_i32, c_i32, c_p, c_p]),
     "exl3_device_status": (c_i32, [c_p, c_p]),
     "exl3_scatter_flags": (c_i32, [c_p, c_i64, c_p, c_i64, c_p]),

@@ -36,7 +36,9 @@ def test_forward_rejects_bad_dtype_and_workspace():
     L = capi.lib()
     assert L.exl3_moe_forward(None, 7, 0, 1, 2048, None, None, 10, None, 512, 3, 512, None, 0, None, 0, None) == 1
     assert L.exl3_moe_forward(None, 1, 0, 0, 2048, None, None, 10, None, 512, 3, 512, None, 0, None, 0, None) == 0
-    assert L.exl3_moe_forward_workspace(1, 2048, 512, 10) > 0
+    assert L.exl3_moe_forward_workspace(1, 2048, 512, 10, 512) > 0
+    assert L.exl3_moe_forward_workspace(8192, 2048, 512, 10, 512) > L.exl3_moe_forward_workspace(4, 2048, 512, 10, 512)
+    assert L.exl3_moe_align_workspace(8192, 10, 512) == 80 * 512 * 4
 
 
 def test_setters():

@@ -1,0 +1,159 @@
+"""GPU parity of the prefill path (M >= prefill_min_m): the token sort (moe_align) bit for bit against the oracle's
+canonical stable counting sort, and the grouped MFMA GEMMs against the oracle's prefill rounding points (y stored in
+fp16 like the reference's DownDpasKernel<.., fp16>, a8:802) within rel-L2 2e-3. At the full prefill size (8,192
+tokens x 512 experts, top-10) the oracle is too slow, so there the prefill output is checked against the decode
+kernel on the same inputs (itself checked against the oracle in test_gpu_decode.py)."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import exl3, synth
+
+pytestmark = pytest.mark.gpu
+TOL = 2e-3
+
+
+def _ops():
+    from exl3xpu.moe_offload import ops
+    return ops()
+
+
+def rel_l2(a, b):
+    a = np.asarray(a, np.float64)
+    b = np.asarray(b, np.float64)
+    return float(np.linalg.norm(a - b) / np.linalg.norm(b))
+
+
+class _PrefillFrom:
+    """Route calls with M >= m to the prefill path for the duration of a test."""
+
+    def __init__(self, m):
+        self.m = m
+
+    def __enter__(self):
+        _ops().moe_set_prefill_min_m(self.m)
+
+    def __exit__(self, *exc):
+        _ops().moe_set_prefill_min_m(256)
+
+
+@pytest.mark.parametrize("M,topk,E,pad", [(300, 10, 64, 32), (1000, 8, 1024, 1), (3, 2, 16, 32), (257, 10, 512, 32)])
+def test_align_matches_oracle(M, topk, E, pad):
+    print(f"case align M={M} topk={topk} E={E} pad={pad}", flush=True)
+    ids, w = synth.softmax_topk(900 + M, M, E, topk)
+    ib, fb = _ops().moe_align(torch.from_numpy(ids).cuda(), torch.from_numpy(w).cuda(), E, pad)
+    torch.cuda.synchronize()
+    ib, fb = ib.cpu().numpy(), fb.cpu().numpy()
+    ref = exl3.align(ids, w, E, pad)
+    npairs, A = M * topk, min(M * topk, E)
+    na = int(ib[4 * A])
+    assert na == ref["n_act"]
+    for i, key in enumerate(("act_expert", "act_start", "act_cnt", "act_pstart")):
+        assert np.array_equal(ib[i * A:i * A + na], ref[key]), key
+    p0 = 4 * A + 1
+    assert np.array_equal(ib[p0:p0 + npairs], ref["pair_tok"])
+    assert np.array_equal(ib[p0 + npairs:p0 + 2 * npairs], ref["pair_of"])
+    assert np.array_equal(fb, ref["pair_w"])
+
+
+def test_align_empty():
+    ib, fb = _ops().moe_align(torch.zeros((0, 4), dtype=torch.int32, device="cuda"),
+                              torch.zeros((0, 4), dtype=torch.float32, device="cuda"), 16, 32)
+    torch.cuda.synchronize()
+    assert int(ib[0]) == 0 and fb.numel() == 0
+
+
+def _case(H, I, K, E, M, topk, seed, n_distinct=None):
+    ids, w = synth.softmax_topk(seed, M, E, topk)
+    used = sorted(set(ids.reshape(-1).tolist()))
+    nd = n_distinct or E
+    made = {}
+    for e in used:
+        if e % nd not in made:
+            made[e % nd] = synth.expert_blob(seed, e % nd, H, I, K)
+    blobs = {e: made[e % nd] for e in used}
+    dev = torch.from_numpy(np.stack([blobs[e] for e in used])).cuda()
+    table = np.zeros(E, dtype=np.int64)
+    for i, e in enumerate(used):
+        table[e] = dev[i].data_ptr()
+    x = synth.activations(seed, M, H)
+    return x, ids, w, blobs, torch.from_numpy(table).cuda(), dev
+
+
+def _run(x_bits, ids, w, table, I, K, E, fp32=False):
+    xs = torch.from_numpy(exl3.bf16_to_f32(x_bits)).cuda()
+    if not fp32:
+        xs = xs.to(torch.bfloat16)
+    out = _ops().moe_forward(xs, torch.from_numpy(ids).cuda(), torch.from_numpy(w).cuda(), table, I, K, E)
+    torch.cuda.synchronize()
+    return out.float().cpu().numpy()
+
+
+def _check_vs_oracle(H, I, K, E, M, topk, seed, min_m):
+    x, ids, w, blobs, table, keep = _case(H, I, K, E, M, topk, seed)
+    ews = {e: exl3.ExpertWeights(b, H, I, K) for e, b in blobs.items()}
+    ob, of = exl3.moe_forward(x, ids, w, ews, variant="prefill")
+    with _PrefillFrom(min_m):
+        gb = _run(x, ids, w, table, I, K, E)
+        gf = _run(x, ids, w, table, I, K, E, fp32=True)
+    rb, rf = rel_l2(gb, exl3.bf16_to_f32(ob)), rel_l2(gf, of)
+    print(f"prefill H={H} I={I} K={K} E={E} M={M} top-{topk}: rel-L2 bf16 {rb:.2e} fp32 {rf:.2e}", flush=True)
+    assert np.isfinite(gb).all() and np.isfinite(gf).all()
+    assert rb <= TOL and rf <= TOL
+
+
+def test_prefill_golden():
+    import os
+    g = np.load(os.path.join(os.path.dirname(__file__), "golden", "moe_small.npz"))
+    H, I, K = int(g["H"]), int(g["I"]), int(g["K"])
+    print(f"case prefill golden H={H} I={I} K={K}", flush=True)
+    blobs = torch.from_numpy(g["blobs"]).cuda()
+    E = blobs.shape[0]
+    table = torch.tensor([blobs[e].data_ptr() for e in range(E)], dtype=torch.int64, device="cuda")
+    with _PrefillFrom(1):
+        gf = _run(g["x"], g["ids"], g["w"], table, I, K, E, fp32=True)
+    r = rel_l2(gf, g["out_prefill_f32"])
+    print(f"prefill golden rel-L2 fp32 {r:.2e}", flush=True)
+    assert r <= TOL
+
+
+@pytest.mark.parametrize("K", [2, 3, 4])
+def test_prefill_c0_shapes(K):
+    """H 2048 / I 512 experts; 256 rows (the default prefill threshold) x top-4 over 32 experts."""
+    print(f"case prefill c0 K={K}", flush=True)
+    _check_vs_oracle(2048, 512, K, 32, 256, 4, 7000 + K, 256)
+
+
+def test_prefill_expert_with_more_than_256_rows():
+    """Every row picks both of 2 experts: 300 rows per expert, two row passes of the GEMM workgroups."""
+    print("case prefill 300 rows per expert", flush=True)
+    _check_vs_oracle(256, 256, 3, 2, 300, 2, 7100, 1)
+
+
+@pytest.mark.parametrize("K", [2, 3, 4])
+def test_prefill_large_expert_shapes(K):
+    """H 4096 / I 1536 (12 column blocks of I, 16 column tiles of H), each bitrate."""
+    print(f"case prefill c4 K={K}", flush=True)
+    _check_vs_oracle(4096, 1536, K, 8, 32, 2, 7200 + K, 1)
+
+
+def test_prefill_full_chunk_vs_decode():
+    """8,192 tokens x 512 experts (H 2048, I 512, K=3), top-10: the prefill output against the decode kernel run on
+    64-row slices of the same inputs (fp32 activations and outputs: the only difference is the prefill's fp16 y)."""
+    H, I, K, E, M, topk = 2048, 512, 3, 512, 8192, 10
+    print("case prefill full chunk vs decode", flush=True)
+    x, ids, w, blobs, table, keep = _case(H, I, K, E, M, topk, 7300, n_distinct=64)
+    pf = _run(x, ids, w, table, I, K, E, fp32=True)
+    xs = torch.from_numpy(exl3.bf16_to_f32(x)).cuda()
+    it, wt = torch.from_numpy(ids).cuda(), torch.from_numpy(w).cuda()
+    dec = []
+    for m0 in range(0, M, 64):
+        dec.append(_ops().moe_forward(xs[m0:m0 + 64], it[m0:m0 + 64].contiguous(), wt[m0:m0 + 64].contiguous(),
+                                      table, I, K, E))
+    torch.cuda.synchronize()
+    dc = torch.cat(dec).cpu().numpy()
+    r = rel_l2(pf, dc)
+    rows = np.linalg.norm(pf - dc, axis=1) / np.linalg.norm(dc, axis=1)
+    print(f"full chunk: rel-L2 prefill vs decode {r:.2e}, worst row {rows.max():.2e}", flush=True)
+    assert np.isfinite(pf).all()
+    assert r <= TOL and rows.max() <= 4 * TOL
