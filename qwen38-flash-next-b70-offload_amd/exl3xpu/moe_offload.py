@@ -269,11 +269,14 @@ class ExpertStore:
         self._resync()
         so = self.slot_of[key]
         miss = (so < 0).nonzero().flatten().tolist()
+        # runs of consecutive experts are one copy when host copies are packed at the blob size (a TierStore arena
+        # has a 4 KiB-rounded stride: one copy per expert there)
+        packed = self._host_addr(key, 1) - self._host_addr(key, 0) == self.blob if self.E > 1 else True
         with torch.cuda.stream(stream):
             i = 0
             while i < len(miss):
                 j = i
-                while j + 1 < len(miss) and miss[j + 1] == miss[j] + 1:
+                while packed and j + 1 < len(miss) and miss[j + 1] == miss[j] + 1:
                     j += 1
                 n = j - i + 1
                 self.X.memcpy_async(s64(st[miss[i]].data_ptr()), self._host_addr(key, miss[i]), n * self.blob)

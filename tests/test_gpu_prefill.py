@@ -157,3 +157,35 @@ def test_prefill_full_chunk_vs_decode():
     print(f"full chunk: rel-L2 prefill vs decode {r:.2e}, worst row {rows.max():.2e}", flush=True)
     assert np.isfinite(pf).all()
     assert r <= TOL and rows.max() <= 4 * TOL
+
+
+def test_prefill_staged_matches_resident():
+    """ExpertStore.forward_prefill_staged (non-resident experts copied from the pinned RAM arena into a staging buffer
+    on a copy stream, double-buffered across layers) gives the same bits as the prefill on an all-resident table."""
+    import ctypes
+    from exl3xpu import nvtier
+    H, I, K, E, S, L, M, topk = 256, 128, 3, 16, 20, 3, 300, 4
+    print("case prefill staged vs resident", flush=True)
+    store = nvtier.TierStore(H, I, K, E, S, n_layers=L)
+    keys = [f"model.layers.{li}.mlp" for li in range(L)]
+    for k in keys:
+        store.add_layer(k)
+    src = nvtier.SyntheticExpertSource(H, I, K, 11, n_distinct=L * E)
+    for key in range(L * E):
+        ctypes.memmove(store.addr(key), src.buf[key].ctypes.data, store.blob)
+    rng = np.random.default_rng(5)
+    for li in range(L):
+        store.make_resident(keys[li], sorted(rng.choice(E, size=6, replace=False).tolist()))
+    blobs = torch.from_numpy(src.buf).cuda()
+    xs, outs, refs = [], [], []
+    for rep in range(2):                           # the second pass reuses the buffers staged at the end of the first
+        for li in range(L):
+            ids, w = synth.softmax_topk(40 + li, M, E, topk)
+            x = torch.from_numpy(exl3.bf16_to_f32(synth.activations(50 + li, M, H))).to(torch.bfloat16).cuda()
+            it, wt = torch.from_numpy(ids).cuda(), torch.from_numpy(w).cuda()
+            outs.append(store.forward_prefill_staged(keys[li], x, it, wt))
+            table = torch.tensor([blobs[li * E + e].data_ptr() for e in range(E)], dtype=torch.int64, device="cuda")
+            refs.append(_ops().moe_forward(x, it, wt, table, I, K, E))
+    torch.cuda.synchronize()
+    for n, (o, r) in enumerate(zip(outs, refs)):
+        assert torch.equal(o, r), n
