@@ -12,6 +12,11 @@ constexpr int kMaxRows = 256;       // rows of one decode call
 constexpr int kMaxExperts = 1024;   // experts per layer (one ensure work-item per expert)
 constexpr int kMaxI = 4096;         // intermediate size of the decode kernels (abuf staged in LDS)
 
+struct VictimArgs {
+    const int32_t* vict; const int64_t* host_base; int64_t slot_base; int64_t blob; int64_t hstride; int E;
+    uint8_t* ram_res; int chunk_bytes;
+};
+
 struct DecodeArgs {
     const void* x; int x_dt; int64_t x_stride;     // activations [M, H], dt 0 = fp16, 1 = bf16
     const int32_t* ids; const float* w;            // [M * topk] (post-mask when cached)
@@ -27,6 +32,8 @@ struct DecodeArgs {
     float* part_gu;                                // [npairs, I/128, H/128, 256]
     void* out; int64_t out_stride;                 // [M, H], same dtype as x
     BlobGeom g;
+    VictimArgs va;                                 // victim write-back (cached calls with victims on)
+    int n_vict_wg, vict_chunks;                    // victim-copy workgroups (first in the grid) and chunks per victim
 };
 
 struct EnsureArgs {
@@ -41,10 +48,6 @@ struct EnsureArgs {
     int64_t* pair_ptr;                             // out: blob pointer of every post-mask pick [P] (or null)
 };
 
-struct VictimArgs {
-    const int32_t* vict; const int64_t* host_base; int64_t slot_base; int64_t blob; int64_t hstride; int E;
-    uint8_t* ram_res; int chunk_bytes;
-};
 
 // token sort (reference launch_align a8:639-680): pairs sorted by expert, ascending pair index inside an expert
 struct AlignOut {
@@ -73,7 +76,6 @@ int read_status(int* out, hipStream_t s);
 hipError_t launch_dequant(int K, const uint32_t* tr, _Float16* out, int k_tiles, int n_tiles, hipStream_t s);
 // cache.hip
 hipError_t launch_ensure(const EnsureArgs& a, hipStream_t s);
-hipError_t launch_victim_copy(const VictimArgs& a, int max_victims, hipStream_t s);
 hipError_t launch_scatter_flags(uint8_t* flags, int64_t n_flags, const int32_t* packed, int64_t n, hipStream_t s);
 // prefill.hip
 hipError_t launch_align(const int32_t* ids, const float* w, int npairs, int topk, int E, int pad, int* chunk_scratch,

@@ -14,8 +14,8 @@
 // The reference builds the miss and victim lists with SLM fetch_add, so its pairing is not deterministic; here every
 // list is produced by prefix sums in work-item order, which defines the canonical decisions the oracle restates.
 //
-// victim_copy_kernel (reference a8:1168-1189): copies each victim slot whose old owner is not RAM-resident back to the
-// owner's RAM-tier page and flags it resident.
+// The victim write-back (reference VictimCopyKernel a8:1168-1189) runs as the first workgroups of the layer kernel
+// (moe_decode.hip).
 #include <climits>
 
 #include "exl3_common.cuh"
@@ -291,19 +291,6 @@ __global__ void __launch_bounds__(kEnsureThreads) ensure_kernel(EnsureArgs A) {
     }
 }
 
-__global__ void __launch_bounds__(256) victim_copy_kernel(VictimArgs A, int chunks) {
-    const int i = blockIdx.x / chunks, c = blockIdx.x % chunks;
-    if (i >= A.vict[0]) return;
-    const int old = A.vict[1 + 2 * i], s = A.vict[2 + 2 * i];
-    if (old < 0) return;
-    if (A.ram_res && c == 0 && threadIdx.x == 0) A.ram_res[old] = 1;
-    const uint4* src = (const uint4*)(A.slot_base + (int64_t)s * A.blob);
-    uint4* dst = (uint4*)(A.host_base[old / A.E] + (int64_t)(old % A.E) * A.hstride);
-    const int64_t n16 = A.blob >> 4, per = A.chunk_bytes >> 4;
-    const int64_t b0 = (int64_t)c * per, b1 = min(n16, b0 + per);
-    for (int64_t q = b0 + threadIdx.x; q < b1; q += 256) dst[q] = src[q];
-}
-
 // ---- host launchers ------------------------------------------------------------------------------------------------
 
 hipError_t launch_ensure(const EnsureArgs& a, hipStream_t s) {
@@ -317,13 +304,6 @@ hipError_t launch_ensure(const EnsureArgs& a, hipStream_t s) {
     }
     if (lds > 120 * 1024) return hipErrorInvalidValue;
     hipLaunchKernelGGL(ensure_kernel, dim3(1), dim3(kEnsureThreads), lds, s, a);
-    return hipGetLastError();
-}
-
-hipError_t launch_victim_copy(const VictimArgs& a, int max_victims, hipStream_t s) {
-    const int chunks = (int)((a.blob + a.chunk_bytes - 1) / a.chunk_bytes);
-    if (max_victims <= 0) return hipSuccess;
-    hipLaunchKernelGGL(victim_copy_kernel, dim3((unsigned)(max_victims * chunks)), dim3(256), 0, s, a, chunks);
     return hipGetLastError();
 }
 

@@ -135,7 +135,8 @@ static int64_t* pair_ptr_area(void* ws, int npairs, int H, int I) {
 static int forward_impl(const void* x, int x_dtype, int64_t x_stride, int M, int H, const int32_t* ids, const float* w,
                         int topk, const int64_t* ptrs, int I, int K, int E, void* out, int64_t out_stride, void* ws,
                         size_t ws_bytes, hipStream_t st, const int64_t* fill, int64_t* commit_ptrs, int64_t* commit_fill,
-                        const int32_t* fill_list, const int64_t* pair_ptr) {
+                        const int32_t* fill_list, const int64_t* pair_ptr, const VictimArgs* va = nullptr,
+                        int max_victims = 0) {
     if (!fill && use_prefill(M)) {
         if (H % 256) return fail(EXL3_EUNSUPPORTED, "moe prefill: H %% 256 == 0 required (H=%d)", H);
         if ((int64_t)M * topk > (1 << 28)) return fail(EXL3_EUNSUPPORTED, "moe prefill: %d x %d pairs", M, topk);
@@ -189,6 +190,11 @@ static int forward_impl(const void* x, int x_dtype, int64_t x_stride, int M, int
     a.out = out;
     a.out_stride = out_stride;
     a.g = blob_geom(H, I, K);
+    if (va && max_victims > 0) {                  // victim write-back: the first workgroups of the layer kernel
+        a.va = *va;
+        a.vict_chunks = (int)((a.g.blob + va->chunk_bytes - 1) / va->chunk_bytes);
+        a.n_vict_wg = max_victims * a.vict_chunks;
+    }
     hipError_t e = launch_moe_layer(K, a, st);
     if (e != hipSuccess) return hip_fail(e, "moe layer launch");
     return EXL3_OK;
@@ -261,8 +267,9 @@ int exl3_moe_forward_cached(const void* x, int x_dtype, int64_t x_stride, int M,
     ea.pair_ptr = pair_ptr_area(workspace, P, H, I);
     hipError_t e = launch_ensure(ea, st);
     if (e != hipSuccess) return hip_fail(e, "ensure launch");
+    VictimArgs va{};
+    int mv = 0;
     if (g_cfg.vict) {
-        VictimArgs va{};
         va.vict = g_cfg.vict;
         va.host_base = host_base;
         va.slot_base = slot_base;
@@ -271,14 +278,12 @@ int exl3_moe_forward_cached(const void* x, int x_dtype, int64_t x_stride, int M,
         va.E = E;
         va.ram_res = g_cfg.ram_res;
         va.chunk_bytes = 64 * 1024;
-        const int mv = std::min(std::min(ea.max_fill, E), P);
-        e = launch_victim_copy(va, mv, st);
-        if (e != hipSuccess) return hip_fail(e, "victim copy launch");
+        mv = std::min(std::min(ea.max_fill, E), P);
     }
     int64_t* pl = ptrs_all + (int64_t)layer * E;
     int64_t* fl = fill_all + (int64_t)layer * E;
     return forward_impl(x, x_dtype, x_stride, M, H, topk_ids, topk_w, topk, pl, I, K, E, out, out_stride, workspace,
-                        workspace_bytes, st, fl, pl, fl, fill_list, ea.pair_ptr);
+                        workspace_bytes, st, fl, pl, fl, fill_list, ea.pair_ptr, &va, mv);
 }
 
 size_t exl3_moe_align_workspace(int M, int topk, int n_experts) {

@@ -143,6 +143,41 @@ struct LayerShared {
     int last;
 };
 
+// bounded wait until *c >= target (one lane); a timeout is counted in g_status[0]
+__device__ __forceinline__ void wait_count(const int* c, int target) {
+    int it = 0;
+    while (__hip_atomic_load(c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target) {
+        __builtin_amdgcn_s_sleep(1);
+        if (++it > kSpinMax) {
+            atomicAdd(&g_status[0], 1);
+            break;
+        }
+    }
+}
+
+// victim write-back (VictimCopyKernel, a8:1168-1189): workgroup (victim i, 64 KiB chunk c) copies its chunk of the
+// victim's slot to the old owner's RAM-tier address and flags the owner RAM-resident; every victim workgroup then
+// counts itself done (g_cnt_all[1]), so the write-through of a miss into a reassigned slot starts after the old bytes
+// were read
+__device__ __forceinline__ void victim_wg(const DecodeArgs& A, int blk) {
+    const VictimArgs& V = A.va;
+    const int i = blk / A.vict_chunks, c = blk % A.vict_chunks;
+    if (i < V.vict[0]) {
+        const int old = V.vict[1 + 2 * i], s = V.vict[2 + 2 * i];
+        if (old >= 0) {
+            if (V.ram_res && c == 0 && threadIdx.x == 0) V.ram_res[old] = 1;
+            const uint4* src = (const uint4*)(V.slot_base + (int64_t)s * V.blob);
+            uint4* dst = (uint4*)(V.host_base[old / V.E] + (int64_t)(old % V.E) * V.hstride);
+            const int64_t n16 = V.blob >> 4, per = V.chunk_bytes >> 4;
+            const int64_t b0 = (int64_t)c * per, b1 = min(n16, b0 + per);
+            for (int64_t q = b0 + threadIdx.x; q < b1; q += kThreads) dst[q] = src[q];
+        }
+    }
+    wait_stores();
+    __syncthreads();
+    if (threadIdx.x == 0) counter_add(&g_cnt_all[1], 1);
+}
+
 // pointer of the blob of pair a: precomputed by the cache's ensure (pair_ptr) or looked up through ids/ptrs
 __device__ __forceinline__ const uint8_t* pair_base(const DecodeArgs& A, int a, int& e) {
     e = min(max(A.ids[a], 0), A.E - 1);          // out-of-range ids are clamped, never dereferenced
@@ -187,6 +222,10 @@ __device__ __forceinline__ void gateup_wg(const DecodeArgs& A, int blk, LayerSha
         if (l == 0) S.ssum[pj][hb] = s;
     }
     if (dst) {                                   // write-through of a cache miss into its HBM slot
+        if (A.n_vict_wg) {                       // after the victim write-back read the slot's old bytes
+            if (tid == 0) wait_count(&g_cnt_all[1], A.n_vict_wg);
+            __syncthreads();
+        }
         if (live) g.write_through((uint32_t*)dst, tiles_n, r0, ct0);
         if (nb == 0 && ks == 0) {
             const uint32_t* sv = (const uint32_t*)(base + A.g.off_suh_g);
@@ -272,6 +311,7 @@ __device__ __forceinline__ void down_wg(const DecodeArgs& A, int blk, LayerShare
     if (nch > 0) g0.load(tr, tiles_n, wv * 4, ct0);
     if (nch > 1) g1.load(tr, tiles_n, (wv + kWaves) * 4, ct0);
     if (tid == 0) {                              // wait for the pair's whole abuf (all I/128 gate/up epilogues)
+        if (trd && A.n_vict_wg) wait_count(&g_cnt_all[1], A.n_vict_wg);   // and for the victim write-back
         int it = 0;
         while (__hip_atomic_load(&g_ready[a], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < I / 128) {
             __builtin_amdgcn_s_sleep(1);
@@ -363,7 +403,13 @@ __device__ __forceinline__ void down_wg(const DecodeArgs& A, int blk, LayerShare
     if (l == 0) old = counter_add(&g_cnt_all[0], 1);
     old = __shfl(old, 0, 64);
     if (old != A.M * nbn - 1) return;
-    if (l == 0) counter_reset(&g_cnt_all[0]);
+    if (l == 0) {
+        counter_reset(&g_cnt_all[0]);
+        if (A.n_vict_wg) {                       // every victim workgroup has counted itself: clear for the next call
+            wait_count(&g_cnt_all[1], A.n_vict_wg);
+            counter_reset(&g_cnt_all[1]);
+        }
+    }
     for (int i = l; i < A.npairs; i += 64) counter_reset(&g_ready[i]);
     if (!A.commit_ptrs) return;
     const int nf = A.fill_list[0];
@@ -377,9 +423,12 @@ __device__ __forceinline__ void down_wg(const DecodeArgs& A, int blk, LayerShare
 template <int K>
 __global__ void __launch_bounds__(kThreads) moe_layer_kernel(DecodeArgs A) {
     __shared__ LayerShared S;
+    const int nv = A.n_vict_wg;
     const int n_gu = A.npairs * (A.g.I / 128) * gu_slices(A.g.H);
-    if ((int)blockIdx.x < n_gu) gateup_wg<K>(A, blockIdx.x, S);
-    else down_wg<K>(A, blockIdx.x - n_gu, S);
+    const int b = blockIdx.x;
+    if (b < nv) victim_wg(A, b);
+    else if (b < nv + n_gu) gateup_wg<K>(A, b - nv, S);
+    else down_wg<K>(A, b - nv - n_gu, S);
 }
 
 // bit-exact dequantization of one trellis matrix (PLANAR4 words [k_tiles][n_tiles][8K]) -> fp16 [16 k_tiles][16 n_tiles]
@@ -412,7 +461,7 @@ __global__ void __launch_bounds__(256) dequant_kernel(const uint32_t* __restrict
 hipError_t launch_moe_layer(int K, const DecodeArgs& a, hipStream_t s) {
     const int n_gu = a.npairs * (a.g.I / 128) * gu_slices(a.g.H);
     const int n_dn = a.npairs * (a.g.H / 128);
-    dim3 grid((unsigned)(n_gu + n_dn));
+    dim3 grid((unsigned)(a.n_vict_wg + n_gu + n_dn));
     if (K == 2) hipLaunchKernelGGL(moe_layer_kernel<2>, grid, dim3(kThreads), 0, s, a);
     else if (K == 3) hipLaunchKernelGGL(moe_layer_kernel<3>, grid, dim3(kThreads), 0, s, a);
     else if (K == 4) hipLaunchKernelGGL(moe_layer_kernel<4>, grid, dim3(kThreads), 0, s, a);
