@@ -206,6 +206,13 @@ __device__ __forceinline__ void gateup_wg(const DecodeArgs& A, int blk, LayerSha
     const bool live = ks * 256 + (qt >> 1) * 128 < H;
     GV g;
     if (live) g.load((const uint32_t*)base, tiles_n, r0, ct0);
+    half2_t sc_g{}, sc_u{}, sc_d{};              // epilogue scales (wave 0), loaded early: off the critical path
+    if (wv == 0) {
+        const int c = nb * 128 + 2 * l;
+        sc_g = *(const half2_t*)((const half_t*)(base + A.g.off_svh_g) + c);
+        sc_u = *(const half2_t*)((const half_t*)(base + A.g.off_svh_u) + c);
+        sc_d = *(const half2_t*)((const half_t*)(base + A.g.off_suh_d) + c);
+    }
     if (wv < 4 && ks * 256 + (wv >> 1) * 128 >= H) {
         if (l == 0) S.ssum[wv & 1][wv >> 1] = 0.f;
     } else if (wv < 4) {                         // input Hadamards of x * suh: (proj, 128-row block) per wave
@@ -270,17 +277,14 @@ __device__ __forceinline__ void gateup_wg(const DecodeArgs& A, int blk, LayerSha
     wave_fwht128(g0, g1);
     wave_fwht128(u0, u1);
     const int c = nb * 128 + 2 * l;
-    const half_t* svg = (const half_t*)(base + A.g.off_svh_g) + c;
-    const half_t* svu = (const half_t*)(base + A.g.off_svh_u) + c;
-    const half_t* sud = (const half_t*)(base + A.g.off_suh_d) + c;
-    g0 = (float)(half_t)(g0 * kRsqrt128 * (float)svg[0]);
-    g1 = (float)(half_t)(g1 * kRsqrt128 * (float)svg[1]);
-    u0 = (float)(half_t)(u0 * kRsqrt128 * (float)svu[0]);
-    u1 = (float)(half_t)(u1 * kRsqrt128 * (float)svu[1]);
+    g0 = (float)(half_t)(g0 * kRsqrt128 * (float)sc_g.x);
+    g1 = (float)(half_t)(g1 * kRsqrt128 * (float)sc_g.y);
+    u0 = (float)(half_t)(u0 * kRsqrt128 * (float)sc_u.x);
+    u1 = (float)(half_t)(u1 * kRsqrt128 * (float)sc_u.y);
     float a0 = (float)(half_t)(g0 / (1.0f + expf(-g0)) * u0);
     float a1 = (float)(half_t)(g1 / (1.0f + expf(-g1)) * u1);
-    a0 = (float)(half_t)(a0 * (float)sud[0]);
-    a1 = (float)(half_t)(a1 * (float)sud[1]);
+    a0 = (float)(half_t)(a0 * (float)sc_d.x);
+    a1 = (float)(half_t)(a1 * (float)sc_d.y);
     wave_fwht128(a0, a1);
     const half2_t hv = half2_t{(half_t)(a0 * kRsqrt128), (half_t)(a1 * kRsqrt128)};
     __hip_atomic_store((uint32_t*)(A.abuf + (size_t)a * I + c), __builtin_bit_cast(uint32_t, hv), __ATOMIC_RELAXED,
@@ -310,6 +314,12 @@ __device__ __forceinline__ void down_wg(const DecodeArgs& A, int blk, LayerShare
     GV g0, g1;
     if (nch > 0) g0.load(tr, tiles_n, wv * 4, ct0);
     if (nch > 1) g1.load(tr, tiles_n, (wv + kWaves) * 4, ct0);
+    half2_t sc_d{};                              // epilogue scale and routing weight (wave 0), loaded early
+    float wgt = 0.f;
+    if (wv == 0) {
+        sc_d = *(const half2_t*)((const half_t*)(base + A.g.off_svh_d) + nb * 128 + 2 * l);
+        wgt = A.w[a];
+    }
     if (tid == 0) {                              // wait for the pair's whole abuf (all I/128 gate/up epilogues)
         if (trd && A.n_vict_wg) wait_count(&g_cnt_all[1], A.n_vict_wg);   // and for the victim write-back
         int it = 0;
@@ -367,11 +377,10 @@ __device__ __forceinline__ void down_wg(const DecodeArgs& A, int blk, LayerShare
     }
     wave_fwht128(v0, v1);
     const int c = nb * 128 + 2 * l;
-    const half_t* svd = (const half_t*)(base + A.g.off_svh_d) + c;
-    const float sc = kRsqrt128 * A.w[a];
+    const float sc = kRsqrt128 * wgt;
     float* y = A.ybuf + (size_t)a * H + c;
-    st_agent(y, v0 * sc * (float)svd[0]);
-    st_agent(y + 1, v1 * sc * (float)svd[1]);
+    st_agent(y, v0 * sc * (float)sc_d.x);
+    st_agent(y + 1, v1 * sc * (float)sc_d.y);
     // combine: the last pair of row m to finish this 128-column block sums the top-k outputs in k order
     wait_stores();
     int old = 0;
@@ -381,16 +390,16 @@ __device__ __forceinline__ void down_wg(const DecodeArgs& A, int blk, LayerShare
     if (l == 0) counter_reset(&g_cnt_c[m * nbn + nb]);
     const float* yb = A.ybuf + (size_t)(m * A.topk) * H + c;
     float o0 = 0.f, o1 = 0.f;
-    for (int k0 = 0; k0 < A.topk; k0 += 8) {     // 16 loads in flight per round
-        float v[8][2];
+    for (int k0 = 0; k0 < A.topk; k0 += 16) {    // one round of loads for up to 16 picks
+        float v[16][2];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
+        for (int j = 0; j < 16; ++j) {
             const bool ok = k0 + j < A.topk;
             v[j][0] = ok ? ld_agent(yb + (size_t)(k0 + j) * H) : 0.f;
             v[j][1] = ok ? ld_agent(yb + (size_t)(k0 + j) * H + 1) : 0.f;
         }
 #pragma unroll
-        for (int j = 0; j < 8; ++j)
+        for (int j = 0; j < 16; ++j)
             if (k0 + j < A.topk) {
                 o0 += v[j][0];
                 o1 += v[j][1];

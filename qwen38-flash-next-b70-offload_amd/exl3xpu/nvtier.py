@@ -175,6 +175,93 @@ class NvTier:
         self.res_dev.copy_(torch.from_numpy(self.res))
         return len(todo), time.perf_counter() - t
 
+    # ---- tier-mode prefill streaming (nvtier.py:534-640) ------------------------------------------------------------
+    def stage_forward(self, store, key, li: int, x: torch.Tensor, ids: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
+        """Prefill-size MoE for layer `li` with its non-HBM experts streamed: reader threads copy the layer's records
+        from the fill source into a pinned host ring buffer (read-ahead of NB-1 layers, EXL3_NVTIER_STAGE_HOSTBUF,
+        default 4), a side stream copies them into one of two HBM staging buffers (runs of consecutive experts in one
+        copy), and the layer runs from the device table where(slot_of >= 0, slot, staging). The first layer of a
+        forward synchronises once and snapshots the HBM slot map; layers follow the checkpoint order."""
+        sg = getattr(self, "_sg", None) or self._stage_setup()
+        E, rec = self.E, sg["rec"]
+        pos = sg["pos"][li]
+        if pos == 0 or li not in sg["pending"]:
+            torch.cuda.synchronize(self.dev)
+            sod = self.st.slot_of_dev[:self.L * E]
+            sg["snap_dev"] = sod.to(torch.int64)
+            sg["snap"] = sod.cpu().numpy()
+            for _, _, fs in sg["pending"].values():
+                for f in fs:
+                    f.result()
+            sg["pending"].clear()
+            for q in range(pos, min(pos + sg["NB"], len(sg["order"]))):
+                self._stage_kick(sg["order"][q])
+        hb, miss, futs = sg["pending"].pop(li)
+        for f in futs:
+            f.result()
+        buf = sg["dbuf"]
+        sg["dbuf"] = 1 - buf
+        cur = torch.cuda.current_stream(self.dev)
+        dbase, hbase = s64(sg["dev"][buf].data_ptr()), s64(sg["host"][hb].data_ptr())
+        with torch.cuda.stream(sg["cs"]):
+            if sg["comp_ev"][buf] is not None:
+                sg["cs"].wait_event(sg["comp_ev"][buf])      # the layer that last read this staging buffer is done
+            m, i = miss.tolist(), 0
+            while i < len(m):
+                j = i
+                while j + 1 < len(m) and m[j + 1] == m[j] + 1:
+                    j += 1
+                self.st.X.memcpy_async(dbase + m[i] * rec, hbase + m[i] * rec, (j - i + 1) * rec)
+                i = j + 1
+            ev = torch.cuda.Event()
+            ev.record(sg["cs"])
+        sg["hfree"][hb] = ev
+        cur.wait_event(ev)
+        so = sg["snap_dev"][li * E:(li + 1) * E]
+        table = torch.where(so >= 0, self.st.slot_base + so.clamp_min(0) * self.st.blob, dbase + sg["ar"])
+        y = store.forward(key, x, ids, w, ptrs=table)
+        ce = torch.cuda.Event()
+        ce.record(cur)
+        sg["comp_ev"][buf] = ce
+        nq = pos + sg["NB"]
+        if nq < len(sg["order"]) and sg["order"][nq] not in sg["pending"]:
+            self._stage_kick(sg["order"][nq])
+        sg["bytes"] += len(miss) * rec
+        return y
+
+    def _stage_setup(self):
+        E = self.E
+        rec = self.st.stride
+        NB = max(2, int(os.environ.get("EXL3_NVTIER_STAGE_HOSTBUF", "4")))
+        X = self.st.X
+        order = [int(li) for li in np.argsort(self.ckpt, kind="stable")]
+        sg = dict(rec=rec, NB=NB, dev=[torch.empty(E * rec, dtype=torch.uint8, device=self.dev) for _ in range(2)],
+                  host=[X.host_alloc(E * rec) for _ in range(NB)], cs=torch.cuda.Stream(self.dev),
+                  comp_ev=[None, None], hfree={}, pending={}, nexth=0, dbuf=0, order=order,
+                  pos={li: i for i, li in enumerate(order)}, snap=None, snap_dev=None, bytes=0,
+                  ar=torch.arange(E, dtype=torch.int64, device=self.dev) * rec,
+                  pool=ThreadPoolExecutor(int(os.environ.get("EXL3_NVTIER_FILL_THREADS", "16"))))
+        self._sg = sg
+        return sg
+
+    def _stage_kick(self, li: int) -> None:
+        """Start the reads of layer li's non-HBM experts into the next host ring buffer."""
+        sg, E, rec = self._sg, self.E, self._sg["rec"]
+        hb = sg["nexth"]
+        sg["nexth"] = (hb + 1) % sg["NB"]
+        ev = sg["hfree"].pop(hb, None)
+        if ev is not None:
+            ev.synchronize()                        # the copy that last read this host buffer is done
+        miss = np.nonzero(sg["snap"][li * E:(li + 1) * E] < 0)[0]
+        hp = s64(sg["host"][hb].data_ptr())
+        keys = [int(e) for e in miss]
+        per = max(1, -(-len(keys) // 8))
+
+        def rd(part):
+            for e in part:
+                self.src.read(self.rec_index(li * E + e), hp + e * rec)
+        sg["pending"][li] = (hb, miss, [sg["pool"].submit(rd, keys[i:i + per]) for i in range(0, len(keys), per)])
+
     def log_stats(self, logger=None, every=200):
         logger = logger or log
         if self.stats["steps"] % every or not self.stats["steps"]:

@@ -189,3 +189,42 @@ def test_prefill_staged_matches_resident():
     torch.cuda.synchronize()
     for n, (o, r) in enumerate(zip(outs, refs)):
         assert torch.equal(o, r), n
+
+
+def test_tier_stage_forward_matches_resident():
+    """NvTier.stage_forward (non-HBM experts read from the fill source into a pinned host ring, copied to an HBM
+    staging buffer on a side stream, read-ahead across layers) gives the same bits as the all-resident table; two
+    passes over the layers so the host ring and both staging buffers are reused."""
+    import ctypes
+    from exl3xpu import nvtier
+    H, I, K, E, S, L, M, topk = 256, 128, 3, 16, 20, 3, 300, 4
+    print("case tier stage_forward vs resident", flush=True)
+    store = nvtier.TierStore(H, I, K, E, S, n_layers=L)
+    keys = [f"model.layers.{li}.mlp" for li in range(L)]
+    for k in keys:
+        store.add_layer(k)
+    src = nvtier.SyntheticExpertSource(H, I, K, 13, n_distinct=L * E)
+    for key in range(L * E):                       # RAM copies, the source of make_resident
+        ctypes.memmove(store.addr(key), src.buf[key].ctypes.data, store.blob)
+    tier = nvtier.NvTier(store, src, budget_records=L * E)
+    try:
+        rng = np.random.default_rng(6)
+        for li in range(L):
+            store.make_resident(keys[li], sorted(rng.choice(np.arange(1, E), size=5, replace=False).tolist()))
+        blobs = torch.from_numpy(src.buf).cuda()
+        outs, refs = [], []
+        for rep in range(2):
+            for li in range(L):
+                ids, w = synth.softmax_topk(60 + li + 7 * rep, M, E, topk)
+                x = torch.from_numpy(exl3.bf16_to_f32(synth.activations(70 + li, M, H))).to(torch.bfloat16).cuda()
+                it, wt = torch.from_numpy(ids).cuda(), torch.from_numpy(w).cuda()
+                outs.append(tier.stage_forward(store, keys[li], li, x, it, wt))
+                table = torch.tensor([blobs[li * E + e].data_ptr() for e in range(E)], dtype=torch.int64,
+                                     device="cuda")
+                refs.append(_ops().moe_forward(x, it, wt, table, I, K, E))
+        torch.cuda.synchronize()
+        for n, (o, r) in enumerate(zip(outs, refs)):
+            assert torch.equal(o, r), n
+        assert tier._sg["bytes"] == 2 * L * (E - 5) * store.stride     # every non-HBM expert, each pass
+    finally:
+        tier.close()
