@@ -48,8 +48,12 @@ int64_t exl3_blob_bytes(int H, int I, int K);
 int exl3_set_tier(uint8_t* ram_res, int32_t* miss_ring, int64_t ring_numel, const int32_t* safe);
 /* moe_set_victims (a8:757): device int32 [1 + 2E] victim list, NULL = no victim write-back */
 int exl3_set_victims(int32_t* vict);
-/* moe_set_host_stride (a8:765): stride of a key's RAM-tier address, 0 = the blob size */
+/* moe_set_host_stride (a8:765): stride of a key's RAM-tier address, 0 = the slot stride */
 int exl3_set_host_stride(int64_t stride);
+/* Bytes between HBM slots, 0 = the blob size of the call (no reference counterpart: the reference assumes one expert
+ * geometry per store, plugin/sglang_plugin.tier.py:166-167). Set to the largest blob when layers of one store use
+ * different bitrates K; victims are then written back as whole slots. */
+int exl3_set_slot_stride(int64_t stride);
 /* moe_set_prefill_min_m (a8:775), moe_set_pair_max_m (a8:727), moe_set_splits (a8:685), moe_set_mr (a8:729) */
 int exl3_set_prefill_min_m(int64_t m);
 int exl3_set_pair_max_m(int64_t m);

@@ -22,6 +22,7 @@ struct Config {
     const int32_t* safe = nullptr;
     int32_t* vict = nullptr;
     int64_t host_stride = 0;
+    int64_t slot_stride = 0;                      // bytes between HBM slots (0: the blob size of the call)
     int prefill_min_m = 256;
     int pair_max_m = 4;
     int gu_p = 0, dn_p = 0, mr = 0, debug = 0;
@@ -78,6 +79,12 @@ int exl3_set_tier(uint8_t* ram_res, int32_t* miss_ring, int64_t ring_numel, cons
 
 int exl3_set_victims(int32_t* vict) {
     g_cfg.vict = vict;
+    return EXL3_OK;
+}
+
+int exl3_set_slot_stride(int64_t stride) {
+    if (stride < 0 || stride % 16) return fail(EXL3_EINVAL, "moe_set_slot_stride: stride must be a non-negative multiple of 16");
+    g_cfg.slot_stride = stride;
     return EXL3_OK;
 }
 
@@ -249,8 +256,10 @@ int exl3_moe_forward_cached(const void* x, int x_dtype, int64_t x_stride, int M,
     ea.tick = tick;
     ea.host_base = host_base;
     ea.slot_base = slot_base;
-    ea.blob = g.blob;
-    ea.hstride = g_cfg.host_stride ? g_cfg.host_stride : g.blob;
+    ea.blob = g_cfg.slot_stride ? g_cfg.slot_stride : g.blob;        // slot stride (slot s at slot_base + s * stride)
+    if (ea.blob < g.blob) return fail(EXL3_EINVAL, "moe_forward_cached: slot stride %lld < blob %lld",
+                                      (long long)ea.blob, (long long)g.blob);
+    ea.hstride = g_cfg.host_stride ? g_cfg.host_stride : ea.blob;
     ea.fill_all = fill_all;
     ea.fill_list = fill_list;
     ea.max_fill = std::min(max_fill, E);
@@ -273,7 +282,7 @@ int exl3_moe_forward_cached(const void* x, int x_dtype, int64_t x_stride, int M,
         va.vict = g_cfg.vict;
         va.host_base = host_base;
         va.slot_base = slot_base;
-        va.blob = g.blob;
+        va.blob = ea.blob;                        // a victim may be an expert of another bitrate: copy the slot
         va.hstride = ea.hstride;
         va.E = E;
         va.ram_res = g_cfg.ram_res;

@@ -127,6 +127,7 @@ void moe_set_tier(at::Tensor ram_res, at::Tensor miss, at::Tensor safe) {
           "moe_set_tier");
 }
 void moe_set_host_stride(int64_t s) { check(exl3_set_host_stride(s), "moe_set_host_stride"); }
+void moe_set_slot_stride(int64_t s) { check(exl3_set_slot_stride(s), "moe_set_slot_stride"); }
 // pinned host memory is device-mapped on MI355X: nothing to prefetch (the reference maps xe-SVM pages, a8:777-781)
 void moe_svm_prefetch(at::Tensor ptrs, int64_t nbytes, at::Tensor like) {
     (void)ptrs;
@@ -171,6 +172,7 @@ TORCH_LIBRARY(exl3xpu_moe, m) {
     m.def("moe_set_victims(Tensor v) -> ()", &moe_set_victims);
     m.def("moe_set_tier(Tensor ram_res, Tensor miss, Tensor safe) -> ()", &moe_set_tier);
     m.def("moe_set_host_stride(int s) -> ()", &moe_set_host_stride);
+    m.def("moe_set_slot_stride(int s) -> ()", &moe_set_slot_stride);
     m.def("moe_svm_prefetch(Tensor ptrs, int nbytes, Tensor like) -> ()", &moe_svm_prefetch);
     m.def("moe_set_decision_log(Tensor buf) -> ()", &moe_set_decision_log);
     m.def("dequant(Tensor trellis, int k_tiles, int n_tiles, int K) -> Tensor");

@@ -127,6 +127,8 @@ class ExpertStore:
         self.done_seq = torch.zeros(0, dtype=torch.int32, device=self.dev)
         self.slot_base = s64(self.slots.data_ptr()) if n_slots else 0
         self._cache_used = False
+        self.K_of: dict = {}                                # key -> bitrate of the layer (default K)
+        self.X.moe_set_slot_stride(0)                       # slots at the blob size (mixed_bitrates() widens)
 
     # ---- layers
     def add_layer(self, key, blobs: torch.Tensor | None = None) -> torch.Tensor:
@@ -147,6 +149,15 @@ class ExpertStore:
 
     def host_view(self, key) -> torch.Tensor:
         return self.host[key]
+
+    def mixed_bitrates(self) -> None:
+        """Layers of this store use different bitrates K <= the store's K: slots (and host records) keep the size of
+        the largest blob, and the device cache addresses slots at that stride (moe_set_slot_stride). Layers with a
+        smaller K read and write only their own blob bytes; victims are written back as whole slots."""
+        self.X.moe_set_slot_stride(self.blob)
+
+    def k_of(self, key) -> int:
+        return self.K_of.get(key, self.K)
 
     def ptrs(self, key) -> torch.Tensor:
         li = self.layer_index[key]
@@ -238,7 +249,7 @@ class ExpertStore:
 
     def forward(self, key, x: torch.Tensor, topk_ids: torch.Tensor, topk_w: torch.Tensor, ptrs=None) -> torch.Tensor:
         ids, w = self._rt(topk_ids, topk_w)
-        return self.X.moe_forward(x, ids, w, self.ptrs(key) if ptrs is None else ptrs, self.I, self.K, self.E)
+        return self.X.moe_forward(x, ids, w, self.ptrs(key) if ptrs is None else ptrs, self.I, self.k_of(key), self.E)
 
     def forward_cached(self, key, x: torch.Tensor, topk_ids: torch.Tensor, topk_w: torch.Tensor,
                        max_fill: int | None = None) -> torch.Tensor:
@@ -251,7 +262,7 @@ class ExpertStore:
         return self.X.moe_forward_cached(x, ids, w, self.ptrs_all, self.layer_index[key], self.slot_of_dev,
                                          self.slot_key, self.slot_last, self.tick, self.host_base, self.slot_base,
                                          self.fill_all, self.fill_list, self.E if max_fill is None else max_fill,
-                                         self.I, self.K, self.E, self.pend, self.done_seq)
+                                         self.I, self.k_of(key), self.E, self.pend, self.done_seq)
 
     def prefetch(self, key, ids: torch.Tensor, max_fill: int = 16) -> None:
         raise NotImplementedError("exl3xpu: predicted-expert prefetch (moe_prefetch) is not built in this library")
@@ -337,7 +348,7 @@ class ExpertStore:
         rdy = pf["ready"].pop(key)
         cs.wait_event(rdy)
         ids, w = self._rt(topk_ids, topk_w)
-        y = self.X.moe_forward(x, ids, w, table, self.I, self.K, self.E)
+        y = self.X.moe_forward(x, ids, w, table, self.I, self.k_of(key), self.E)
         ev = torch.cuda.Event()
         ev.record(cs)
         pf["free"][buf] = ev

@@ -32,8 +32,14 @@ class TierStore(ExpertStore):
     """ExpertStore whose host copies live at fixed-stride addresses of one pinned arena (the reference uses a sparse
     2 MiB-stride memfd, nvtier.py:22-53). stride defaults to the blob size rounded up to 4 KiB."""
 
-    def __init__(self, H, I, K, E, n_slots, n_layers, stride=None, device=None):
-        super().__init__(H, I, K, E, n_slots, device=device, max_layers=n_layers)
+    def __init__(self, H, I, K, E, n_slots, n_layers, stride=None, device=None, Ks=None):
+        """Ks: bitrate per layer (in add_layer order) when layers differ; slots and records take the largest blob."""
+        self.Ks = [int(k) for k in Ks] if Ks is not None else None
+        if self.Ks is not None and len(self.Ks) != n_layers:
+            raise ValueError(f"TierStore: {len(self.Ks)} bitrates for {n_layers} layers")
+        super().__init__(H, I, max(self.Ks) if self.Ks else K, E, n_slots, device=device, max_layers=n_layers)
+        if self.Ks and len(set(self.Ks)) > 1:
+            self.mixed_bitrates()
         self.stride = int(stride) if stride else (self.blob + 4095) // 4096 * 4096
         assert self.blob <= self.stride and self.stride % 16 == 0
         self.L = n_layers
@@ -47,6 +53,8 @@ class TierStore(ExpertStore):
         if li >= self.L:
             raise RuntimeError(f"TierStore: more than n_layers={self.L} MoE layers")
         self.layer_index[key] = li
+        if self.Ks:
+            self.K_of[key] = self.Ks[li]
         base = self.base + li * self.E * self.stride
         self._host_ptr[key] = base + torch.arange(self.E, dtype=torch.int64) * self.stride
         self.ptrs_all[li * self.E:(li + 1) * self.E].copy_(self._host_ptr[key])
@@ -82,6 +90,21 @@ class SyntheticExpertSource:
 
     def blob_of(self, rec_index: int) -> np.ndarray:
         return self.buf[rec_index % self.n]
+
+
+class LayeredExpertSource:
+    """Fill source for a store whose layers differ in bitrate: record r = layer * E + e is read from sources[layer]
+    (a source of that layer's geometry)."""
+
+    def __init__(self, sources, E: int):
+        self.sources, self.E = list(sources), int(E)
+        self.blob = max(s.blob for s in self.sources)
+
+    def read(self, rec_index: int, dst: int) -> None:
+        self.sources[rec_index // self.E].read(rec_index, dst)
+
+    def blob_of(self, rec_index: int) -> np.ndarray:
+        return self.sources[rec_index // self.E].blob_of(rec_index)
 
 
 class NvTier:
@@ -124,6 +147,7 @@ class NvTier:
                        torch.zeros(0, dtype=torch.int32, device=self.dev))
         X.moe_set_victims(torch.zeros(0, dtype=torch.int32, device=self.dev))
         X.moe_set_host_stride(0)
+        X.moe_set_slot_stride(0)
 
     def rec_index(self, key: int) -> int:
         return int(self.ckpt[key // self.E]) * self.E + key % self.E

@@ -98,3 +98,61 @@ def test_cache_config1_trace_bitexact():
         assert a1.tolist() == a2.tolist() and e1.tolist() == e2.tolist(), n
     assert bad == 0
     tier.close()
+
+
+@pytest.mark.parametrize("H,I,steps", [(128, 128, 200), (4096, 1536, 12)])
+def test_cache_mixed_bitrates(H, I, steps):
+    """Layers of one store at K = 2, 3, 4 (128 experts, top-8, uniform routing), HBM slots for 30 % of the expert
+    bytes (slot stride = the largest blob), every expert in the pinned RAM arena, no tier: each ensure decision equals
+    the oracle's (plain device LRU) and every cached output equals the uncached output on the true blobs."""
+    import ctypes
+    from exl3xpu import nvtier
+    L, E, P, Ks, nd = 3, 128, 8, [2, 3, 4], 4
+    print(f"case mixed bitrates H={H} I={I} steps={steps}", flush=True)
+    blob = [int(_blob(H, I, k)) for k in Ks]
+    S = int(0.3 * E * sum(blob) / max(blob))
+    store = nvtier.TierStore(H, I, 4, E, S, n_layers=L, Ks=Ks)
+    keys = [f"model.layers.{li}.mlp" for li in range(L)]
+    for k in keys:
+        store.add_layer(k)
+    srcs = [nvtier.SyntheticExpertSource(H, I, K, 90 + li, n_distinct=nd) for li, K in enumerate(Ks)]
+    for key in range(L * E):
+        ctypes.memmove(store.addr(key), srcs[key // E].buf[key % nd].ctypes.data, srcs[key // E].blob)
+    dev = [torch.from_numpy(s.buf).cuda() for s in srcs]
+    tables = [torch.tensor([dev[li][e % nd].data_ptr() for e in range(E)], dtype=torch.int64, device="cuda")
+              for li in range(L)]
+    ids, w = synth.uniform_trace(91, steps, L, E, P)
+    ids, w = ids[:, :, 0], w[:, :, 0]
+    co = cache.CacheOracle(L, E, S, tier=False)
+    orecs = np.stack([np.stack([co.ensure(li, ids[n, li].copy(), w[n, li].copy()) for li in range(L)])
+                      for n in range(steps)])
+    X = store.X
+    rl = cache.rec_len(P)
+    logbuf = torch.zeros(1 + steps * L * rl, dtype=torch.int32, device="cuda")
+    X.moe_set_decision_log(logbuf)
+    x = torch.randn(L, 1, H, generator=torch.Generator().manual_seed(1)).to(torch.bfloat16).cuda()
+    bad = 0
+    try:
+        for n in range(steps):
+            for li in range(L):
+                it = torch.from_numpy(ids[n, li]).view(1, P).cuda()
+                wt = torch.from_numpy(w[n, li]).view(1, P).cuda()
+                out = store.forward_cached(keys[li], x[li], it, wt)
+                ref = X.moe_forward(x[li], it, wt, tables[li], I, Ks[li], E)
+                bad += int(not torch.equal(out, ref))
+        torch.cuda.synchronize()
+    finally:
+        X.moe_set_decision_log(torch.zeros(0, dtype=torch.int32, device="cuda"))
+        X.moe_set_slot_stride(0)
+    lg = logbuf.cpu().numpy()
+    assert lg[0] == steps * L
+    recs = lg[1:].reshape(steps, L, rl)
+    mism = np.nonzero((recs != orecs).any(axis=-1))
+    assert mism[0].size == 0, f"first mismatch at step/layer {mism[0][0]}/{mism[1][0]}"
+    assert recs[:, :, 2 + P].sum() > 0                     # misses (and write-throughs) happened
+    assert bad == 0
+
+
+def _blob(H, I, K):
+    from exl3xpu.moe_offload import ops
+    return ops().blob_bytes(H, I, K)
