@@ -33,6 +33,7 @@ __device__ int g_cnt_all[4];
 __device__ int g_status[4];          // [0]: spin timeouts (should stay 0)
 
 constexpr int kSpinMax = 1 << 22;
+constexpr uint64_t kDownLoadDelay = 120;         // 1.2 us in s_memrealtime ticks
 
 // one period of one tile-row: xv[a][qq] holds activation rows (8a + 2q, 8a + 2q + 1), q = (qb + qq) & 3
 template <int K, int NQ, int u>
@@ -311,6 +312,11 @@ __device__ __forceinline__ void down_wg(const DecodeArgs& A, int blk, LayerShare
     const uint32_t* tr = (const uint32_t*)(base + A.g.gu_bytes);
     uint32_t* trd = dst ? (uint32_t*)(dst + A.g.gu_bytes) : nullptr;
     const int nch = (kt / 4 + kWaves - 1 - wv) / kWaves;      // 4-row chunks of this wave: q = wv + kWaves * c
+    {   // the down weights are needed only after the gate/up phase: let the gate/up loads (the critical path) take
+        // HBM first, then issue these (constant 100 MHz clock)
+        const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+        while (__builtin_amdgcn_s_memrealtime() - t0 < kDownLoadDelay) __builtin_amdgcn_s_sleep(4);
+    }
     GV g0, g1;
     if (nch > 0) g0.load(tr, tiles_n, wv * 4, ct0);
     if (nch > 1) g1.load(tr, tiles_n, (wv + kWaves) * 4, ct0);
