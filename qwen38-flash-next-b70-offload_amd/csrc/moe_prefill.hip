@@ -4,8 +4,8 @@
 //
 //   align      three small kernels (count per chunk of 1,024 pairs, scan, scatter): pairs sorted by expert in
 //              ascending pair order inside an expert (deterministic; wave ballots for in-chunk ranks)
-//   xh         one wave per (sorted pair, projection, 128-row block of H): xh = fp16(H(fp16(x * suh)) / sqrt(128)),
-//              computed once per pair (the column-tile workgroups of an expert all read it)
+//   xh         input Hadamards xh = fp16(H(fp16(x * suh)) / sqrt(128)) once per (sorted pair, projection), as MFMA
+//              products with the +-1 matrix H128 (the column-tile workgroups of an expert all read them)
 //   gate/up    one workgroup of 8 waves per (active expert, 128-column block of I), over the expert's rows in chunks of
 //              256: the 4 tile-rows x (8 gate + 8 up) tiles of each 64-deep K chunk are decoded once into LDS as the
 //              fp16 B operand of v_mfma_f32_32x32x16_f16 (double-buffered; one barrier per chunk), A = xh rows read
@@ -159,25 +159,86 @@ hipError_t launch_align(const int32_t* ids, const float* w, int npairs, int topk
     return hipGetLastError();
 }
 
-// ---- xh pre-pass ---------------------------------------------------------------------------------------------------
-__global__ void __launch_bounds__(kPfThreads) prefill_xh_kernel(PrefillArgs A) {
-    const int l = lane_id();
-    const int nkb = A.g.H / 128;
-    const int64_t item = (int64_t)blockIdx.x * kPfWaves + (threadIdx.x >> 6);
-    if (item >= (int64_t)A.npairs * 2 * nkb) return;
-    const int s = (int)(item / (2 * nkb));
-    const int rem = (int)(item % (2 * nkb));
-    const int pj = rem / nkb, kb = rem % nkb;
-    const int tok = A.pair_tok[s], e = A.pair_exp[s];
-    const uint8_t* base = (const uint8_t*)A.ptrs[e];
-    const half_t* suh = (const half_t*)(base + (pj ? A.g.off_suh_u : A.g.off_suh_g));
-    const int k0 = kb * 128 + 2 * l;
-    const size_t xo = (size_t)tok * A.x_stride + k0;
-    float v0 = (float)(half_t)(ld_act(A.x, A.x_dt, xo) * (float)suh[k0]);
-    float v1 = (float)(half_t)(ld_act(A.x, A.x_dt, xo + 1) * (float)suh[k0 + 1]);
-    wave_fwht128(v0, v1);
-    half2_t* dst = (half2_t*)(A.xh + ((size_t)s * 2 + pj) * A.g.H + k0);
-    *dst = half2_t{(half_t)(v0 * kRsqrt128), (half_t)(v1 * kRsqrt128)};
+// ---- xh pre-pass: input Hadamards as MFMA products with the +-1 matrix H128 ------------------------------------------
+// xh[s][pj][kb*128 + n] = fp16(sum_k H[n][k] * fp16(x[tok(s)][kb*128 + k] * suh_pj(e(s))[kb*128 + k]) / sqrt(128)).
+// Computed transposed (C^T = H * xt^T) with v_mfma_f32_32x32x16_f16: A = rows n of H (LDS table), B = 32 pair rows of
+// xt (built in registers from x and the pair's expert's suh), so each lane ends with 4 consecutive columns of one
+// pair row per accumulator group and stores them as 8 bytes. The fp32 sums differ from the butterfly order only in
+// rounding. Workgroup of 4 waves per (64 sorted pairs, projection): wave w takes the 32 rows 32 (w & 1) .. and the
+// 128-column blocks kb = (w >> 1), (w >> 1) + 2, ...
+constexpr int kXhWaves = 4;
+
+// 8 consecutive activations as fp32 (exact for every input dtype)
+__device__ __forceinline__ void ld_act8(const void* x, int dt, size_t i, float (&v)[8]) {
+    if (dt == 2) {
+        const float4 a = *(const float4*)((const float*)x + i), b = *(const float4*)((const float*)x + i + 4);
+        v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+    } else if (dt == 1) {
+        const uint4 u = *(const uint4*)((const bf16_bits*)x + i);
+        const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            v[2 * j] = __uint_as_float(w[j] << 16);
+            v[2 * j + 1] = __uint_as_float(w[j] & 0xFFFF0000u);
+        }
+    } else {
+        const half8_t h = *(const half8_t*)((const half_t*)x + i);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[j] = (float)h[j];
+    }
+}
+
+__global__ void __launch_bounds__(64 * kXhWaves) prefill_xh_kernel(PrefillArgs A) {
+    __shared__ __align__(16) half_t hmat[128 * 128];             // H128, row n contiguous in k
+    for (int i = threadIdx.x; i < 128 * 128; i += 64 * kXhWaves)
+        hmat[i] = (__popc((i >> 7) & (i & 127)) & 1) ? (half_t)-1.0f : (half_t)1.0f;
+    __syncthreads();
+    const int H = A.g.H, nkb = H / 128;
+    const int l = lane_id(), wv = threadIdx.x >> 6;
+    const int pj = blockIdx.x & 1, blk = blockIdx.x >> 1;
+    const int s = blk * 64 + (wv & 1) * 32 + (l & 31);           // this lane's pair row (B operand column)
+    const bool valid = s < A.npairs;
+    const size_t xrow = valid ? (size_t)A.pair_tok[s] * A.x_stride : 0;
+    const half_t* suh = valid ? (const half_t*)((const uint8_t*)A.ptrs[A.pair_exp[s]] +
+                                                (pj ? A.g.off_suh_u : A.g.off_suh_g))
+                              : nullptr;
+    half_t* out = A.xh + ((size_t)(valid ? s : 0) * 2 + pj) * H;
+    for (int kb = (wv >> 1); kb < nkb; kb += 2) {
+        half8_t bx[8];                                           // xt fragments: k = 16 ks + 8 (l / 32) .. + 7
+#pragma unroll
+        for (int ks = 0; ks < 8; ++ks) {
+            const int k = kb * 128 + ks * 16 + (l >> 5) * 8;
+            if (valid) {
+                float xv[8];
+                ld_act8(A.x, A.x_dt, xrow + k, xv);
+                const half8_t sv = *(const half8_t*)(suh + k);
+#pragma unroll
+                for (int j = 0; j < 8; ++j) bx[ks][j] = (half_t)(xv[j] * (float)sv[j]);
+            } else {
+                bx[ks] = half8_t{};
+            }
+        }
+#pragma unroll
+        for (int nb = 0; nb < 4; ++nb) {
+            float16_t acc = float16_t{};
+#pragma unroll
+            for (int ks = 0; ks < 8; ++ks) {
+                const half8_t ha = *(const half8_t*)(hmat + (nb * 32 + (l & 31)) * 128 + ks * 16 + (l >> 5) * 8);
+                acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(ha, bx[ks], acc, 0, 0, 0);
+            }
+            if (valid) {
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {                    // rows n = 32 nb + 8 q + 4 (l / 32) + 0..3
+                    const int n = nb * 32 + q * 8 + (l >> 5) * 4;
+                    typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
+                    const half4_t hv = half4_t{(half_t)(acc[4 * q] * kRsqrt128), (half_t)(acc[4 * q + 1] * kRsqrt128),
+                                               (half_t)(acc[4 * q + 2] * kRsqrt128),
+                                               (half_t)(acc[4 * q + 3] * kRsqrt128)};
+                    *(half4_t*)(out + kb * 128 + n) = hv;
+                }
+            }
+        }
+    }
 }
 
 // ---- decode of one K chunk (4 tile-rows x 16 tiles) into LDS ----------------------------------------------------------
@@ -458,8 +519,7 @@ hipError_t launch_prefill(PrefillArgs a, int E, void* ws, hipStream_t s) {
     a.pair_exp = o.pair_exp;
     hipError_t e = launch_align(a.ids, a.w, np, a.topk, E, 1, chunk, o, s);
     if (e != hipSuccess) return e;
-    const int64_t nxh = (int64_t)np * 2 * (H / 128);
-    hipLaunchKernelGGL(prefill_xh_kernel, dim3((unsigned)((nxh + kPfWaves - 1) / kPfWaves)), dim3(kPfThreads), 0, s, a);
+    hipLaunchKernelGGL(prefill_xh_kernel, dim3((unsigned)(2 * ((np + 63) / 64))), dim3(64 * kXhWaves), 0, s, a);
     const dim3 ggu((unsigned)(A * (I / 128))), gdn((unsigned)(A * (H / 256)));
     switch (a.g.K) {
         case 2:
