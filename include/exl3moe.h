@@ -54,6 +54,11 @@ int exl3_set_host_stride(int64_t stride);
  * geometry per store, plugin/sglang_plugin.tier.py:166-167). Set to the largest blob when layers of one store use
  * different bitrates K; victims are then written back as whole slots. */
 int exl3_set_slot_stride(int64_t stride);
+/* 1 (default): a cached decode call within the fused limits (<= 512 experts, <= 64 picks, <= 16384 slots, K <= 3)
+ * runs the ensure as the first workgroup of the layer kernel, so pairs that hit start streaming at once; 0: the
+ * ensure is a separate launch before the layer kernel. The decisions are the same either way (no reference
+ * counterpart: the reference always launches its ensure kernel first, kernels/moe-a8/exl3_moe.a8.sycl:1040). */
+int exl3_set_fused_ensure(int64_t enable);
 /* moe_set_prefill_min_m (a8:775), moe_set_pair_max_m (a8:727), moe_set_splits (a8:685), moe_set_mr (a8:729) */
 int exl3_set_prefill_min_m(int64_t m);
 int exl3_set_pair_max_m(int64_t m);

@@ -11,10 +11,28 @@ constexpr int kMaxPairs = 1024;     // pairs (rows x top-k) of one decode call
 constexpr int kMaxRows = 256;       // rows of one decode call
 constexpr int kMaxExperts = 1024;   // experts per layer (one ensure work-item per expert)
 constexpr int kMaxI = 4096;         // intermediate size of the decode kernels (abuf staged in LDS)
+// ensure inside the layer kernel (one 512-thread workgroup): its limits
+constexpr int kEnsRegSlots = 32;    // slot_last values held in registers per thread: S <= 512 * 32
+constexpr int kEnsMaxP = 64;        // picks (one per lane of wave 0)
+constexpr int kEnsMaxE = 512;       // experts (one per thread)
+
+constexpr int kVictimChunkBytes = 64 * 1024;   // bytes of a victim slot copied by one workgroup
 
 struct VictimArgs {
     const int32_t* vict; const int64_t* host_base; int64_t slot_base; int64_t blob; int64_t hstride; int E;
     uint8_t* ram_res; int chunk_bytes;
+};
+
+struct EnsureArgs {
+    int32_t* ids; float* w; int P;                 // picks (masked in place)
+    int layer, E, S;
+    int64_t* ptrs_all; int32_t* slot_of; int32_t* slot_key; int32_t* slot_last; int32_t* tick;
+    const int64_t* host_base; int64_t slot_base; int64_t blob; int64_t hstride;
+    int64_t* fill_all; int32_t* fill_list; int max_fill;
+    const uint8_t* ram_res; int32_t* ring; int ring_cap; const int32_t* safe;   // tier (null ram_res: off)
+    int32_t* vict;                                 // victim list [1 + 2E] or null
+    int32_t* log; int64_t log_cap;                 // decision log (debug) or null: [count, records...]
+    int64_t* pair_ptr;                             // out: blob pointer of every post-mask pick [P] (or null)
 };
 
 struct DecodeArgs {
@@ -34,20 +52,9 @@ struct DecodeArgs {
     BlobGeom g;
     VictimArgs va;                                 // victim write-back (cached calls with victims on)
     int n_vict_wg, vict_chunks;                    // victim-copy workgroups (first in the grid) and chunks per victim
+    int fused;                                     // 1: workgroup 0 runs the cache's ensure (ens) inside the launch
+    EnsureArgs ens;
 };
-
-struct EnsureArgs {
-    int32_t* ids; float* w; int P;                 // picks (masked in place)
-    int layer, E, S;
-    int64_t* ptrs_all; int32_t* slot_of; int32_t* slot_key; int32_t* slot_last; int32_t* tick;
-    const int64_t* host_base; int64_t slot_base; int64_t blob; int64_t hstride;
-    int64_t* fill_all; int32_t* fill_list; int max_fill;
-    const uint8_t* ram_res; int32_t* ring; int ring_cap; const int32_t* safe;   // tier (null ram_res: off)
-    int32_t* vict;                                 // victim list [1 + 2E] or null
-    int32_t* log; int64_t log_cap;                 // decision log (debug) or null: [count, records...]
-    int64_t* pair_ptr;                             // out: blob pointer of every post-mask pick [P] (or null)
-};
-
 
 // token sort (reference launch_align a8:639-680): pairs sorted by expert, ascending pair index inside an expert
 struct AlignOut {

@@ -11,6 +11,8 @@
 //   5. victims = ascending-slot({u < tau}) ++ first `want` of ascending-slot({u == tau}) (ordered compaction over
 //      per-thread contiguous slot chunks), paired with misses in order; the old owner is repointed to its host copy,
 //      the miss gets the slot and a write-through target fill_all[key]
+// Calls of at most 64 picks whose post-mask picks all hold a slot finish in wave 0 after step 2 (stamps, pair pointers,
+// empty lists): the same decisions without the slot-table staging, the block scans and their barriers.
 // The reference builds the miss and victim lists with SLM fetch_add, so its pairing is not deterministic; here every
 // list is produced by prefix sums in work-item order, which defines the canonical decisions the oracle restates.
 //
@@ -98,41 +100,109 @@ __global__ void __launch_bounds__(kEnsureThreads) ensure_kernel(EnsureArgs A) {
     const bool sl_lds = S <= kEnsureLdsSlots;
     const int32_t* slg = A.slot_last;
 
-    if (tid == 0) sh[0] = ++A.tick[0];
+    // Calls of at most 64 picks keep pick `lane`'s post-mask slot and blob pointer in wave 0's registers: loaded in the
+    // same round as the tier mask, they serve the fast path, the slow path's hit stamps and the pair pointers.
+    const bool small = P <= 64;
+    int pslot = -1;
     if (wv == 0) {                                            // tier mask, ascending pick order
+        const int kb = A.layer * E;
         int cnt = A.ram_res ? A.ring[0] : 0;
+        const int safe = A.ram_res ? A.safe[A.layer] : 0;
+        const int safe_slot = A.ram_res ? A.slot_of[kb + safe] : -1;
+        const int64_t safe_ptr = A.ram_res && small ? A.ptrs_all[kb + safe] : 0;
+        int T = 0;
+        if (lane == 0) {
+            T = A.tick[0] + 1;
+            A.tick[0] = T;
+            sh[0] = T;
+        }
+        T = __shfl(T, 0, 64);
+        int64_t pptr = 0;
         for (int b = 0; b < P; b += 64) {
             const int i = b + lane;
             int id = i < P ? min(max(A.ids[i], 0), E - 1) : 0;
-            bool msk = false;
-            if (A.ram_res && i < P) {
-                const int key = A.layer * E + id;
-                msk = A.slot_of[key] < 0 && !A.ram_res[key];
-            }
+            int so = i < P ? A.slot_of[kb + id] : -1;
+            if (small && i < P) pptr = A.ptrs_all[kb + id];
+            const bool msk = A.ram_res && i < P && so < 0 && !A.ram_res[kb + id];
             const uint64_t bal = __ballot(msk);
             if (msk) {
                 const int pos = cnt + __popcll(bal & ((1ull << lane) - 1ull));
-                A.ring[1 + (int)((uint32_t)pos % (uint32_t)A.ring_cap)] = A.layer * E + id;
-                id = A.safe[A.layer];
+                A.ring[1 + (int)((uint32_t)pos % (uint32_t)A.ring_cap)] = kb + id;
+                id = safe;
+                so = safe_slot;
+                pptr = safe_ptr;
                 A.ids[i] = id;
                 A.w[i] = 0.0f;
             }
             if (i < P) pid[i] = id;
+            pslot = so;
             cnt += __popcll(bal);
         }
         if (A.ram_res && lane == 0) A.ring[0] = cnt;
         if (lane == 0) sh[5] = cnt;
+        // blob pointer of every post-mask pick (read by the GEMV workgroups). Assignments below never touch it: a
+        // victim slot's owner is not a pick of this call (hits are stamped T, so their slots are not eligible), and
+        // a miss keeps its host copy's pointer until the fill is committed at the end of the call.
+        if (small && lane < P && A.pair_ptr) A.pair_ptr[lane] = pptr;
+        // no-miss fast path: every post-mask pick holds a slot, so the call's only decisions are the hit stamps;
+        // fills, victims and the LRU scan are empty. The stamp rule "slot_last = T unless pinned (INT_MAX)" is an
+        // atomic max here: every other slot_last value is a tick of an earlier call, 0 (loaded by the host) or -1
+        // (empty), all below T, and the max needs no read round trip.
+        const bool fast = small && __ballot(lane < P && pslot < 0) == 0ull;
+        if (fast) {
+            if (lane < P) atomicMax(A.slot_last + pslot, T);
+            if (lane == 0) {
+                A.fill_list[0] = 0;
+                if (A.vict) A.vict[0] = 0;
+            }
+            if (A.log) {
+                const int idx = A.log[0];
+                if (idx < A.log_cap) {
+                    int32_t* r = A.log + 1 + (int64_t)idx * (3 + 4 * P);
+                    if (lane == 0) {
+                        r[0] = T;
+                        r[1] = cnt;
+                        r[2 + P] = 0;
+                    }
+                    if (lane < P) {
+                        r[2 + lane] = pid[lane];
+                        r[3 + P + lane] = -1;
+                        r[3 + 2 * P + 2 * lane] = -2;
+                        r[4 + 2 * P + 2 * lane] = -2;
+                    }
+                }
+                if (lane == 0) A.log[0] = idx + 1;
+            }
+        }
+        if (lane == 0) sh[6] = fast ? 1 : 0;
     }
     for (int e = tid; e < E; e += kEnsureThreads) need[e] = 0;
     if (sl_lds)
         for (int s = tid; s < S; s += kEnsureThreads) sl[s] = slg[s];
     __syncthreads();
+    if (sh[6]) return;                                         // uniform: the fast path finished the call
     const int T = sh[0];
-    for (int i = tid; i < P; i += kEnsureThreads) need[pid[i]] = 1;
+    if (small) {
+        // need[e] = 1 hit, 2 miss; hits stamp slot_last = T unless pinned (duplicate picks write the same value)
+        if (tid < P) {
+            need[pid[tid]] = pslot >= 0 ? 1 : 2;
+            if (pslot >= 0) {
+                const int la = sl_lds ? sl[pslot] : slg[pslot];
+                if (la != INT_MAX) {
+                    A.slot_last[pslot] = T;
+                    if (sl_lds) sl[pslot] = T;
+                }
+            }
+        }
+    } else {
+        for (int i = tid; i < P; i += kEnsureThreads) need[pid[i]] = 1;
+    }
     __syncthreads();
     // hits and misses: work-item e = expert e (E <= 1024)
     bool is_miss = false;
-    if (tid < E && need[tid]) {
+    if (small) {
+        is_miss = tid < E && need[tid] == 2;
+    } else if (tid < E && need[tid]) {
         const int s = A.slot_of[A.layer * E + tid];
         if (s >= 0) {
             const int la = sl_lds ? sl[s] : slg[s];
@@ -267,9 +337,8 @@ __global__ void __launch_bounds__(kEnsureThreads) ensure_kernel(EnsureArgs A) {
         A.fill_list[0] = nm;
         if (A.vict) A.vict[0] = nm;
     }
-    // blob pointer of every post-mask pick (read by the GEMV workgroups; the slots of hits and the host copies of
-    // misses stay valid for the whole call, fills are committed at its end)
-    if (A.pair_ptr)
+    // blob pointer of every post-mask pick (calls of more than 64 picks; see the wave-0 block for the others)
+    if (A.pair_ptr && !small)
         for (int i = tid; i < P; i += kEnsureThreads) A.pair_ptr[i] = A.ptrs_all[A.layer * E + pid[i]];
     if (A.log && wv == 0) {                                   // decision record, same layout as the oracle's
         const int idx = A.log[0];

@@ -23,6 +23,7 @@ struct Config {
     int32_t* vict = nullptr;
     int64_t host_stride = 0;
     int64_t slot_stride = 0;                      // bytes between HBM slots (0: the blob size of the call)
+    int fused_ensure = 1;                         // ensure inside the layer kernel when the call fits
     int prefill_min_m = 256;
     int pair_max_m = 4;
     int gu_p = 0, dn_p = 0, mr = 0, debug = 0;
@@ -88,6 +89,11 @@ int exl3_set_slot_stride(int64_t stride) {
     return EXL3_OK;
 }
 
+int exl3_set_fused_ensure(int64_t enable) {
+    g_cfg.fused_ensure = enable != 0;
+    return EXL3_OK;
+}
+
 int exl3_set_host_stride(int64_t stride) {
     if (stride < 0 || stride % 16) return fail(EXL3_EINVAL, "moe_set_host_stride: stride must be a non-negative multiple of 16");
     g_cfg.host_stride = stride;
@@ -143,7 +149,7 @@ static int forward_impl(const void* x, int x_dtype, int64_t x_stride, int M, int
                         int topk, const int64_t* ptrs, int I, int K, int E, void* out, int64_t out_stride, void* ws,
                         size_t ws_bytes, hipStream_t st, const int64_t* fill, int64_t* commit_ptrs, int64_t* commit_fill,
                         const int32_t* fill_list, const int64_t* pair_ptr, const VictimArgs* va = nullptr,
-                        int max_victims = 0) {
+                        int max_victims = 0, const EnsureArgs* fused_ens = nullptr) {
     if (!fill && use_prefill(M)) {
         if (H % 256) return fail(EXL3_EUNSUPPORTED, "moe prefill: H %% 256 == 0 required (H=%d)", H);
         if ((int64_t)M * topk > (1 << 28)) return fail(EXL3_EUNSUPPORTED, "moe prefill: %d x %d pairs", M, topk);
@@ -201,6 +207,10 @@ static int forward_impl(const void* x, int x_dtype, int64_t x_stride, int M, int
         a.va = *va;
         a.vict_chunks = (int)((a.g.blob + va->chunk_bytes - 1) / va->chunk_bytes);
         a.n_vict_wg = max_victims * a.vict_chunks;
+    }
+    if (fused_ens) {                              // the ensure runs as workgroup 0 of the layer kernel
+        a.fused = 1;
+        a.ens = *fused_ens;
     }
     hipError_t e = launch_moe_layer(K, a, st);
     if (e != hipSuccess) return hip_fail(e, "moe layer launch");
@@ -273,9 +283,15 @@ int exl3_moe_forward_cached(const void* x, int x_dtype, int64_t x_stride, int M,
     const size_t need = decode_workspace_bytes(P, H, I);
     if (!workspace || workspace_bytes < need)
         return fail(EXL3_EWORKSPACE, "moe_forward_cached: workspace %zu < %zu bytes", workspace_bytes, need);
-    ea.pair_ptr = pair_ptr_area(workspace, P, H, I);
-    hipError_t e = launch_ensure(ea, st);
-    if (e != hipSuccess) return hip_fail(e, "ensure launch");
+    // the ensure inside the layer kernel needs one thread per expert, one lane per pick and the slot stamps in
+    // registers; K = 4 kernels run one workgroup per CU, too few to let the victim workgroups wait for it
+    const bool fused = g_cfg.fused_ensure && E <= kEnsMaxE && P <= kEnsMaxP && n_slots <= kEnsMaxE * kEnsRegSlots &&
+                       K <= 3;
+    if (!fused) {
+        ea.pair_ptr = pair_ptr_area(workspace, P, H, I);
+        hipError_t e = launch_ensure(ea, st);
+        if (e != hipSuccess) return hip_fail(e, "ensure launch");
+    }
     VictimArgs va{};
     int mv = 0;
     if (g_cfg.vict) {
@@ -286,13 +302,13 @@ int exl3_moe_forward_cached(const void* x, int x_dtype, int64_t x_stride, int M,
         va.hstride = ea.hstride;
         va.E = E;
         va.ram_res = g_cfg.ram_res;
-        va.chunk_bytes = 64 * 1024;
+        va.chunk_bytes = kVictimChunkBytes;
         mv = std::min(std::min(ea.max_fill, E), P);
     }
     int64_t* pl = ptrs_all + (int64_t)layer * E;
     int64_t* fl = fill_all + (int64_t)layer * E;
     return forward_impl(x, x_dtype, x_stride, M, H, topk_ids, topk_w, topk, pl, I, K, E, out, out_stride, workspace,
-                        workspace_bytes, st, fl, pl, fl, fill_list, ea.pair_ptr, &va, mv);
+                        workspace_bytes, st, fl, pl, fl, fill_list, ea.pair_ptr, &va, mv, fused ? &ea : nullptr);
 }
 
 size_t exl3_moe_align_workspace(int M, int topk, int n_experts) {

@@ -20,6 +20,7 @@
 // The codebook affine w = c1*h + c2 is applied to the dot product: sum_k w_k x_k = c1 sum_k h_k x_k + c2 sum_k x_k,
 // with h the exact fp16 1024 + bytesum, so the inner loop is bfe, mul, sad and one mixed-precision FMA per weight.
 #include "exl3_common.cuh"
+#include "exl3_ensure.cuh"
 #include "exl3_geom.h"
 #include "exl3_kernels.h"
 
@@ -29,7 +30,7 @@ __device__ int g_cnt_gu[kMaxPairs * 64];
 __device__ int g_cnt_d[kMaxPairs * 64];
 __device__ int g_cnt_c[kMaxRows * 64];
 __device__ int g_ready[kMaxPairs];
-__device__ int g_cnt_all[4];
+__device__ int g_cnt_all[4];          // [0] combines done, [1] victim reads done, [2] fused ensure done
 __device__ int g_status[4];          // [0]: spin timeouts (should stay 0)
 
 constexpr int kSpinMax = 1 << 22;
@@ -141,6 +142,7 @@ struct LayerShared {
     float red[kWaves][128];  // per-wave column sums
     float tot[256];          // reduced split-K partials of the last-arriving gate/up WG
     half2_t xd[kMaxI / 2];   // down WG: the pair's abuf
+    int64_t fdst;            // write-through target of the pair (0: none)
     int last;
 };
 
@@ -157,32 +159,81 @@ __device__ __forceinline__ void wait_count(const int* c, int target) {
 }
 
 // victim write-back (VictimCopyKernel, a8:1168-1189): workgroup (victim i, 64 KiB chunk c) copies its chunk of the
-// victim's slot to the old owner's RAM-tier address and flags the owner RAM-resident; every victim workgroup then
-// counts itself done (g_cnt_all[1]), so the write-through of a miss into a reassigned slot starts after the old bytes
-// were read
+// victim's slot to the old owner's RAM-tier address and flags the owner RAM-resident. The chunk is read into registers
+// first; once every load has returned the workgroup counts itself (g_cnt_all[1]), so the write-through of a miss into
+// the reassigned slot can start while the copy's stores to host memory are still in flight. With the ensure inside
+// the launch, the victim list is read after the ensure workgroup raised its flag.
+constexpr int kVictChunk = kVictimChunkBytes;
+constexpr int kVictPer = kVictChunk / 16 / kThreads;    // 16-byte words per thread
 __device__ __forceinline__ void victim_wg(const DecodeArgs& A, int blk) {
     const VictimArgs& V = A.va;
     const int i = blk / A.vict_chunks, c = blk % A.vict_chunks;
-    if (i < V.vict[0]) {
-        const int old = V.vict[1 + 2 * i], s = V.vict[2 + 2 * i];
+    if (A.fused) {
+        if (threadIdx.x == 0) wait_count(&g_cnt_all[2], 1);
+        __syncthreads();
+    }
+    const int nv = A.fused ? ld_agent_i32(V.vict) : V.vict[0];
+    const uint4* src = nullptr;
+    uint4* dst = nullptr;
+    int64_t q0 = 0, q1 = 0;
+    if (i < nv) {
+        const int old = A.fused ? ld_agent_i32(V.vict + 1 + 2 * i) : V.vict[1 + 2 * i];
+        const int s = A.fused ? ld_agent_i32(V.vict + 2 + 2 * i) : V.vict[2 + 2 * i];
         if (old >= 0) {
             if (V.ram_res && c == 0 && threadIdx.x == 0) V.ram_res[old] = 1;
-            const uint4* src = (const uint4*)(V.slot_base + (int64_t)s * V.blob);
-            uint4* dst = (uint4*)(V.host_base[old / V.E] + (int64_t)(old % V.E) * V.hstride);
-            const int64_t n16 = V.blob >> 4, per = V.chunk_bytes >> 4;
-            const int64_t b0 = (int64_t)c * per, b1 = min(n16, b0 + per);
-            for (int64_t q = b0 + threadIdx.x; q < b1; q += kThreads) dst[q] = src[q];
+            src = (const uint4*)(V.slot_base + (int64_t)s * V.blob);
+            dst = (uint4*)(V.host_base[old / V.E] + (int64_t)(old % V.E) * V.hstride);
+            q0 = (int64_t)c * (kVictChunk >> 4);
+            q1 = min(V.blob >> 4, q0 + (kVictChunk >> 4));
         }
     }
-    wait_stores();
+    uint4 v[kVictPer];
+#pragma unroll
+    for (int k = 0; k < kVictPer; ++k) {
+        const int64_t q = q0 + threadIdx.x + (int64_t)k * kThreads;
+        v[k] = q < q1 ? src[q] : uint4{0u, 0u, 0u, 0u};
+    }
+    wait_stores();                               // vmcnt(0): every load of the old bytes has returned
     __syncthreads();
     if (threadIdx.x == 0) counter_add(&g_cnt_all[1], 1);
+#pragma unroll
+    for (int k = 0; k < kVictPer; ++k) {
+        const int64_t q = q0 + threadIdx.x + (int64_t)k * kThreads;
+        if (q < q1) dst[q] = v[k];
+    }
 }
 
 // pointer of the blob of pair a: precomputed by the cache's ensure (pair_ptr) or looked up through ids/ptrs
 __device__ __forceinline__ const uint8_t* pair_base(const DecodeArgs& A, int a, int& e) {
     e = min(max(A.ids[a], 0), A.E - 1);          // out-of-range ids are clamped, never dereferenced
     return A.pair_ptr ? (const uint8_t*)A.pair_ptr[a] : (const uint8_t*)A.ptrs[e];
+}
+
+// the same with the ensure running inside the launch: the pair applies the tier mask itself (expert in neither HBM
+// nor RAM -> the layer's safe expert, weight 0). Neither input changes during the call for a masked key (the ensure
+// never gives it a slot; write-back victims are slot owners, never picks), and a key the ensure turns from miss into
+// fill keeps ram_res = 1, so the pair and the ensure agree. ptrs[e] of every pick stays as it was at the start until
+// the last workgroup commits the fills, so a pointer outside the slot arena marks a miss (a host copy).
+__device__ __forceinline__ const uint8_t* pair_lookup(const DecodeArgs& A, int a, int& e, bool& miss, bool& masked) {
+    const EnsureArgs& Q = A.ens;
+    int id = min(max(A.ids[a], 0), A.E - 1);
+    const int kb = Q.layer * A.E;
+    int64_t p = A.ptrs[id];
+    masked = false;
+    if (Q.ram_res) {
+        const int safe = Q.safe[Q.layer];
+        const int64_t ps = A.ptrs[safe];
+        const uint8_t rr = Q.ram_res[kb + id];
+        const int so = Q.slot_of[kb + id];
+        masked = !rr && so < 0;
+        if (masked) {
+            id = safe;
+            p = ps;
+        }
+    }
+    e = id;
+    miss = p < Q.slot_base || p >= Q.slot_base + (int64_t)Q.S * Q.blob;
+    return (const uint8_t*)p;
 }
 
 // gate/up WG per (pair, 128-column block of I, 256-row slice of H): waves (proj = w & 1, quarter = w >> 1) each cover
@@ -197,9 +248,10 @@ __device__ __forceinline__ void gateup_wg(const DecodeArgs& A, int blk, LayerSha
     const int nb = blk % nbn, a = blk / nbn;
     const int tid = threadIdx.x, wv = tid >> 6, l = tid & 63;
     int e;
-    const uint8_t* base = pair_base(A, a, e);
+    bool miss = false, masked = false;
+    const uint8_t* base = A.fused ? pair_lookup(A, a, e, miss, masked) : pair_base(A, a, e);
     const int m = a / A.topk;
-    uint8_t* dst = A.fill ? (uint8_t*)A.fill[e] : nullptr;
+    uint8_t* dst = !A.fused && A.fill ? (uint8_t*)A.fill[e] : nullptr;
     const int proj = wv & 1, qt = wv >> 1;
     const int tiles_n = 2 * I / 16, r0 = ks * 16 + qt * 4, ct0 = proj * (I / 16) + nb * 8;
 
@@ -229,11 +281,20 @@ __device__ __forceinline__ void gateup_wg(const DecodeArgs& A, int blk, LayerSha
         const float s = wave_sum((float)h0 + (float)h1);
         if (l == 0) S.ssum[pj][hb] = s;
     }
-    if (dst) {                                   // write-through of a cache miss into its HBM slot
-        if (A.n_vict_wg) {                       // after the victim write-back read the slot's old bytes
-            if (tid == 0) wait_count(&g_cnt_all[1], A.n_vict_wg);
-            __syncthreads();
+    if (A.fused ? miss : dst != nullptr) {       // write-through of a cache miss into its HBM slot
+        if (tid == 0) {
+            int64_t f = (int64_t)dst;
+            if (A.fused) {                       // the target is the ensure's decision
+                wait_count(&g_cnt_all[2], 1);
+                f = ld_agent_i64(A.fill + e);
+            }
+            if (f && A.n_vict_wg) wait_count(&g_cnt_all[1], A.n_vict_wg);   // after the victims' old bytes were read
+            S.fdst = f;
         }
+        __syncthreads();
+        dst = (uint8_t*)S.fdst;
+    }
+    if (dst) {
         if (live) g.write_through((uint32_t*)dst, tiles_n, r0, ct0);
         if (nb == 0 && ks == 0) {
             const uint32_t* sv = (const uint32_t*)(base + A.g.off_suh_g);
@@ -305,12 +366,11 @@ __device__ __forceinline__ void down_wg(const DecodeArgs& A, int blk, LayerShare
     const int nb = blk % nbn, a = blk / nbn;
     const int tid = threadIdx.x, wv = tid >> 6, l = tid & 63;
     int e;
-    const uint8_t* base = pair_base(A, a, e);
+    bool miss = false, masked = false;
+    const uint8_t* base = A.fused ? pair_lookup(A, a, e, miss, masked) : pair_base(A, a, e);
     const int m = a / A.topk;
-    uint8_t* dst = A.fill ? (uint8_t*)A.fill[e] : nullptr;
     const int tiles_n = H / 16, ct0 = nb * 8;
     const uint32_t* tr = (const uint32_t*)(base + A.g.gu_bytes);
-    uint32_t* trd = dst ? (uint32_t*)(dst + A.g.gu_bytes) : nullptr;
     const int nch = (kt / 4 + kWaves - 1 - wv) / kWaves;      // 4-row chunks of this wave: q = wv + kWaves * c
     {   // the down weights are needed only after the gate/up phase: let the gate/up loads (the critical path) take
         // HBM first, then issue these (constant 100 MHz clock)
@@ -324,10 +384,16 @@ __device__ __forceinline__ void down_wg(const DecodeArgs& A, int blk, LayerShare
     float wgt = 0.f;
     if (wv == 0) {
         sc_d = *(const half2_t*)((const half_t*)(base + A.g.off_svh_d) + nb * 128 + 2 * l);
-        wgt = A.w[a];
+        wgt = masked ? 0.f : A.w[a];
     }
     if (tid == 0) {                              // wait for the pair's whole abuf (all I/128 gate/up epilogues)
-        if (trd && A.n_vict_wg) wait_count(&g_cnt_all[1], A.n_vict_wg);   // and for the victim write-back
+        int64_t f = !A.fused && A.fill ? A.fill[e] : 0;
+        if (A.fused && miss) {                   // the write-through target is the ensure's decision
+            wait_count(&g_cnt_all[2], 1);
+            f = ld_agent_i64(A.fill + e);
+        }
+        if (f && A.n_vict_wg) wait_count(&g_cnt_all[1], A.n_vict_wg);      // and for the victims' old bytes
+        S.fdst = f;
         int it = 0;
         while (__hip_atomic_load(&g_ready[a], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < I / 128) {
             __builtin_amdgcn_s_sleep(1);
@@ -338,6 +404,7 @@ __device__ __forceinline__ void down_wg(const DecodeArgs& A, int blk, LayerShare
         }
     }
     __syncthreads();
+    uint32_t* trd = S.fdst ? (uint32_t*)((uint8_t*)S.fdst + A.g.gu_bytes) : nullptr;
     half2_t* xs = S.xd;                          // abuf of the pair, [I/2] half2
     for (int i = tid; i < I / 2; i += kThreads)
         xs[i] = __builtin_bit_cast(half2_t, __hip_atomic_load((const uint32_t*)(A.abuf + (size_t)a * I) + i,
@@ -424,8 +491,32 @@ __device__ __forceinline__ void down_wg(const DecodeArgs& A, int blk, LayerShare
             wait_count(&g_cnt_all[1], A.n_vict_wg);
             counter_reset(&g_cnt_all[1]);
         }
+        if (A.fused) wait_count(&g_cnt_all[2], 1);
     }
     for (int i = l; i < A.npairs; i += 64) counter_reset(&g_ready[i]);
+    if (A.fused) {
+        // the ensure's in-place rewrite of the caller's picks (masked -> safe expert, weight 0), deferred to here
+        // because every pair read them during the call; the mask rule gives the same answer now (see pair_lookup)
+        const EnsureArgs& Q = A.ens;
+        if (Q.ram_res) {
+            const int kb = Q.layer * A.E, safe = Q.safe[Q.layer];
+            for (int i = l; i < A.npairs; i += 64) {
+                const int id = min(max(Q.ids[i], 0), A.E - 1);
+                if (!Q.ram_res[kb + id] && Q.slot_of[kb + id] < 0) {
+                    Q.ids[i] = safe;
+                    Q.w[i] = 0.f;
+                }
+            }
+        }
+        const int nf = A.commit_ptrs ? ld_agent_i32(A.fill_list) : 0;
+        for (int i = l; i < nf; i += 64) {
+            const int ef = ld_agent_i32(A.fill_list + 1 + i);
+            A.commit_ptrs[ef] = ld_agent_i64(A.commit_fill + ef);
+            A.commit_fill[ef] = 0;
+        }
+        if (l == 0) counter_reset(&g_cnt_all[2]);
+        return;
+    }
     if (!A.commit_ptrs) return;
     const int nf = A.fill_list[0];
     for (int i = l; i < nf; i += 64) {
@@ -437,10 +528,19 @@ __device__ __forceinline__ void down_wg(const DecodeArgs& A, int blk, LayerShare
 
 template <int K>
 __global__ void __launch_bounds__(kThreads) moe_layer_kernel(DecodeArgs A) {
-    __shared__ LayerShared S;
+    __shared__ __align__(16) uint8_t lds[sizeof(LayerShared) > sizeof(EnsureShared) ? sizeof(LayerShared)
+                                                                                     : sizeof(EnsureShared)];
+    LayerShared& S = *reinterpret_cast<LayerShared*>(lds);
     const int nv = A.n_vict_wg;
     const int n_gu = A.npairs * (A.g.I / 128) * gu_slices(A.g.H);
-    const int b = blockIdx.x;
+    int b = blockIdx.x;
+    if (A.fused) {                               // workgroup 0: the cache's ensure (never waits on another workgroup)
+        if (b == 0) {
+            ensure_wg<kThreads>(A.ens, *reinterpret_cast<EnsureShared*>(lds), &g_cnt_all[2]);
+            return;
+        }
+        --b;
+    }
     if (b < nv) victim_wg(A, b);
     else if (b < nv + n_gu) gateup_wg<K>(A, b - nv, S);
     else down_wg<K>(A, b - nv - n_gu, S);
@@ -476,7 +576,7 @@ __global__ void __launch_bounds__(256) dequant_kernel(const uint32_t* __restrict
 hipError_t launch_moe_layer(int K, const DecodeArgs& a, hipStream_t s) {
     const int n_gu = a.npairs * (a.g.I / 128) * gu_slices(a.g.H);
     const int n_dn = a.npairs * (a.g.H / 128);
-    dim3 grid((unsigned)(a.n_vict_wg + n_gu + n_dn));
+    dim3 grid((unsigned)(a.fused + a.n_vict_wg + n_gu + n_dn));
     if (K == 2) hipLaunchKernelGGL(moe_layer_kernel<2>, grid, dim3(kThreads), 0, s, a);
     else if (K == 3) hipLaunchKernelGGL(moe_layer_kernel<3>, grid, dim3(kThreads), 0, s, a);
     else if (K == 4) hipLaunchKernelGGL(moe_layer_kernel<4>, grid, dim3(kThreads), 0, s, a);

@@ -128,6 +128,7 @@ void moe_set_tier(at::Tensor ram_res, at::Tensor miss, at::Tensor safe) {
 }
 void moe_set_host_stride(int64_t s) { check(exl3_set_host_stride(s), "moe_set_host_stride"); }
 void moe_set_slot_stride(int64_t s) { check(exl3_set_slot_stride(s), "moe_set_slot_stride"); }
+void moe_set_fused_ensure(int64_t v) { check(exl3_set_fused_ensure(v), "moe_set_fused_ensure"); }
 // pinned host memory is device-mapped on MI355X: nothing to prefetch (the reference maps xe-SVM pages, a8:777-781)
 void moe_svm_prefetch(at::Tensor ptrs, int64_t nbytes, at::Tensor like) {
     (void)ptrs;
@@ -173,6 +174,7 @@ TORCH_LIBRARY(exl3xpu_moe, m) {
     m.def("moe_set_tier(Tensor ram_res, Tensor miss, Tensor safe) -> ()", &moe_set_tier);
     m.def("moe_set_host_stride(int s) -> ()", &moe_set_host_stride);
     m.def("moe_set_slot_stride(int s) -> ()", &moe_set_slot_stride);
+    m.def("moe_set_fused_ensure(int v) -> ()", &moe_set_fused_ensure);
     m.def("moe_svm_prefetch(Tensor ptrs, int nbytes, Tensor like) -> ()", &moe_svm_prefetch);
     m.def("moe_set_decision_log(Tensor buf) -> ()", &moe_set_decision_log);
     m.def("dequant(Tensor trellis, int k_tiles, int n_tiles, int K) -> Tensor");

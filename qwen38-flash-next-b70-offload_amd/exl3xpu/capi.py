@@ -24,6 +24,7 @@ SIGNATURES = {
     "exl3_set_victims": (c_i32, [c_p]),
     "exl3_set_host_stride": (c_i32, [c_i64]),
     "exl3_set_slot_stride": (c_i32, [c_i64]),
+    "exl3_set_fused_ensure": (c_i32, [c_i64]),
     "exl3_set_prefill_min_m": (c_i32, [c_i64]),
     "exl3_set_pair_max_m": (c_i32, [c_i64]),
     "exl3_set_splits": (c_i32, [c_i64, c_i64]),

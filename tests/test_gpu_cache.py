@@ -60,14 +60,20 @@ def _run(store, tier, ids, w, H, check_out_every=0, ref_ptr=None):
     return lg[1:].reshape(steps, L, rl), bad
 
 
-def test_cache_golden_small():
+@pytest.mark.parametrize("fused", [1, 0])
+def test_cache_golden_small(fused):
+    """fused 1: the ensure runs inside the layer kernel; 0: as its own launch before it."""
     g = np.load(os.path.join(GOLD, "cache_small.npz"))
     L, E, S, P = int(g["L"]), int(g["E"]), int(g["S"]), int(g["P"])
-    print(f"case cache golden L={L} E={E} S={S}", flush=True)
+    print(f"case cache golden L={L} E={E} S={S} fused={fused}", flush=True)
     H = I = 128
     store, tier, blobs, ref_ptr = _setup(L, E, S, H, I, 3, int(g["budget"]), int(g["qmax"]), int(g["age"]),
                                          int(g["latency"]), int(g["ring_cap"]), 3)
-    recs, bad = _run(store, tier, g["ids"], g["w"], H, check_out_every=1, ref_ptr=ref_ptr)
+    store.X.moe_set_fused_ensure(fused)
+    try:
+        recs, bad = _run(store, tier, g["ids"], g["w"], H, check_out_every=1, ref_ptr=ref_ptr)
+    finally:
+        store.X.moe_set_fused_ensure(1)
     assert np.array_equal(recs, g["recs"])
     flat, pos = g["host_log"], 0
     for n, (adm, ev) in enumerate(tier.decisions):
@@ -156,3 +162,72 @@ def test_cache_mixed_bitrates(H, I, steps):
 def _blob(H, I, K):
     from exl3xpu.moe_offload import ops
     return ops().blob_bytes(H, I, K)
+
+
+@pytest.mark.parametrize("M,topk,fused", [(1, 8, 1), (1, 8, 0), (10, 8, 1)])
+def test_cache_pinned_slots(M, topk, fused):
+    """Slots pinned mid-trace (slot_last = INT_MAX, the reference's never-evict stamp) keep their stamp through hits
+    and are never chosen as victims. 1 x top-8 runs the no-miss fast path and the full path; 10 x top-8 (80 picks)
+    runs the full path only (as its own launch: more than 64 picks). fused 0 launches the ensure before the layer
+    kernel. Every decision and the final slot_last table equal the oracle's."""
+    import ctypes
+    from exl3xpu import nvtier
+    L, E, H, I, K, nd, steps, n0 = 2, 128, 128, 128, 3, 4, 60, 20
+    P = M * topk
+    print(f"case cache pinned slots M={M} top-{topk} fused={fused}", flush=True)
+    S = 100
+    store = nvtier.TierStore(H, I, K, E, S, n_layers=L)
+    keys = [f"model.layers.{li}.mlp" for li in range(L)]
+    for k in keys:
+        store.add_layer(k)
+    src = nvtier.SyntheticExpertSource(H, I, K, 77, n_distinct=nd)
+    for key in range(L * E):
+        ctypes.memmove(store.addr(key), src.buf[key % nd].ctypes.data, src.blob)
+    rng = np.random.default_rng(78)
+    # skewed routing so that hits (fast-path calls) and misses both occur
+    pr = 1.0 / np.arange(1, E + 1) ** 1.5
+    pr /= pr.sum()
+    ids = np.stack([[np.stack([rng.choice(E, topk, replace=False, p=pr) for _ in range(M)]).reshape(-1)
+                     for _ in range(L)] for _ in range(steps)]).astype(np.int32)
+    w = rng.random(ids.shape, dtype=np.float32)
+    co = cache.CacheOracle(L, E, S, tier=False)
+    X = store.X
+    rl = cache.rec_len(P)
+    logbuf = torch.zeros(1 + steps * L * rl, dtype=torch.int32, device="cuda")
+    X.moe_set_decision_log(logbuf)
+    X.moe_set_fused_ensure(fused)
+    x = torch.randn(M, H, generator=torch.Generator().manual_seed(2)).to(torch.bfloat16).cuda()
+    orecs = []
+    try:
+        for n in range(steps):
+            if n == n0:
+                torch.cuda.synchronize()
+                held = np.nonzero(store.slot_key.cpu().numpy() >= 0)[0]
+                assert held.size > 3 and np.array_equal(store.slot_last.cpu().numpy(), co.slot_last)
+                pin = held[::3]
+                store.slot_last[torch.from_numpy(pin).cuda()] = 0x7FFFFFFF
+                co.slot_last[pin] = 0x7FFFFFFF
+            for li in range(L):
+                orecs.append(co.ensure(li, ids[n, li].copy(), w[n, li].copy()))
+                it = torch.from_numpy(ids[n, li]).view(M, topk).cuda()
+                wt = torch.from_numpy(w[n, li]).view(M, topk).cuda()
+                store.forward_cached(keys[li], x, it, wt)
+        torch.cuda.synchronize()
+    finally:
+        X.moe_set_decision_log(torch.zeros(0, dtype=torch.int32, device="cuda"))
+        X.moe_set_fused_ensure(1)
+    lg = logbuf.cpu().numpy()
+    assert lg[0] == steps * L
+    recs = lg[1:].reshape(steps * L, rl)
+    orecs = np.stack(orecs)
+    mism = np.nonzero((recs != orecs).any(axis=-1))[0]
+    assert mism.size == 0, f"first mismatch at call {mism[0]}"
+    sl = store.slot_last.cpu().numpy()
+    assert np.array_equal(sl, co.slot_last)
+    assert (sl[pin] == 0x7FFFFFFF).all()
+    pinned_keys = store.slot_key.cpu().numpy()[pin]
+    assert (pinned_keys >= 0).all()
+    nm = recs[:, 2 + P]
+    assert nm[n0 * L:].sum() > 0
+    if P <= 64:
+        assert (nm[n0 * L:] == 0).any()                    # no-miss (fast-path) calls after pinning too
