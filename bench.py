@@ -221,8 +221,9 @@ def main():
     torch.cuda.synchronize()
     el = time.perf_counter() - t1
     tok_s = steps * bs / el if steps else 0.0
-    d = {k: tier.stats.get(k, 0) - st0.get(k, 0) for k in ("masked", "evicts", "nvme_reads", "admit_dropped")}
+    d = {k: tier.stats.get(k, 0) - st0.get(k, 0) for k in ("masked", "evicts", "nvme_reads", "admit_dropped", "wait_ms")}
     host_ms = {k: round(v / max(steps, 1) * 1e3, 4) for k, v in host_s.items()}
+    host_ms["tier_wait"] = round(d.pop("wait_ms") / max(steps, 1), 4)     # of tier_step: waiting for the GPU
     sd = max(steps, 1)
     log(f"decode ({'eager' if graph is None else 'graph'}) {steps} steps in {el:.3f} s: {tok_s:.1f} tok/s; per step masked {d['masked'] / sd:.1f} "
         f"fills {d['nvme_reads'] / sd:.2f} evicts {d['evicts'] / sd:.2f}; host ms per step {host_ms}")

@@ -485,7 +485,9 @@ class NvTierAsync(NvTierFast):
             if self.log_decisions:
                 self.decisions.append((np.zeros(0, np.int64), np.zeros(0, np.int64)))
             return 0
+        tw = time.perf_counter()
         self._snap_ev[j].synchronize()
+        self.stats["wait_ms"] = self.stats.get("wait_ms", 0.0) + (time.perf_counter() - tw) * 1e3
         view = self._view
         np.copyto(view, self._np_res[j])
         if self._last_diff is not None:
