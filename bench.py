@@ -4,9 +4,9 @@ Workload (one "step" = one decode token through 48 MoE layers): 512 experts per 
 top-10 routing, EXL3 K=3 (3 bpw) weights, bs=1; 8,000 HBM expert slots managed on the device (exact LRU, write-through
 of misses), a pinned-host RAM tier with a 1,075-record budget (2 GB of 1.86 MB records) and admission control (AGE 4,
 QMAX 256, 8-step fill latency), picks in neither tier masked to weight 0; routing follows a seeded Zipf(1.1) trace.
-Each timed step copies the step's routing into the static input buffers of a HIP graph holding the 48 cached MoE
-calls, replays it and runs the host tier step (the way a serving engine replays decode; --eager launches the calls one
-by one instead); `value` is tokens per second over the timed steps.
+Each timed step replays a HIP graph whose first kernels take the step's routing from a device-resident trace into the
+static inputs of the 48 cached MoE calls that follow, then runs the host tier step (the way a serving engine replays
+decode; --eager launches the kernels one by one instead); `value` is tokens per second over the timed steps.
 
 roofline: the fused dequant-GEMV layer kernel (moe_layer_kernel, one moe_forward call per layer) on HBM-resident experts,
 R x 48 calls captured in one HIP graph and timed with HIP events around its replay on the launch stream: algorithmic
@@ -176,8 +176,14 @@ def main():
 
     ids_s = torch.empty(L, bs, TOPK, dtype=torch.int32, device=dev)     # static graph inputs
     w_s = torch.empty(L, bs, TOPK, dtype=torch.float32, device=dev)
+    step_t = torch.zeros(1, dtype=torch.int64, device=dev)              # index of the step's routing in the trace
 
     def layers():
+        # the router's output of this step, taken from the device-resident trace by the step's first kernels (a model
+        # computes it on the device inside the step too)
+        torch.index_select(ids_all, 0, step_t, out=ids_s.view(1, L, bs, TOPK))
+        torch.index_select(w_all, 0, step_t, out=w_s.view(1, L, bs, TOPK))
+        step_t.add_(1)
         return [store.forward_cached(keys[li], xs[li], ids_s[li], w_s[li]) for li in range(L)]
 
     graph = None
@@ -185,8 +191,6 @@ def main():
 
     def decode_step(n):
         t = time.perf_counter()
-        ids_s.copy_(ids_all[n])
-        w_s.copy_(w_all[n])
         if graph is None:
             layers()
         else:

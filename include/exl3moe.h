@@ -113,6 +113,16 @@ int exl3_moe_align(const int32_t* topk_ids, const float* topk_w, int M, int topk
  * [0, n_flags) are skipped. */
 int exl3_scatter_flags(uint8_t* flags, int64_t n_flags, const int32_t* packed, int64_t n, void* stream);
 
+/* The device side of one host tier step as one launch (replaces the snapshot .to("cpu") copies and the flag
+ * index_copy_ of plugin/exl3xpu/nvtier.py:282-386 and 791-793): applies the diff as exl3_scatter_flags; mirrors the
+ * miss ring (int32 [1 + ring_cap], [0] = count) into ring_mirror (same layout, device-mapped pinned): the entries at
+ * positions [ring_from, count) (the last ring_cap of them at most) and the count; then copies src[k] -> dst[k]
+ * (nbytes[k] bytes, k < n_copies <= 4; dst device-mapped pinned host memory, both 16-byte aligned). ring may be NULL.
+ * A flag the diff sets may be snapshotted before or after its update. */
+int exl3_tier_exchange(uint8_t* flags, int64_t n_flags, const int32_t* packed, int64_t n_diff, const int32_t* ring,
+                       int64_t ring_cap, int64_t ring_from, int32_t* ring_mirror, const void* const* src,
+                       void* const* dst, const int64_t* nbytes, int n_copies, void* stream);
+
 /* Device health flags (no reference counterpart): flags4[0] = bounded waits of the fused decode kernel that timed
  * out since load (0 in a healthy run; a timeout means an output was computed from an incomplete intermediate).
  * Synchronises `stream`. */

@@ -84,6 +84,11 @@ hipError_t launch_dequant(int K, const uint32_t* tr, _Float16* out, int k_tiles,
 // cache.hip
 hipError_t launch_ensure(const EnsureArgs& a, hipStream_t s);
 hipError_t launch_scatter_flags(uint8_t* flags, int64_t n_flags, const int32_t* packed, int64_t n, hipStream_t s);
+struct TierCopy { const uint8_t* src; uint8_t* dst; int64_t n; };   // n bytes, device -> pinned host
+struct TierCopies { TierCopy c[4]; int n; };
+struct TierRing { const int32_t* ring; int64_t cap, from; int32_t* mirror; };  // ring null: no mirroring
+hipError_t launch_tier_exchange(uint8_t* flags, int64_t n_flags, const int32_t* packed, int64_t n_diff,
+                                const TierRing& rg, const TierCopies& cp, hipStream_t s);
 // prefill.hip
 hipError_t launch_align(const int32_t* ids, const float* w, int npairs, int topk, int E, int pad, int* chunk_scratch,
                         const AlignOut& o, hipStream_t s);

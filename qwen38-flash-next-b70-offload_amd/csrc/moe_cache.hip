@@ -18,6 +18,7 @@
 //
 // The victim write-back (reference VictimCopyKernel a8:1168-1189) runs as the first workgroups of the layer kernel
 // (moe_decode.hip).
+#include <algorithm>
 #include <climits>
 
 #include "exl3_common.cuh"
@@ -388,6 +389,50 @@ __global__ void scatter_flags_kernel(uint8_t* flags, int64_t n_flags, const int3
 hipError_t launch_scatter_flags(uint8_t* flags, int64_t n_flags, const int32_t* packed, int64_t n, hipStream_t s) {
     if (n <= 0) return hipSuccess;
     hipLaunchKernelGGL(scatter_flags_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, flags, n_flags, packed, n);
+    return hipGetLastError();
+}
+
+// The whole device side of one host tier step in one launch: the flag diff of the step (as scatter_flags_kernel), the
+// miss-ring entries appended since position `from` (the count the host last read) into a pinned mirror of the ring,
+// with the count itself, and the snapshot copies of the device state into device-mapped pinned host buffers (16-byte
+// words, then the tail bytes). A flag being set by the diff may be copied before or after its update; the host
+// overlays the diff on the snapshot, so either is fine. More than ring_cap entries since `from` keeps the last
+// ring_cap, as the ring itself does.
+__device__ __forceinline__ void copy_part(const TierCopy& c, int64_t t, int64_t nt) {
+    const int64_t n16 = c.n >> 4;
+    const uint4* s16 = (const uint4*)c.src;
+    uint4* d16 = (uint4*)c.dst;
+    for (int64_t i = t; i < n16; i += nt) d16[i] = s16[i];
+    for (int64_t i = (n16 << 4) + t; i < c.n; i += nt) c.dst[i] = c.src[i];
+}
+
+__global__ void __launch_bounds__(256) tier_exchange_kernel(uint8_t* flags, int64_t n_flags, const int32_t* packed,
+                                                            int64_t n_diff, TierRing rg, TierCopies cp) {
+    const int64_t nt = (int64_t)gridDim.x * blockDim.x;
+    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    for (int64_t i = t; i < n_diff; i += nt) {
+        const int32_t p = packed[i];
+        const int64_t key = p >> 1;
+        if (p >= 0 && key < n_flags) flags[key] = (uint8_t)(p & 1);
+    }
+    if (rg.ring) {
+        const int64_t cnt = rg.ring[0];
+        for (int64_t p = max(rg.from, cnt - rg.cap) + t; p < cnt; p += nt) {
+            const int64_t q = 1 + p % rg.cap;
+            rg.mirror[q] = rg.ring[q];
+        }
+        if (t == 0) rg.mirror[0] = (int32_t)cnt;
+    }
+    for (int k = 0; k < cp.n; ++k) copy_part(cp.c[k], t, nt);
+}
+
+hipError_t launch_tier_exchange(uint8_t* flags, int64_t n_flags, const int32_t* packed, int64_t n_diff,
+                                const TierRing& rg, const TierCopies& cp, hipStream_t s) {
+    int64_t work = std::max<int64_t>(n_diff, rg.ring ? 256 : 0);
+    for (int k = 0; k < cp.n; ++k) work = std::max(work, cp.c[k].n >> 4);
+    if (work <= 0) return hipSuccess;
+    const unsigned blocks = (unsigned)std::min<int64_t>(128, (work + 255) / 256);
+    hipLaunchKernelGGL(tier_exchange_kernel, dim3(blocks), dim3(256), 0, s, flags, n_flags, packed, n_diff, rg, cp);
     return hipGetLastError();
 }
 

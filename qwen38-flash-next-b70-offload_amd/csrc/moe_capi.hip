@@ -348,6 +348,27 @@ int exl3_scatter_flags(uint8_t* flags, int64_t n_flags, const int32_t* packed, i
     return e == hipSuccess ? EXL3_OK : hip_fail(e, "scatter_flags");
 }
 
+int exl3_tier_exchange(uint8_t* flags, int64_t n_flags, const int32_t* packed, int64_t n_diff, const int32_t* ring,
+                       int64_t ring_cap, int64_t ring_from, int32_t* ring_mirror, const void* const* src,
+                       void* const* dst, const int64_t* nbytes, int n_copies, void* stream) {
+    if (n_diff < 0 || n_flags < 0 || n_diff > (int64_t)1 << 31 || n_copies < 0 || n_copies > 4)
+        return fail(EXL3_EINVAL, "tier_exchange: n_diff=%lld n_copies=%d", (long long)n_diff, n_copies);
+    if (n_diff && (!flags || !packed)) return fail(EXL3_EINVAL, "tier_exchange: null flags / diff");
+    if (ring && (!ring_mirror || ring_cap <= 0 || ring_from < 0))
+        return fail(EXL3_EINVAL, "tier_exchange: ring cap=%lld from=%lld", (long long)ring_cap, (long long)ring_from);
+    const TierRing rg{ring, ring_cap, ring_from, ring_mirror};
+    TierCopies cp{};
+    for (int k = 0; k < n_copies; ++k) {
+        if (!src || !dst || !nbytes || nbytes[k] < 0 || (nbytes[k] && (!src[k] || !dst[k])))
+            return fail(EXL3_EINVAL, "tier_exchange: copy %d", k);
+        if (((uintptr_t)src[k] | (uintptr_t)dst[k]) & 15)
+            return fail(EXL3_EINVAL, "tier_exchange: copy %d not 16-byte aligned", k);
+        cp.c[cp.n++] = TierCopy{(const uint8_t*)src[k], (uint8_t*)dst[k], nbytes[k]};
+    }
+    hipError_t e = launch_tier_exchange(flags, n_flags, packed, n_diff, rg, cp, (hipStream_t)stream);
+    return e == hipSuccess ? EXL3_OK : hip_fail(e, "tier_exchange");
+}
+
 int exl3_device_status(int32_t* flags4, void* stream) {
     if (!flags4) return fail(EXL3_EINVAL, "device_status: null output");
     hipError_t e = (hipError_t)read_status(flags4, (hipStream_t)stream);

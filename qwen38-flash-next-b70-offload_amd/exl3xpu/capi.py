@@ -42,6 +42,7 @@ SIGNATURES = {
     "exl3_dequant": (c_i32, [c_p, c_i32, c_i32, c_i32, c_p, c_p]),
     "exl3_device_status": (c_i32, [c_p, c_p]),
     "exl3_scatter_flags": (c_i32, [c_p, c_i64, c_p, c_i64, c_p]),
+    "exl3_tier_exchange": (c_i32, [c_p, c_i64, c_p, c_i64, c_p, c_i64, c_i64, c_p, c_p, c_p, c_p, c_i32, c_p]),
     "exl3_admit_decide": (c_i32, [c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_i64, c_p, c_p, c_p, c_p, c_p, c_p, c_p]),
     "exl3_host_alloc": (c_p, [c_i64]),
     "exl3_host_free": (c_i32, [c_p]),

@@ -426,8 +426,11 @@ class NvTierAsync(NvTierFast):
     admission policy (AdmissionPolicy): AGE = EXL3_NVTIER_ADMIT_AGE (default 4), QMAX = EXL3_NVTIER_ADMIT_QMAX
     (default 256). Host step n snapshots the device state after decode step n and acts on the snapshot of step n-1.
 
-    Per step on the stream: three snapshot copies into pinned double buffers and one flag-scatter kernel that reads
-    the (key, value) diff in place from a pinned double buffer; no host allocation, no extra synchronisation."""
+    Per step on the stream: one exchange kernel (exl3_tier_exchange) that applies the step's (key, value) flag diff,
+    read in place from a pinned double buffer, mirrors the miss-ring entries appended since the last snapshot into a
+    pinned ring mirror, and writes the snapshot of the RAM flags and the slot table into pinned double buffers; no
+    host allocation, no extra synchronisation. The host reads the mirror only between the wait for one exchange and
+    the launch of the next, so one mirror suffices."""
 
     def __init__(self, *a, **k):
         super().__init__(*a, **k)
@@ -436,15 +439,25 @@ class NvTierAsync(NvTierFast):
         n = self.L * self.E
         self._n = n
         X = self.st.X
-        self._h_res = [torch.empty(n, dtype=torch.uint8).pin_memory() for _ in range(2)]
-        self._h_ring = [torch.empty(self.ring.numel(), dtype=torch.int32).pin_memory() for _ in range(2)]
-        self._h_slot = [torch.empty(n, dtype=torch.int32).pin_memory() for _ in range(2)]
+        # device-mapped pinned buffers: the exchange kernel writes the snapshots and reads the diffs in place
+        self._h_res = [X.host_alloc(n) for _ in range(2)]
+        self._h_ring = X.host_alloc(4 * self.ring.numel()).view(torch.int32)
+        self._h_ring.zero_()
+        self._ring_from = 0                # ring count of the last snapshot read (the next exchange mirrors from it)
+        self._h_slot = [X.host_alloc(4 * n).view(torch.int32) for _ in range(2)]
         self._np_res = [t.numpy() for t in self._h_res]
-        self._np_ring = [t.numpy() for t in self._h_ring]
+        self._np_ring = self._h_ring.numpy()
         self._np_slot = [t.numpy() for t in self._h_slot]
         self._h_diff = [X.host_alloc(4 * n).view(torch.int32) for _ in range(2)]   # device-mapped pinned
         self._np_diff = [t.numpy() for t in self._h_diff]
         self._snap_ev = [torch.cuda.Event(), torch.cuda.Event()]
+        import ctypes
+        self._xargs = []                   # (src, dst, nbytes) ctypes arrays of the two snapshot copies per buffer
+        for b in range(2):
+            pairs = ((self.res_dev, self._h_res[b], n), (self.st.slot_of_dev, self._h_slot[b], 4 * n))
+            self._xargs.append(((ctypes.c_void_p * 2)(*[p[0].data_ptr() for p in pairs]),
+                                (ctypes.c_void_p * 2)(*[p[1].data_ptr() for p in pairs]),
+                                (ctypes.c_int64 * 2)(*[p[2] for p in pairs])))
         self._have = [False, False]
         self._k = 0
         self._last_diff = None
@@ -472,45 +485,43 @@ class NvTierAsync(NvTierFast):
         L, sh = self._capi.lib(), cur.cuda_stream
         k = self._k
         self._k ^= 1
-        for dst, src, nb in ((self._h_res[k], self.res_dev, n), (self._h_ring[k], self.ring, 4 * self.ring.numel()),
-                             (self._h_slot[k], self.st.slot_of_dev, 4 * n)):
-            rc = L.exl3_memcpy_async(dst.data_ptr(), src.data_ptr(), nb, sh)
-            if rc:
-                self._capi.check(rc, "nvtier snapshot")
+        j = k ^ 1
+        n_diff = 0
+        seen0 = pol.ring_seen
+        if self._have[j]:
+            tw = time.perf_counter()
+            self._snap_ev[j].synchronize()
+            self.stats["wait_ms"] = self.stats.get("wait_ms", 0.0) + (time.perf_counter() - tw) * 1e3
+            view = self._view
+            np.copyto(view, self._np_res[j])
+            if self._last_diff is not None:         # the flags uploaded with that snapshot
+                dk, dv = self._last_diff
+                view[dk] = dv
+            adm, ev_keys, diff, vals = pol.decide(view, self._np_ring, self._np_slot[j], self._completed(hs))
+            self._ring_from = int(self._np_ring[0])
+            self._queue_fills(adm, hs)
+            if len(diff):
+                # buffer k was last read by the exchange of step n-2, which ran before the snapshot just waited for
+                self._np_diff[k][:len(diff)] = (diff << 1) | vals
+                n_diff = len(diff)
+                self._last_diff = (diff, vals)
+            else:
+                self._last_diff = None
+            self.res = pol.res
+            self.age, self.inflight, self.ring_seen = pol.age, pol.inflight, pol.ring_seen
+            if self.log_decisions:
+                self.decisions.append((adm.copy(), ev_keys.copy()))
+            for key, v in pol.stats.items():
+                self.stats[key] = v
+        elif self.log_decisions:
+            self.decisions.append((np.zeros(0, np.int64), np.zeros(0, np.int64)))
+        # this step's diff and the snapshot of the device state after decode step n, in one launch
+        srcs, dsts, nbs = self._xargs[k]
+        self._capi.check(L.exl3_tier_exchange(self.res_dev.data_ptr(), n, self._h_diff[k].data_ptr(), n_diff,
+                                              self.ring.data_ptr(), self.ring.numel() - 1, self._ring_from,
+                                              self._h_ring.data_ptr(), srcs, dsts, nbs, 2, sh), "nvtier exchange")
         self._snap_ev[k].record(cur)
         self._have[k] = True
-        j = k ^ 1
-        if not self._have[j]:
-            self.stats["steps"] += 1
-            if self.log_decisions:
-                self.decisions.append((np.zeros(0, np.int64), np.zeros(0, np.int64)))
-            return 0
-        tw = time.perf_counter()
-        self._snap_ev[j].synchronize()
-        self.stats["wait_ms"] = self.stats.get("wait_ms", 0.0) + (time.perf_counter() - tw) * 1e3
-        view = self._view
-        np.copyto(view, self._np_res[j])
-        if self._last_diff is not None:
-            dk, dv = self._last_diff
-            view[dk] = dv
-        seen0 = pol.ring_seen
-        adm, ev_keys, diff, vals = pol.decide(view, self._np_ring[j], self._np_slot[j], self._completed(hs))
-        self._queue_fills(adm, hs)
-        if len(diff):
-            # buffer k was last read by the scatter of step n-2, which ran before the snapshot just waited for
-            buf = self._np_diff[k]
-            buf[:len(diff)] = (diff << 1) | vals
-            self._capi.check(L.exl3_scatter_flags(self.res_dev.data_ptr(), n, self._h_diff[k].data_ptr(), len(diff),
-                                                  sh), "nvtier flag upload")
-            self._last_diff = (diff, vals)
-        else:
-            self._last_diff = None
-        self.res = pol.res
-        self.age, self.inflight, self.ring_seen = pol.age, pol.inflight, pol.ring_seen
-        if self.log_decisions:
-            self.decisions.append((adm.copy(), ev_keys.copy()))
-        for key, v in pol.stats.items():
-            self.stats[key] = v
         self.stats["steps"] += 1
         self.stats["fill_ms"] += (time.perf_counter() - t0) * 1e3
         return int(max(0, pol.ring_seen - seen0))

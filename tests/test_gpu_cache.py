@@ -231,3 +231,69 @@ def test_cache_pinned_slots(M, topk, fused):
     assert nm[n0 * L:].sum() > 0
     if P <= 64:
         assert (nm[n0 * L:] == 0).any()                    # no-miss (fast-path) calls after pinning too
+
+
+def test_tier_exchange():
+    """exl3_tier_exchange: the flag diff (keys outside [0, n) and negative entries skipped), the ring mirror (only the
+    entries since `from`, wrapping, at most the last cap of them) and up to four copies into device-mapped pinned
+    buffers, sizes that are not multiples of 16 included; misaligned copies are refused."""
+    import ctypes
+    from exl3xpu import capi
+    from exl3xpu.moe_offload import ops
+    X = ops()
+    L = capi.lib()
+    print("case tier exchange", flush=True)
+    n = 24576
+    g = torch.Generator().manual_seed(5)
+    flags = torch.randint(0, 2, (n,), generator=g, dtype=torch.uint8).cuda()
+    before = flags.cpu().numpy()
+    diff = X.host_alloc(4 * 1000).view(torch.int32)
+    keys = torch.randperm(n, generator=g)[:990].to(torch.int32)     # unique, as the tier's diffs are
+    vals = torch.randint(0, 2, (990,), generator=g, dtype=torch.int32)
+    dn = diff.numpy()
+    dn[:990] = (keys.numpy() << 1) | vals.numpy()
+    dn[990:995] = ((n + np.arange(5)) << 1) | 1          # beyond n_flags: skipped
+    dn[995:1000] = -2                                     # negative: skipped
+    sizes = [n, 4 * 24577 + 12]
+    srcs = [flags, torch.randint(0, 255, (sizes[1],), generator=g, dtype=torch.uint8).cuda()]
+    dsts = [X.host_alloc(sz) for sz in sizes]
+    for d in dsts:
+        d.fill_(0xAB)
+    c_src = (ctypes.c_void_p * 2)(*[t.data_ptr() for t in srcs])
+    c_dst = (ctypes.c_void_p * 2)(*[t.data_ptr() for t in dsts])
+    c_n = (ctypes.c_int64 * 2)(*sizes)
+    cap = 1000
+    ring = torch.randint(0, n, (1 + cap,), generator=g, dtype=torch.int32)
+    mirror = X.host_alloc(4 * (1 + cap)).view(torch.int32)
+    mirror.fill_(-7)
+    st = torch.cuda.current_stream().cuda_stream
+
+    def run(n_diff, cnt, frm, nc=2, src=c_src):
+        ring[0] = cnt
+        rd = ring.cuda()
+        rc = L.exl3_tier_exchange(flags.data_ptr(), n, diff.data_ptr(), n_diff, rd.data_ptr(), cap, frm,
+                                  mirror.data_ptr(), src, c_dst, c_n, nc, st)
+        torch.cuda.synchronize()
+        return rc, rd
+    # copies and the ring first: the snapshot of the flags is their state before any diff
+    rc, _ = run(0, 700, 650)
+    assert rc == 0
+    assert np.array_equal(dsts[0].numpy(), before)
+    assert np.array_equal(dsts[1].numpy(), srcs[1].cpu().numpy())
+    m, r = mirror.numpy(), ring.numpy()
+    assert m[0] == 700 and np.array_equal(m[1 + 650:1 + 700], r[1 + 650:1 + 700])
+    assert (m[1:1 + 650] == -7).all() and (m[1 + 700:] == -7).all()
+    rc, _ = run(0, 1300, 900)                             # wraps: positions 900..999, then 0..299
+    assert rc == 0 and m[0] == 1300
+    assert np.array_equal(m[1 + 900:], r[1 + 900:]) and np.array_equal(m[1:1 + 300], r[1:1 + 300])
+    assert (m[1 + 300:1 + 650] == -7).all()
+    mirror.fill_(-7)
+    rc, _ = run(0, 5000, 100)                             # more than cap since `from`: the last cap entries
+    assert rc == 0 and m[0] == 5000 and np.array_equal(m[1:], r[1:])
+    rc, _ = run(1000, 5000, 5000, nc=0)
+    assert rc == 0
+    want = before.copy()
+    want[keys.numpy()] = vals.numpy()
+    assert np.array_equal(flags.cpu().numpy(), want)
+    bad = (ctypes.c_void_p * 1)(srcs[1].data_ptr() + 4)
+    assert run(0, 5000, 5000, nc=1, src=bad)[0] != 0
