@@ -28,15 +28,15 @@ def _setup(L, E, S, H, I, K, budget, qmax, age, latency, ring_cap, seed):
     return store, tier, blobs, ref_ptr
 
 
-def _run(store, tier, ids, w, H, check_out_every=0, ref_ptr=None):
-    """ids/w [steps, L, P]: 48-layer decode steps through forward_cached + the host step; returns the device
-    decision log (records) and optionally checks outputs against the plain forward."""
+def _run(store, tier, ids, w, H, check_out_every=0, ref_ptr=None, M=1):
+    """ids/w [steps, L, P]: decode steps of M rows (P = M x top-k picks, row-major) through forward_cached + the host
+    step; returns the device decision log (records) and optionally checks outputs against the plain forward."""
     X = store.X
     steps, L, P = ids.shape
     rl = cache.rec_len(P)
     logbuf = torch.zeros(1 + steps * L * rl, dtype=torch.int32, device="cuda")
     X.moe_set_decision_log(logbuf)
-    x = torch.randn(1, H, generator=torch.Generator().manual_seed(0)).to(torch.bfloat16).cuda()
+    x = torch.randn(M, H, generator=torch.Generator().manual_seed(0)).to(torch.bfloat16).cuda()
     ids_d = torch.from_numpy(ids).cuda()
     w_d = torch.from_numpy(w).cuda()
     keys = list(store.layer_index)
@@ -44,8 +44,8 @@ def _run(store, tier, ids, w, H, check_out_every=0, ref_ptr=None):
     try:
         for n in range(steps):
             for li in range(L):
-                it = ids_d[n, li].view(1, P).clone()
-                wt = w_d[n, li].view(1, P).clone()
+                it = ids_d[n, li].view(M, P // M).clone()
+                wt = w_d[n, li].view(M, P // M).clone()
                 out = store.forward_cached(keys[li], x, it, wt)
                 if check_out_every and n % check_out_every == 0:
                     E = store.E
@@ -103,6 +103,33 @@ def test_cache_config1_trace_bitexact():
     for n, ((a1, e1), (a2, e2)) in enumerate(zip(tier.decisions, olog)):
         assert a1.tolist() == a2.tolist() and e1.tolist() == e2.tolist(), n
     assert bad == 0
+    tier.close()
+
+
+@pytest.mark.parametrize("fused", [1, 0])
+def test_cache_multirow_tier(fused):
+    """4 rows x top-10 per call (40 picks, duplicates across rows: the ensure inside the layer kernel when fused),
+    6 layers x 128 experts, 150 slots, RAM tier of 160 records (AGE 4, QMAX 64, 3-step fill latency), Zipf(1.1)
+    routing: every device record and host decision equals the oracle's and every output equals the plain forward."""
+    L, E, S, M, TK, steps = 6, 128, 150, 4, 10, 80
+    print(f"case cache multirow tier M={M} top-{TK} fused={fused}", flush=True)
+    ids, w = synth.zipf_trace(20261203, steps, L, E, TK, M=M)
+    ids = np.ascontiguousarray(ids.reshape(steps, L, M * TK))
+    w = np.ascontiguousarray(w.reshape(steps, L, M * TK))
+    co = cache.CacheOracle(L, E, S, ring_cap=1 << 12, budget=160, age=4, qmax=64, latency=3)
+    orecs, olog = co.run(ids, w)
+    store, tier, blobs, ref_ptr = _setup(L, E, S, 128, 128, 3, 160, 64, 4, 3, 1 << 12, 11)
+    store.X.moe_set_fused_ensure(fused)
+    try:
+        recs, bad = _run(store, tier, ids, w, 128, check_out_every=1, ref_ptr=ref_ptr, M=M)
+    finally:
+        store.X.moe_set_fused_ensure(1)
+    mism = np.nonzero((recs != orecs).any(axis=-1))
+    assert mism[0].size == 0, f"first mismatch at step/layer {mism[0][0]}/{mism[1][0]}"
+    for n, ((a1, e1), (a2, e2)) in enumerate(zip(tier.decisions, olog)):
+        assert a1.tolist() == a2.tolist() and e1.tolist() == e2.tolist(), n
+    assert bad == 0
+    assert recs[:, :, 1].sum() > 0 and recs[:, :, 2 + M * TK].sum() > 0   # masked picks and fills happened
     tier.close()
 
 
