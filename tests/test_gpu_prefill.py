@@ -228,3 +228,53 @@ def test_tier_stage_forward_matches_resident():
         assert tier._sg["bytes"] == 2 * L * (E - 5) * store.stride     # every non-HBM expert, each pass
     finally:
         tier.close()
+
+
+def test_tier_ensure_for_prefill():
+    """NvTier.ensure_for_prefill (nvtier.py:389-457): before a prefill layer, every expert of the batch is made
+    RAM-resident (filled from the source) and flagged on the device within the record budget, evicting first the
+    transient fills of other layers, then RAM copies of HBM-resident experts, then the rest, oldest first with ties by
+    ascending key; never the layer's own keys or pinned keys. The eviction set below is derived by hand from that
+    rule for this state; the prefill kernels then read the batch zero-copy from the RAM arena and give the same bits
+    as an all-resident table."""
+    from exl3xpu import nvtier
+    H, I, K, E, S, L, M, topk = 256, 128, 3, 16, 20, 3, 300, 4
+    print("case tier ensure_for_prefill", flush=True)
+    store = nvtier.TierStore(H, I, K, E, S, n_layers=L)
+    keys = [f"model.layers.{li}.mlp" for li in range(L)]
+    for k in keys:
+        store.add_layer(k)
+    src = nvtier.SyntheticExpertSource(H, I, K, 17, n_distinct=L * E)
+    tier = nvtier.NvTier(store, src, budget_records=20)           # pinned safe experts 0, 16, 32 filled at init
+    try:
+        ram = list(range(1, 7)) + list(range(17, 23)) + list(range(33, 37))
+        tier.fill_many(ram)
+        store.make_resident(keys[1], [1, 2, 3])                    # keys 17, 18, 19 also in HBM
+        store.make_resident(keys[2], [1])                          # key 33
+        tier.transient = np.zeros(L * E, dtype=bool)
+        tier.transient[[21, 22]] = True                            # fills of an earlier prefill of layer 1
+        tier.res_dev.copy_(torch.from_numpy(tier.res))
+        assert int(tier.res.sum()) == 19
+        ids, w = synth.softmax_topk(81, M, E, topk)
+        assert len(np.unique(ids)) == E                            # the batch uses every expert of layer 0
+        it, wt = torch.from_numpy(ids).cuda(), torch.from_numpy(w).cuda()
+        n_fill = tier.ensure_for_prefill(0, it)
+        torch.cuda.synchronize()
+        # 9 misses (keys 7..15) over a budget of 20 with 19 resident: 8 evictions, by class then (age, key)
+        evicted = {21, 22, 17, 18, 19, 33, 20, 34}
+        assert n_fill == 9
+        want = set([0, 16, 32] + list(range(1, 16)) + list(range(17, 23)) + list(range(33, 37))) - evicted
+        assert set(np.nonzero(tier.res)[0].tolist()) == want
+        assert int(tier.res.sum()) == 20
+        assert np.array_equal(tier.res_dev.cpu().numpy(), tier.res)
+        assert set(np.nonzero(tier.transient)[0].tolist()) == set(range(7, 16))
+        x = torch.from_numpy(exl3.bf16_to_f32(synth.activations(82, M, H))).to(torch.bfloat16).cuda()
+        table = store.ptrs_all[0:E].clone()                         # layer 0: host copies, read zero-copy
+        out = _ops().moe_forward(x, it, wt, table, I, K, E)
+        blobs = torch.from_numpy(src.buf).cuda()
+        ref_t = torch.tensor([blobs[e].data_ptr() for e in range(E)], dtype=torch.int64, device="cuda")
+        ref = _ops().moe_forward(x, it, wt, ref_t, I, K, E)
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref)
+    finally:
+        tier.close()
