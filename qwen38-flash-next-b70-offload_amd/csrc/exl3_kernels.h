@@ -45,9 +45,8 @@ struct DecodeArgs {
     int64_t* commit_ptrs;                          // cache commit: ptrs[e] = fill[e] for e in fill_list
     int64_t* commit_fill;
     const int32_t* fill_list;                      // [1 + E]
-    _Float16* abuf;                                // [npairs, I]
-    float* ybuf;                                   // [npairs, H]
-    float* part_gu;                                // [npairs, I/128, H/128, 256]
+    uint64_t* xpart;                               // tagged gate/up sums [npairs][H/1024 slices][2I] (exchange buffer)
+    uint64_t* xy;                                  // tagged y of every pick [npairs][H] (exchange buffer)
     void* out; int64_t out_stride;                 // [M, H], same dtype as x
     BlobGeom g;
     VictimArgs va;                                 // victim write-back (cached calls with victims on)
@@ -96,14 +95,19 @@ size_t align_scratch_bytes(int npairs, int E);
 size_t prefill_workspace_bytes(int M, int H, int I, int topk, int E);
 hipError_t launch_prefill(PrefillArgs a, int E, void* ws, hipStream_t s);
 
-// 256-row slices of H handled by the split-K gate/up workgroups (H is a multiple of 128)
-__host__ __device__ static inline int gu_slices(int H) { return (H + 255) / 256; }
+// 1024-row slices of H of the decode gate/up workgroups (one 128-row block per wave; H is a multiple of 128)
+__host__ __device__ static inline int gu_kslices(int H) { return (H + 1023) / 1024; }
 
-// workspace of a decode call (bytes, 256-aligned parts)
+// workspace of a decode call (bytes, 256-aligned parts): the blob pointer of every pick
 static inline size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
 static inline size_t decode_workspace_bytes(int npairs, int H, int I) {
-    return align256((size_t)npairs * I * 2) + align256((size_t)npairs * H * 4) +
-           align256((size_t)npairs * (I / 128) * gu_slices(H) * 256 * 4) + align256((size_t)npairs * 8);
+    (void)H;
+    (void)I;
+    return align256((size_t)npairs * 8);
+}
+// tagged words a decode call exchanges between workgroups (library-owned buffer, zeroed when allocated)
+static inline size_t decode_exchange_words(int npairs, int H, int I) {
+    return (size_t)npairs * ((size_t)gu_kslices(H) * 2 * I + H);
 }
 
 }  // namespace exl3

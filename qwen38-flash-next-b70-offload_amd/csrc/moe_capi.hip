@@ -4,6 +4,7 @@
 #include <algorithm>
 #include <cstdarg>
 #include <cstdio>
+#include <mutex>
 #include <string>
 
 #include "../../include/exl3moe.h"
@@ -141,8 +142,53 @@ size_t exl3_moe_forward_workspace(int M, int H, int I, int topk, int n_experts) 
 }
 
 static int64_t* pair_ptr_area(void* ws, int npairs, int H, int I) {
-    return (int64_t*)((uint8_t*)ws + align256((size_t)npairs * I * 2) + align256((size_t)npairs * H * 4) +
-                      align256((size_t)npairs * (I / 128) * gu_slices(H) * 256 * 4));
+    (void)npairs;
+    (void)H;
+    (void)I;
+    return (int64_t*)ws;
+}
+
+// The decode kernel's cross-workgroup exchange buffer: library-owned, one per device, zeroed when (re)allocated so that
+// no word carries a live tag before the kernel writes it. It grows to the largest call seen; growing synchronizes the
+// device and cannot happen while the stream is being captured into a graph.
+struct Exchange {
+    uint64_t* p = nullptr;
+    size_t words = 0;
+};
+static constexpr int kMaxDevices = 64;
+static std::mutex g_exch_mu;
+static Exchange g_exch[kMaxDevices];
+
+static int exchange_buffer(size_t words, hipStream_t st, uint64_t** out) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+    if (dev < 0 || dev >= kMaxDevices) return fail(EXL3_EUNSUPPORTED, "device %d >= %d", dev, kMaxDevices);
+    std::lock_guard<std::mutex> lk(g_exch_mu);
+    Exchange& x = g_exch[dev];
+    if (words <= x.words) {
+        *out = x.p;
+        return EXL3_OK;
+    }
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    e = hipStreamIsCapturing(st, &cs);
+    if (e != hipSuccess) return hip_fail(e, "hipStreamIsCapturing");
+    if (cs != hipStreamCaptureStatusNone)
+        return fail(EXL3_EUNSUPPORTED, "moe decode: exchange buffer of %zu words needed inside a graph capture (have "
+                    "%zu): run one call of this size before capturing", words, x.words);
+    const size_t n = std::max(words, std::max((size_t)1 << 16, 2 * x.words));
+    uint64_t* p = nullptr;
+    if ((e = hipDeviceSynchronize()) != hipSuccess) return hip_fail(e, "exchange buffer: synchronize");
+    if ((e = hipMalloc((void**)&p, n * 8)) != hipSuccess) return hip_fail(e, "exchange buffer: hipMalloc");
+    if ((e = hipMemset(p, 0, n * 8)) != hipSuccess || (e = hipDeviceSynchronize()) != hipSuccess) {
+        (void)hipFree(p);
+        return hip_fail(e, "exchange buffer: zero fill");
+    }
+    if (x.p) (void)hipFree(x.p);
+    x.p = p;
+    x.words = n;
+    *out = p;
+    return EXL3_OK;
 }
 
 static int forward_impl(const void* x, int x_dtype, int64_t x_stride, int M, int H, const int32_t* ids, const float* w,
@@ -178,6 +224,9 @@ static int forward_impl(const void* x, int x_dtype, int64_t x_stride, int M, int
                     topk, kMaxPairs, kMaxRows);
     const size_t need = decode_workspace_bytes(npairs, H, I);
     if (!ws || ws_bytes < need) return fail(EXL3_EWORKSPACE, "moe_forward: workspace %zu < %zu bytes", ws_bytes, need);
+    uint64_t* xb = nullptr;
+    int rx = exchange_buffer(decode_exchange_words(npairs, H, I), st, &xb);
+    if (rx) return rx;
     DecodeArgs a{};
     a.x = x;
     a.x_dt = x_dtype;
@@ -194,12 +243,8 @@ static int forward_impl(const void* x, int x_dtype, int64_t x_stride, int M, int
     a.commit_ptrs = commit_ptrs;
     a.commit_fill = commit_fill;
     a.fill_list = fill_list;
-    uint8_t* p = (uint8_t*)ws;
-    a.abuf = (_Float16*)p;
-    p += align256((size_t)npairs * I * 2);
-    a.ybuf = (float*)p;
-    p += align256((size_t)npairs * H * 4);
-    a.part_gu = (float*)p;
+    a.xpart = xb;
+    a.xy = xb + (size_t)npairs * gu_kslices(H) * 2 * I;
     a.out = out;
     a.out_stride = out_stride;
     a.g = blob_geom(H, I, K);

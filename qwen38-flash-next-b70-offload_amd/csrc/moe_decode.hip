@@ -1,15 +1,21 @@
 // Decode-size routed-expert MoE (pair mode: one row per (token, expert) pair), EXL3 trellis dequantization fused into
 // the expert GEMVs, for CDNA4. One launch per MoE layer (moe_layer_kernel), two kinds of workgroups:
 //
-//   gate/up WGs (ids 0 .. n_gu-1), one per (pair, 128-column block of I, 256-row slice of H): issue their trellis-word
-//     loads first, then the input Hadamard of x*suh for gate and up, the trellis GEMV (one period per lane: bfe + mul
-//     + sad + fma_mix per weight) and split-K partials; the last-arriving WG of a (pair, block) reduces the partials in
-//     fixed order and runs the epilogue (output Hadamards * svh, SiLU(g)*u, *suh_d, down-input Hadamard) -> abuf
-//     (fp16) and counts the block as ready for the pair.
+//   gate/up WGs (ids 0 .. n_gu-1), one per (pair, projection, PLANAR4 group of 4 tile-columns = 64 columns of I,
+//     1024-row slice of H): issue their trellis-word loads first, then the input Hadamard of x*suh (one 128-row block
+//     per wave), the trellis GEMV (one period per lane: bfe + mul + sad + fma_mix per weight) with an in-WG reduction,
+//     and publish the 64 column sums (fp32) of the slice for the pair.
 //   down WGs (ids n_gu ..), one per (pair, 128-column block of H) over the whole K = I: issue their word loads, wait
-//     (bounded) until the pair's abuf is complete, GEMV with an in-WG reduction, epilogue (output Hadamard * w *
-//     svh_d) -> y (fp32); the last pair of a (row, block) sums the top-k y's in k order into out (the combine); the
-//     last (row, block) commits the expert-cache fills (ptrs[e] = fill[e]; fill[e] = 0) and clears the ready counts.
+//     (bounded) for the pair's gate/up sums, run the gate/up epilogue of the pair themselves (output Hadamards * svh,
+//     SiLU(g)*u, *suh_d, down-input Hadamard -> the down input in LDS, fp16), GEMV with an in-WG reduction, epilogue
+//     (output Hadamard * w * svh_d) -> y (fp32). The WG of the last pick of a row (the combiner of that row and block)
+//     waits for the other picks' y and sums the top-k y's in k order into out; the combiner of the last (row, block)
+//     waits for every other combiner, commits the expert-cache fills (ptrs[e] = fill[e]; fill[e] = 0) and advances
+//     the call epoch.
+// Every value handed from one workgroup to another is a tagged word (tag = call epoch + 1 in the high half, the fp32
+// value in the low half) written with one 64-bit agent-scope store into a library-owned zeroed buffer: a consumer polls
+// the data itself, so no producer waits for its stores and no counter is shared (same-address atomics serialize at
+// the coherence point). A consumer needing many words (the gate/up sums) first polls one word per producer.
 // Gate/up WGs have lower ids, so on every XCD they are dispatched before any down WG and never wait: the down WGs'
 // wait always ends (it is also bounded, with an error flag, so a broken assumption cannot hang the GPU).
 //
@@ -26,15 +32,36 @@
 
 namespace exl3 {
 
-__device__ int g_cnt_gu[kMaxPairs * 64];
-__device__ int g_cnt_d[kMaxPairs * 64];
-__device__ int g_cnt_c[kMaxRows * 64];
-__device__ int g_ready[kMaxPairs];
-__device__ int g_cnt_all[4];          // [0] combines done, [1] victim reads done, [2] fused ensure done
+__device__ unsigned g_cflag[kMaxRows * 64];  // combiner of (row m, block nb) sets g_cflag[m * nbn + nb] = tag
+__device__ unsigned g_epoch;                 // call epoch (advanced by the last workgroup of each call; never ~0u)
+
+__device__ int g_cnt_all[4];          // [1] victim reads done, [2] fused ensure done
 __device__ int g_status[4];          // [0]: spin timeouts (should stay 0)
 
 constexpr int kSpinMax = 1 << 22;
 constexpr uint64_t kDownLoadDelay = 120;         // 1.2 us in s_memrealtime ticks
+
+// tagged exchange words: (tag << 32) | fp32 bits, one single-copy-atomic 64-bit agent-scope access
+__device__ __forceinline__ void st_tag(uint64_t* p, unsigned tag, float v) {
+    __hip_atomic_store(p, ((uint64_t)tag << 32) | __float_as_uint(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint64_t ld_tag(const uint64_t* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ bool tag_is(uint64_t w, unsigned tag) { return (unsigned)(w >> 32) == tag; }
+__device__ __forceinline__ float tag_val(uint64_t w) { return __uint_as_float((uint32_t)w); }
+__device__ __forceinline__ unsigned call_tag() {
+    return __hip_atomic_load(&g_epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u;
+}
+// bounded-spin bookkeeping shared by the polls: true once the budget is spent (counted in g_status[0])
+__device__ __forceinline__ bool spin_out(int& it) {
+    if (++it > kSpinMax) {
+        if (lane_id() == 0) atomicAdd(&g_status[0], 1);
+        return true;
+    }
+    __builtin_amdgcn_s_sleep(1);
+    return false;
+}
 
 // one period of one tile-row: xv[a][qq] holds activation rows (8a + 2q, 8a + 2q + 1), q = (qb + qq) & 3
 template <int K, int NQ, int u>
@@ -133,15 +160,99 @@ struct Gemv8 {
     }
 };
 
+// GEMV of 8 tile-rows x 4 tile-columns per wave (gate/up): one PLANAR4 group, whose 4 tile-columns share every
+// 128-byte line of words. Tile tau = pass * NTW + j of the wave's 32 is (tile-row tau / 4, tile-column tau % 4), so a
+// lane keeps NCQ = max(1, 4 / NTW) column pairs over all passes.
+template <int K>
+struct Gemv4 {
+    using GM = Geo<K>;
+    static constexpr int G = GM::G, D = GM::D, V = GM::V, NTW = GM::NTW, L = 32 / V;
+    static constexpr int NQ = V / 8;
+    static constexpr int NPS = 32 / NTW;                 // passes
+    static constexpr int NCQ = NTW >= 4 ? 1 : 4 / NTW;   // column pairs per lane
+
+    uint32_t wd[NPS][D];
+
+    __device__ __forceinline__ static int trow(int ps, int j) { return (ps * NTW + j) >> 2; }
+    __device__ __forceinline__ static int tcol(int ps, int j) { return (ps * NTW + j) & 3; }
+
+    __device__ __forceinline__ void load(const uint32_t* tr, int tiles_n, int rt0, int ct0) {
+        const int l = lane_id();
+        const int p = l % G, j = l / G;
+#pragma unroll
+        for (int ps = 0; ps < NPS; ++ps)
+#pragma unroll
+            for (int i = 0; i < D; ++i)
+                wd[ps][i] = __builtin_nontemporal_load(as_global(tr) +
+                                                       word_off<K>(rt0 + trow(ps, j), tiles_n, ct0 + tcol(ps, j), p, i));
+    }
+
+    __device__ __forceinline__ void write_through(uint32_t* trd, int tiles_n, int rt0, int ct0) const {
+        const int l = lane_id();
+        const int p = l % G, j = l / G;
+#pragma unroll
+        for (int ps = 0; ps < NPS; ++ps)
+#pragma unroll
+            for (int i = 0; i < D; ++i) trd[word_off<K>(rt0 + trow(ps, j), tiles_n, ct0 + tcol(ps, j), p, i)] = wd[ps][i];
+    }
+
+    // xq: the wave's 128-row block, [tile-row][8] half2
+    __device__ __forceinline__ void compute(const half2_t* xq, float (&acc)[NCQ][2]) const {
+        const int l = lane_id();
+        const int p = l % G, j = l / G;
+        const int src_lane = j * G + ((p + G - 1) % G);
+        const int qb = ((V * p) >> 3) & 3;
+#pragma unroll
+        for (int ps = 0; ps < NPS; ++ps) {
+            const uint32_t prev = (uint32_t)__shfl((int)wd[ps][D - 1], src_lane, 64);
+            Period<K> P;
+            P.set(wd[ps], prev);
+            const half2_t* xr = xq + trow(ps, j) * 8;
+            half2_t xv[2][NQ];
+#pragma unroll
+            for (int a = 0; a < 2; ++a)
+#pragma unroll
+                for (int qq = 0; qq < NQ; ++qq) xv[a][qq] = xr[4 * a + ((qb + qq) & 3)];
+            accum_period<K, NQ, 0>(P, xv, acc[ps % NCQ]);
+        }
+    }
+
+    // sum the lanes sharing column pair q (L within a tile, and the tile-rows of one pass when NTW > 4); true for the
+    // lane owning it, col0 = its column of h = 0 within the 64-column group (h = 1 is col0 + 8)
+    __device__ __forceinline__ static bool reduce(float (&acc)[2], int q, int& col0) {
+        const int l = lane_id();
+        const int p = l % G, j = l / G;
+#pragma unroll
+        for (int mm = 1; mm < L; mm <<= 1) {
+            acc[0] += __shfl_xor(acc[0], mm, 64);
+            acc[1] += __shfl_xor(acc[1], mm, 64);
+        }
+#pragma unroll
+        for (int mm = 4 * G; mm < 64; mm <<= 1) {
+            acc[0] += __shfl_xor(acc[0], mm, 64);
+            acc[1] += __shfl_xor(acc[1], mm, 64);
+        }
+        col0 = tcol(q, j) * 16 + ((V * p) >> 5);
+        return j < 4 && (p % L) == 0;
+    }
+};
+
 constexpr int kWaves = 8;                    // waves per workgroup (both kinds)
 constexpr int kThreads = 64 * kWaves;
 
+struct GateUpShared {
+    half2_t xq[kWaves][64];                  // per wave: Hadamard-transformed x * suh of its 128-row block
+    float ssw[kWaves];                       // their sums
+};
+struct DownShared {
+    half2_t xd[kMaxI / 2];                   // the pair's down input (fp16), [I/2]
+};
 struct LayerShared {
-    half2_t xh[2][2][64];    // gate/up WG: activations of its two 128-row blocks, [proj][block][64] half2
-    float ssum[2][2];
+    union {
+        GateUpShared gu;
+        DownShared dn;
+    } u;
     float red[kWaves][128];  // per-wave column sums
-    float tot[256];          // reduced split-K partials of the last-arriving gate/up WG
-    half2_t xd[kMaxI / 2];   // down WG: the pair's abuf
     int64_t fdst;            // write-through target of the pair (0: none)
     int last;
 };
@@ -236,50 +347,39 @@ __device__ __forceinline__ const uint8_t* pair_lookup(const DecodeArgs& A, int a
     return (const uint8_t*)p;
 }
 
-// gate/up WG per (pair, 128-column block of I, 256-row slice of H): waves (proj = w & 1, quarter = w >> 1) each cover
-// 4 tile-rows x 8 tile-columns.
+// gate/up WG per (pair, projection, PLANAR4 group cg of 4 tile-columns, 1024-row slice ks of H): wave w covers the
+// 128-row block hb = 8 ks + w (8 tile-rows x 4 tile-columns) and its input Hadamard; waves past the end of H add 0.
 template <int K>
 __device__ __forceinline__ void gateup_wg(const DecodeArgs& A, int blk, LayerShared& S) {
-    using GV = Gemv8<K>;
+    using GQ = Gemv4<K>;
     const int H = A.g.H, I = A.g.I;
-    const int nbn = I / 128, ksn = gu_slices(H);
-    const int ks = blk % ksn;
-    blk /= ksn;
-    const int nb = blk % nbn, a = blk / nbn;
+    const int nhb = H / 128, ksn = gu_kslices(H), ncg = I / 64;
+    const int per = 2 * ncg * ksn;               // gate/up workgroups per pair
+    const int a = blk / per, r = blk % per;
+    const int ks = r % ksn, cg = (r / ksn) % ncg, pj = r / (ksn * ncg);
     const int tid = threadIdx.x, wv = tid >> 6, l = tid & 63;
     int e;
     bool miss = false, masked = false;
     const uint8_t* base = A.fused ? pair_lookup(A, a, e, miss, masked) : pair_base(A, a, e);
     const int m = a / A.topk;
     uint8_t* dst = !A.fused && A.fill ? (uint8_t*)A.fill[e] : nullptr;
-    const int proj = wv & 1, qt = wv >> 1;
-    const int tiles_n = 2 * I / 16, r0 = ks * 16 + qt * 4, ct0 = proj * (I / 16) + nb * 8;
-
-    // the last slice of an H that is an odd multiple of 128 has one 128-row block: its second-block waves only add 0
-    const bool live = ks * 256 + (qt >> 1) * 128 < H;
-    GV g;
-    if (live) g.load((const uint32_t*)base, tiles_n, r0, ct0);
-    half2_t sc_g{}, sc_u{}, sc_d{};              // epilogue scales (wave 0), loaded early: off the critical path
-    if (wv == 0) {
-        const int c = nb * 128 + 2 * l;
-        sc_g = *(const half2_t*)((const half_t*)(base + A.g.off_svh_g) + c);
-        sc_u = *(const half2_t*)((const half_t*)(base + A.g.off_svh_u) + c);
-        sc_d = *(const half2_t*)((const half_t*)(base + A.g.off_suh_d) + c);
-    }
-    if (wv < 4 && ks * 256 + (wv >> 1) * 128 >= H) {
-        if (l == 0) S.ssum[wv & 1][wv >> 1] = 0.f;
-    } else if (wv < 4) {                         // input Hadamards of x * suh: (proj, 128-row block) per wave
-        const int pj = wv & 1, hb = wv >> 1;
+    const int hb = ks * 8 + wv;
+    const bool live = hb < nhb;
+    const int tiles_n = 2 * I / 16, ct0 = pj * (I / 16) + cg * 4, rt0 = hb * 8;
+    GQ g;
+    if (live) g.load((const uint32_t*)base, tiles_n, rt0, ct0);
+    const unsigned tag = wv == 0 ? call_tag() : 0u;
+    float ssum = 0.f;
+    if (live) {                                  // input Hadamard of x * suh over this wave's block
         const half_t* suh = (const half_t*)(base + (pj ? A.g.off_suh_u : A.g.off_suh_g));
-        const int k0 = ks * 256 + hb * 128 + 2 * l;
+        const int k0 = hb * 128 + 2 * l;
         const size_t xo = (size_t)m * A.x_stride + k0;
         float v0 = (float)(half_t)(ld_act(A.x, A.x_dt, xo) * (float)suh[k0]);
         float v1 = (float)(half_t)(ld_act(A.x, A.x_dt, xo + 1) * (float)suh[k0 + 1]);
         wave_fwht128(v0, v1);
         const half_t h0 = (half_t)(v0 * kRsqrt128), h1 = (half_t)(v1 * kRsqrt128);
-        S.xh[pj][hb][l] = half2_t{h0, h1};
-        const float s = wave_sum((float)h0 + (float)h1);
-        if (l == 0) S.ssum[pj][hb] = s;
+        S.u.gu.xq[wv][l] = half2_t{h0, h1};
+        ssum = wave_sum((float)h0 + (float)h1);
     }
     if (A.fused ? miss : dst != nullptr) {       // write-through of a cache miss into its HBM slot
         if (tid == 0) {
@@ -294,65 +394,38 @@ __device__ __forceinline__ void gateup_wg(const DecodeArgs& A, int blk, LayerSha
         __syncthreads();
         dst = (uint8_t*)S.fdst;
     }
-    if (dst) {
-        if (live) g.write_through((uint32_t*)dst, tiles_n, r0, ct0);
-        if (nb == 0 && ks == 0) {
-            const uint32_t* sv = (const uint32_t*)(base + A.g.off_suh_g);
-            uint32_t* dv = (uint32_t*)(dst + A.g.off_suh_g);
-            const int n = (int)((A.g.blob - A.g.off_suh_g) >> 2);
-            for (int i = tid; i < n; i += kThreads) dv[i] = sv[i];
-        }
+    if (dst && r == 0) {                         // the vectors (suh, svh) after the trellis words
+        const uint32_t* sv = (const uint32_t*)(base + A.g.off_suh_g);
+        uint32_t* dv = (uint32_t*)(dst + A.g.off_suh_g);
+        const int n = (int)((A.g.blob - A.g.off_suh_g) >> 2);
+        for (int i = tid; i < n; i += kThreads) dv[i] = sv[i];
     }
-    __syncthreads();
-    float acc[GV::NCP][2];
+    float acc[GQ::NCQ][2];
+#pragma unroll
+    for (int q = 0; q < GQ::NCQ; ++q) acc[q][0] = acc[q][1] = 0.f;
     if (live) {
-        g.compute((qt & 1) * 4, &S.xh[proj][qt >> 1][0], acc);
-    } else {
-#pragma unroll
-        for (int cp = 0; cp < GV::NCP; ++cp) acc[cp][0] = acc[cp][1] = 0.f;
+        if (dst) g.write_through((uint32_t*)dst, tiles_n, rt0, ct0);
+        g.compute(&S.u.gu.xq[wv][0], acc);       // the wave's own LDS rows: no barrier
     }
+    if (!live) S.red[wv][l] = 0.f;
 #pragma unroll
-    for (int cp = 0; cp < GV::NCP; ++cp) {
+    for (int q = 0; q < GQ::NCQ; ++q) {
         int c0;
-        if (GV::reduce(acc[cp], cp, c0)) {
-            S.red[wv][c0] = acc[cp][0];
-            S.red[wv][c0 + 8] = acc[cp][1];
+        if (GQ::reduce(acc[q], q, c0) && live) {
+            S.red[wv][c0] = acc[q][0];
+            S.red[wv][c0 + 8] = acc[q][1];
         }
     }
-    __syncthreads();
-    if (tid < 256) {                             // column tid of [gate 128 | up 128]: sum the 4 quarters in order
-        const int pj = tid >> 7, c = tid & 127;
-        const float t = S.red[pj][c] + S.red[pj + 2][c] + S.red[pj + 4][c] + S.red[pj + 6][c];
-        st_agent(A.part_gu + ((size_t)(a * nbn + nb) * ksn + ks) * 256 + tid,
-                 kC1 * t + kC2 * (S.ssum[pj][0] + S.ssum[pj][1]));
-    }
-    wait_stores();
-    __syncthreads();
-    if (tid == 0) S.last = counter_add(&g_cnt_gu[a * nbn + nb], 1) == ksn - 1;
-    __syncthreads();
-    if (!S.last) return;
-    if (tid == 0) counter_reset(&g_cnt_gu[a * nbn + nb]);
-    if (tid < 256) S.tot[tid] = sum_agent(A.part_gu + (size_t)(a * nbn + nb) * ksn * 256 + tid, ksn, 256);
+    if (l == 0) S.u.gu.ssw[wv] = ssum;
     __syncthreads();
     if (wv != 0) return;
-    float g0 = S.tot[2 * l], g1 = S.tot[2 * l + 1], u0 = S.tot[128 + 2 * l], u1 = S.tot[129 + 2 * l];
-    wave_fwht128(g0, g1);
-    wave_fwht128(u0, u1);
-    const int c = nb * 128 + 2 * l;
-    g0 = (float)(half_t)(g0 * kRsqrt128 * (float)sc_g.x);
-    g1 = (float)(half_t)(g1 * kRsqrt128 * (float)sc_g.y);
-    u0 = (float)(half_t)(u0 * kRsqrt128 * (float)sc_u.x);
-    u1 = (float)(half_t)(u1 * kRsqrt128 * (float)sc_u.y);
-    float a0 = (float)(half_t)(g0 / (1.0f + expf(-g0)) * u0);
-    float a1 = (float)(half_t)(g1 / (1.0f + expf(-g1)) * u1);
-    a0 = (float)(half_t)(a0 * (float)sc_d.x);
-    a1 = (float)(half_t)(a1 * (float)sc_d.y);
-    wave_fwht128(a0, a1);
-    const half2_t hv = half2_t{(half_t)(a0 * kRsqrt128), (half_t)(a1 * kRsqrt128)};
-    __hip_atomic_store((uint32_t*)(A.abuf + (size_t)a * I + c), __builtin_bit_cast(uint32_t, hv), __ATOMIC_RELAXED,
-                       __HIP_MEMORY_SCOPE_AGENT);
-    wait_stores();
-    if (l == 0) counter_add(&g_ready[a], 1);
+    float t = 0.f, xs = 0.f;                     // column l of the group: the eight blocks in order
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+        t += S.red[w][l];
+        xs += S.u.gu.ssw[w];
+    }
+    st_tag(A.xpart + ((size_t)a * ksn + ks) * 2 * I + pj * I + cg * 64 + l, tag, kC1 * t + kC2 * xs);
 }
 
 // down WG per (pair, 128-column block of H) over the full K = I: the 4-row chunks of the I/16 tile-rows go round-robin
@@ -386,7 +459,15 @@ __device__ __forceinline__ void down_wg(const DecodeArgs& A, int blk, LayerShare
         sc_d = *(const half2_t*)((const half_t*)(base + A.g.off_svh_d) + nb * 128 + 2 * l);
         wgt = masked ? 0.f : A.w[a];
     }
-    if (tid == 0) {                              // wait for the pair's whole abuf (all I/128 gate/up epilogues)
+    half2_t e_g{}, e_u{}, e_d{};                 // gate/up epilogue scales of this wave's first 128-column block of I
+    if (wv < I / 128) {
+        const int cI = wv * 128 + 2 * l;
+        e_g = *(const half2_t*)((const half_t*)(base + A.g.off_svh_g) + cI);
+        e_u = *(const half2_t*)((const half_t*)(base + A.g.off_svh_u) + cI);
+        e_d = *(const half2_t*)((const half_t*)(base + A.g.off_suh_d) + cI);
+    }
+    const unsigned tag = call_tag();
+    if (tid == 0) {                              // write-through target of a miss
         int64_t f = !A.fused && A.fill ? A.fill[e] : 0;
         if (A.fused && miss) {                   // the write-through target is the ensure's decision
             wait_count(&g_cnt_all[2], 1);
@@ -394,22 +475,74 @@ __device__ __forceinline__ void down_wg(const DecodeArgs& A, int blk, LayerShare
         }
         if (f && A.n_vict_wg) wait_count(&g_cnt_all[1], A.n_vict_wg);      // and for the victims' old bytes
         S.fdst = f;
-        int it = 0;
-        while (__hip_atomic_load(&g_ready[a], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < I / 128) {
-            __builtin_amdgcn_s_sleep(1);
-            if (++it > kSpinMax) {
-                atomicAdd(&g_status[0], 1);
-                break;
+    }
+    const int ksn = gu_kslices(H);
+    half2_t* xs = S.u.dn.xd;                     // the pair's down input, [I/2] half2
+    // gate/up epilogue of the pair, one 128-column block b of I per wave and round: wait for the sums of its 4 * ksn
+    // gate/up workgroups (gate and up, column groups 2b and 2b + 1, every K-slice), then output Hadamards * svh,
+    // SiLU(g)*u, * suh_d, down-input Hadamard (the reference's fp16 rounding points)
+    {
+        const uint64_t* pg = A.xpart + (size_t)a * ksn * 2 * I;
+        for (int b = wv; b < I / 128; b += kWaves) {
+            const int cI = b * 128 + 2 * l;
+            {   // one word per producing workgroup first: lane s < 4 ksn watches (slice s >> 2, proj, group)
+                const int sk = l >> 2, sp = (l >> 1) & 1, sg = l & 1;
+                const uint64_t* q = pg + (size_t)sk * 2 * I + sp * I + (2 * b + sg) * 64;
+                int it = 0;
+                for (;;) {
+                    const bool ok = l >= 4 * ksn || tag_is(ld_tag(q), tag);
+                    if (__all(ok) || spin_out(it)) break;
+                }
             }
+            float g0 = 0.f, g1 = 0.f, u0 = 0.f, u1 = 0.f;
+            for (int k0 = 0; k0 < ksn; k0 += 2) {        // the K-slices in order, two at a time
+                uint64_t v[2][4];
+                int it = 0;
+                for (;;) {
+                    bool ok = true;
+#pragma unroll
+                    for (int k = 0; k < 2; ++k) {
+                        const uint64_t* q = pg + (size_t)(k0 + k) * 2 * I + cI;
+                        const bool in = k0 + k < ksn;
+                        v[k][0] = in ? ld_tag(q) : 0;
+                        v[k][1] = in ? ld_tag(q + 1) : 0;
+                        v[k][2] = in ? ld_tag(q + I) : 0;
+                        v[k][3] = in ? ld_tag(q + I + 1) : 0;
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) ok = ok && (!in || tag_is(v[k][i], tag));
+                    }
+                    if (__all(ok) || spin_out(it)) break;
+                }
+#pragma unroll
+                for (int k = 0; k < 2; ++k)
+                    if (k0 + k < ksn) {
+                        g0 += tag_val(v[k][0]);
+                        g1 += tag_val(v[k][1]);
+                        u0 += tag_val(v[k][2]);
+                        u1 += tag_val(v[k][3]);
+                    }
+            }
+            if (b != wv) {
+                e_g = *(const half2_t*)((const half_t*)(base + A.g.off_svh_g) + cI);
+                e_u = *(const half2_t*)((const half_t*)(base + A.g.off_svh_u) + cI);
+                e_d = *(const half2_t*)((const half_t*)(base + A.g.off_suh_d) + cI);
+            }
+            wave_fwht128(g0, g1);
+            wave_fwht128(u0, u1);
+            g0 = (float)(half_t)(g0 * kRsqrt128 * (float)e_g.x);
+            g1 = (float)(half_t)(g1 * kRsqrt128 * (float)e_g.y);
+            u0 = (float)(half_t)(u0 * kRsqrt128 * (float)e_u.x);
+            u1 = (float)(half_t)(u1 * kRsqrt128 * (float)e_u.y);
+            float a0 = (float)(half_t)(g0 / (1.0f + expf(-g0)) * u0);
+            float a1 = (float)(half_t)(g1 / (1.0f + expf(-g1)) * u1);
+            a0 = (float)(half_t)(a0 * (float)e_d.x);
+            a1 = (float)(half_t)(a1 * (float)e_d.y);
+            wave_fwht128(a0, a1);
+            xs[b * 64 + l] = half2_t{(half_t)(a0 * kRsqrt128), (half_t)(a1 * kRsqrt128)};
         }
     }
     __syncthreads();
     uint32_t* trd = S.fdst ? (uint32_t*)((uint8_t*)S.fdst + A.g.gu_bytes) : nullptr;
-    half2_t* xs = S.xd;                          // abuf of the pair, [I/2] half2
-    for (int i = tid; i < I / 2; i += kThreads)
-        xs[i] = __builtin_bit_cast(half2_t, __hip_atomic_load((const uint32_t*)(A.abuf + (size_t)a * I) + i,
-                                                              __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
-    __syncthreads();
     float acc[GV::NCP][2], tacc[GV::NCP][2];
     float xsum = 0.f;
 #pragma unroll
@@ -451,49 +584,68 @@ __device__ __forceinline__ void down_wg(const DecodeArgs& A, int blk, LayerShare
     wave_fwht128(v0, v1);
     const int c = nb * 128 + 2 * l;
     const float sc = kRsqrt128 * wgt;
-    float* y = A.ybuf + (size_t)a * H + c;
-    st_agent(y, v0 * sc * (float)sc_d.x);
-    st_agent(y + 1, v1 * sc * (float)sc_d.y);
-    // combine: the last pair of row m to finish this 128-column block sums the top-k outputs in k order
-    wait_stores();
-    int old = 0;
-    if (l == 0) old = counter_add(&g_cnt_c[m * nbn + nb], 1);
-    old = __shfl(old, 0, 64);
-    if (old != A.topk - 1) return;
-    if (l == 0) counter_reset(&g_cnt_c[m * nbn + nb]);
-    const float* yb = A.ybuf + (size_t)(m * A.topk) * H + c;
+    v0 = v0 * sc * (float)sc_d.x;
+    v1 = v1 * sc * (float)sc_d.y;
+    const int k = a % A.topk;
+    uint64_t* yb = A.xy + (size_t)(m * A.topk) * H + c;
+    if (k != A.topk - 1) {                       // y of this pick for the row's combiner
+        st_tag(yb + (size_t)k * H, tag, v0);
+        st_tag(yb + (size_t)k * H + 1, tag, v1);
+        return;
+    }
+    // combiner of (row m, block nb): the other picks' y in k order (they have lower workgroup ids), then its own
     float o0 = 0.f, o1 = 0.f;
-    for (int k0 = 0; k0 < A.topk; k0 += 16) {    // one round of loads for up to 16 picks
-        float v[16][2];
+    for (int k0 = 0; k0 < A.topk - 1; k0 += 8) {
+        uint64_t w[8][2];
+        int it = 0;
+        for (;;) {
+            bool ok = true;
 #pragma unroll
-        for (int j = 0; j < 16; ++j) {
-            const bool ok = k0 + j < A.topk;
-            v[j][0] = ok ? ld_agent(yb + (size_t)(k0 + j) * H) : 0.f;
-            v[j][1] = ok ? ld_agent(yb + (size_t)(k0 + j) * H + 1) : 0.f;
+            for (int j = 0; j < 8; ++j) {
+                const bool in = k0 + j < A.topk - 1;
+                w[j][0] = in ? ld_tag(yb + (size_t)(k0 + j) * H) : 0;
+                w[j][1] = in ? ld_tag(yb + (size_t)(k0 + j) * H + 1) : 0;
+                ok = ok && (!in || (tag_is(w[j][0], tag) && tag_is(w[j][1], tag)));
+            }
+            if (__all(ok) || spin_out(it)) break;
         }
 #pragma unroll
-        for (int j = 0; j < 16; ++j)
-            if (k0 + j < A.topk) {
-                o0 += v[j][0];
-                o1 += v[j][1];
+        for (int j = 0; j < 8; ++j)
+            if (k0 + j < A.topk - 1) {
+                o0 += tag_val(w[j][0]);
+                o1 += tag_val(w[j][1]);
             }
     }
+    o0 += v0;
+    o1 += v1;
     const size_t oo = (size_t)m * A.out_stride + c;
     st_act(A.out, A.x_dt, oo, o0);
     st_act(A.out, A.x_dt, oo + 1, o1);
-    // the last (row, block) of the layer: clear the ready counts and commit the cache fills
-    if (l == 0) old = counter_add(&g_cnt_all[0], 1);
-    old = __shfl(old, 0, 64);
-    if (old != A.M * nbn - 1) return;
+    const int nfin = A.M * nbn, me = m * nbn + nb;
+    if (me != nfin - 1) {                        // done: the last combiner finishes the call
+        if (l == 0) __hip_atomic_store(&g_cflag[me], tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        return;
+    }
+    // the last (row, block) of the layer: wait for every other combiner (lower ids), then advance the epoch and commit
+    // the cache fills
+    {
+        int it = 0;
+        for (;;) {
+            bool ok = true;
+            for (int i = l; i < nfin - 1; i += 64)
+                ok = ok && __hip_atomic_load(&g_cflag[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == tag;
+            if (__all(ok) || spin_out(it)) break;
+        }
+    }
     if (l == 0) {
-        counter_reset(&g_cnt_all[0]);
         if (A.n_vict_wg) {                       // every victim workgroup has counted itself: clear for the next call
             wait_count(&g_cnt_all[1], A.n_vict_wg);
             counter_reset(&g_cnt_all[1]);
         }
         if (A.fused) wait_count(&g_cnt_all[2], 1);
+        const unsigned ep = tag == ~0u ? 0u : tag;   // the next call's tag is never 0 (the zeroed buffer)
+        __hip_atomic_store(&g_epoch, ep, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
-    for (int i = l; i < A.npairs; i += 64) counter_reset(&g_ready[i]);
     if (A.fused) {
         // the ensure's in-place rewrite of the caller's picks (masked -> safe expert, weight 0), deferred to here
         // because every pair read them during the call; the mask rule gives the same answer now (see pair_lookup)
@@ -532,7 +684,7 @@ __global__ void __launch_bounds__(kThreads) moe_layer_kernel(DecodeArgs A) {
                                                                                      : sizeof(EnsureShared)];
     LayerShared& S = *reinterpret_cast<LayerShared*>(lds);
     const int nv = A.n_vict_wg;
-    const int n_gu = A.npairs * (A.g.I / 128) * gu_slices(A.g.H);
+    const int n_gu = A.npairs * 4 * (A.g.I / 128) * gu_kslices(A.g.H);
     int b = blockIdx.x;
     if (A.fused) {                               // workgroup 0: the cache's ensure (never waits on another workgroup)
         if (b == 0) {
@@ -574,7 +726,7 @@ __global__ void __launch_bounds__(256) dequant_kernel(const uint32_t* __restrict
 // ---- host launchers ------------------------------------------------------------------------------------------------
 
 hipError_t launch_moe_layer(int K, const DecodeArgs& a, hipStream_t s) {
-    const int n_gu = a.npairs * (a.g.I / 128) * gu_slices(a.g.H);
+    const int n_gu = a.npairs * 4 * (a.g.I / 128) * gu_kslices(a.g.H);
     const int n_dn = a.npairs * (a.g.H / 128);
     dim3 grid((unsigned)(a.fused + a.n_vict_wg + n_gu + n_dn));
     if (K == 2) hipLaunchKernelGGL(moe_layer_kernel<2>, grid, dim3(kThreads), 0, s, a);
