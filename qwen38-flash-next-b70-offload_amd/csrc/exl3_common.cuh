@@ -112,9 +112,33 @@ __host__ __device__ constexpr int val_col(int p, int u) {
 
 __device__ __forceinline__ int lane_id() { return __lane_id(); }
 
+// v of lane (lane ^ m) for m = 1, 2, ..., 32 without the LDS crossbar: DPP within 16-lane rows (xor 1, 2: quad
+// permutes; xor 4: half-row mirror then quad xor 3; xor 8: row rotate by 8), gfx950 permlane swaps across rows
+// (xor 16, 32: swap, then take the half holding the partner). The whole wave must be active.
+__device__ __forceinline__ float lane_xor(float v, int m) {
+    const int x = __float_as_int(v);
+    switch (m) {
+        case 1: return __int_as_float(__builtin_amdgcn_mov_dpp(x, 0xB1, 0xF, 0xF, false));    // quad_perm [1,0,3,2]
+        case 2: return __int_as_float(__builtin_amdgcn_mov_dpp(x, 0x4E, 0xF, 0xF, false));    // quad_perm [2,3,0,1]
+        case 4: {
+            const int h = __builtin_amdgcn_mov_dpp(x, 0x141, 0xF, 0xF, false);                // row_half_mirror: ^7
+            return __int_as_float(__builtin_amdgcn_mov_dpp(h, 0x1B, 0xF, 0xF, false));        // quad_perm [3,2,1,0]
+        }
+        case 8: return __int_as_float(__builtin_amdgcn_mov_dpp(x, 0x128, 0xF, 0xF, false));   // row_ror:8
+        case 16: {
+            const auto r = __builtin_amdgcn_permlane16_swap((unsigned)x, (unsigned)x, false, false);
+            return __uint_as_float((__lane_id() & 16) ? r[0] : r[1]);
+        }
+        default: {
+            const auto r = __builtin_amdgcn_permlane32_swap((unsigned)x, (unsigned)x, false, false);
+            return __uint_as_float((__lane_id() & 32) ? r[0] : r[1]);
+        }
+    }
+}
+
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
+    for (int m = 32; m >= 1; m >>= 1) v += lane_xor(v, m);
     return v;
 }
 
@@ -130,7 +154,7 @@ __device__ __forceinline__ void wave_fwht128(float& v0, float& v1) {
     const int l = lane_id();
 #pragma unroll
     for (int m = 1; m < 64; m <<= 1) {
-        float p0 = __shfl_xor(v0, m, 64), p1 = __shfl_xor(v1, m, 64);
+        float p0 = lane_xor(v0, m), p1 = lane_xor(v1, m);
         bool up = (l & m) != 0;
         v0 = up ? p0 - v0 : v0 + p0;
         v1 = up ? p1 - v1 : v1 + p1;

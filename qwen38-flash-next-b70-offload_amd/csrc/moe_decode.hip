@@ -152,8 +152,8 @@ struct Gemv8 {
         const int p = l % G, j = l / G;
 #pragma unroll
         for (int mm = 1; mm < L; mm <<= 1) {
-            acc[0] += __shfl_xor(acc[0], mm, 64);
-            acc[1] += __shfl_xor(acc[1], mm, 64);
+            acc[0] += lane_xor(acc[0], mm);
+            acc[1] += lane_xor(acc[1], mm);
         }
         col0 = (cp * NTW + j) * 16 + ((V * p) >> 5);
         return (p % L) == 0;
@@ -224,13 +224,13 @@ struct Gemv4 {
         const int p = l % G, j = l / G;
 #pragma unroll
         for (int mm = 1; mm < L; mm <<= 1) {
-            acc[0] += __shfl_xor(acc[0], mm, 64);
-            acc[1] += __shfl_xor(acc[1], mm, 64);
+            acc[0] += lane_xor(acc[0], mm);
+            acc[1] += lane_xor(acc[1], mm);
         }
 #pragma unroll
         for (int mm = 4 * G; mm < 64; mm <<= 1) {
-            acc[0] += __shfl_xor(acc[0], mm, 64);
-            acc[1] += __shfl_xor(acc[1], mm, 64);
+            acc[0] += lane_xor(acc[0], mm);
+            acc[1] += lane_xor(acc[1], mm);
         }
         col0 = tcol(q, j) * 16 + ((V * p) >> 5);
         return j < 4 && (p % L) == 0;
