@@ -47,6 +47,8 @@ struct DecodeArgs {
     const int32_t* fill_list;                      // [1 + E]
     uint64_t* xpart;                               // tagged gate/up sums [npairs][H/1024 slices][2I] (exchange buffer)
     uint64_t* xy;                                  // tagged y of every pick [npairs][H] (exchange buffer)
+    uint64_t* xstart;                              // started word of every gate/up and down workgroup (exchange buffer)
+    int n_gu;                                      // gate/up workgroups
     void* out; int64_t out_stride;                 // [M, H], same dtype as x
     BlobGeom g;
     VictimArgs va;                                 // victim write-back (cached calls with victims on)
@@ -106,8 +108,10 @@ static inline size_t decode_workspace_bytes(int npairs, int H, int I) {
     return align256((size_t)npairs * 8);
 }
 // tagged words a decode call exchanges between workgroups (library-owned buffer, zeroed when allocated)
+static inline int decode_gu_workgroups(int npairs, int H, int I) { return npairs * 4 * (I / 128) * gu_kslices(H); }
 static inline size_t decode_exchange_words(int npairs, int H, int I) {
-    return (size_t)npairs * ((size_t)gu_kslices(H) * 2 * I + H);
+    return (size_t)npairs * ((size_t)gu_kslices(H) * 2 * I + H) + decode_gu_workgroups(npairs, H, I) +
+           (size_t)npairs * (H / 128);
 }
 
 }  // namespace exl3

@@ -245,6 +245,8 @@ static int forward_impl(const void* x, int x_dtype, int64_t x_stride, int M, int
     a.fill_list = fill_list;
     a.xpart = xb;
     a.xy = xb + (size_t)npairs * gu_kslices(H) * 2 * I;
+    a.xstart = a.xy + (size_t)npairs * H;
+    a.n_gu = decode_gu_workgroups(npairs, H, I);
     a.out = out;
     a.out_stride = out_stride;
     a.g = blob_geom(H, I, K);

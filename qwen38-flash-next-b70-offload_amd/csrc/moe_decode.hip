@@ -9,8 +9,9 @@
 //     (bounded) for the pair's gate/up sums, run the gate/up epilogue of the pair themselves (output Hadamards * svh,
 //     SiLU(g)*u, *suh_d, down-input Hadamard -> the down input in LDS, fp16), GEMV with an in-WG reduction, epilogue
 //     (output Hadamard * w * svh_d) -> y (fp32). The WG of the last pick of a row (the combiner of that row and block)
-//     waits for the other picks' y and sums the top-k y's in k order into out; the combiner of the last (row, block)
-//     waits for every other combiner, commits the expert-cache fills (ptrs[e] = fill[e]; fill[e] = 0) and advances
+//     waits with all its waves for the other picks' y and sums the top-k y's in k order into out; the combiner of the
+//     last (row, block) also checks that every other gate/up and down workgroup has consumed its inputs (each raises
+//     a started word once it has), then commits the expert-cache fills (ptrs[e] = fill[e]; fill[e] = 0) and advances
 //     the call epoch.
 // Every value handed from one workgroup to another is a tagged word (tag = call epoch + 1 in the high half, the fp32
 // value in the low half) written with one 64-bit agent-scope store into a library-owned zeroed buffer: a consumer polls
@@ -32,7 +33,6 @@
 
 namespace exl3 {
 
-__device__ unsigned g_cflag[kMaxRows * 64];  // combiner of (row m, block nb) sets g_cflag[m * nbn + nb] = tag
 __device__ unsigned g_epoch;                 // call epoch (advanced by the last workgroup of each call; never ~0u)
 
 __device__ int g_cnt_all[4];          // [1] victim reads done, [2] fused ensure done
@@ -239,6 +239,7 @@ struct Gemv4 {
 
 constexpr int kWaves = 8;                    // waves per workgroup (both kinds)
 constexpr int kThreads = 64 * kWaves;
+constexpr int kCombRound = 2 * kWaves;       // picks whose y a combiner loads per round (two per wave)
 
 struct GateUpShared {
     half2_t xq[kWaves][64];                  // per wave: Hadamard-transformed x * suh of its 128-row block
@@ -246,6 +247,7 @@ struct GateUpShared {
 };
 struct DownShared {
     half2_t xd[kMaxI / 2];                   // the pair's down input (fp16), [I/2]
+    float yc[kCombRound][128];               // combiner: the other picks' y of its block, one round of picks
 };
 struct LayerShared {
     union {
@@ -426,6 +428,7 @@ __device__ __forceinline__ void gateup_wg(const DecodeArgs& A, int blk, LayerSha
         xs += S.u.gu.ssw[w];
     }
     st_tag(A.xpart + ((size_t)a * ksn + ks) * 2 * I + pj * I + cg * 64 + l, tag, kC1 * t + kC2 * xs);
+    if (l == 0) st_tag(A.xstart + blk, tag, 0.f);    // its inputs (ids, pointers, fill target) are consumed
 }
 
 // down WG per (pair, 128-column block of H) over the full K = I: the 4-row chunks of the I/16 tile-rows go round-robin
@@ -542,6 +545,7 @@ __device__ __forceinline__ void down_wg(const DecodeArgs& A, int blk, LayerShare
         }
     }
     __syncthreads();
+    if (tid == 0) st_tag(A.xstart + A.n_gu + blk, tag, 0.f);     // ids, pointers, w and fill target consumed
     uint32_t* trd = S.fdst ? (uint32_t*)((uint8_t*)S.fdst + A.g.gu_bytes) : nullptr;
     float acc[GV::NCP][2], tacc[GV::NCP][2];
     float xsum = 0.f;
@@ -574,69 +578,77 @@ __device__ __forceinline__ void down_wg(const DecodeArgs& A, int blk, LayerShare
         }
     }
     __syncthreads();
-    if (wv != 0) return;
-    float v0 = 0.f, v1 = 0.f;
-#pragma unroll
-    for (int w = 0; w < kWaves; ++w) {
-        v0 += S.red[w][2 * l];
-        v1 += S.red[w][2 * l + 1];
-    }
-    wave_fwht128(v0, v1);
-    const int c = nb * 128 + 2 * l;
-    const float sc = kRsqrt128 * wgt;
-    v0 = v0 * sc * (float)sc_d.x;
-    v1 = v1 * sc * (float)sc_d.y;
     const int k = a % A.topk;
+    const bool comb = k == A.topk - 1;           // combiner of (row m, block nb): the row's last pick, highest id
+    if (wv != 0 && !comb) return;
+    const int c = nb * 128 + 2 * l;
+    float v0 = 0.f, v1 = 0.f;
     uint64_t* yb = A.xy + (size_t)(m * A.topk) * H + c;
-    if (k != A.topk - 1) {                       // y of this pick for the row's combiner
-        st_tag(yb + (size_t)k * H, tag, v0);
-        st_tag(yb + (size_t)k * H + 1, tag, v1);
-        return;
+    if (wv == 0) {
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) {
+            v0 += S.red[w][2 * l];
+            v1 += S.red[w][2 * l + 1];
+        }
+        wave_fwht128(v0, v1);
+        const float sc = kRsqrt128 * wgt;
+        v0 = v0 * sc * (float)sc_d.x;
+        v1 = v1 * sc * (float)sc_d.y;
+        if (!comb) {                             // y of this pick for the row's combiner
+            st_tag(yb + (size_t)k * H, tag, v0);
+            st_tag(yb + (size_t)k * H + 1, tag, v1);
+            return;
+        }
     }
-    // combiner of (row m, block nb): the other picks' y in k order (they have lower workgroup ids), then its own
+    // combiner: the other picks' y (lower workgroup ids) loaded by all waves, two picks per wave and round, summed by
+    // wave 0 in k order after its own pick's; the last combiner also polls every other workgroup's started word in
+    // the first round
+    const int nfin = A.M * nbn, me = m * nbn + nb;
+    const bool fin = me == nfin - 1;
+    const int nstart = A.n_gu + A.npairs * nbn - 1;       // every workgroup before this one
     float o0 = 0.f, o1 = 0.f;
-    for (int k0 = 0; k0 < A.topk - 1; k0 += 8) {
-        uint64_t w[8][2];
+    for (int k0 = 0; k0 < A.topk - 1 || (fin && k0 == 0); k0 += kCombRound) {
+        uint64_t yw[2][2];
         int it = 0;
         for (;;) {
             bool ok = true;
 #pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const bool in = k0 + j < A.topk - 1;
-                w[j][0] = in ? ld_tag(yb + (size_t)(k0 + j) * H) : 0;
-                w[j][1] = in ? ld_tag(yb + (size_t)(k0 + j) * H + 1) : 0;
-                ok = ok && (!in || (tag_is(w[j][0], tag) && tag_is(w[j][1], tag)));
+            for (int i = 0; i < 2; ++i) {
+                const int j = k0 + wv + kWaves * i;
+                const bool in = j < A.topk - 1;
+                yw[i][0] = in ? ld_tag(yb + (size_t)j * H) : 0;
+                yw[i][1] = in ? ld_tag(yb + (size_t)j * H + 1) : 0;
+                ok = ok && (!in || (tag_is(yw[i][0], tag) && tag_is(yw[i][1], tag)));
             }
-            if (__all(ok) || spin_out(it)) break;
+            if (fin && k0 == 0)
+                for (int i = tid; i < nstart; i += kThreads) ok = ok && tag_is(ld_tag(A.xstart + i), tag);
+            if (__syncthreads_and(ok) || spin_out(it)) break;
         }
 #pragma unroll
-        for (int j = 0; j < 8; ++j)
+        for (int i = 0; i < 2; ++i) {
+            const int j = wv + kWaves * i;
             if (k0 + j < A.topk - 1) {
-                o0 += tag_val(w[j][0]);
-                o1 += tag_val(w[j][1]);
+                S.u.dn.yc[j][2 * l] = tag_val(yw[i][0]);
+                S.u.dn.yc[j][2 * l + 1] = tag_val(yw[i][1]);
             }
+        }
+        __syncthreads();
+        if (wv == 0)
+            for (int j = 0; j < kCombRound && k0 + j < A.topk - 1; ++j) {
+                o0 += S.u.dn.yc[j][2 * l];
+                o1 += S.u.dn.yc[j][2 * l + 1];
+            }
+        __syncthreads();
     }
+    if (wv != 0) return;
     o0 += v0;
     o1 += v1;
     const size_t oo = (size_t)m * A.out_stride + c;
     st_act(A.out, A.x_dt, oo, o0);
     st_act(A.out, A.x_dt, oo + 1, o1);
-    const int nfin = A.M * nbn, me = m * nbn + nb;
-    if (me != nfin - 1) {                        // done: the last combiner finishes the call
-        if (l == 0) __hip_atomic_store(&g_cflag[me], tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        return;
-    }
-    // the last (row, block) of the layer: wait for every other combiner (lower ids), then advance the epoch and commit
+    if (!fin) return;
+    // the last (row, block) of the layer: every other workgroup has consumed its inputs; advance the epoch and commit
     // the cache fills
-    {
-        int it = 0;
-        for (;;) {
-            bool ok = true;
-            for (int i = l; i < nfin - 1; i += 64)
-                ok = ok && __hip_atomic_load(&g_cflag[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == tag;
-            if (__all(ok) || spin_out(it)) break;
-        }
-    }
     if (l == 0) {
         if (A.n_vict_wg) {                       // every victim workgroup has counted itself: clear for the next call
             wait_count(&g_cnt_all[1], A.n_vict_wg);
@@ -684,7 +696,7 @@ __global__ void __launch_bounds__(kThreads) moe_layer_kernel(DecodeArgs A) {
                                                                                      : sizeof(EnsureShared)];
     LayerShared& S = *reinterpret_cast<LayerShared*>(lds);
     const int nv = A.n_vict_wg;
-    const int n_gu = A.npairs * 4 * (A.g.I / 128) * gu_kslices(A.g.H);
+    const int n_gu = A.n_gu;
     int b = blockIdx.x;
     if (A.fused) {                               // workgroup 0: the cache's ensure (never waits on another workgroup)
         if (b == 0) {
@@ -726,7 +738,7 @@ __global__ void __launch_bounds__(256) dequant_kernel(const uint32_t* __restrict
 // ---- host launchers ------------------------------------------------------------------------------------------------
 
 hipError_t launch_moe_layer(int K, const DecodeArgs& a, hipStream_t s) {
-    const int n_gu = a.npairs * 4 * (a.g.I / 128) * gu_kslices(a.g.H);
+    const int n_gu = a.n_gu;
     const int n_dn = a.npairs * (a.g.H / 128);
     dim3 grid((unsigned)(a.fused + a.n_vict_wg + n_gu + n_dn));
     if (K == 2) hipLaunchKernelGGL(moe_layer_kernel<2>, grid, dim3(kThreads), 0, s, a);
