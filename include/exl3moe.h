@@ -73,8 +73,12 @@ int exl3_set_decision_log(int32_t* buf, int64_t cap_records);
 
 /* ---- routed-expert MoE --------------------------------------------------------------------------------------------- */
 
-/* workspace bytes of an exl3_moe_forward call with these sizes (decode kernels for M < prefill_min_m, the prefill
- * path otherwise: sorted routing, input Hadamards [M topk][2][H] fp16, abuf [M topk][I] fp16, y [M topk][H] fp16) */
+/* workspace bytes of an exl3_moe_forward call with these sizes (decode kernels for M < prefill_min_m: the blob
+ * pointer of every pick; the prefill path otherwise: sorted routing, input Hadamards [M topk][2][H] fp16, abuf
+ * [M topk][I] fp16, y [M topk][H] fp16). The decode kernel's cross-workgroup exchange is not in the workspace: the
+ * library owns one zeroed device buffer per device and grows it when a call needs more (hipMalloc + hipMemset, after
+ * a device synchronisation); a call that would grow it while its stream is being captured fails with
+ * EXL3_EUNSUPPORTED, so run one call of the largest size before capturing. */
 size_t exl3_moe_forward_workspace(int M, int H, int I, int topk, int n_experts);
 
 /* moe_forward (a8:1221-1225 -> moe_forward_impl a8:1263-1314): out[m] = sum_k w[m,k] * expert(ids[m,k])(x[m]).
