@@ -135,6 +135,15 @@ __device__ void ensure_wg(const EnsureArgs& A, EnsureShared& Z, int* done) {
         }
         if (lane < P) Z.pid[lane] = id;
         pslot = so;
+        if (A.pair_own && lane < P) {            // the first pick of each post-mask expert writes it through
+            int own = 1;
+            for (int j = 0; j < lane; ++j)
+                if (Z.pid[j] == id) {
+                    own = 0;
+                    break;
+                }
+            st_agent_i32(A.pair_own + lane, own);
+        }
         cnt += __popcll(bal);
         if (A.ram_res && lane == 0) A.ring[0] = cnt;
         if (lane == 0) Z.sh[5] = cnt;

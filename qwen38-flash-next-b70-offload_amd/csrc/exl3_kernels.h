@@ -33,6 +33,8 @@ struct EnsureArgs {
     int32_t* vict;                                 // victim list [1 + 2E] or null
     int32_t* log; int64_t log_cap;                 // decision log (debug) or null: [count, records...]
     int64_t* pair_ptr;                             // out: blob pointer of every post-mask pick [P] (or null)
+    int32_t* pair_own;                             // out (ensure inside the layer kernel): 1 if pick i is the first
+                                                   // pick of its post-mask expert [P] (or null)
 };
 
 struct DecodeArgs {
@@ -54,6 +56,7 @@ struct DecodeArgs {
     VictimArgs va;                                 // victim write-back (cached calls with victims on)
     int n_vict_wg, vict_chunks;                    // victim-copy workgroups (first in the grid) and chunks per victim
     int fused;                                     // 1: workgroup 0 runs the cache's ensure (ens) inside the launch
+    int vict_inline;                               // 1: the writers of a miss copy the victim's old bytes themselves
     EnsureArgs ens;
 };
 

@@ -195,7 +195,7 @@ static int forward_impl(const void* x, int x_dtype, int64_t x_stride, int M, int
                         int topk, const int64_t* ptrs, int I, int K, int E, void* out, int64_t out_stride, void* ws,
                         size_t ws_bytes, hipStream_t st, const int64_t* fill, int64_t* commit_ptrs, int64_t* commit_fill,
                         const int32_t* fill_list, const int64_t* pair_ptr, const VictimArgs* va = nullptr,
-                        int max_victims = 0, const EnsureArgs* fused_ens = nullptr) {
+                        int max_victims = 0, const EnsureArgs* fused_ens = nullptr, bool vict_inline = false) {
     if (!fill && use_prefill(M)) {
         if (H % 256) return fail(EXL3_EUNSUPPORTED, "moe prefill: H %% 256 == 0 required (H=%d)", H);
         if ((int64_t)M * topk > (1 << 28)) return fail(EXL3_EUNSUPPORTED, "moe prefill: %d x %d pairs", M, topk);
@@ -250,10 +250,14 @@ static int forward_impl(const void* x, int x_dtype, int64_t x_stride, int M, int
     a.out = out;
     a.out_stride = out_stride;
     a.g = blob_geom(H, I, K);
-    if (va && max_victims > 0) {                  // victim write-back: the first workgroups of the layer kernel
+    if (va && max_victims > 0) {
         a.va = *va;
-        a.vict_chunks = (int)((a.g.blob + va->chunk_bytes - 1) / va->chunk_bytes);
-        a.n_vict_wg = max_victims * a.vict_chunks;
+        if (vict_inline) {                        // victim write-back by the writers of each miss
+            a.vict_inline = 1;
+        } else {                                  // victim write-back: the first workgroups of the layer kernel
+            a.vict_chunks = (int)((a.g.blob + va->chunk_bytes - 1) / va->chunk_bytes);
+            a.n_vict_wg = max_victims * a.vict_chunks;
+        }
     }
     if (fused_ens) {                              // the ensure runs as workgroup 0 of the layer kernel
         a.fused = 1;
@@ -339,6 +343,10 @@ int exl3_moe_forward_cached(const void* x, int x_dtype, int64_t x_stride, int M,
         hipError_t e = launch_ensure(ea, st);
         if (e != hipSuccess) return hip_fail(e, "ensure launch");
     }
+    // with the ensure inside the layer kernel and slots at the blob size (one layout for victim and miss), the writers
+    // of each miss copy the victim's old bytes before overwriting them: no victim workgroups in the launch
+    const bool vict_inline = fused && g_cfg.vict && ea.blob == g.blob;
+    if (vict_inline) ea.pair_own = (int32_t*)pair_ptr_area(workspace, P, H, I);
     VictimArgs va{};
     int mv = 0;
     if (g_cfg.vict) {
@@ -355,7 +363,8 @@ int exl3_moe_forward_cached(const void* x, int x_dtype, int64_t x_stride, int M,
     int64_t* pl = ptrs_all + (int64_t)layer * E;
     int64_t* fl = fill_all + (int64_t)layer * E;
     return forward_impl(x, x_dtype, x_stride, M, H, topk_ids, topk_w, topk, pl, I, K, E, out, out_stride, workspace,
-                        workspace_bytes, st, fl, pl, fl, fill_list, ea.pair_ptr, &va, mv, fused ? &ea : nullptr);
+                        workspace_bytes, st, fl, pl, fl, fill_list, ea.pair_ptr, &va, mv, fused ? &ea : nullptr,
+                        vict_inline);
 }
 
 size_t exl3_moe_align_workspace(int M, int topk, int n_experts) {

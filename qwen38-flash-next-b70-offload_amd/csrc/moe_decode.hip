@@ -119,6 +119,29 @@ struct Gemv8 {
                 for (int i = 0; i < D; ++i) trd[word_off<K>(r0 + rr, tiles_n, col_tile0 + cp * NTW + j, p, i)] = wd[cp][rr][i];
     }
 
+    // victim write-back at this wave's word positions of chunk r0: the slot's old words to the victim's RAM copy,
+    // read before the write-through replaces them (every load has returned when the stores are issued)
+    __device__ __forceinline__ void copy_old(const uint32_t* slot, uint32_t* host, int tiles_n, int r0,
+                                             int col_tile0) const {
+        const int l = lane_id();
+        const int p = l % G, j = l / G;
+#pragma unroll 1
+        for (int cp = 0; cp < NCP; ++cp) {      // one column pair at a time: few registers on the miss path
+            uint32_t old[4][D];
+#pragma unroll
+            for (int rr = 0; rr < 4; ++rr)
+#pragma unroll
+                for (int i = 0; i < D; ++i)
+                    old[rr][i] = slot[word_off<K>(r0 + rr, tiles_n, col_tile0 + cp * NTW + j, p, i)];
+            wait_stores();
+#pragma unroll
+            for (int rr = 0; rr < 4; ++rr)
+#pragma unroll
+                for (int i = 0; i < D; ++i)
+                    host[word_off<K>(r0 + rr, tiles_n, col_tile0 + cp * NTW + j, p, i)] = old[rr][i];
+        }
+    }
+
     // xh: activations of the 128-row block, [tile-row][8] half2; xrow0 = first tile-row of this wave in the block
     __device__ __forceinline__ void compute(int xrow0, const half2_t* xh, float (&acc)[NCP][2]) const {
         const int l = lane_id();
@@ -196,6 +219,22 @@ struct Gemv4 {
             for (int i = 0; i < D; ++i) trd[word_off<K>(rt0 + trow(ps, j), tiles_n, ct0 + tcol(ps, j), p, i)] = wd[ps][i];
     }
 
+    // victim write-back at this wave's word positions (see Gemv8::copy_old), one pass at a time
+    __device__ __forceinline__ void copy_old(const uint32_t* slot, uint32_t* host, int tiles_n, int rt0, int ct0) const {
+        const int l = lane_id();
+        const int p = l % G, j = l / G;
+#pragma unroll 1
+        for (int ps = 0; ps < NPS; ++ps) {
+            uint32_t old[D];
+            const int rt = rt0 + trow(ps, j), ct = ct0 + tcol(ps, j);
+#pragma unroll
+            for (int i = 0; i < D; ++i) old[i] = slot[word_off<K>(rt, tiles_n, ct, p, i)];
+            wait_stores();
+#pragma unroll
+            for (int i = 0; i < D; ++i) host[word_off<K>(rt, tiles_n, ct, p, i)] = old[i];
+        }
+    }
+
     // xq: the wave's 128-row block, [tile-row][8] half2
     __device__ __forceinline__ void compute(const half2_t* xq, float (&acc)[NCQ][2]) const {
         const int l = lane_id();
@@ -256,6 +295,7 @@ struct LayerShared {
     } u;
     float red[kWaves][128];  // per-wave column sums
     int64_t fdst;            // write-through target of the pair (0: none)
+    int fwb;                 // victims copied inline: write-back owner of that slot's old bytes (-1: none)
     int last;
 };
 
@@ -320,6 +360,22 @@ __device__ __forceinline__ void victim_wg(const DecodeArgs& A, int blk) {
 __device__ __forceinline__ const uint8_t* pair_base(const DecodeArgs& A, int a, int& e) {
     e = min(max(A.ids[a], 0), A.E - 1);          // out-of-range ids are clamped, never dereferenced
     return A.pair_ptr ? (const uint8_t*)A.pair_ptr[a] : (const uint8_t*)A.ptrs[e];
+}
+
+// Victims copied inline (slots at the blob size: a victim and the expert that replaces it share one layout): the one
+// writer of each miss (the first pick of its expert) copies the victim's old bytes at exactly the positions it is
+// about to overwrite to the victim's RAM copy (the reference's VictimCopyKernel a8:1168-1189, split over the
+// writers); the last workgroup flags the victims RAM-resident. Returns the write-back owner of the slot at f, or -1.
+__device__ __forceinline__ int inline_victim(const DecodeArgs& A, int64_t f) {
+    const int32_t* vl = A.va.vict;               // fields read once: the loop below has only loads
+    const int s = (int)((f - A.va.slot_base) / A.va.blob);
+    const int nv = ld_agent_i32(vl);
+    for (int i = 0; i < nv; ++i)
+        if (ld_agent_i32(vl + 2 + 2 * i) == s) return ld_agent_i32(vl + 1 + 2 * i);
+    return -1;
+}
+__device__ __forceinline__ uint8_t* victim_host(const DecodeArgs& A, int wb) {
+    return (uint8_t*)(A.va.host_base[wb / A.va.E] + (int64_t)(wb % A.va.E) * A.va.hstride);
 }
 
 // the same with the ensure running inside the launch: the pair applies the tier mask itself (expert in neither HBM
@@ -389,23 +445,48 @@ __device__ __forceinline__ void gateup_wg(const DecodeArgs& A, int blk, LayerSha
             if (A.fused) {                       // the target is the ensure's decision
                 wait_count(&g_cnt_all[2], 1);
                 f = ld_agent_i64(A.fill + e);
+                if (A.vict_inline && f && !ld_agent_i32(A.ens.pair_own + a)) f = 0;   // another pick writes it
             }
             if (f && A.n_vict_wg) wait_count(&g_cnt_all[1], A.n_vict_wg);   // after the victims' old bytes were read
             S.fdst = f;
+            S.fwb = f && A.vict_inline ? inline_victim(A, f) : -1;
         }
         __syncthreads();
         dst = (uint8_t*)S.fdst;
     }
+    uint8_t* hv = dst && S.fwb >= 0 ? victim_host(A, S.fwb) : nullptr;     // the victim's RAM copy
     if (dst && r == 0) {                         // the vectors (suh, svh) after the trellis words
         const uint32_t* sv = (const uint32_t*)(base + A.g.off_suh_g);
         uint32_t* dv = (uint32_t*)(dst + A.g.off_suh_g);
         const int n = (int)((A.g.blob - A.g.off_suh_g) >> 2);
-        for (int i = tid; i < n; i += kThreads) dv[i] = sv[i];
+        if (hv) {                                // the victim's old vectors first, 8 words per thread and round
+            uint32_t* ov = (uint32_t*)(hv + A.g.off_suh_g);
+            for (int i0 = 0; i0 < n; i0 += 8 * kThreads) {
+                uint32_t w8[8];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const int i = i0 + j * kThreads + tid;
+                    w8[j] = i < n ? dv[i] : 0u;
+                }
+                wait_stores();
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const int i = i0 + j * kThreads + tid;
+                    if (i < n) {
+                        ov[i] = w8[j];
+                        dv[i] = sv[i];
+                    }
+                }
+            }
+        } else {
+            for (int i = tid; i < n; i += kThreads) dv[i] = sv[i];
+        }
     }
     float acc[GQ::NCQ][2];
 #pragma unroll
     for (int q = 0; q < GQ::NCQ; ++q) acc[q][0] = acc[q][1] = 0.f;
     if (live) {
+        if (hv) g.copy_old((const uint32_t*)dst, (uint32_t*)hv, tiles_n, rt0, ct0);
         if (dst) g.write_through((uint32_t*)dst, tiles_n, rt0, ct0);
         g.compute(&S.u.gu.xq[wv][0], acc);       // the wave's own LDS rows: no barrier
     }
@@ -475,9 +556,11 @@ __device__ __forceinline__ void down_wg(const DecodeArgs& A, int blk, LayerShare
         if (A.fused && miss) {                   // the write-through target is the ensure's decision
             wait_count(&g_cnt_all[2], 1);
             f = ld_agent_i64(A.fill + e);
+            if (A.vict_inline && f && !ld_agent_i32(A.ens.pair_own + a)) f = 0;       // another pick writes it
         }
         if (f && A.n_vict_wg) wait_count(&g_cnt_all[1], A.n_vict_wg);      // and for the victims' old bytes
         S.fdst = f;
+        S.fwb = f && A.vict_inline ? inline_victim(A, f) : -1;
     }
     const int ksn = gu_kslices(H);
     half2_t* xs = S.u.dn.xd;                     // the pair's down input, [I/2] half2
@@ -547,6 +630,10 @@ __device__ __forceinline__ void down_wg(const DecodeArgs& A, int blk, LayerShare
     __syncthreads();
     if (tid == 0) st_tag(A.xstart + A.n_gu + blk, tag, 0.f);     // ids, pointers, w and fill target consumed
     uint32_t* trd = S.fdst ? (uint32_t*)((uint8_t*)S.fdst + A.g.gu_bytes) : nullptr;
+    if (trd && S.fwb >= 0) {                     // the victim's old down words at this wave's positions, first
+        uint32_t* tro = (uint32_t*)(victim_host(A, S.fwb) + A.g.gu_bytes);
+        for (int c = 0; c < nch; ++c) g0.copy_old(trd, tro, tiles_n, (wv + kWaves * c) * 4, ct0);
+    }
     float acc[GV::NCP][2], tacc[GV::NCP][2];
     float xsum = 0.f;
 #pragma unroll
@@ -657,6 +744,15 @@ __device__ __forceinline__ void down_wg(const DecodeArgs& A, int blk, LayerShare
         if (A.fused) wait_count(&g_cnt_all[2], 1);
         const unsigned ep = tag == ~0u ? 0u : tag;   // the next call's tag is never 0 (the zeroed buffer)
         __hip_atomic_store(&g_epoch, ep, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    if (A.vict_inline && A.va.ram_res) {         // every writer has copied its part: the victims' RAM copies are valid
+        const int32_t* vl = A.va.vict;           // fields read before the stores
+        uint8_t* rr = (uint8_t*)A.va.ram_res;
+        const int nv = ld_agent_i32(vl);
+        for (int i = l; i < nv; i += 64) {
+            const int wb = ld_agent_i32(vl + 1 + 2 * i);
+            if (wb >= 0) rr[wb] = 1;
+        }
     }
     if (A.fused) {
         // the ensure's in-place rewrite of the caller's picks (masked -> safe expert, weight 0), deferred to here
