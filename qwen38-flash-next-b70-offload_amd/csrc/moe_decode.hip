@@ -287,6 +287,12 @@ struct GateUpShared {
 struct DownShared {
     half2_t xd[kMaxI / 2];                   // the pair's down input (fp16), [I/2]
     float yc[kCombRound][128];               // combiner: the other picks' y of its block, one round of picks
+    // the last workgroup of a call with the ensure inside: the commit, victim and mask-rewrite inputs, loaded early
+    int fin_nf, fin_nv;
+    int fin_ef[kEnsMaxP];                    // filled experts
+    int64_t fin_fv[kEnsMaxP];                // their new slot addresses
+    int fin_wb[kEnsMaxP];                    // victims copied inline (write-back keys)
+    int fin_id[kEnsMaxP];                    // rewritten id of masked pick i (-1: unchanged)
 };
 struct LayerShared {
     union {
@@ -551,6 +557,33 @@ __device__ __forceinline__ void down_wg(const DecodeArgs& A, int blk, LayerShare
         e_d = *(const half2_t*)((const half_t*)(base + A.g.off_suh_d) + cI);
     }
     const unsigned tag = call_tag();
+    if (A.fused && a == A.npairs - 1 && nb == nbn - 1 && wv == kWaves - 1) {
+        // the last workgroup of the call (it combines the last row and block): once the ensure's decisions are final,
+        // load what the end of the call stores, so that the end has no dependent loads left (at most kEnsMaxP picks)
+        if (l == 0) wait_count(&g_cnt_all[2], 1);
+        const int nf = A.commit_ptrs ? ld_agent_i32(A.fill_list) : 0;
+        const int nvv = A.vict_inline && A.va.ram_res ? ld_agent_i32(A.va.vict) : 0;
+        int ef = -1, wb = -1, nid = -1;
+        int64_t fv = 0;
+        if (l < nf) {
+            ef = ld_agent_i32(A.fill_list + 1 + l);
+            fv = ld_agent_i64(A.commit_fill + ef);
+        }
+        if (l < nvv) wb = ld_agent_i32(A.va.vict + 1 + 2 * l);
+        const EnsureArgs& Q = A.ens;
+        if (Q.ram_res && l < A.npairs) {         // the mask rule gives the same answer as at the pairs' start
+            const int kb = Q.layer * A.E, id = min(max(Q.ids[l], 0), A.E - 1);
+            if (!Q.ram_res[kb + id] && Q.slot_of[kb + id] < 0) nid = Q.safe[Q.layer];
+        }
+        S.u.dn.fin_ef[l] = ef;
+        S.u.dn.fin_fv[l] = fv;
+        S.u.dn.fin_wb[l] = wb;
+        S.u.dn.fin_id[l] = nid;
+        if (l == 0) {
+            S.u.dn.fin_nf = nf;
+            S.u.dn.fin_nv = nvv;
+        }
+    }
     if (tid == 0) {                              // write-through target of a miss
         int64_t f = !A.fused && A.fill ? A.fill[e] : 0;
         if (A.fused && miss) {                   // the write-through target is the ensure's decision
@@ -741,38 +774,21 @@ __device__ __forceinline__ void down_wg(const DecodeArgs& A, int blk, LayerShare
             wait_count(&g_cnt_all[1], A.n_vict_wg);
             counter_reset(&g_cnt_all[1]);
         }
-        if (A.fused) wait_count(&g_cnt_all[2], 1);
         const unsigned ep = tag == ~0u ? 0u : tag;   // the next call's tag is never 0 (the zeroed buffer)
         __hip_atomic_store(&g_epoch, ep, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
-    if (A.vict_inline && A.va.ram_res) {         // every writer has copied its part: the victims' RAM copies are valid
-        const int32_t* vl = A.va.vict;           // fields read before the stores
-        uint8_t* rr = (uint8_t*)A.va.ram_res;
-        const int nv = ld_agent_i32(vl);
-        for (int i = l; i < nv; i += 64) {
-            const int wb = ld_agent_i32(vl + 1 + 2 * i);
-            if (wb >= 0) rr[wb] = 1;
-        }
-    }
-    if (A.fused) {
+    if (A.fused) {                               // stores only: the inputs were loaded at the workgroup's start
+        // every writer has copied its part: the victims' RAM copies are valid
+        if (l < S.u.dn.fin_nv && S.u.dn.fin_wb[l] >= 0) A.va.ram_res[S.u.dn.fin_wb[l]] = 1;
         // the ensure's in-place rewrite of the caller's picks (masked -> safe expert, weight 0), deferred to here
-        // because every pair read them during the call; the mask rule gives the same answer now (see pair_lookup)
-        const EnsureArgs& Q = A.ens;
-        if (Q.ram_res) {
-            const int kb = Q.layer * A.E, safe = Q.safe[Q.layer];
-            for (int i = l; i < A.npairs; i += 64) {
-                const int id = min(max(Q.ids[i], 0), A.E - 1);
-                if (!Q.ram_res[kb + id] && Q.slot_of[kb + id] < 0) {
-                    Q.ids[i] = safe;
-                    Q.w[i] = 0.f;
-                }
-            }
+        // because every pair read them during the call
+        if (l < A.npairs && S.u.dn.fin_id[l] >= 0) {
+            A.ens.ids[l] = S.u.dn.fin_id[l];
+            A.ens.w[l] = 0.f;
         }
-        const int nf = A.commit_ptrs ? ld_agent_i32(A.fill_list) : 0;
-        for (int i = l; i < nf; i += 64) {
-            const int ef = ld_agent_i32(A.fill_list + 1 + i);
-            A.commit_ptrs[ef] = ld_agent_i64(A.commit_fill + ef);
-            A.commit_fill[ef] = 0;
+        if (l < S.u.dn.fin_nf) {                 // commit the fills
+            A.commit_ptrs[S.u.dn.fin_ef[l]] = S.u.dn.fin_fv[l];
+            A.commit_fill[S.u.dn.fin_ef[l]] = 0;
         }
         if (l == 0) counter_reset(&g_cnt_all[2]);
         return;
