@@ -165,8 +165,10 @@ hipError_t launch_align(const int32_t* ids, const float* w, int npairs, int topk
 // xt (built in registers from x and the pair's expert's suh), so each lane ends with 4 consecutive columns of one
 // pair row per accumulator group and stores them as 8 bytes. The fp32 sums differ from the butterfly order only in
 // rounding. Workgroup of 4 waves per (64 sorted pairs, projection): wave w takes the 32 rows 32 (w & 1) .. and the
-// 128-column blocks kb = (w >> 1), (w >> 1) + 2, ...
+// 128-column blocks kb = (w >> 1), (w >> 1) + 2, ... The fp16 results of a block go through LDS ([pair][column]) so
+// that 16 lanes store one pair's 256-byte row segment with 16-byte stores.
 constexpr int kXhWaves = 4;
+constexpr int kXhRow = 128 + 8;                                  // LDS row of one pair's block (halfs, padded)
 
 // 8 consecutive activations as fp32 (exact for every input dtype)
 __device__ __forceinline__ void ld_act8(const void* x, int dt, size_t i, float (&v)[8]) {
@@ -190,6 +192,7 @@ __device__ __forceinline__ void ld_act8(const void* x, int dt, size_t i, float (
 
 __global__ void __launch_bounds__(64 * kXhWaves) prefill_xh_kernel(PrefillArgs A) {
     __shared__ __align__(16) half_t hmat[128 * 128];             // H128, row n contiguous in k
+    __shared__ __align__(16) half_t tbuf[kXhWaves][32 * kXhRow]; // per wave: [pair][column] of one block
     for (int i = threadIdx.x; i < 128 * 128; i += 64 * kXhWaves)
         hmat[i] = (__popc((i >> 7) & (i & 127)) & 1) ? (half_t)-1.0f : (half_t)1.0f;
     __syncthreads();
@@ -202,7 +205,8 @@ __global__ void __launch_bounds__(64 * kXhWaves) prefill_xh_kernel(PrefillArgs A
     const half_t* suh = valid ? (const half_t*)((const uint8_t*)A.ptrs[A.pair_exp[s]] +
                                                 (pj ? A.g.off_suh_u : A.g.off_suh_g))
                               : nullptr;
-    half_t* out = A.xh + ((size_t)(valid ? s : 0) * 2 + pj) * H;
+    const int s0 = blk * 64 + (wv & 1) * 32;                    // the wave's 32 pairs
+    half_t* tb = tbuf[wv];
     for (int kb = (wv >> 1); kb < nkb; kb += 2) {
         half8_t bx[8];                                           // xt fragments: k = 16 ks + 8 (l / 32) .. + 7
 #pragma unroll
@@ -226,17 +230,21 @@ __global__ void __launch_bounds__(64 * kXhWaves) prefill_xh_kernel(PrefillArgs A
                 const half8_t ha = *(const half8_t*)(hmat + (nb * 32 + (l & 31)) * 128 + ks * 16 + (l >> 5) * 8);
                 acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(ha, bx[ks], acc, 0, 0, 0);
             }
-            if (valid) {
 #pragma unroll
-                for (int q = 0; q < 4; ++q) {                    // rows n = 32 nb + 8 q + 4 (l / 32) + 0..3
-                    const int n = nb * 32 + q * 8 + (l >> 5) * 4;
-                    typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
-                    const half4_t hv = half4_t{(half_t)(acc[4 * q] * kRsqrt128), (half_t)(acc[4 * q + 1] * kRsqrt128),
-                                               (half_t)(acc[4 * q + 2] * kRsqrt128),
-                                               (half_t)(acc[4 * q + 3] * kRsqrt128)};
-                    *(half4_t*)(out + kb * 128 + n) = hv;
-                }
+            for (int q = 0; q < 4; ++q) {                        // rows n = 32 nb + 8 q + 4 (l / 32) + 0..3
+                const int n = nb * 32 + q * 8 + (l >> 5) * 4;
+                typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
+                const half4_t hv = half4_t{(half_t)(acc[4 * q] * kRsqrt128), (half_t)(acc[4 * q + 1] * kRsqrt128),
+                                           (half_t)(acc[4 * q + 2] * kRsqrt128), (half_t)(acc[4 * q + 3] * kRsqrt128)};
+                *(half4_t*)(tb + (l & 31) * kXhRow + n) = hv;
             }
+        }
+        // the block's 32 rows x 128 columns: 16 lanes per pair row, 16 bytes each (the wave's own LDS rows)
+#pragma unroll
+        for (int r = 0; r < 8; ++r) {
+            const int pr = r * 4 + (l >> 4), col = (l & 15) * 8;
+            const half8_t v = *(const half8_t*)(tb + pr * kXhRow + col);
+            if (s0 + pr < A.npairs) *(half8_t*)(A.xh + ((size_t)(s0 + pr) * 2 + pj) * H + kb * 128 + col) = v;
         }
     }
 }
