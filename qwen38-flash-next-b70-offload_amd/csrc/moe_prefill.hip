@@ -6,11 +6,11 @@
 //              ascending pair order inside an expert (deterministic; wave ballots for in-chunk ranks)
 //   xh         input Hadamards xh = fp16(H(fp16(x * suh)) / sqrt(128)) once per (sorted pair, projection), as MFMA
 //              products with the +-1 matrix H128 (the column-tile workgroups of an expert all read them)
-//   gate/up    one workgroup of 8 waves per (active expert, 128-column block of I), over the expert's rows in chunks of
-//              256: the 4 tile-rows x (8 gate + 8 up) tiles of each 64-deep K chunk are decoded once into LDS as the
-//              fp16 B operand of v_mfma_f32_32x32x16_f16 (double-buffered; one barrier per chunk), A = xh rows read
-//              from HBM, fp32 accumulation over all of H; epilogue through LDS: g/u Hadamards, SwiGLU, * suh_d,
-//              Hadamard -> abuf (fp16), with the reference's rounding points
+//   gate/up    one workgroup of 8 waves per (active expert, 128-column block of I), over the expert's rows in passes
+//              of 192: the 4 tile-rows x (8 gate + 8 up) tiles of each 64-deep K chunk are decoded once into LDS as
+//              the fp16 B operand of v_mfma_f32_32x32x16_f16, the chunk's xh rows staged into LDS with 128-byte row
+//              loads (both double-buffered; one barrier per chunk), fp32 accumulation over all of H; epilogue through
+//              LDS: g/u Hadamards, SwiGLU, * suh_d, Hadamard -> abuf (fp16), with the reference's rounding points
 //   down       one workgroup per (active expert, 256 columns of H), K = I, same decode/MFMA scheme, A = abuf rows;
 //              epilogue: output Hadamard * (w * svh_d) -> y (fp16, as the reference's prefill stores it)
 //   combine    out[m] = sum_k y[pair_of[m, k]] in k order (fp32), converted to the activation dtype
@@ -19,6 +19,7 @@
 #include "exl3_kernels.h"
 
 #include <algorithm>
+#include <utility>
 
 namespace exl3 {
 
@@ -27,12 +28,17 @@ typedef float float16_t __attribute__((ext_vector_type(16)));
 
 constexpr int kAlignChunk = 1024;
 constexpr int kPfWaves = 8, kPfThreads = 64 * kPfWaves;
-constexpr int kPfRows = 256;                    // rows per pass of a GEMM workgroup (4 wave rows x 64)
-constexpr int kTileBytes = 16 * 16 * 2 + 16;    // one decoded 16x16 fp16 tile in LDS ([col][k]) + 16 B pad
-constexpr int kRowBytes = 16 * kTileBytes;      // one tile-row of the 16 tiles of a workgroup
-constexpr int kChunkBytes = 4 * kRowBytes;      // 4 tile-rows (K = 64)
-constexpr int kPfLds = 2 * kChunkBytes;         // double buffer; also holds the fp32 epilogue tile [64][256]
-static_assert(kPfLds >= 64 * 256 * 4, "epilogue tile must fit the B buffers");
+constexpr int kPfRows = 192;                    // rows per pass of a GEMM workgroup (6 blocks of 32)
+constexpr int kPfRb = kPfRows / 64;             // 32-row blocks per wave (a wave takes the even or the odd blocks)
+constexpr int kTileB = 16 * 16 * 2;             // one decoded 16x16 fp16 tile in LDS: [col][k], k-halves swizzled
+constexpr int kBRow = 16 * kTileB;              // one tile-row of the 16 tiles (256 columns) of a workgroup
+constexpr int kBChunk = 4 * kBRow;              // B of one K chunk (4 tile-rows, K = 64): 32 KB
+constexpr int kARow = 64 * 2;                   // one A row of a K chunk (64 fp16), 16-byte pieces swizzled
+constexpr int kAProj = kPfRows * kARow;         // A of one projection and K chunk: 24 KB
+// double-buffered B and A (gate/up: both projections); the fp32 epilogue tile [64][256] reuses the B buffers
+constexpr int pf_lds(int nproj) { return 2 * (kBChunk + nproj * kAProj); }
+static_assert(2 * kBChunk >= 64 * 256 * 4, "epilogue tile must fit the B buffers");
+static_assert(pf_lds(2) <= 160 * 1024, "gate/up buffers exceed the LDS of a CU");
 
 // ---- block scan helpers (1,024 threads) ---------------------------------------------------------------------------
 __device__ __forceinline__ int wave_incl_scan(int v) {
@@ -249,15 +255,29 @@ __global__ void __launch_bounds__(64 * kXhWaves) prefill_xh_kernel(PrefillArgs A
     }
 }
 
+// ---- LDS layouts of one K chunk ----------------------------------------------------------------------------------------
+// B: tile j of tile-row kt at kt * kBRow + j * kTileB, column c of the tile at 32 c, its k-half h (k = 8 h .. 8 h + 7)
+// in the 16-byte slot h ^ (c >> 3) ^ (j & 1). The 16 lanes of a B-fragment read (16 columns of one tile) and the 16 lanes
+// of a decoder store (8 periods of two neighbouring tiles) each cover 16 distinct slots of the 64 banks.
+__device__ __forceinline__ int b_slot(int tile, int c, int h) {
+    return tile * kTileB + c * 32 + ((h ^ (c >> 3) ^ (tile & 1)) << 4);
+}
+// A: row r of the chunk at r * kARow, its 16-byte piece j (k = 8 j .. 8 j + 7) in slot j ^ ((r >> 1) & 7): 16 rows of one
+// piece (an A-fragment read) and 2 rows of 8 pieces (a staging store) each hit 16 distinct slots.
+__device__ __forceinline__ int a_slot(int r, int j) { return r * kARow + ((j ^ ((r >> 1) & 7)) << 4); }
+
 // ---- decode of one K chunk (4 tile-rows x 16 tiles) into LDS ----------------------------------------------------------
 // The 16 tiles of a workgroup: local tile j lives at global tile column tcol(j). Period q of the chunk:
 // tile-row q / (16 G), local tile (q / G) % 16, period p = q % G; G consecutive lanes hold one tile's periods, so the
-// circular previous word of a period comes from the neighbouring lane.
+// circular previous word of a period comes from the neighbouring lane. Value u of period p (t = V p + u) lies in column
+// (V p >> 5) + 8 ((u >> 2) & 1) and k-half (u >> 1) & 1, at position 2 ((V p >> 3) & 3) + 2 (u >> 3) + (u & 1) of that
+// half: a period fills V / 4 consecutive k of 4 (column, k-half) slots, so it is stored as 4 vector writes of V / 2 bytes.
 template <int K>
 struct ChunkDecoder {
     using GM = Geo<K>;
     static constexpr int G = GM::G, D = GM::D, V = GM::V;
     static constexpr int PER = 4 * 16 * G / kPfThreads;     // periods per thread per chunk (1, 2 or 4)
+    static constexpr int E = V / 4;                         // values per (column, k-half) slot of a period
     static_assert(PER >= 1 && 4 * 16 * G == PER * kPfThreads, "chunk periods must split evenly");
     uint32_t wd[PER][D];
 
@@ -265,143 +285,232 @@ struct ChunkDecoder {
     __device__ __forceinline__ static int trow_of(int q) { return q / (16 * G); }
 
     template <typename TCol>
-    __device__ __forceinline__ void load(const uint32_t* tr, int tiles_n, int kt0, TCol tcol) {
+    __device__ __forceinline__ static void load(uint32_t (&w)[PER][D], const uint32_t* tr, int tiles_n, int kt0,
+                                                TCol tcol) {
 #pragma unroll
         for (int j = 0; j < PER; ++j) {
             const int q = threadIdx.x + j * kPfThreads;
             const int p = q % G;
 #pragma unroll
             for (int i = 0; i < D; ++i)
-                wd[j][i] = __builtin_nontemporal_load(as_global(tr) +
-                                                      word_off<K>(kt0 + trow_of(q), tiles_n, tcol(tile_of(q)), p, i));
+                w[j][i] = __builtin_nontemporal_load(as_global(tr) +
+                                                     word_off<K>(kt0 + trow_of(q), tiles_n, tcol(tile_of(q)), p, i));
         }
     }
 
-    // decode and store: value t = V p + u of tile j at (row(t), col(t)) -> LDS [trow][j][col][k = row]
-    template <int u>
-    __device__ __forceinline__ static void put(const Period<K>& P, uint8_t* tb, int p) {
-        if constexpr (u + 1 < V) {
-            const half_t w0 = cb_w(P.template state<u>());
-            const half_t w1 = cb_w(P.template state<u + 1>());
-            const int t = V * p + u;
-            const int row = 8 * ((t >> 1) & 1) + 2 * ((t >> 3) & 3);    // t even: rows row, row + 1
-            const int col = (t >> 5) + 8 * ((t >> 2) & 1);
-            *(half2_t*)(tb + col * 32 + row * 2) = half2_t{w0, w1};
-            put<u + 2>(P, tb, p);
-        }
+    // slot (column 8 ci + (V p >> 5), k-half kh): values u = 8 (e >> 1) + 4 ci + 2 kh + (e & 1), e = 0 .. E - 1
+    typedef _Float16 hv_t __attribute__((ext_vector_type(E)));
+    template <int ci, int kh, int... e>
+    __device__ __forceinline__ static hv_t slot_vals(const Period<K>& P, std::integer_sequence<int, e...>) {
+        return hv_t{cb_w(P.template state<((e >> 1) << 3) | (ci << 2) | (kh << 1) | (e & 1)>())...};
     }
 
-    __device__ __forceinline__ void decode_store(uint8_t* buf) const {
+    // this thread's periods of the chunk (the previous word of each comes from the neighbouring lane)
+    __device__ __forceinline__ void prep(Period<K> (&P)[PER]) const {
         const int l = lane_id();
 #pragma unroll
         for (int j = 0; j < PER; ++j) {
             const int q = threadIdx.x + j * kPfThreads;
             const int p = q % G;
             const int src = (l / G) * G + (p + G - 1) % G;
-            const uint32_t prev = (uint32_t)__shfl((int)wd[j][D - 1], src, 64);
-            Period<K> P;
-            P.set(wd[j], prev);
-            put<0>(P, buf + trow_of(q) * kRowBytes + tile_of(q) * kTileBytes, p);
+            P[j].set(wd[j], (uint32_t)__shfl((int)wd[j][D - 1], src, 64));
+        }
+    }
+    // slot s (= 2 ci + kh) of every period: a quarter of the chunk's values of this thread
+    template <int s>
+    __device__ __forceinline__ static void slot(const Period<K> (&P)[PER], hv_t (&o)[PER][4]) {
+        constexpr auto es = std::make_integer_sequence<int, E>{};
+#pragma unroll
+        for (int j = 0; j < PER; ++j) o[j][s] = slot_vals<(s >> 1), (s & 1)>(P[j], es);
+    }
+    // the chunk's values of this thread: 4 slots per period (16 VGPRs for every K)
+    __device__ __forceinline__ void decode(hv_t (&o)[PER][4]) const {
+        Period<K> P[PER];
+        prep(P);
+        slot<0>(P, o);
+        slot<1>(P, o);
+        slot<2>(P, o);
+        slot<3>(P, o);
+    }
+
+    __device__ __forceinline__ static void store(const hv_t (&o)[PER][4], uint8_t* buf) {
+#pragma unroll
+        for (int j = 0; j < PER; ++j) {
+            const int q = threadIdx.x + j * kPfThreads;
+            const int p = q % G, tile = tile_of(q);
+            uint8_t* tb = buf + trow_of(q) * kBRow + tile * kTileB + ((V * p) >> 5) * 32 + 4 * ((V * p >> 3) & 3);
+            const int sw = (tile & 1) << 4;
+            *(hv_t*)(tb + (0 ^ sw)) = o[j][0];
+            *(hv_t*)(tb + (16 ^ sw)) = o[j][1];
+            *(hv_t*)(tb + 8 * 32 + (16 ^ sw)) = o[j][2];
+            *(hv_t*)(tb + 8 * 32 + (0 ^ sw)) = o[j][3];
+        }
+    }
+
+    // decode and store slot by slot (fewer live registers than decode + store)
+    __device__ __forceinline__ void decode_store(uint8_t* buf) const {
+        Period<K> P[PER];
+        prep(P);
+        constexpr auto es = std::make_integer_sequence<int, E>{};
+#pragma unroll
+        for (int j = 0; j < PER; ++j) {
+            const int q = threadIdx.x + j * kPfThreads;
+            const int p = q % G, tile = tile_of(q);
+            uint8_t* tb = buf + trow_of(q) * kBRow + tile * kTileB + ((V * p) >> 5) * 32 + 4 * ((V * p >> 3) & 3);
+            const int sw = (tile & 1) << 4;
+            *(hv_t*)(tb + (0 ^ sw)) = slot_vals<0, 0>(P[j], es);
+            *(hv_t*)(tb + (16 ^ sw)) = slot_vals<0, 1>(P[j], es);
+            *(hv_t*)(tb + 8 * 32 + (16 ^ sw)) = slot_vals<1, 0>(P[j], es);
+            *(hv_t*)(tb + 8 * 32 + (0 ^ sw)) = slot_vals<1, 1>(P[j], es);
         }
     }
 };
 
-// B fragment of v_mfma_f32_32x32x16_f16 for columns n0..n0+31 of tile-row kt of a chunk buffer:
-// lane l: column n0 + l % 32, k = 8 (l / 32) .. + 7
-__device__ __forceinline__ half8_t ld_bfrag(const uint8_t* buf, int kt, int n0) {
-    const int l = lane_id();
-    const int n = n0 + (l & 31);
-    return *(const half8_t*)(buf + kt * kRowBytes + (n >> 4) * kTileBytes + (n & 15) * 32 + (l >> 5) * 16);
-}
+// ---- the GEMM core shared by gate/up and down -------------------------------------------------------------------------
+// C[rows][256] (rows <= 192) over nchunks K chunks of 64: wave w takes the 32-row blocks rb = (w >> 2) + 2 j (j < 3) and
+// the 64 columns 64 (w & 3) .. + 63 (2 fragments of 32), so the two waves of a SIMD (w, w + 4) share its matrix core
+// evenly. A (the workgroup's rows of NPROJ fp16 matrices, projection of wave w = (w & 3) >> 1 when NPROJ = 2) and B
+// (the decoded trellis) of a chunk sit in LDS, double-buffered, one barrier per chunk. In the loop, waves 0-3 multiply
+// chunk c first and then produce chunk c + 1 (decode B, store the staged A, issue the loads for chunk c + 2) while
+// waves 4-7 produce first and multiply after.
 
-// A fragments (rows r0 + 32 rb + l % 32 of a [rows][lda] fp16 matrix, k = k0 + 16 ks + 8 (l / 32) .. + 7), zero rows
-// at or beyond `rows`
-__device__ __forceinline__ void ld_afrags(const half_t* a, size_t lda, int r0, int rows, int k0, half8_t (&f)[2][4]) {
-    const int l = lane_id();
+// A of a K chunk staged through registers: group g = wave + 8 i covers projection g / 24, rows 8 (g % 24) .. + 7 with
+// 16-byte loads (lane: row + l / 8, piece l % 8, so 8 lanes read one row's 128 bytes) and 16-byte LDS stores into the
+// swizzled slots; rows at or beyond `rows` are zero
+template <int NPROJ>
+struct AStage {
+    static constexpr int NL = NPROJ * kPfRows / 64;          // 16-byte loads per lane per chunk (8 rows x 128 B each)
+    uint4 v[NL];
+    __device__ __forceinline__ void load(const half_t* a, size_t lda, size_t proj_off, int rows, int k0) {
+        const int l = lane_id(), wv = threadIdx.x >> 6;
 #pragma unroll
-    for (int rb = 0; rb < 2; ++rb) {
-        const int r = r0 + rb * 32 + (l & 31);
-#pragma unroll
-        for (int ks = 0; ks < 4; ++ks) {
-            if (r < rows) f[rb][ks] = *(const half8_t*)(a + (size_t)r * lda + k0 + ks * 16 + (l >> 5) * 8);
-            else f[rb][ks] = half8_t{};
+        for (int i = 0; i < NL; ++i) {
+            const int g = wv + 8 * i, pj = g / (kPfRows / 8), r = (g % (kPfRows / 8)) * 8 + (l >> 3);
+            v[i] = r < rows ? *(const uint4*)(a + pj * proj_off + (size_t)r * lda + k0 + (l & 7) * 8)
+                            : make_uint4(0, 0, 0, 0);
         }
     }
-}
+    __device__ __forceinline__ void store(uint8_t* buf, int nrb) const {
+        const int l = lane_id(), wv = threadIdx.x >> 6;
+#pragma unroll
+        for (int i = 0; i < NL; ++i) {
+            const int g = wv + 8 * i, pj = g / (kPfRows / 8), r8 = (g % (kPfRows / 8)) * 8;
+            if (r8 < nrb * 32) *(uint4*)(buf + pj * kAProj + a_slot(r8 + (l >> 3), l & 7)) = v[i];
+        }
+    }
+};
 
-// the GEMM core shared by gate/up and down: acc[rb][cb] (rows 64 mw + 32 rb, columns 128 nw + 32 cb) over K chunks
-template <int K, typename TCol>
-__device__ __forceinline__ void grouped_gemm(const uint32_t* tr, int tiles_n, int nchunks, TCol tcol, const half_t* a,
-                                             size_t lda, int rows, uint8_t* lds, float16_t (&acc)[2][4]) {
-    const int wv = threadIdx.x >> 6, mw = wv >> 1, nw = wv & 1;
-    const bool active = mw * 64 < rows;
+template <int K, int NPROJ, typename TCol>
+__device__ __forceinline__ void gemm_core(const uint32_t* tr, int tiles_n, int nchunks, TCol tcol, const half_t* a,
+                                          size_t lda, size_t proj_off, int rows, uint8_t* lds,
+                                          float16_t (&acc)[kPfRb][2]) {
+    using Dec = ChunkDecoder<K>;
+    const int wv = threadIdx.x >> 6, l = lane_id();
+    const int rpar = wv >> 2, q = wv & 3, proj = NPROJ == 2 ? (q >> 1) : 0;
+    const int nrb = (rows + 31) >> 5;
+    const bool mfma_first = rpar == 0;
 #pragma unroll
-    for (int rb = 0; rb < 2; ++rb)
+    for (int j = 0; j < kPfRb; ++j) acc[j][0] = acc[j][1] = float16_t{};
+    uint8_t* const b0 = lds;
+    uint8_t* const a0 = lds + 2 * kBChunk;
+    Dec dec;
+    AStage<NPROJ> ast;
+    // this lane's B-fragment offsets (columns 64 q + l % 32 and + 32, k-half l / 32)
+    const int n = q * 64 + (l & 31);
+    const int boff0 = b_slot(n >> 4, n & 15, l >> 5), boff1 = b_slot((n + 32) >> 4, n & 15, l >> 5);
+    auto mfma = [&](int cur) {
+        const uint8_t* bb = b0 + cur * kBChunk;
+        const uint8_t* ab = a0 + cur * (NPROJ * kAProj) + proj * kAProj;
 #pragma unroll
-        for (int cb = 0; cb < 4; ++cb) acc[rb][cb] = float16_t{};
-    ChunkDecoder<K> dec;
-    dec.load(tr, tiles_n, 0, tcol);
-    half8_t af[2][4];
-    for (int c = 0; c < nchunks; ++c) {
-        uint8_t* buf = lds + (c & 1) * kChunkBytes;
-        dec.decode_store(buf);
-        if (c + 1 < nchunks) dec.load(tr, tiles_n, 4 * (c + 1), tcol);
-        if (active) ld_afrags(a, lda, mw * 64, rows, c * 64, af);
-        __syncthreads();
-        if (active) {
+        for (int ks = 0; ks < 4; ++ks) {
+            const half8_t f0 = *(const half8_t*)(bb + ks * kBRow + boff0);
+            const half8_t f1 = *(const half8_t*)(bb + ks * kBRow + boff1);
 #pragma unroll
-            for (int ks = 0; ks < 4; ++ks) {
-#pragma unroll
-                for (int cb = 0; cb < 4; ++cb) {
-                    const half8_t b = ld_bfrag(buf, ks, nw * 128 + cb * 32);
-#pragma unroll
-                    for (int rb = 0; rb < 2; ++rb)
-                        acc[rb][cb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[rb][ks], b, acc[rb][cb], 0, 0, 0);
+            for (int j = 0; j < kPfRb; ++j) {
+                const int rb = rpar + 2 * j;
+                if (rb < nrb) {
+                    const half8_t fa = *(const half8_t*)(ab + a_slot(rb * 32 + (l & 31), 2 * ks + (l >> 5)));
+                    acc[j][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa, f0, acc[j][0], 0, 0, 0);
+                    acc[j][1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa, f1, acc[j][1], 0, 0, 0);
                 }
             }
         }
+    };
+    auto produce = [&](int c) {                   // chunk c + 1 into its buffers, loads of chunk c + 2
+        if (c + 1 < nchunks) {
+            dec.decode_store(b0 + ((c + 1) & 1) * kBChunk);
+            ast.store(a0 + ((c + 1) & 1) * (NPROJ * kAProj), nrb);
+        }
+        if (c + 2 < nchunks) {
+            Dec::load(dec.wd, tr, tiles_n, 4 * (c + 2), tcol);
+            ast.load(a, lda, proj_off, rows, (c + 2) * 64);
+        }
+    };
+    Dec::load(dec.wd, tr, tiles_n, 0, tcol);
+    ast.load(a, lda, proj_off, rows, 0);
+    produce(-1);
+    __syncthreads();
+    for (int c = 0; c < nchunks; ++c) {
+        if (mfma_first) {
+            mfma(c & 1);
+            produce(c);
+        } else {
+            produce(c);
+            mfma(c & 1);
+        }
+        __syncthreads();
     }
-    __syncthreads();                              // every wave is done with the B buffers (epilogue reuses them)
 }
 
-// C tile of wave (mw, nw) -> LDS fp32 [64 rows][256 columns] (row = local row inside the wave row mw)
-__device__ __forceinline__ void stash_acc(const float16_t (&acc)[2][4], float* ep, int nw) {
-    const int l = lane_id();
+// 32-row blocks 2 g (waves 0-3) and 2 g + 1 (waves 4-7) -> LDS fp32 [64 rows][256 columns]
+__device__ __forceinline__ void stash_acc(const float16_t (&acc)[2], float* ep) {
+    const int l = lane_id(), wv = threadIdx.x >> 6, rpar = wv >> 2, q = wv & 3;
 #pragma unroll
-    for (int rb = 0; rb < 2; ++rb)
+    for (int cb = 0; cb < 2; ++cb)
 #pragma unroll
-        for (int cb = 0; cb < 4; ++cb)
-#pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                const int row = rb * 32 + (i & 3) + 8 * (i >> 2) + 4 * (l >> 5);
-                ep[row * 256 + nw * 128 + cb * 32 + (l & 31)] = acc[rb][cb][i];
-            }
+        for (int i = 0; i < 16; ++i) {
+            const int row = rpar * 32 + (i & 3) + 8 * (i >> 2) + 4 * (l >> 5);
+            ep[row * 256 + q * 64 + cb * 32 + (l & 31)] = acc[cb][i];
+        }
+}
+
+// workgroup -> (active expert a, column block): the nblk workgroups of an expert share blockIdx % 8, i.e. one XCD and
+// its L2, which serves the expert's A rows to all of them
+__device__ __forceinline__ void pf_block(int nblk, int& a, int& blk) {
+    const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3;
+    a = (slot / nblk) * 8 + xcd;
+    blk = slot % nblk;
 }
 
 template <int K>
 __global__ void __launch_bounds__(kPfThreads) prefill_gateup_kernel(PrefillArgs A) {
-    __shared__ __align__(16) uint8_t lds[kPfLds];
+    __shared__ __align__(16) uint8_t lds[pf_lds(2)];
     const int I = A.g.I, H = A.g.H, nbn = I / 128;
-    const int a = blockIdx.x / nbn, nb = blockIdx.x % nbn;
+    int a, nb;
+    pf_block(nbn, a, nb);
     if (a >= A.n_act[0]) return;
     const int e = A.act_expert[a], s0 = A.act_start[a], cnt = A.act_cnt[a];
     const uint8_t* base = (const uint8_t*)A.ptrs[e];
-    const int wv = threadIdx.x >> 6, mw = wv >> 1, nw = wv & 1, l = lane_id();
+    const int wv = threadIdx.x >> 6, l = lane_id();
     const int tiles_n = 2 * I / 16;
     auto tcol = [nb, I](int j) { return j < 8 ? nb * 8 + j : I / 16 + nb * 8 + (j - 8); };
     const half_t* svg = (const half_t*)(base + A.g.off_svh_g);
     const half_t* svu = (const half_t*)(base + A.g.off_svh_u);
     const half_t* sud = (const half_t*)(base + A.g.off_suh_d);
     float* ep = (float*)lds;
+    const int c = nb * 128 + 2 * l;               // this lane's two columns of the block
     for (int r0 = 0; r0 < cnt; r0 += kPfRows) {
         const int rows = min(kPfRows, cnt - r0);
-        float16_t acc[2][4];
-        // A = xh rows of this projection: xh[(s, pj)][H] with row stride 2H
-        grouped_gemm<K>((const uint32_t*)base, tiles_n, H / 64, tcol, A.xh + ((size_t)(s0 + r0) * 2 + nw) * H,
-                        2 * (size_t)H, rows, lds, acc);
-        for (int m = 0; m < 4; ++m) {
+        float16_t acc[kPfRb][2];
+        // A = xh rows of both projections: xh[(s, pj)][H], row stride 2H, projection offset H
+        gemm_core<K, 2>((const uint32_t*)base, tiles_n, H / 64, tcol, A.xh + (size_t)(s0 + r0) * 2 * H, 2 * (size_t)H,
+                        (size_t)H, rows, lds, acc);
+        const float sg0 = (float)svg[c], sg1 = (float)svg[c + 1], su0 = (float)svu[c], su1 = (float)svu[c + 1];
+        const float sd0 = (float)sud[c], sd1 = (float)sud[c + 1];
+#pragma unroll
+        for (int m = 0; m < kPfRb; ++m) {
             if (m * 64 >= rows) break;
-            if (mw == m) stash_acc(acc, ep, nw);
+            stash_acc(acc[m], ep);
             __syncthreads();
             for (int rr = wv; rr < 64; rr += kPfWaves) {
                 const int row = m * 64 + rr;
@@ -410,15 +519,14 @@ __global__ void __launch_bounds__(kPfThreads) prefill_gateup_kernel(PrefillArgs 
                 float u0 = ep[rr * 256 + 128 + 2 * l], u1 = ep[rr * 256 + 129 + 2 * l];
                 wave_fwht128(g0, g1);
                 wave_fwht128(u0, u1);
-                const int c = nb * 128 + 2 * l;
-                g0 = (float)(half_t)(g0 * kRsqrt128 * (float)svg[c]);
-                g1 = (float)(half_t)(g1 * kRsqrt128 * (float)svg[c + 1]);
-                u0 = (float)(half_t)(u0 * kRsqrt128 * (float)svu[c]);
-                u1 = (float)(half_t)(u1 * kRsqrt128 * (float)svu[c + 1]);
+                g0 = (float)(half_t)(g0 * kRsqrt128 * sg0);
+                g1 = (float)(half_t)(g1 * kRsqrt128 * sg1);
+                u0 = (float)(half_t)(u0 * kRsqrt128 * su0);
+                u1 = (float)(half_t)(u1 * kRsqrt128 * su1);
                 float a0 = (float)(half_t)(g0 / (1.0f + expf(-g0)) * u0);
                 float a1 = (float)(half_t)(g1 / (1.0f + expf(-g1)) * u1);
-                a0 = (float)(half_t)(a0 * (float)sud[c]);
-                a1 = (float)(half_t)(a1 * (float)sud[c + 1]);
+                a0 = (float)(half_t)(a0 * sd0);
+                a1 = (float)(half_t)(a1 * sd1);
                 wave_fwht128(a0, a1);
                 *(half2_t*)(A.abuf + (size_t)(s0 + r0 + row) * I + c) =
                     half2_t{(half_t)(a0 * kRsqrt128), (half_t)(a1 * kRsqrt128)};
@@ -430,38 +538,56 @@ __global__ void __launch_bounds__(kPfThreads) prefill_gateup_kernel(PrefillArgs 
 
 template <int K>
 __global__ void __launch_bounds__(kPfThreads) prefill_down_kernel(PrefillArgs A) {
-    __shared__ __align__(16) uint8_t lds[kPfLds];
+    __shared__ __align__(16) uint8_t lds[pf_lds(1)];
     const int I = A.g.I, H = A.g.H, ntn = H / 256;
-    const int a = blockIdx.x / ntn, nt = blockIdx.x % ntn;
+    int a, nt;
+    pf_block(ntn, a, nt);
     if (a >= A.n_act[0]) return;
     const int e = A.act_expert[a], s0 = A.act_start[a], cnt = A.act_cnt[a];
     const uint8_t* base = (const uint8_t*)A.ptrs[e];
-    const int wv = threadIdx.x >> 6, mw = wv >> 1, nw = wv & 1, l = lane_id();
+    const int wv = threadIdx.x >> 6, l = lane_id();
     const int tiles_n = H / 16;
     auto tcol = [nt](int j) { return nt * 16 + j; };
     const half_t* svd = (const half_t*)(base + A.g.off_svh_d);
     float* ep = (float*)lds;
     for (int r0 = 0; r0 < cnt; r0 += kPfRows) {
         const int rows = min(kPfRows, cnt - r0);
-        float16_t acc[2][4];
-        grouped_gemm<K>((const uint32_t*)(base + A.g.gu_bytes), tiles_n, I / 64, tcol, A.abuf + (size_t)(s0 + r0) * I,
-                        (size_t)I, rows, lds, acc);
-        for (int m = 0; m < 4; ++m) {
+        float16_t acc[kPfRb][2];
+        gemm_core<K, 1>((const uint32_t*)(base + A.g.gu_bytes), tiles_n, I / 64, tcol, A.abuf + (size_t)(s0 + r0) * I,
+                        (size_t)I, 0, rows, lds, acc);
+        // the lane's 4 output-column scales and, per 64-row group, the routing weights of the wave's 8 rows are
+        // loaded ahead of the rows' Hadamards (no global load inside the row loop)
+        float sv[2][2];
+#pragma unroll
+        for (int hb = 0; hb < 2; ++hb) {
+            sv[hb][0] = (float)svd[nt * 256 + hb * 128 + 2 * l];
+            sv[hb][1] = (float)svd[nt * 256 + hb * 128 + 2 * l + 1];
+        }
+        constexpr int kRpw = 64 / kPfWaves;       // rows per wave and 64-row group
+#pragma unroll
+        for (int m = 0; m < kPfRb; ++m) {
             if (m * 64 >= rows) break;
-            if (mw == m) stash_acc(acc, ep, nw);
+            float pw[kRpw];
+#pragma unroll
+            for (int i = 0; i < kRpw; ++i) {
+                const int row = m * 64 + wv + kPfWaves * i;
+                pw[i] = row < rows ? A.pair_w[s0 + r0 + row] : 0.f;
+            }
+            stash_acc(acc[m], ep);
             __syncthreads();
-            for (int rr = wv; rr < 64; rr += kPfWaves) {
-                const int row = m * 64 + rr;
+#pragma unroll
+            for (int i = 0; i < kRpw; ++i) {
+                const int rr = wv + kPfWaves * i, row = m * 64 + rr;
                 if (row >= rows) break;
                 const int s = s0 + r0 + row;
-                const float sc = kRsqrt128 * A.pair_w[s];
+                const float sc = kRsqrt128 * pw[i];
 #pragma unroll
                 for (int hb = 0; hb < 2; ++hb) {
                     float v0 = ep[rr * 256 + hb * 128 + 2 * l], v1 = ep[rr * 256 + hb * 128 + 2 * l + 1];
                     wave_fwht128(v0, v1);
                     const int c = nt * 256 + hb * 128 + 2 * l;
                     *(half2_t*)(A.y + (size_t)s * H + c) =
-                        half2_t{(half_t)(v0 * sc * (float)svd[c]), (half_t)(v1 * sc * (float)svd[c + 1])};
+                        half2_t{(half_t)(v0 * sc * sv[hb][0]), (half_t)(v1 * sc * sv[hb][1])};
                 }
             }
             __syncthreads();
@@ -528,7 +654,8 @@ hipError_t launch_prefill(PrefillArgs a, int E, void* ws, hipStream_t s) {
     hipError_t e = launch_align(a.ids, a.w, np, a.topk, E, 1, chunk, o, s);
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(prefill_xh_kernel, dim3((unsigned)(2 * ((np + 63) / 64))), dim3(64 * kXhWaves), 0, s, a);
-    const dim3 ggu((unsigned)(A * (I / 128))), gdn((unsigned)(A * (H / 256)));
+    const unsigned A8 = (unsigned)((A + 7) / 8 * 8);   // workgroups of an expert share blockIdx % 8
+    const dim3 ggu(A8 * (unsigned)(I / 128)), gdn(A8 * (unsigned)(H / 256));
     switch (a.g.K) {
         case 2:
             hipLaunchKernelGGL(prefill_gateup_kernel<2>, ggu, dim3(kPfThreads), 0, s, a);
