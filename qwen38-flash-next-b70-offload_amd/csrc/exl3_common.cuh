@@ -161,6 +161,29 @@ __device__ __forceinline__ void wave_fwht128(float& v0, float& v1) {
     }
 }
 
+// The same transform over the 16 lanes of a DPP row, lane l holding x[8 (l % 16) + j] in v[j]: butterflies h = 1, 2, 4
+// in registers, h = 8 .. 64 across lanes (xor 1, 2, 4, 8 inside the row) as one FMA with the lane's sign (+1 lower,
+// -1 upper: v + p and p - v, each rounded once like the add and subtract). Same order and operations as wave_fwht128,
+// so the fp32 results are identical; a wave transforms 4 rows at once. The whole wave must be active.
+__device__ __forceinline__ void row_fwht128(float (&v)[8]) {
+#pragma unroll
+    for (int h = 1; h < 8; h <<= 1)
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+            if (!(j & h)) {
+                const float a = v[j], b = v[j + h];
+                v[j] = a + b;
+                v[j + h] = a - b;
+            }
+    const int l = lane_id();
+#pragma unroll
+    for (int m = 1; m < 16; m <<= 1) {
+        const float sg = (l & m) ? -1.0f : 1.0f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[j] = __builtin_fmaf(v[j], sg, lane_xor(v[j], m));
+    }
+}
+
 __device__ __forceinline__ float bf16_to_f32(bf16_bits b) { return __uint_as_float((uint32_t)b << 16); }
 __device__ __forceinline__ bf16_bits f32_to_bf16(float f) {
     uint32_t u = __float_as_uint(f);

@@ -498,38 +498,45 @@ __global__ void __launch_bounds__(kPfThreads) prefill_gateup_kernel(PrefillArgs 
     const half_t* svu = (const half_t*)(base + A.g.off_svh_u);
     const half_t* sud = (const half_t*)(base + A.g.off_suh_d);
     float* ep = (float*)lds;
-    const int c = nb * 128 + 2 * l;               // this lane's two columns of the block
+    const int cb8 = nb * 128 + (l & 15) * 8;      // this lane's 8 columns of the block (16-lane row layout)
     for (int r0 = 0; r0 < cnt; r0 += kPfRows) {
         const int rows = min(kPfRows, cnt - r0);
         float16_t acc[kPfRb][2];
         // A = xh rows of both projections: xh[(s, pj)][H], row stride 2H, projection offset H
         gemm_core<K, 2>((const uint32_t*)base, tiles_n, H / 64, tcol, A.xh + (size_t)(s0 + r0) * 2 * H, 2 * (size_t)H,
                         (size_t)H, rows, lds, acc);
-        const float sg0 = (float)svg[c], sg1 = (float)svg[c + 1], su0 = (float)svu[c], su1 = (float)svu[c + 1];
-        const float sd0 = (float)sud[c], sd1 = (float)sud[c + 1];
+        const half8_t hg = *(const half8_t*)(svg + cb8), hu = *(const half8_t*)(svu + cb8);
+        const half8_t hd = *(const half8_t*)(sud + cb8);
 #pragma unroll
         for (int m = 0; m < kPfRb; ++m) {
             if (m * 64 >= rows) break;
             stash_acc(acc[m], ep);
             __syncthreads();
-            for (int rr = wv; rr < 64; rr += kPfWaves) {
-                const int row = m * 64 + rr;
-                if (row >= rows) break;
-                float g0 = ep[rr * 256 + 2 * l], g1 = ep[rr * 256 + 2 * l + 1];
-                float u0 = ep[rr * 256 + 128 + 2 * l], u1 = ep[rr * 256 + 129 + 2 * l];
-                wave_fwht128(g0, g1);
-                wave_fwht128(u0, u1);
-                g0 = (float)(half_t)(g0 * kRsqrt128 * sg0);
-                g1 = (float)(half_t)(g1 * kRsqrt128 * sg1);
-                u0 = (float)(half_t)(u0 * kRsqrt128 * su0);
-                u1 = (float)(half_t)(u1 * kRsqrt128 * su1);
-                float a0 = (float)(half_t)(g0 / (1.0f + expf(-g0)) * u0);
-                float a1 = (float)(half_t)(g1 / (1.0f + expf(-g1)) * u1);
-                a0 = (float)(half_t)(a0 * sd0);
-                a1 = (float)(half_t)(a1 * sd1);
-                wave_fwht128(a0, a1);
-                *(half2_t*)(A.abuf + (size_t)(s0 + r0 + row) * I + c) =
-                    half2_t{(half_t)(a0 * kRsqrt128), (half_t)(a1 * kRsqrt128)};
+            // 4 rows per wave pass, 16 lanes per row; rows past `rows` are transformed (every lane takes part in the
+            // cross-lane butterflies) but not stored
+            for (int r4 = wv * 4; r4 < 64; r4 += 4 * kPfWaves) {
+                const int rr = r4 + (l >> 4), row = m * 64 + rr;
+                const float* er = ep + rr * 256 + (l & 15) * 8;
+                float g[8], u[8], av[8];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    g[j] = er[j];
+                    u[j] = er[128 + j];
+                }
+                row_fwht128(g);
+                row_fwht128(u);
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const float gj = (float)(half_t)(g[j] * kRsqrt128 * (float)hg[j]);
+                    const float uj = (float)(half_t)(u[j] * kRsqrt128 * (float)hu[j]);
+                    const float aj = (float)(half_t)(gj / (1.0f + expf(-gj)) * uj);
+                    av[j] = (float)(half_t)(aj * (float)hd[j]);
+                }
+                row_fwht128(av);
+                half8_t o;
+#pragma unroll
+                for (int j = 0; j < 8; ++j) o[j] = (half_t)(av[j] * kRsqrt128);
+                if (row < rows) *(half8_t*)(A.abuf + (size_t)(s0 + r0 + row) * I + cb8) = o;
             }
             __syncthreads();
         }
@@ -555,40 +562,36 @@ __global__ void __launch_bounds__(kPfThreads) prefill_down_kernel(PrefillArgs A)
         float16_t acc[kPfRb][2];
         gemm_core<K, 1>((const uint32_t*)(base + A.g.gu_bytes), tiles_n, I / 64, tcol, A.abuf + (size_t)(s0 + r0) * I,
                         (size_t)I, 0, rows, lds, acc);
-        // the lane's 4 output-column scales and, per 64-row group, the routing weights of the wave's 8 rows are
-        // loaded ahead of the rows' Hadamards (no global load inside the row loop)
-        float sv[2][2];
-#pragma unroll
-        for (int hb = 0; hb < 2; ++hb) {
-            sv[hb][0] = (float)svd[nt * 256 + hb * 128 + 2 * l];
-            sv[hb][1] = (float)svd[nt * 256 + hb * 128 + 2 * l + 1];
-        }
-        constexpr int kRpw = 64 / kPfWaves;       // rows per wave and 64-row group
+        // 16-lane row layout: lanes 0-31 one row, 32-63 the next; lanes 16-31 and 48-63 the second 128 columns. The
+        // lane's 8 output-column scales and the routing weights of the wave's rows are loaded ahead of the rows'
+        // Hadamards (no global load inside the row loop)
+        const int hb = (l >> 4) & 1, cb8 = nt * 256 + hb * 128 + (l & 15) * 8;
+        const half8_t hs = *(const half8_t*)(svd + cb8);
+        constexpr int kPass = 64 / (2 * kPfWaves);   // wave passes per 64-row group
 #pragma unroll
         for (int m = 0; m < kPfRb; ++m) {
             if (m * 64 >= rows) break;
-            float pw[kRpw];
+            float pw[kPass];
 #pragma unroll
-            for (int i = 0; i < kRpw; ++i) {
-                const int row = m * 64 + wv + kPfWaves * i;
-                pw[i] = row < rows ? A.pair_w[s0 + r0 + row] : 0.f;
+            for (int i = 0; i < kPass; ++i) {
+                const int row = m * 64 + 2 * (wv + kPfWaves * i) + (l >> 5);
+                pw[i] = A.pair_w[s0 + r0 + min(row, rows - 1)];
             }
             stash_acc(acc[m], ep);
             __syncthreads();
 #pragma unroll
-            for (int i = 0; i < kRpw; ++i) {
-                const int rr = wv + kPfWaves * i, row = m * 64 + rr;
-                if (row >= rows) break;
-                const int s = s0 + r0 + row;
-                const float sc = kRsqrt128 * pw[i];
+            for (int i = 0; i < kPass; ++i) {
+                const int rr = 2 * (wv + kPfWaves * i) + (l >> 5), row = m * 64 + rr;
+                const float* er = ep + rr * 256 + hb * 128 + (l & 15) * 8;
+                float v[8];
 #pragma unroll
-                for (int hb = 0; hb < 2; ++hb) {
-                    float v0 = ep[rr * 256 + hb * 128 + 2 * l], v1 = ep[rr * 256 + hb * 128 + 2 * l + 1];
-                    wave_fwht128(v0, v1);
-                    const int c = nt * 256 + hb * 128 + 2 * l;
-                    *(half2_t*)(A.y + (size_t)s * H + c) =
-                        half2_t{(half_t)(v0 * sc * sv[hb][0]), (half_t)(v1 * sc * sv[hb][1])};
-                }
+                for (int j = 0; j < 8; ++j) v[j] = er[j];
+                row_fwht128(v);
+                const float sc = kRsqrt128 * pw[i];
+                half8_t o;
+#pragma unroll
+                for (int j = 0; j < 8; ++j) o[j] = (half_t)(v[j] * sc * (float)hs[j]);
+                if (row < rows) *(half8_t*)(A.y + (size_t)(s0 + r0 + row) * H + cb8) = o;
             }
             __syncthreads();
         }
