@@ -101,6 +101,18 @@ int exl3_moe_forward_cached(const void* x, int x_dtype, int64_t x_stride, int M,
                             int n_experts, void* out, int64_t out_stride, void* workspace, size_t workspace_bytes,
                             void* stream);
 
+/* moe_prefetch (a8:1194-1222): claim slots for the (predicted) experts `ids` of layer `layer` with the ensure in
+ * prefetch mode (launch_ensure a8:846-851: the tick is not advanced, so slots stamped by the last MoE call stay
+ * protected; hits re-stamped, misses up to max_fill get exact-LRU slots older than the tick, old owners repointed to
+ * their host records; no tier mask, no write-back), copy each assigned expert from its host record into its slot
+ * (PrefetchCopyKernel), then repoint ptrs_all. pf_list int32 [1 + n_experts] = [n, e...], pf_slot int32
+ * [n_experts]. Enqueued on `stream`: run it on a side stream that waited for the previous MoE call and make the
+ * compute stream wait for it before the next one. n_slots == 0 or n_ids == 0: nothing is done. */
+int exl3_moe_prefetch(const int32_t* ids, int n_ids, int64_t* ptrs_all, int layer, int32_t* slot_of,
+                      int32_t* slot_key, int32_t* slot_last, int32_t* tick, int n_slots, const int64_t* host_base,
+                      int64_t slot_base, int32_t* pf_list, int32_t* pf_slot, int max_fill, int n_experts, int64_t blob,
+                      void* stream);
+
 /* moe_align (a8:1316-1323 -> launch_align a8:639-680): token sort by expert into the reference's packed buffers:
  * ib int32 [4A + 1 + 2*npairs + 16] = act_expert[A] act_start[A] act_cnt[A] act_pstart[A] n_act pair_tok[npairs]
  * pair_of[npairs] ..., fb fp32 [npairs] = pair_w, A = min(npairs, n_experts); active experts ascending, act_pstart the

@@ -51,6 +51,8 @@ def lib():
         L.co_rec_len.argtypes = [I32]
         L.co_ensure.restype = I32
         L.co_ensure.argtypes = [P, I32, P, P, I32, I32, P]
+        L.co_prefetch.restype = I32
+        L.co_prefetch.argtypes = [P, I32, P, I32, I32, P]
         L.co_host_step.restype = I64
         L.co_host_step.argtypes = [P, P, P, P, P]
         L.co_run.restype = I64
@@ -112,6 +114,15 @@ class CacheOracle:
         P = ids.size
         rec = np.zeros(rec_len(P), dtype=np.int32)
         lib().co_ensure(self._c, layer, _ptr(ids), _ptr(w), P, self.E if max_fill is None else max_fill, _ptr(rec))
+        return rec
+
+    def prefetch(self, layer: int, ids: np.ndarray, max_fill: int | None = None):
+        """One prefetch-mode ensure (moe_prefetch): tick not advanced, no mask, no write-back. Returns the decision
+        record (int32 [3 + 4P]); its assigned experts and slots are the prefetch's fill_list and pf_slot."""
+        assert ids.dtype == np.int32 and ids.flags.c_contiguous
+        P = ids.size
+        rec = np.zeros(rec_len(P), dtype=np.int32)
+        lib().co_prefetch(self._c, layer, _ptr(ids), P, self.E if max_fill is None else max_fill, _ptr(rec))
         return rec
 
     def host_step(self):

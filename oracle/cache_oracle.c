@@ -9,6 +9,10 @@
  *                                              exact-LRU victims by the nm-th smallest u = slot_last + 1 among slots not
  *                                              touched this tick (929-1000), assignment + old-owner repoint (1003-1023)
  *   kernels/moe-a8/exl3_moe.a8.sycl:1168-1189  VictimCopyKernel: ram_res[old] = 1 for written-back victims
+ *   kernels/moe-a8/exl3_moe.a8.sycl:846-851, 884, 1019-1021, 1194-1222
+ *                                              prefetch mode (moe_prefetch): the tick is not advanced (slots of the last
+ *                                              call, last == T, stay protected), no tier mask, no write-back, the
+ *                                              assigned slots are the pf_slot list
  *   plugin/exl3xpu/nvtier.py:57-87, 179-188    tier init (pinned safe expert per layer, tick = 1)
  *   plugin/exl3xpu/nvtier.py:282-386, 708-806  NvTierAsync one-step-lagged snapshot + _async_step_admit
  *
@@ -133,12 +137,13 @@ static uint32_t kth_smallest(uint32_t *a, int n, int k) {
  */
 int co_rec_len(int P) { return 3 + 4 * P; }
 
-int co_ensure(co_t *c, int layer, int32_t *ids, float *w, int P, int max_fill, int32_t *rec) {
+static int ensure_impl(co_t *c, int layer, int32_t *ids, float *w, int P, int max_fill, int32_t *rec, int prefetch) {
     const int E = c->E, S = c->S;
-    const int32_t T = ++c->tick;                               /* a8:884 */
+    const int32_t T = prefetch ? c->tick : ++c->tick;          /* a8:884 */
+    const int tier = c->tier && !prefetch;                     /* prefetch: no mask, no write-back (a8:846-851) */
     int32_t *need = c->cnt_tmp;                                /* E entries used */
     int32_t *miss = c->i_tmp;
-    if (c->tier) {                                             /* a8:902-914 */
+    if (tier) {                                                /* a8:902-914 */
         for (int i = 0; i < P; ++i) {
             int key = layer * E + ids[i];
             if (c->slot_of[key] < 0 && !c->ram_res[key]) {
@@ -187,17 +192,27 @@ int co_ensure(co_t *c, int layer, int32_t *ids, float *w, int P, int max_fill, i
             int s = V[mi], e = miss[mi];
             int old = c->slot_key[s];
             int wb = old;
-            if (c->tier && old >= 0 && c->ram_res[old]) wb = -1;
+            if (tier && old >= 0 && c->ram_res[old]) wb = -1;
             if (old >= 0) c->slot_of[old] = -1;
             int key = layer * E + e;
             c->slot_key[s] = key; c->slot_of[key] = s; c->slot_last[s] = T;
             if (rec) { rec[3 + P + mi] = e; rec[3 + 2 * P + 2 * mi] = wb; rec[3 + 2 * P + 2 * mi + 1] = s; }
-            if (c->tier && wb >= 0) c->ram_res[wb] = 1;         /* VictimCopyKernel a8:1180 */
+            if (tier && wb >= 0) c->ram_res[wb] = 1;            /* VictimCopyKernel a8:1180 */
         }
         free(V);
     }
     if (rec) { rec[1] = c->ring[0]; rec[2 + P] = nm; }
     return nm;
+}
+
+int co_ensure(co_t *c, int layer, int32_t *ids, float *w, int P, int max_fill, int32_t *rec) {
+    return ensure_impl(c, layer, ids, w, P, max_fill, rec, 0);
+}
+
+/* moe_prefetch's ensure (a8:1194-1222): same record layout; the assigned (expert, slot) pairs are the fill_list /
+ * pf_slot lists, and the old owner's record field holds the old key (no write-back decision) */
+int co_prefetch(co_t *c, int layer, int32_t *ids, int P, int max_fill, int32_t *rec) {
+    return ensure_impl(c, layer, ids, NULL, P, max_fill, rec, 1);
 }
 
 /* stable sort of keys[0..n) by age ascending (ties: keys are already ascending) */

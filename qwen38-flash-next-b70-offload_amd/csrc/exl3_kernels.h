@@ -35,6 +35,8 @@ struct EnsureArgs {
     int64_t* pair_ptr;                             // out: blob pointer of every post-mask pick [P] (or null)
     int32_t* pair_own;                             // out (ensure inside the layer kernel): 1 if pick i is the first
                                                    // pick of its post-mask expert [P] (or null)
+    int32_t* pf_slot;                              // prefetch mode when set: tick not advanced, no fill_all; the
+                                                   // slot of each assigned expert (fill_list order) [max_fill]
 };
 
 struct DecodeArgs {
@@ -87,6 +89,9 @@ int read_status(int* out, hipStream_t s);
 hipError_t launch_dequant(int K, const uint32_t* tr, _Float16* out, int k_tiles, int n_tiles, hipStream_t s);
 // cache.hip
 hipError_t launch_ensure(const EnsureArgs& a, hipStream_t s);
+// prefetch (moe_prefetch a8:1194-1222): ensure in prefetch mode, then copy every assigned expert from its host record
+// (host_base[layer] + e * hstride) into its slot (slot_base + s * sstride, `copy_bytes` bytes) and repoint ptrs_all
+hipError_t launch_prefetch(const EnsureArgs& a, int64_t sstride, int64_t copy_bytes, hipStream_t s);
 hipError_t launch_scatter_flags(uint8_t* flags, int64_t n_flags, const int32_t* packed, int64_t n, hipStream_t s);
 struct TierCopy { const uint8_t* src; uint8_t* dst; int64_t n; };   // n bytes, device -> pinned host
 struct TierCopies { TierCopy c[4]; int n; };

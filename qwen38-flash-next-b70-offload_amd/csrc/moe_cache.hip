@@ -13,6 +13,9 @@
 //      the miss gets the slot and a write-through target fill_all[key]
 // Calls of at most 64 picks whose post-mask picks all hold a slot finish in wave 0 after step 2 (stamps, pair pointers,
 // empty lists): the same decisions without the slot-table staging, the block scans and their barriers.
+// Prefetch mode (pf_slot set; reference moe_prefetch a8:1194-1222 and the prefetch branch of launch_ensure a8:846-851,
+// 884, 1019-1021): T = tick (not advanced, so slots stamped by the last MoE call stay protected), no tier mask, no
+// victims or write-through targets; the assigned slots go to pf_slot for prefetch_copy_kernel and the commit.
 // The reference builds the miss and victim lists with SLM fetch_add, so its pairing is not deterministic; here every
 // list is produced by prefix sums in work-item order, which defines the canonical decisions the oracle restates.
 //
@@ -113,8 +116,8 @@ __global__ void __launch_bounds__(kEnsureThreads) ensure_kernel(EnsureArgs A) {
         const int64_t safe_ptr = A.ram_res && small ? A.ptrs_all[kb + safe] : 0;
         int T = 0;
         if (lane == 0) {
-            T = A.tick[0] + 1;
-            A.tick[0] = T;
+            T = A.pf_slot ? A.tick[0] : A.tick[0] + 1;    // prefetch mode: the tick is not advanced
+            if (!A.pf_slot) A.tick[0] = T;
             sh[0] = T;
         }
         T = __shfl(T, 0, 64);
@@ -328,7 +331,8 @@ __global__ void __launch_bounds__(kEnsureThreads) ensure_kernel(EnsureArgs A) {
                 A.slot_key[s] = key;
                 A.slot_of[key] = s;
                 A.slot_last[s] = T;
-                A.fill_all[key] = A.slot_base + (int64_t)s * A.blob;
+                if (A.pf_slot) A.pf_slot[mi] = s;
+                else A.fill_all[key] = A.slot_base + (int64_t)s * A.blob;
                 A.fill_list[1 + mi] = e;
             }
         }
@@ -374,6 +378,47 @@ hipError_t launch_ensure(const EnsureArgs& a, hipStream_t s) {
     }
     if (lds > 120 * 1024) return hipErrorInvalidValue;
     hipLaunchKernelGGL(ensure_kernel, dim3(1), dim3(kEnsureThreads), lds, s, a);
+    return hipGetLastError();
+}
+
+// ---- prefetch copy and commit ------------------------------------------------------------------------------------------
+// (reference PrefetchCopyKernel and the commit task of moe_prefetch a8:1208-1221) workgroup (mi, chunk) copies 64 KiB of
+// the mi-th assigned expert from its host record (device-mapped pinned memory) into its slot with 16-byte accesses;
+// workgroups past the call's count return. The commit runs after the copy on the same stream, so a reader of ptrs_all
+// that is ordered after it sees the whole blob.
+constexpr int kPrefetchChunk = 64 * 1024;
+
+__global__ void __launch_bounds__(256) prefetch_copy_kernel(const int32_t* fill_list, const int32_t* pf_slot,
+                                                            const int64_t* host_base, int64_t hstride,
+                                                            int64_t slot_base, int64_t sstride, int64_t bytes,
+                                                            int layer, int chunks) {
+    const int mi = blockIdx.x / chunks, ch = blockIdx.x % chunks;
+    if (mi >= fill_list[0]) return;
+    const int e = fill_list[1 + mi], s = pf_slot[mi];
+    const uint8_t* src = (const uint8_t*)(host_base[layer] + (int64_t)e * hstride);
+    uint8_t* dst = (uint8_t*)(slot_base + (int64_t)s * sstride);
+    const int64_t b1 = min(bytes, (int64_t)(ch + 1) * kPrefetchChunk);
+    for (int64_t o = (int64_t)ch * kPrefetchChunk + threadIdx.x * 16; o < b1; o += 256 * 16)
+        *(uint4*)(dst + o) = *(const uint4*)(src + o);
+}
+
+__global__ void __launch_bounds__(256) prefetch_commit_kernel(const int32_t* fill_list, const int32_t* pf_slot,
+                                                              int64_t* ptrs_all, int layer, int E, int64_t slot_base,
+                                                              int64_t sstride) {
+    const int n = fill_list[0];
+    for (int mi = threadIdx.x; mi < n; mi += 256)
+        ptrs_all[(int64_t)layer * E + fill_list[1 + mi]] = slot_base + (int64_t)pf_slot[mi] * sstride;
+}
+
+hipError_t launch_prefetch(const EnsureArgs& a, int64_t sstride, int64_t copy_bytes, hipStream_t s) {
+    hipError_t e = launch_ensure(a, s);
+    if (e != hipSuccess) return e;
+    const int chunks = (int)((copy_bytes + kPrefetchChunk - 1) / kPrefetchChunk);
+    if (a.max_fill > 0 && chunks > 0)
+        hipLaunchKernelGGL(prefetch_copy_kernel, dim3((unsigned)(a.max_fill * chunks)), dim3(256), 0, s, a.fill_list,
+                           a.pf_slot, a.host_base, a.hstride, a.slot_base, sstride, copy_bytes, a.layer, chunks);
+    hipLaunchKernelGGL(prefetch_commit_kernel, dim3(1), dim3(256), 0, s, a.fill_list, a.pf_slot, a.ptrs_all, a.layer,
+                       a.E, a.slot_base, sstride);
     return hipGetLastError();
 }
 

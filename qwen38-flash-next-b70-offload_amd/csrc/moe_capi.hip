@@ -281,6 +281,50 @@ int exl3_moe_forward(const void* x, int x_dtype, int64_t x_stride, int M, int H,
                         workspace, workspace_bytes, (hipStream_t)stream, nullptr, nullptr, nullptr, nullptr, nullptr);
 }
 
+int exl3_moe_prefetch(const int32_t* ids, int n_ids, int64_t* ptrs_all, int layer, int32_t* slot_of,
+                      int32_t* slot_key, int32_t* slot_last, int32_t* tick, int n_slots, const int64_t* host_base,
+                      int64_t slot_base, int32_t* pf_list, int32_t* pf_slot, int max_fill, int n_experts, int64_t blob,
+                      void* stream) {
+    const int E = n_experts;
+    if (n_ids < 0 || layer < 0 || max_fill < 0 || blob <= 0)
+        return fail(EXL3_EINVAL, "moe_prefetch: n_ids=%d layer=%d max_fill=%d blob=%lld", n_ids, layer, max_fill,
+                    (long long)blob);
+    if (E <= 0 || E > kMaxExperts) return fail(EXL3_EINVAL, "moe_prefetch: n_experts=%d must be in 1..%d", E, kMaxExperts);
+    if (n_slots <= 0 || n_ids == 0) return EXL3_OK;            // as the reference: nothing to claim
+    if (!ids || !ptrs_all || !slot_of || !slot_key || !slot_last || !tick || !host_base || !pf_list || !pf_slot)
+        return fail(EXL3_EINVAL, "moe_prefetch: null argument");
+    const int64_t sstride = g_cfg.slot_stride ? g_cfg.slot_stride : blob;
+    const int64_t hstride = g_cfg.host_stride ? g_cfg.host_stride : sstride;
+    if (sstride < blob) return fail(EXL3_EINVAL, "moe_prefetch: slot stride %lld < blob %lld", (long long)sstride,
+                                    (long long)blob);
+    if (blob % 16 || sstride % 16 || hstride % 16 || slot_base % 16)
+        return fail(EXL3_EUNSUPPORTED, "moe_prefetch: blob, strides and slot base must be multiples of 16 bytes");
+    EnsureArgs ea{};
+    ea.ids = const_cast<int32_t*>(ids);           // never written: prefetch mode has no tier mask
+    ea.P = n_ids;
+    ea.layer = layer;
+    ea.E = E;
+    ea.S = n_slots;
+    ea.ptrs_all = ptrs_all;
+    ea.slot_of = slot_of;
+    ea.slot_key = slot_key;
+    ea.slot_last = slot_last;
+    ea.tick = tick;
+    ea.host_base = host_base;
+    ea.slot_base = slot_base;
+    ea.blob = sstride;
+    ea.hstride = hstride;
+    ea.fill_list = pf_list;
+    ea.max_fill = std::min(max_fill, E);
+    ea.log = g_cfg.log;
+    ea.log_cap = g_cfg.log_cap;
+    ea.pf_slot = pf_slot;
+    hipError_t e = launch_prefetch(ea, sstride, blob, (hipStream_t)stream);
+    if (e == hipErrorInvalidValue) return fail(EXL3_EUNSUPPORTED, "moe_prefetch: ensure state does not fit in LDS");
+    if (e != hipSuccess) return hip_fail(e, "prefetch launch");
+    return EXL3_OK;
+}
+
 int exl3_moe_forward_cached(const void* x, int x_dtype, int64_t x_stride, int M, int H, int32_t* topk_ids,
                             float* topk_w, int topk, int64_t* ptrs_all, int layer, int32_t* slot_of, int32_t* slot_key,
                             int32_t* slot_last, int32_t* tick, int n_slots, const int64_t* host_base,

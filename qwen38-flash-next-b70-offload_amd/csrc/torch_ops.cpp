@@ -43,6 +43,28 @@ at::Tensor moe_forward(at::Tensor x, at::Tensor topk_ids, at::Tensor topk_w, at:
     return out;
 }
 
+// moe_prefetch (a8:1194-1222): claim slots for predicted experts of `layer`, copy them from host, repoint the table,
+// on the current stream (use a side stream; make the compute stream wait before the next MoE call)
+void moe_prefetch(at::Tensor ids, at::Tensor ptrs_all, int64_t layer, at::Tensor slot_of, at::Tensor slot_key,
+                  at::Tensor slot_last, at::Tensor tick, at::Tensor host_base, int64_t slot_base, at::Tensor pf_list,
+                  at::Tensor pf_slot, int64_t max_fill, int64_t n_experts, int64_t blob) {
+    TORCH_CHECK(ids.scalar_type() == at::kInt && ids.is_contiguous(), "moe_prefetch: ids int32 contiguous");
+    TORCH_CHECK(ptrs_all.scalar_type() == at::kLong && slot_of.scalar_type() == at::kInt &&
+                    pf_list.scalar_type() == at::kInt && pf_slot.scalar_type() == at::kInt,
+                "moe_prefetch: ptrs_all int64, slot_of / pf_list / pf_slot int32");
+    TORCH_CHECK(ptrs_all.numel() >= (layer + 1) * n_experts && slot_of.numel() == ptrs_all.numel() &&
+                    host_base.numel() > layer && pf_list.numel() >= 1 + n_experts &&
+                    slot_last.numel() == slot_key.numel(),
+                "moe_prefetch: cache state sizes");
+    const int64_t mf = std::min<int64_t>(max_fill, pf_slot.numel());
+    check(exl3_moe_prefetch(ids.data_ptr<int>(), (int)ids.numel(), ptrs_all.data_ptr<int64_t>(), (int)layer,
+                            slot_of.data_ptr<int>(), slot_key.data_ptr<int>(), slot_last.data_ptr<int>(),
+                            tick.data_ptr<int>(), (int)slot_key.numel(), host_base.data_ptr<int64_t>(), slot_base,
+                            pf_list.data_ptr<int>(), pf_slot.data_ptr<int>(), (int)mf, (int)n_experts, blob,
+                            cur_stream(ids)),
+          "moe_prefetch");
+}
+
 at::Tensor moe_forward_cached(at::Tensor x, at::Tensor topk_ids, at::Tensor topk_w, at::Tensor ptrs_all, int64_t layer,
                               at::Tensor slot_of, at::Tensor slot_key, at::Tensor slot_last, at::Tensor tick,
                               at::Tensor host_base, int64_t slot_base, at::Tensor fill_all, at::Tensor fill_list,
@@ -159,6 +181,10 @@ TORCH_LIBRARY(exl3xpu_moe, m) {
           "int slot_base, Tensor(f!) fill_all, Tensor(g!) fill_list, int max_fill, int I, int K, int n_experts, "
           "Tensor(h!) pend, Tensor done_seq) -> Tensor");
     m.impl("moe_forward_cached", c10::DispatchKey::CUDA, &moe_forward_cached);
+    m.def("moe_prefetch(Tensor ids, Tensor(a!) ptrs_all, int layer, Tensor(b!) slot_of, Tensor(c!) slot_key, "
+          "Tensor(d!) slot_last, Tensor tick, Tensor host_base, int slot_base, Tensor(e!) pf_list, Tensor(f!) pf_slot, "
+          "int max_fill, int n_experts, int blob) -> ()");
+    m.impl("moe_prefetch", c10::DispatchKey::CUDA, &moe_prefetch);
     m.def("moe_align(Tensor topk_ids, Tensor topk_w, int n_experts, int pad) -> Tensor[]");
     m.impl("moe_align", c10::DispatchKey::CUDA, &moe_align);
     m.def("host_alloc(int nbytes) -> Tensor", &host_alloc);

@@ -37,6 +37,8 @@ SIGNATURES = {
     "exl3_moe_forward_cached": (c_i32, [c_p, c_i32, c_i64, c_i32, c_i32, c_p, c_p, c_i32, c_p, c_i32, c_p, c_p, c_p, c_p,
                                         c_i32, c_p, c_i64, c_p, c_p, c_i32, c_i32, c_i32, c_i32, c_p, c_i64, c_p, c_sz,
                                         c_p]),
+    "exl3_moe_prefetch": (c_i32, [c_p, c_i32, c_p, c_i32, c_p, c_p, c_p, c_p, c_i32, c_p, c_i64, c_p, c_p, c_i32, c_i32,
+                                  c_i64, c_p]),
     "exl3_moe_align_workspace": (c_sz, [c_i32, c_i32, c_i32]),
     "exl3_moe_align": (c_i32, [c_p, c_p, c_i32, c_i32, c_i32, c_i32, c_p, c_p, c_p, c_sz, c_p]),
     "exl3_dequant": (c_i32, [c_p, c_i32, c_i32, c_i32, c_p, c_p]),

@@ -123,6 +123,8 @@ class ExpertStore:
         self.host_base = torch.zeros(max_layers, dtype=torch.int64, device=self.dev)
         self.fill_all = torch.zeros(LE, dtype=torch.int64, device=self.dev)
         self.fill_list = torch.zeros(1 + n_experts, dtype=torch.int32, device=self.dev)
+        self.pf_list = torch.zeros(1 + n_experts, dtype=torch.int32, device=self.dev)   # prefetch: [n, e...]
+        self.pf_slot = torch.zeros(n_experts, dtype=torch.int32, device=self.dev)       # prefetch: slot of each
         self.pend = torch.zeros(max_layers * 35, dtype=torch.int32, device=self.dev)
         self.done_seq = torch.zeros(0, dtype=torch.int32, device=self.dev)
         self.slot_base = s64(self.slots.data_ptr()) if n_slots else 0
@@ -265,7 +267,18 @@ class ExpertStore:
                                          self.I, self.k_of(key), self.E, self.pend, self.done_seq)
 
     def prefetch(self, key, ids: torch.Tensor, max_fill: int = 16) -> None:
-        raise NotImplementedError("exl3xpu: predicted-expert prefetch (moe_prefetch) is not built in this library")
+        """Bring the predicted experts `ids` of layer `key` into HBM slots ahead of their MoE call (moe_offload.py:
+        251-262): the device cache claims exact-LRU slots for up to `max_fill` of them that are not resident, without
+        advancing the tick (slots used by the last MoE call are never taken), copies them from their host records and
+        repoints the layer's table. Everything is enqueued on the current stream; run it on a side stream that has
+        waited for the previous MoE call, and make the compute stream wait for that stream before the next one."""
+        if not self.n_slots:
+            return
+        ids = ids if ids.dtype == torch.int32 and ids.is_contiguous() else ids.to(torch.int32).contiguous()
+        self._cache_used = True
+        self.X.moe_prefetch(ids.flatten(), self.ptrs_all, self.layer_index[key], self.slot_of_dev, self.slot_key,
+                            self.slot_last, self.tick, self.host_base, self.slot_base, self.pf_list, self.pf_slot,
+                            max_fill, self.E, int(self.X.blob_bytes(self.H, self.I, self.k_of(key))))
 
     def start_copy_prefetch(self) -> None:
         raise NotImplementedError("exl3xpu: the copy-engine prefetch worker is not built in this library")

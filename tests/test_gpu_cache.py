@@ -324,3 +324,79 @@ def test_tier_exchange():
     assert np.array_equal(flags.cpu().numpy(), want)
     bad = (ctypes.c_void_p * 1)(srcs[1].data_ptr() + 4)
     assert run(0, 5000, 5000, nc=1, src=bad)[0] != 0
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("fused", [1, 0])
+def test_cache_prefetch(fused):
+    """moe_prefetch between MoE calls, on a side stream ordered after the previous call and before the next one (the
+    reference caller's protocol, moe_offload.py:251-262): every prefetch and ensure decision equals the oracle's
+    (prefetch mode: tick not advanced, slots of the last call protected, exact LRU, max_fill cap), every slot holds
+    its expert's blob, the final slot tables equal the oracle's, and every cached output equals the uncached one."""
+    import ctypes
+    from exl3xpu import nvtier
+    L, E, H, I, K, nd, steps, P, S, mf = 2, 128, 128, 128, 3, 16, 40, 8, 60, 5
+    print(f"case cache prefetch fused={fused}", flush=True)
+    store = nvtier.TierStore(H, I, K, E, S, n_layers=L)
+    keys = [f"model.layers.{li}.mlp" for li in range(L)]
+    for k in keys:
+        store.add_layer(k)
+    src = nvtier.SyntheticExpertSource(H, I, K, 81, n_distinct=nd)
+    for key in range(L * E):
+        ctypes.memmove(store.addr(key), src.buf[key % nd].ctypes.data, src.blob)
+    dev = torch.from_numpy(src.buf).cuda()
+    table = torch.tensor([dev[e % nd].data_ptr() for e in range(E)], dtype=torch.int64, device="cuda")
+    rng = np.random.default_rng(82)
+    pr = 1.0 / np.arange(1, E + 1) ** 1.2
+    pr /= pr.sum()
+    ids = np.stack([[rng.choice(E, P, replace=False, p=pr) for _ in range(L)] for _ in range(steps + 1)]).astype(np.int32)
+    w = rng.random(ids.shape, dtype=np.float32)
+    # predicted experts of the next call: half of the true next picks, the rest drawn uniformly
+    pred = np.zeros((steps, L, P), np.int32)
+    for n in range(steps):
+        for li in range(L):
+            keep = list(ids[n + 1, li][:P // 2])
+            rest = [e for e in rng.permutation(E) if e not in keep][:P - len(keep)]
+            pred[n, li] = np.array(keep + rest, np.int32)
+    co = cache.CacheOracle(L, E, S, tier=False)
+    X = store.X
+    rl = cache.rec_len(P)
+    logbuf = torch.zeros(1 + 2 * steps * L * rl, dtype=torch.int32, device="cuda")
+    X.moe_set_decision_log(logbuf)
+    X.moe_set_fused_ensure(fused)
+    side = torch.cuda.Stream()
+    x = torch.randn(1, H, generator=torch.Generator().manual_seed(3)).to(torch.bfloat16).cuda()
+    orecs, bad = [], 0
+    try:
+        for n in range(steps):
+            for li in range(L):
+                orecs.append(co.ensure(li, ids[n, li].copy(), w[n, li].copy()))
+                it = torch.from_numpy(ids[n, li]).view(1, P).cuda()
+                wt = torch.from_numpy(w[n, li]).view(1, P).cuda()
+                out = store.forward_cached(keys[li], x, it, wt)
+                ref = X.moe_forward(x, it, wt, table, I, K, E)
+                bad += int(not torch.equal(out, ref))
+                orecs.append(co.prefetch(li, pred[n, li].copy(), max_fill=mf))
+                side.wait_stream(torch.cuda.current_stream())
+                with torch.cuda.stream(side):
+                    store.prefetch(keys[li], torch.from_numpy(pred[n, li]).cuda(), max_fill=mf)
+                torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+    finally:
+        X.moe_set_decision_log(torch.zeros(0, dtype=torch.int32, device="cuda"))
+        X.moe_set_fused_ensure(1)
+    lg = logbuf.cpu().numpy()
+    assert lg[0] == 2 * steps * L
+    recs = lg[1:].reshape(2 * steps * L, rl)
+    orecs = np.stack(orecs)
+    mism = np.nonzero((recs != orecs).any(axis=-1))[0]
+    assert mism.size == 0, f"first mismatch at call {mism[0]} ({'prefetch' if mism[0] % 2 else 'ensure'})"
+    pf_nm = recs[1::2, 2 + P]
+    assert pf_nm.sum() > 0 and pf_nm.max() <= mf and (pf_nm == mf).any()   # prefetches claimed slots, capped
+    assert (recs[0::2, 2 + P] < P).any()                                   # some picks were already prefetched
+    sk = store.slot_key.cpu().numpy()
+    assert np.array_equal(sk, co.slot_key) and np.array_equal(store.slot_last.cpu().numpy(), co.slot_last)
+    slots = store.slots.cpu().numpy()
+    for s in np.nonzero(sk >= 0)[0]:
+        assert np.array_equal(slots[s, :src.blob], src.buf[sk[s] % nd]), f"slot {s}"
+    assert bad == 0

@@ -183,3 +183,34 @@ def test_cache_invariants_zipf():
         assert int((co.slot_of >= 0).sum()) == own.size <= S
         # budget holds after eviction, except for device write-backs flagged during the step
         assert int(co.res.sum()) + int(co.inflight.sum()) <= 60 + 2 * L * P
+
+
+def test_cache_oracle_prefetch_hand_case():
+    """Prefetch mode (moe_prefetch, a8:846-851, 1194-1222) on a case derived by hand: 4 slots, 8 experts, no tier.
+    The tick is not advanced, so slots stamped by the last MoE call stay protected; hits are re-stamped with the
+    current tick; misses take exact-LRU slots among those older than the tick."""
+    L, E, S, P = 1, 8, 4, 2
+    co = cache.CacheOracle(L, E, S, tier=False)
+    k = cache.rec_len
+    # MoE call 1 (T = 1): experts 0, 1 miss and take the empty slots 0, 1 (u = 0, ascending slot)
+    r = co.ensure(0, np.array([0, 1], np.int32), np.ones(2, np.float32))
+    assert r[0] == 1 and r[2 + P] == 2 and r[3 + P:3 + 2 * P].tolist() == [0, 1]
+    assert r[3 + 2 * P:].tolist() == [-1, 0, -1, 1]
+    # prefetch of [2, 3, 1] (T stays 1): 1 hits; 2, 3 take the empty slots 2, 3; nothing is advanced
+    r = co.prefetch(0, np.array([2, 3, 1], np.int32))
+    assert len(r) == k(3) and r[0] == 1 and r[2 + 3] == 2
+    assert r[3 + 3:3 + 6].tolist() == [2, 3, -1] and r[3 + 6:3 + 10].tolist() == [-1, 2, -1, 3]
+    assert co.tick[0] == 1 and co.slot_last.tolist() == [1, 1, 1, 1] and co.slot_key.tolist() == [0, 1, 2, 3]
+    # prefetch of [4]: every slot was stamped by the current tick, so none is eligible
+    r = co.prefetch(0, np.array([4], np.int32))
+    assert r[2 + 1] == 0 and co.slot_of[4] == -1 and co.slot_key.tolist() == [0, 1, 2, 3]
+    # MoE call 2 (T = 2) with [3, 4]: 3 hits (stamped 2); 4 misses; eligible slots 0, 1, 2 all hold u = 2 -> slot 0,
+    # whose owner (expert 0) goes back to host
+    r = co.ensure(0, np.array([3, 4], np.int32), np.ones(2, np.float32))
+    assert r[0] == 2 and r[2 + P] == 1 and r[3 + P] == 4 and r[3 + 2 * P:3 + 2 * P + 2].tolist() == [0, 0]
+    assert co.slot_of[0] == -1 and co.slot_of[4] == 0 and co.slot_last.tolist() == [2, 1, 1, 2]
+    # prefetch of [0, 5, 6] with max_fill 2 (T stays 2): misses 0, 5 (ascending, capped at 2) take the LRU slots 1, 2
+    r = co.prefetch(0, np.array([0, 5, 6], np.int32), max_fill=2)
+    assert r[0] == 2 and r[2 + 3] == 2 and r[3 + 3:3 + 5].tolist() == [0, 5]
+    assert r[3 + 6:3 + 10].tolist() == [1, 1, 2, 2]          # (old key 1, slot 1), (old key 2, slot 2)
+    assert co.slot_key.tolist() == [4, 0, 5, 3] and co.slot_last.tolist() == [2, 2, 2, 2] and co.tick[0] == 2
