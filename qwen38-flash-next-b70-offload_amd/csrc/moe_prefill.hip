@@ -199,8 +199,16 @@ __device__ __forceinline__ void ld_act8(const void* x, int dt, size_t i, float (
 __global__ void __launch_bounds__(64 * kXhWaves) prefill_xh_kernel(PrefillArgs A) {
     __shared__ __align__(16) half_t hmat[128 * 128];             // H128, row n contiguous in k
     __shared__ __align__(16) half_t tbuf[kXhWaves][32 * kXhRow]; // per wave: [pair][column] of one block
-    for (int i = threadIdx.x; i < 128 * 128; i += 64 * kXhWaves)
-        hmat[i] = (__popc((i >> 7) & (i & 127)) & 1) ? (half_t)-1.0f : (half_t)1.0f;
+    // H128[n][k] = (-1)^popc(n & k); 8 consecutive k = k0 + j (k0 a multiple of 8) share the sign of n & k0, so each
+    // thread builds 8 entries from one parity and stores them with one 16-byte write
+    for (int i8 = threadIdx.x; i8 < 128 * 128 / 8; i8 += 64 * kXhWaves) {
+        const int n = i8 >> 4, k0 = (i8 & 15) * 8;
+        const int base = __popc(n & k0) & 1;
+        half8_t v;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[j] = ((base ^ __popc(n & j)) & 1) ? (half_t)-1.0f : (half_t)1.0f;
+        *(half8_t*)(hmat + n * 128 + k0) = v;
+    }
     __syncthreads();
     const int H = A.g.H, nkb = H / 128;
     const int l = lane_id(), wv = threadIdx.x >> 6;
