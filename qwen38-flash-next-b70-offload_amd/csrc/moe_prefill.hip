@@ -176,12 +176,13 @@ hipError_t launch_align(const int32_t* ids, const float* w, int npairs, int topk
 constexpr int kXhWaves = 4;
 constexpr int kXhRow = 128 + 8;                                  // LDS row of one pair's block (halfs, padded)
 
-// 8 consecutive activations as fp32 (exact for every input dtype)
-__device__ __forceinline__ void ld_act8(const void* x, int dt, size_t i, float (&v)[8]) {
-    if (dt == 2) {
+// 8 consecutive activations as fp32 (exact for every input dtype); DT: 0 fp16, 1 bf16, 2 fp32
+template <int DT>
+__device__ __forceinline__ void ld_act8(const void* x, size_t i, float (&v)[8]) {
+    if constexpr (DT == 2) {
         const float4 a = *(const float4*)((const float*)x + i), b = *(const float4*)((const float*)x + i + 4);
         v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
-    } else if (dt == 1) {
+    } else if constexpr (DT == 1) {
         const uint4 u = *(const uint4*)((const bf16_bits*)x + i);
         const uint32_t w[4] = {u.x, u.y, u.z, u.w};
 #pragma unroll
@@ -196,29 +197,16 @@ __device__ __forceinline__ void ld_act8(const void* x, int dt, size_t i, float (
     }
 }
 
-__global__ void __launch_bounds__(64 * kXhWaves) prefill_xh_kernel(PrefillArgs A) {
-    __shared__ __align__(16) half_t hmat[128 * 128];             // H128, row n contiguous in k
-    __shared__ __align__(16) half_t tbuf[kXhWaves][32 * kXhRow]; // per wave: [pair][column] of one block
-    // H128[n][k] = (-1)^popc(n & k); 8 consecutive k = k0 + j (k0 a multiple of 8) share the sign of n & k0, so each
-    // thread builds 8 entries from one parity and stores them with one 16-byte write
-    for (int i8 = threadIdx.x; i8 < 128 * 128 / 8; i8 += 64 * kXhWaves) {
-        const int n = i8 >> 4, k0 = (i8 & 15) * 8;
-        const int base = __popc(n & k0) & 1;
-        half8_t v;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) v[j] = ((base ^ __popc(n & j)) & 1) ? (half_t)-1.0f : (half_t)1.0f;
-        *(half8_t*)(hmat + n * 128 + k0) = v;
-    }
-    __syncthreads();
+template <int DT>
+__device__ __forceinline__ void xh_blocks(const PrefillArgs& A, const half_t* hmat, half_t (*tbuf)[32 * kXhRow]) {
     const int H = A.g.H, nkb = H / 128;
     const int l = lane_id(), wv = threadIdx.x >> 6;
     const int pj = blockIdx.x & 1, blk = blockIdx.x >> 1;
-    const int s = blk * 64 + (wv & 1) * 32 + (l & 31);           // this lane's pair row (B operand column)
-    const bool valid = s < A.npairs;
-    const size_t xrow = valid ? (size_t)A.pair_tok[s] * A.x_stride : 0;
-    const half_t* suh = valid ? (const half_t*)((const uint8_t*)A.ptrs[A.pair_exp[s]] +
-                                                (pj ? A.g.off_suh_u : A.g.off_suh_g))
-                              : nullptr;
+    // this lane's pair row (B operand column); lanes past the last pair read the last pair, so that no load is
+    // conditional and the 16 loads of a block are in flight together (those rows are never stored)
+    const int s = min(blk * 64 + (wv & 1) * 32 + (l & 31), A.npairs - 1);
+    const size_t xrow = (size_t)A.pair_tok[s] * A.x_stride;
+    const half_t* suh = (const half_t*)((const uint8_t*)A.ptrs[A.pair_exp[s]] + (pj ? A.g.off_suh_u : A.g.off_suh_g));
     const int s0 = blk * 64 + (wv & 1) * 32;                    // the wave's 32 pairs
     half_t* tb = tbuf[wv];
     for (int kb = (wv >> 1); kb < nkb; kb += 2) {
@@ -226,15 +214,11 @@ __global__ void __launch_bounds__(64 * kXhWaves) prefill_xh_kernel(PrefillArgs A
 #pragma unroll
         for (int ks = 0; ks < 8; ++ks) {
             const int k = kb * 128 + ks * 16 + (l >> 5) * 8;
-            if (valid) {
-                float xv[8];
-                ld_act8(A.x, A.x_dt, xrow + k, xv);
-                const half8_t sv = *(const half8_t*)(suh + k);
+            float xv[8];
+            ld_act8<DT>(A.x, xrow + k, xv);
+            const half8_t sv = *(const half8_t*)(suh + k);
 #pragma unroll
-                for (int j = 0; j < 8; ++j) bx[ks][j] = (half_t)(xv[j] * (float)sv[j]);
-            } else {
-                bx[ks] = half8_t{};
-            }
+            for (int j = 0; j < 8; ++j) bx[ks][j] = (half_t)(xv[j] * (float)sv[j]);
         }
 #pragma unroll
         for (int nb = 0; nb < 4; ++nb) {
@@ -261,6 +245,26 @@ __global__ void __launch_bounds__(64 * kXhWaves) prefill_xh_kernel(PrefillArgs A
             if (s0 + pr < A.npairs) *(half8_t*)(A.xh + ((size_t)(s0 + pr) * 2 + pj) * H + kb * 128 + col) = v;
         }
     }
+}
+
+__global__ void __launch_bounds__(64 * kXhWaves) prefill_xh_kernel(PrefillArgs A) {
+    __shared__ __align__(16) half_t hmat[128 * 128];             // H128, row n contiguous in k
+    __shared__ __align__(16) half_t tbuf[kXhWaves][32 * kXhRow]; // per wave: [pair][column] of one block
+    // H128[n][k] = (-1)^popc(n & k); 8 consecutive k = k0 + j (k0 a multiple of 8) share the sign of n & k0, so each
+    // thread builds 8 entries from one parity and stores them with one 16-byte write
+    for (int i8 = threadIdx.x; i8 < 128 * 128 / 8; i8 += 64 * kXhWaves) {
+        const int n = i8 >> 4, k0 = (i8 & 15) * 8;
+        const int base = __popc(n & k0) & 1;
+        half8_t v;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[j] = ((base ^ __popc(n & j)) & 1) ? (half_t)-1.0f : (half_t)1.0f;
+        *(half8_t*)(hmat + n * 128 + k0) = v;
+    }
+    __syncthreads();
+    // the block loop per activation dtype (no dtype branch between a block's loads)
+    if (A.x_dt == 1) xh_blocks<1>(A, hmat, tbuf);
+    else if (A.x_dt == 2) xh_blocks<2>(A, hmat, tbuf);
+    else xh_blocks<0>(A, hmat, tbuf);
 }
 
 // ---- LDS layouts of one K chunk ----------------------------------------------------------------------------------------
