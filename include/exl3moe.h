@@ -113,6 +113,29 @@ int exl3_moe_prefetch(const int32_t* ids, int n_ids, int64_t* ptrs_all, int laye
                       int64_t slot_base, int32_t* pf_list, int32_t* pf_slot, int max_fill, int n_experts, int64_t blob,
                       void* stream);
 
+/* Copy-engine prefetch (a8:1047-1142; moe_offload.py:264-302). moe_prefetch_plan: the ensure in plan mode on the
+ * compute stream: claims up to 16 exact-LRU slots (tick not advanced) for predicted experts of `layer`, pins them
+ * (slot_last = INT_MAX), records them in pend[layer] (int32 [n_layers][35]: n, seq, T, e[16], s[16]) and publishes
+ * the plan in pinned host memory (plans int32 [n_layers][4 + 2 n_experts]: seq, n, T, layer, e[], s[]); a layer whose
+ * previous plan is pending is skipped. Every plan call, and every moe_forward_cached call while
+ * exl3_set_prefetch_commit is set, first commits the plans with done_seq[layer] >= their seq (ptrs_all -> slot,
+ * slot_last = the plan's tick; the fused ensure is off meanwhile). */
+int exl3_moe_prefetch_plan(const int32_t* ids, int n_ids, int64_t* ptrs_all, int layer, int32_t* slot_of,
+                           int32_t* slot_key, int32_t* slot_last, int32_t* tick, int n_slots,
+                           const int64_t* host_base, int64_t slot_base, int32_t* pf_list, int32_t* pf_slot,
+                           int32_t* plans, int32_t* plan_seq, int32_t* pend, const int32_t* done_seq, int n_layers,
+                           int max_fill, int n_experts, int64_t blob, void* stream);
+/* moe_prefetch_worker_start / _stop: a host thread polls `plans`; per new plan it copies each claimed expert from
+ * host_base_host[layer] + e * host stride into its slot on `stream` (a dedicated stream), then copies the plan's seq
+ * (from seq_host, pinned int32 [n_layers][2]) into done_seq[layer] on the same stream. Stop drains the stream and
+ * returns [plans handled, experts copied] in counts. */
+int exl3_prefetch_worker_start(int32_t* plans, const int64_t* host_base_host, int64_t slot_base, int64_t blob,
+                               int32_t* done_seq, int32_t* seq_host, int n_layers, int n_experts, void* stream);
+int exl3_prefetch_worker_stop(int64_t* counts);
+/* the pending-plan tables that moe_forward_cached commits from (n_layers 0: off); moe_forward_cached's pend /
+ * done_seq arguments (a8:1229-1261) set it per call */
+int exl3_set_prefetch_commit(int32_t* pend, const int32_t* done_seq, int n_layers);
+
 /* moe_align (a8:1316-1323 -> launch_align a8:639-680): token sort by expert into the reference's packed buffers:
  * ib int32 [4A + 1 + 2*npairs + 16] = act_expert[A] act_start[A] act_cnt[A] act_pstart[A] n_act pair_tok[npairs]
  * pair_of[npairs] ..., fb fp32 [npairs] = pair_w, A = min(npairs, n_experts); active experts ascending, act_pstart the

@@ -53,6 +53,8 @@ def lib():
         L.co_ensure.argtypes = [P, I32, P, P, I32, I32, P]
         L.co_prefetch.restype = I32
         L.co_prefetch.argtypes = [P, I32, P, I32, I32, P]
+        L.co_plan.restype = I32
+        L.co_plan.argtypes = [P, I32, P, I32, I32, P]
         L.co_host_step.restype = I64
         L.co_host_step.argtypes = [P, P, P, P, P]
         L.co_run.restype = I64
@@ -123,6 +125,15 @@ class CacheOracle:
         P = ids.size
         rec = np.zeros(rec_len(P), dtype=np.int32)
         lib().co_prefetch(self._c, layer, _ptr(ids), P, self.E if max_fill is None else max_fill, _ptr(rec))
+        return rec
+
+    def plan(self, layer: int, ids: np.ndarray, max_fill: int | None = None):
+        """One copy-engine plan (moe_prefetch_plan): a prefetch of at most 16 experts whose slots stay pinned until
+        the next call commits them (the caller waits for the copy worker in between). Returns the decision record."""
+        assert ids.dtype == np.int32 and ids.flags.c_contiguous
+        P = ids.size
+        rec = np.zeros(rec_len(P), dtype=np.int32)
+        lib().co_plan(self._c, layer, _ptr(ids), P, self.E if max_fill is None else max_fill, _ptr(rec))
         return rec
 
     def host_step(self):

@@ -13,6 +13,13 @@
  *                                              prefetch mode (moe_prefetch): the tick is not advanced (slots of the last
  *                                              call, last == T, stay protected), no tier mask, no write-back, the
  *                                              assigned slots are the pf_slot list
+ *   kernels/moe-a8/exl3_moe.a8.sycl:853-901, 1013-1038, 1127-1142
+ *                                              copy-engine plan mode (moe_prefetch_plan): prefetch mode with at most 16
+ *                                              misses, claimed slots pinned (slot_last = INT_MAX) and recorded as the
+ *                                              layer's pending plan; a layer with a pending plan is skipped; every call
+ *                                              first commits the finished pending plans (slot_last = the plan's tick).
+ *                                              Here a plan is finished by the next call (the caller waits for the copy
+ *                                              worker), the protocol the tests follow.
  *   plugin/exl3xpu/nvtier.py:57-87, 179-188    tier init (pinned safe expert per layer, tick = 1)
  *   plugin/exl3xpu/nvtier.py:282-386, 708-806  NvTierAsync one-step-lagged snapshot + _async_step_admit
  *
@@ -48,6 +55,8 @@ typedef struct {
     /* scratch */
     uint32_t *u_tmp; int32_t *i_tmp; int64_t *l_tmp, *l_tmp2; int32_t *cnt_tmp; uint8_t *view, *resn;
     int64_t stats_masked, stats_evicts, stats_admit_dropped, stats_ring_overflow;
+    /* pending copy-engine prefetch plans per layer: count, tick, (expert, slot) x 16 */
+    int32_t *pend_n, *pend_T, *pend_e, *pend_s;
 } co_t;
 
 static void *xcalloc(size_t n, size_t s) { void *p = calloc(n ? n : 1, s); return p; }
@@ -82,6 +91,8 @@ co_t *co_new(int L, int E, int S, int ring_cap, int tier, int budget, int age_mi
     c->l_tmp = (int64_t *)xcalloc(n > ring_cap ? n : ring_cap, 8); c->l_tmp2 = (int64_t *)xcalloc(n > ring_cap ? n : ring_cap, 8);
     c->cnt_tmp = (int32_t *)xcalloc(n, 4);
     c->view = (uint8_t *)xcalloc(n, 1); c->resn = (uint8_t *)xcalloc(n, 1);
+    c->pend_n = (int32_t *)xcalloc(L, 4); c->pend_T = (int32_t *)xcalloc(L, 4);
+    c->pend_e = (int32_t *)xcalloc((size_t)L * 16, 4); c->pend_s = (int32_t *)xcalloc((size_t)L * 16, 4);
     return c;
 }
 
@@ -94,6 +105,7 @@ void co_free(co_t *c) {
     for (int i = 0; i <= c->latency; ++i) free(c->done[i]);
     free(c->done); free(c->n_done);
     free(c->u_tmp); free(c->i_tmp); free(c->l_tmp); free(c->l_tmp2); free(c->cnt_tmp); free(c->view); free(c->resn);
+    free(c->pend_n); free(c->pend_T); free(c->pend_e); free(c->pend_s);
     free(c);
 }
 
@@ -137,8 +149,15 @@ static uint32_t kth_smallest(uint32_t *a, int n, int k) {
  */
 int co_rec_len(int P) { return 3 + 4 * P; }
 
-static int ensure_impl(co_t *c, int layer, int32_t *ids, float *w, int P, int max_fill, int32_t *rec, int prefetch) {
+/* mode: 0 decode, 1 prefetch, 2 copy-engine plan */
+static int ensure_impl(co_t *c, int layer, int32_t *ids, float *w, int P, int max_fill, int32_t *rec, int mode) {
     const int E = c->E, S = c->S;
+    const int prefetch = mode != 0, plan = mode == 2;
+    for (int li = 0; li < c->L && mode != 1; ++li) {           /* commit finished plans (a8:856-880; not in a
+                                                                  * prefetch call, which has no pending table) */
+        for (int i = 0; i < c->pend_n[li]; ++i) c->slot_last[c->pend_s[li * 16 + i]] = c->pend_T[li];
+        c->pend_n[li] = 0;
+    }
     const int32_t T = prefetch ? c->tick : ++c->tick;          /* a8:884 */
     const int tier = c->tier && !prefetch;                     /* prefetch: no mask, no write-back (a8:846-851) */
     int32_t *need = c->cnt_tmp;                                /* E entries used */
@@ -165,6 +184,7 @@ static int ensure_impl(co_t *c, int layer, int32_t *ids, float *w, int P, int ma
         else miss[nmiss++] = e;
     }
     int mf = max_fill < E ? max_fill : E;
+    if (plan && mf > 16) mf = 16;                              /* a8:1135 */
     int nm = S > 0 ? (nmiss < mf ? nmiss : mf) : 0;
     int nelig = 0;
     if (nm > 0) {
@@ -195,12 +215,14 @@ static int ensure_impl(co_t *c, int layer, int32_t *ids, float *w, int P, int ma
             if (tier && old >= 0 && c->ram_res[old]) wb = -1;
             if (old >= 0) c->slot_of[old] = -1;
             int key = layer * E + e;
-            c->slot_key[s] = key; c->slot_of[key] = s; c->slot_last[s] = T;
+            c->slot_key[s] = key; c->slot_of[key] = s; c->slot_last[s] = plan ? 0x7FFFFFFF : T;
+            if (plan) { c->pend_e[layer * 16 + mi] = e; c->pend_s[layer * 16 + mi] = s; }
             if (rec) { rec[3 + P + mi] = e; rec[3 + 2 * P + 2 * mi] = wb; rec[3 + 2 * P + 2 * mi + 1] = s; }
             if (tier && wb >= 0) c->ram_res[wb] = 1;            /* VictimCopyKernel a8:1180 */
         }
         free(V);
     }
+    if (plan && nm > 0) { c->pend_n[layer] = nm; c->pend_T[layer] = T; }
     if (rec) { rec[1] = c->ring[0]; rec[2 + P] = nm; }
     return nm;
 }
@@ -213,6 +235,11 @@ int co_ensure(co_t *c, int layer, int32_t *ids, float *w, int P, int max_fill, i
  * pf_slot lists, and the old owner's record field holds the old key (no write-back decision) */
 int co_prefetch(co_t *c, int layer, int32_t *ids, int P, int max_fill, int32_t *rec) {
     return ensure_impl(c, layer, ids, NULL, P, max_fill, rec, 1);
+}
+
+/* moe_prefetch_plan's ensure (a8:1127-1142): a prefetch whose claimed slots stay pinned until the next call */
+int co_plan(co_t *c, int layer, int32_t *ids, int P, int max_fill, int32_t *rec) {
+    return ensure_impl(c, layer, ids, NULL, P, max_fill, rec, 2);
 }
 
 /* stable sort of keys[0..n) by age ascending (ties: keys are already ascending) */

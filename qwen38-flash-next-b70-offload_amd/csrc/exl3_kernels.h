@@ -37,7 +37,15 @@ struct EnsureArgs {
                                                    // pick of its post-mask expert [P] (or null)
     int32_t* pf_slot;                              // prefetch mode when set: tick not advanced, no fill_all; the
                                                    // slot of each assigned expert (fill_list order) [max_fill]
+    int32_t* host_plan;                            // plan mode (with pf_slot): [seq, n, T, layer, e[E], s[E]] in
+                                                   // pinned host memory for the copy worker; claimed slots pinned
+    int32_t* plan_seq;                             // [n_layers] plans published per layer
+    int32_t* pend;                                 // [n_layers][kPendStride] pending plans: n, seq, T, e[16], s[16]
+    const int32_t* done_seq;                       // [n_layers] last plan whose copies finished (copy engine)
+    int n_layers;                                  // commit finished plans first when pend and n_layers > 0
 };
+constexpr int kPendStride = 35;                    // pend record: n, seq, T, e[16], s[16]
+constexpr int kPlanMax = 16;                       // experts per copy-engine plan
 
 struct DecodeArgs {
     const void* x; int x_dt; int64_t x_stride;     // activations [M, H], dt 0 = fp16, 1 = bf16

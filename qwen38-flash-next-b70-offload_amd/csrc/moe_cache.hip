@@ -16,6 +16,11 @@
 // Prefetch mode (pf_slot set; reference moe_prefetch a8:1194-1222 and the prefetch branch of launch_ensure a8:846-851,
 // 884, 1019-1021): T = tick (not advanced, so slots stamped by the last MoE call stay protected), no tier mask, no
 // victims or write-through targets; the assigned slots go to pf_slot for prefetch_copy_kernel and the commit.
+// Plan mode (host_plan set as well; moe_prefetch_plan a8:1127-1142, launch_ensure a8:853-901, 1013-1038): at most 16
+// claims, pinned (slot_last = INT_MAX) and recorded in pend; the plan goes to pinned host memory for the copy worker
+// (entries, a system-scope fence, then the sequence number). A layer whose previous plan is pending is skipped. With
+// pend set, every call first commits the plans whose copies the worker has finished (done_seq >= the plan's sequence
+// number): ptrs_all -> slot, slot_last = the plan's tick.
 // The reference builds the miss and victim lists with SLM fetch_add, so its pairing is not deterministic; here every
 // list is produced by prefix sums in work-item order, which defines the canonical decisions the oracle restates.
 //
@@ -103,6 +108,32 @@ __global__ void __launch_bounds__(kEnsureThreads) ensure_kernel(EnsureArgs A) {
     int* sl = pid + P;                // [S] when staged
     const bool sl_lds = S <= kEnsureLdsSlots;
     const int32_t* slg = A.slot_last;
+    if (A.pend && A.n_layers > 0) {                           // commit finished copy-engine plans first
+        int* vflag = sl + (sl_lds ? S : 0);                   // [n_layers]
+        for (int li = tid; li < A.n_layers; li += kEnsureThreads) {
+            const int32_t* pl = A.pend + li * kPendStride;
+            const int dn = __hip_atomic_load(A.done_seq + li, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+            vflag[li] = (pl[0] > 0 && dn >= pl[1]) ? 1 : 0;
+        }
+        __syncthreads();
+        for (int t = tid; t < A.n_layers * kPlanMax; t += kEnsureThreads) {
+            const int li = t / kPlanMax, i = t % kPlanMax;
+            const int32_t* pl = A.pend + li * kPendStride;
+            if (vflag[li] && i < pl[0]) {
+                const int e = pl[3 + i], s = pl[3 + kPlanMax + i];
+                A.ptrs_all[(int64_t)li * E + e] = A.slot_base + (int64_t)s * A.blob;
+                A.slot_last[s] = pl[2];
+            }
+        }
+        __syncthreads();
+        for (int li = tid; li < A.n_layers; li += kEnsureThreads)
+            if (vflag[li]) A.pend[li * kPendStride] = 0;
+        __syncthreads();
+    }
+    if (A.host_plan && A.pend[A.layer * kPendStride] > 0) {  // this layer's previous plan is still being copied
+        if (tid == 0) A.fill_list[0] = 0;
+        return;
+    }
 
     // Calls of at most 64 picks keep pick `lane`'s post-mask slot and blob pointer in wave 0's registers: loaded in the
     // same round as the tier mask, they serve the fast path, the slow path's hit stamps and the pair pointers.
@@ -330,10 +361,17 @@ __global__ void __launch_bounds__(kEnsureThreads) ensure_kernel(EnsureArgs A) {
                 const int key = A.layer * E + e;
                 A.slot_key[s] = key;
                 A.slot_of[key] = s;
-                A.slot_last[s] = T;
+                A.slot_last[s] = A.host_plan ? INT_MAX : T;
                 if (A.pf_slot) A.pf_slot[mi] = s;
                 else A.fill_all[key] = A.slot_base + (int64_t)s * A.blob;
                 A.fill_list[1 + mi] = e;
+                if (A.host_plan) {
+                    A.host_plan[4 + mi] = e;
+                    A.host_plan[4 + E + mi] = s;
+                    A.pend[A.layer * kPendStride + 3 + mi] = e;
+                    A.pend[A.layer * kPendStride + 3 + kPlanMax + mi] = s;
+                    __threadfence_system();                   // the entries reach host memory before the seq below
+                }
             }
         }
     }
@@ -341,6 +379,19 @@ __global__ void __launch_bounds__(kEnsureThreads) ensure_kernel(EnsureArgs A) {
     if (tid == 0) {
         A.fill_list[0] = nm;
         if (A.vict) A.vict[0] = nm;
+        if (A.host_plan && nm > 0) {                          // publish the plan: header, fence, then the seq
+            A.host_plan[1] = nm;
+            A.host_plan[2] = T;
+            A.host_plan[3] = A.layer;
+            __threadfence_system();
+            const int sq = A.plan_seq[A.layer] + 1;
+            A.plan_seq[A.layer] = sq;
+            int32_t* pl = A.pend + A.layer * kPendStride;
+            pl[1] = sq;
+            pl[2] = T;
+            pl[0] = nm;
+            __hip_atomic_store(A.host_plan, sq, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+        }
     }
     // blob pointer of every post-mask pick (calls of more than 64 picks; see the wave-0 block for the others)
     if (A.pair_ptr && !small)
@@ -368,7 +419,8 @@ __global__ void __launch_bounds__(kEnsureThreads) ensure_kernel(EnsureArgs A) {
 // ---- host launchers ------------------------------------------------------------------------------------------------
 
 hipError_t launch_ensure(const EnsureArgs& a, hipStream_t s) {
-    const size_t lds = (size_t)(4 * a.E + a.P + (a.S <= kEnsureLdsSlots ? a.S : 0)) * sizeof(int);
+    const size_t lds =
+        (size_t)(4 * a.E + a.P + (a.S <= kEnsureLdsSlots ? a.S : 0) + (a.pend ? a.n_layers : 0)) * sizeof(int);
     static bool attr = false;
     if (!attr) {
         hipError_t e = hipFuncSetAttribute((const void*)ensure_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,

@@ -2,10 +2,14 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <atomic>
 #include <cstdarg>
 #include <cstdio>
+#include <memory>
 #include <mutex>
 #include <string>
+#include <thread>
+#include <vector>
 
 #include "../../include/exl3moe.h"
 #include "exl3_kernels.h"
@@ -30,8 +34,64 @@ struct Config {
     int gu_p = 0, dn_p = 0, mr = 0, debug = 0;
     int32_t* log = nullptr;
     int64_t log_cap = 0;
+    int32_t* pend = nullptr;                      // copy-engine prefetch: pending plans committed by every ensure
+    const int32_t* done_seq = nullptr;
+    int n_layers = 0;
 };
 Config g_cfg;
+
+// Copy-engine prefetch worker (reference PfWorker a8:1047-1090): a host thread that polls the plans the plan-mode
+// ensure publishes in pinned host memory and, per new plan, copies each claimed expert from its host record into its
+// slot on the worker's stream, then copies the plan's sequence number into done_seq[layer] on the same stream (after
+// the data). The device commits a plan in the first ensure that sees done_seq >= its sequence number.
+struct PrefetchWorker {
+    std::thread th;
+    std::atomic<bool> stop{false};
+    int32_t* plans = nullptr;                     // [L][4 + 2E]: seq, n, T, layer, e[E], s[E]
+    int L = 0, E = 0, dev = 0;
+    std::vector<int64_t> host_base;               // per layer
+    int64_t slot_base = 0, sstride = 0, hstride = 0, blob = 0;
+    int32_t* done_seq = nullptr;                  // device [L]
+    int32_t* seqv = nullptr;                      // pinned host [L][2]: stable sources of the done_seq copies
+    hipStream_t s = nullptr;
+    std::vector<int> last_seq;
+    std::atomic<int64_t> n_plans{0}, n_copies{0};
+    hipError_t err = hipSuccess;
+
+    void run() {
+        (void)hipSetDevice(dev);
+        const int stride = 4 + 2 * E;
+        while (!stop.load(std::memory_order_relaxed)) {
+            bool any = false;
+            for (int li = 0; li < L; ++li) {
+                int32_t* pl = plans + (size_t)li * stride;
+                const int seq = __atomic_load_n(pl, __ATOMIC_ACQUIRE);
+                if (seq == last_seq[li]) continue;
+                any = true;
+                const int n = __atomic_load_n(pl + 1, __ATOMIC_ACQUIRE);
+                for (int i = 0; i < n && err == hipSuccess; ++i) {
+                    const int e = pl[4 + i], sl = pl[4 + E + i];
+                    err = hipMemcpyAsync((void*)(slot_base + (int64_t)sl * sstride),
+                                         (const void*)(host_base[li] + (int64_t)e * hstride), (size_t)blob,
+                                         hipMemcpyHostToDevice, s);
+                }
+                // one plan per layer is in flight at a time (the plan-mode ensure skips a pending layer), so the two
+                // parity slots keep the source of the previous copy intact
+                int32_t* sv = seqv + li * 2 + (seq & 1);
+                *sv = seq;
+                if (err == hipSuccess) err = hipMemcpyAsync(done_seq + li, sv, 4, hipMemcpyHostToDevice, s);
+                last_seq[li] = seq;
+                n_plans++;
+                n_copies += n;
+            }
+            if (!any) std::this_thread::yield();
+        }
+        const hipError_t e = hipStreamSynchronize(s);
+        if (err == hipSuccess) err = e;
+    }
+};
+std::unique_ptr<PrefetchWorker> g_pfw;
+std::mutex g_pfw_mu;
 
 int fail(int code, const char* fmt, ...) {
     char buf[512];
@@ -325,6 +385,108 @@ int exl3_moe_prefetch(const int32_t* ids, int n_ids, int64_t* ptrs_all, int laye
     return EXL3_OK;
 }
 
+int exl3_set_prefetch_commit(int32_t* pend, const int32_t* done_seq, int n_layers) {
+    if (n_layers < 0 || (n_layers > 0 && (!pend || !done_seq)))
+        return fail(EXL3_EINVAL, "set_prefetch_commit: n_layers=%d with null tables", n_layers);
+    g_cfg.pend = pend;
+    g_cfg.done_seq = done_seq;
+    g_cfg.n_layers = n_layers;
+    return EXL3_OK;
+}
+
+int exl3_moe_prefetch_plan(const int32_t* ids, int n_ids, int64_t* ptrs_all, int layer, int32_t* slot_of,
+                           int32_t* slot_key, int32_t* slot_last, int32_t* tick, int n_slots,
+                           const int64_t* host_base, int64_t slot_base, int32_t* pf_list, int32_t* pf_slot,
+                           int32_t* plans, int32_t* plan_seq, int32_t* pend, const int32_t* done_seq, int n_layers,
+                           int max_fill, int n_experts, int64_t blob, void* stream) {
+    const int E = n_experts;
+    if (n_ids < 0 || layer < 0 || max_fill < 0 || blob <= 0 || n_layers <= layer)
+        return fail(EXL3_EINVAL, "moe_prefetch_plan: n_ids=%d layer=%d n_layers=%d max_fill=%d", n_ids, layer,
+                    n_layers, max_fill);
+    if (E <= 0 || E > kMaxExperts)
+        return fail(EXL3_EINVAL, "moe_prefetch_plan: n_experts=%d must be in 1..%d", E, kMaxExperts);
+    if (n_slots <= 0 || n_ids == 0) return EXL3_OK;
+    if (!ids || !ptrs_all || !slot_of || !slot_key || !slot_last || !tick || !host_base || !pf_list || !pf_slot ||
+        !plans || !plan_seq || !pend || !done_seq)
+        return fail(EXL3_EINVAL, "moe_prefetch_plan: null argument");
+    const int64_t sstride = g_cfg.slot_stride ? g_cfg.slot_stride : blob;
+    if (sstride < blob) return fail(EXL3_EINVAL, "moe_prefetch_plan: slot stride < blob");
+    EnsureArgs ea{};
+    ea.ids = const_cast<int32_t*>(ids);           // never written: no tier mask in plan mode
+    ea.P = n_ids;
+    ea.layer = layer;
+    ea.E = E;
+    ea.S = n_slots;
+    ea.ptrs_all = ptrs_all;
+    ea.slot_of = slot_of;
+    ea.slot_key = slot_key;
+    ea.slot_last = slot_last;
+    ea.tick = tick;
+    ea.host_base = host_base;
+    ea.slot_base = slot_base;
+    ea.blob = sstride;
+    ea.hstride = g_cfg.host_stride ? g_cfg.host_stride : sstride;
+    ea.fill_list = pf_list;
+    ea.max_fill = std::min(std::min(max_fill, E), kPlanMax);
+    ea.log = g_cfg.log;
+    ea.log_cap = g_cfg.log_cap;
+    ea.pf_slot = pf_slot;
+    ea.host_plan = plans + (size_t)layer * (4 + 2 * E);
+    ea.plan_seq = plan_seq;
+    ea.pend = pend;
+    ea.done_seq = done_seq;
+    ea.n_layers = n_layers;
+    const hipError_t e = launch_ensure(ea, (hipStream_t)stream);
+    if (e == hipErrorInvalidValue) return fail(EXL3_EUNSUPPORTED, "moe_prefetch_plan: ensure state does not fit in LDS");
+    if (e != hipSuccess) return hip_fail(e, "prefetch plan launch");
+    return EXL3_OK;
+}
+
+int exl3_prefetch_worker_start(int32_t* plans, const int64_t* host_base_host, int64_t slot_base, int64_t blob,
+                               int32_t* done_seq, int32_t* seq_host, int n_layers, int n_experts, void* stream) {
+    std::lock_guard<std::mutex> lk(g_pfw_mu);
+    if (g_pfw) return fail(EXL3_EINVAL, "prefetch worker already running");
+    if (!plans || !host_base_host || !done_seq || !seq_host || n_layers <= 0 || n_experts <= 0 || blob <= 0)
+        return fail(EXL3_EINVAL, "prefetch_worker_start: bad arguments");
+    auto w = std::make_unique<PrefetchWorker>();
+    hipError_t e = hipGetDevice(&w->dev);
+    if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+    w->plans = plans;
+    w->L = n_layers;
+    w->E = n_experts;
+    w->host_base.assign(host_base_host, host_base_host + n_layers);
+    w->slot_base = slot_base;
+    w->blob = blob;
+    w->sstride = g_cfg.slot_stride ? g_cfg.slot_stride : blob;
+    w->hstride = g_cfg.host_stride ? g_cfg.host_stride : w->sstride;
+    w->done_seq = done_seq;
+    w->seqv = seq_host;
+    w->s = (hipStream_t)stream;
+    w->last_seq.resize(n_layers);
+    for (int li = 0; li < n_layers; ++li)
+        w->last_seq[li] = __atomic_load_n(plans + (size_t)li * (4 + 2 * n_experts), __ATOMIC_ACQUIRE);
+    PrefetchWorker* raw = w.get();
+    w->th = std::thread([raw] { raw->run(); });
+    g_pfw = std::move(w);
+    return EXL3_OK;
+}
+
+int exl3_prefetch_worker_stop(int64_t* counts) {
+    std::lock_guard<std::mutex> lk(g_pfw_mu);
+    if (counts) counts[0] = counts[1] = 0;
+    if (!g_pfw) return EXL3_OK;
+    g_pfw->stop = true;
+    g_pfw->th.join();
+    if (counts) {
+        counts[0] = g_pfw->n_plans.load();
+        counts[1] = g_pfw->n_copies.load();
+    }
+    const hipError_t e = g_pfw->err;
+    g_pfw.reset();
+    if (e != hipSuccess) return hip_fail(e, "prefetch worker copies");
+    return EXL3_OK;
+}
+
 int exl3_moe_forward_cached(const void* x, int x_dtype, int64_t x_stride, int M, int H, int32_t* topk_ids,
                             float* topk_w, int topk, int64_t* ptrs_all, int layer, int32_t* slot_of, int32_t* slot_key,
                             int32_t* slot_last, int32_t* tick, int n_slots, const int64_t* host_base,
@@ -380,8 +542,12 @@ int exl3_moe_forward_cached(const void* x, int x_dtype, int64_t x_stride, int M,
         return fail(EXL3_EWORKSPACE, "moe_forward_cached: workspace %zu < %zu bytes", workspace_bytes, need);
     // the ensure inside the layer kernel needs one thread per expert, one lane per pick and the slot stamps in
     // registers; K = 4 kernels run one workgroup per CU, too few to let the victim workgroups wait for it
+    ea.pend = g_cfg.n_layers > 0 ? g_cfg.pend : nullptr;       // commit finished copy-engine plans first
+    ea.done_seq = g_cfg.done_seq;
+    ea.n_layers = g_cfg.n_layers;
+    // the ensure inside the layer kernel has no plan commit: calls with plans in use run the ensure kernel
     const bool fused = g_cfg.fused_ensure && E <= kEnsMaxE && P <= kEnsMaxP && n_slots <= kEnsMaxE * kEnsRegSlots &&
-                       K <= 3;
+                       K <= 3 && !ea.pend;
     if (!fused) {
         ea.pair_ptr = pair_ptr_area(workspace, P, H, I);
         hipError_t e = launch_ensure(ea, st);

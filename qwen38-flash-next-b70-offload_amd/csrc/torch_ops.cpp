@@ -65,13 +65,61 @@ void moe_prefetch(at::Tensor ids, at::Tensor ptrs_all, int64_t layer, at::Tensor
           "moe_prefetch");
 }
 
+// copy-engine prefetch (a8:1047-1142): plan on the current (compute) stream; the worker copies on the stream that is
+// current when it starts
+void moe_prefetch_plan(at::Tensor ids, at::Tensor ptrs_all, int64_t layer, at::Tensor slot_of, at::Tensor slot_key,
+                       at::Tensor slot_last, at::Tensor tick, at::Tensor host_base, int64_t slot_base, at::Tensor pf_list,
+                       at::Tensor pf_slot, at::Tensor plans, at::Tensor plan_seq, at::Tensor pend, at::Tensor done_seq,
+                       int64_t max_fill, int64_t n_experts, int64_t blob) {
+    TORCH_CHECK(ids.scalar_type() == at::kInt && ids.is_contiguous(), "moe_prefetch_plan: ids int32 contiguous");
+    const int64_t L = done_seq.numel();
+    TORCH_CHECK(L > layer && plan_seq.numel() >= L && pend.numel() >= L * 35 &&
+                    plans.nbytes() >= (size_t)(L * (4 + 2 * n_experts) * 4) && pf_list.numel() >= 1 + n_experts,
+                "moe_prefetch_plan: plan state sizes (start_copy_prefetch first)");
+    check(exl3_moe_prefetch_plan(ids.data_ptr<int>(), (int)ids.numel(), ptrs_all.data_ptr<int64_t>(), (int)layer,
+                                 slot_of.data_ptr<int>(), slot_key.data_ptr<int>(), slot_last.data_ptr<int>(),
+                                 tick.data_ptr<int>(), (int)slot_key.numel(), host_base.data_ptr<int64_t>(), slot_base,
+                                 pf_list.data_ptr<int>(), pf_slot.data_ptr<int>(), (int32_t*)plans.data_ptr(),
+                                 plan_seq.data_ptr<int>(), pend.data_ptr<int>(), done_seq.data_ptr<int>(), (int)L,
+                                 (int)std::min<int64_t>(max_fill, pf_slot.numel()), (int)n_experts, blob,
+                                 cur_stream(ids)),
+          "moe_prefetch_plan");
+}
+
+void moe_prefetch_worker_start(at::Tensor plans, at::Tensor host_base_cpu, int64_t slot_base, int64_t blob,
+                               at::Tensor ptrs_all, at::Tensor slot_last, at::Tensor commit_host, at::Tensor done_seq,
+                               int64_t n_layers, int64_t n_experts) {
+    (void)ptrs_all;
+    (void)slot_last;       // the commit runs on the device (ensure); the worker only publishes done_seq
+    TORCH_CHECK(host_base_cpu.device().is_cpu() && host_base_cpu.scalar_type() == at::kLong &&
+                    host_base_cpu.numel() >= n_layers && commit_host.nbytes() >= (size_t)(n_layers * 2 * 4),
+                "moe_prefetch_worker_start: host_base_cpu int64 [n_layers] on the CPU, commit_host pinned");
+    auto hb = host_base_cpu.contiguous();
+    check(exl3_prefetch_worker_start((int32_t*)plans.data_ptr(), hb.data_ptr<int64_t>(), slot_base, blob,
+                                     done_seq.data_ptr<int>(), (int32_t*)commit_host.data_ptr(), (int)n_layers,
+                                     (int)n_experts, cur_stream(done_seq)),
+          "moe_prefetch_worker_start");
+}
+
+std::vector<int64_t> moe_prefetch_worker_stop() {
+    int64_t c[2] = {0, 0};
+    check(exl3_prefetch_worker_stop(c), "moe_prefetch_worker_stop");
+    return {c[0], c[1]};
+}
+
 at::Tensor moe_forward_cached(at::Tensor x, at::Tensor topk_ids, at::Tensor topk_w, at::Tensor ptrs_all, int64_t layer,
                               at::Tensor slot_of, at::Tensor slot_key, at::Tensor slot_last, at::Tensor tick,
                               at::Tensor host_base, int64_t slot_base, at::Tensor fill_all, at::Tensor fill_list,
                               int64_t max_fill, int64_t I, int64_t K, int64_t n_experts, at::Tensor pend,
                               at::Tensor done_seq) {
-    (void)pend;
-    (void)done_seq;     // copy-engine prefetch commits are not built (the prefetch worker is not part of this library)
+    // plans of the copy-engine prefetch are committed by this call's ensure when done_seq is in use
+    if (done_seq.numel() > 0) {
+        TORCH_CHECK(pend.numel() >= done_seq.numel() * 35, "moe_forward_cached: pend [n_layers * 35]");
+        check(exl3_set_prefetch_commit(pend.data_ptr<int>(), done_seq.data_ptr<int>(), (int)done_seq.numel()),
+              "moe_forward_cached");
+    } else {
+        check(exl3_set_prefetch_commit(nullptr, nullptr, 0), "moe_forward_cached");
+    }
     TORCH_CHECK(x.dim() == 2 && x.stride(1) == 1, "moe_forward_cached: x must be [M, H] with unit column stride");
     TORCH_CHECK(ptrs_all.scalar_type() == at::kLong && fill_all.scalar_type() == at::kLong &&
                     slot_of.scalar_type() == at::kInt,
@@ -185,6 +233,15 @@ TORCH_LIBRARY(exl3xpu_moe, m) {
           "Tensor(d!) slot_last, Tensor tick, Tensor host_base, int slot_base, Tensor(e!) pf_list, Tensor(f!) pf_slot, "
           "int max_fill, int n_experts, int blob) -> ()");
     m.impl("moe_prefetch", c10::DispatchKey::CUDA, &moe_prefetch);
+    m.def("moe_prefetch_plan(Tensor ids, Tensor(a!) ptrs_all, int layer, Tensor(b!) slot_of, Tensor(c!) slot_key, "
+          "Tensor(d!) slot_last, Tensor tick, Tensor host_base, int slot_base, Tensor(e!) pf_list, Tensor(f!) pf_slot, "
+          "Tensor(g!) plans, Tensor(h!) plan_seq, Tensor(i!) pend, Tensor done_seq, int max_fill, int n_experts, "
+          "int blob) -> ()");
+    m.impl("moe_prefetch_plan", c10::DispatchKey::CUDA, &moe_prefetch_plan);
+    m.def("moe_prefetch_worker_start(Tensor plans, Tensor host_base_cpu, int slot_base, int blob, Tensor ptrs_all, "
+          "Tensor slot_last, Tensor commit_host, Tensor done_seq, int n_layers, int n_experts) -> ()",
+          &moe_prefetch_worker_start);
+    m.def("moe_prefetch_worker_stop() -> int[]", &moe_prefetch_worker_stop);
     m.def("moe_align(Tensor topk_ids, Tensor topk_w, int n_experts, int pad) -> Tensor[]");
     m.impl("moe_align", c10::DispatchKey::CUDA, &moe_align);
     m.def("host_alloc(int nbytes) -> Tensor", &host_alloc);

@@ -39,6 +39,11 @@ SIGNATURES = {
                                         c_p]),
     "exl3_moe_prefetch": (c_i32, [c_p, c_i32, c_p, c_i32, c_p, c_p, c_p, c_p, c_i32, c_p, c_i64, c_p, c_p, c_i32, c_i32,
                                   c_i64, c_p]),
+    "exl3_moe_prefetch_plan": (c_i32, [c_p, c_i32, c_p, c_i32, c_p, c_p, c_p, c_p, c_i32, c_p, c_i64, c_p, c_p, c_p,
+                                       c_p, c_p, c_p, c_i32, c_i32, c_i32, c_i64, c_p]),
+    "exl3_prefetch_worker_start": (c_i32, [c_p, c_p, c_i64, c_i64, c_p, c_p, c_i32, c_i32, c_p]),
+    "exl3_prefetch_worker_stop": (c_i32, [c_p]),
+    "exl3_set_prefetch_commit": (c_i32, [c_p, c_p, c_i32]),
     "exl3_moe_align_workspace": (c_sz, [c_i32, c_i32, c_i32]),
     "exl3_moe_align": (c_i32, [c_p, c_p, c_i32, c_i32, c_i32, c_i32, c_p, c_p, c_p, c_sz, c_p]),
     "exl3_dequant": (c_i32, [c_p, c_i32, c_i32, c_i32, c_p, c_p]),

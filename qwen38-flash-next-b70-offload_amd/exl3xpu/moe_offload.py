@@ -280,8 +280,48 @@ class ExpertStore:
                             self.slot_last, self.tick, self.host_base, self.slot_base, self.pf_list, self.pf_slot,
                             max_fill, self.E, int(self.X.blob_bytes(self.H, self.I, self.k_of(key))))
 
+    # ---- copy-engine prefetch (moe_offload.py:264-302): device plan -> host worker -> copies -> device commit
     def start_copy_prefetch(self) -> None:
-        raise NotImplementedError("exl3xpu: the copy-engine prefetch worker is not built in this library")
+        """Start the host worker that copies the experts of published prefetch plans into their slots on a
+        dedicated stream; later ensures (forward_cached, plan_prefetch) commit the plans whose copies finished."""
+        L, E = len(self.layer_index), self.E
+        self._plans = self.X.host_alloc(L * (4 + 2 * E) * 4)
+        self._plans.zero_()
+        self._plan_seq = torch.zeros(L, dtype=torch.int32, device=self.dev)
+        self.done_seq = torch.zeros(L, dtype=torch.int32, device=self.dev)
+        self.pend.zero_()
+        self._commit_host = self.X.host_alloc(L * 2 * 4)
+        hb = torch.zeros(L, dtype=torch.int64)
+        for key, li in self.layer_index.items():
+            hb[li] = int(self._host_ptr[key][0])
+        torch.cuda.synchronize(self.dev)
+        self._pf_stream = torch.cuda.Stream(self.dev)
+        with torch.cuda.stream(self._pf_stream):                 # the worker's copies go to this stream
+            self.X.moe_prefetch_worker_start(self._plans, hb, self.slot_base, self.blob, self.ptrs_all,
+                                             self.slot_last, self._commit_host, self.done_seq, L, E)
+
+    def plan_prefetch(self, key, ids: torch.Tensor, max_fill: int = 16) -> None:
+        """On the compute stream (for instance right after the MoE call of the previous layer): claim and pin slots for
+        up to 16 predicted experts of `key` and publish the plan to the worker. The compute stream never waits for the
+        copies; the experts are used from their slots once a later ensure has committed the plan."""
+        ids = ids if ids.dtype == torch.int32 and ids.is_contiguous() else ids.to(torch.int32).contiguous()
+        self._cache_used = True
+        self.X.moe_prefetch_plan(ids.flatten(), self.ptrs_all, self.layer_index[key], self.slot_of_dev, self.slot_key,
+                                 self.slot_last, self.tick, self.host_base, self.slot_base, self.pf_list, self.pf_slot,
+                                 self._plans, self._plan_seq, self.pend, self.done_seq, max_fill, self.E, self.blob)
+
+    def stop_copy_prefetch(self):
+        """Stop the worker (its stream drained), commit what finished with one empty ensure pass, and return
+        [plans handled, experts copied]; forward_cached then runs without plan commits."""
+        r = self.X.moe_prefetch_worker_stop()
+        if self.done_seq.numel():
+            k0 = next(iter(self.layer_index))
+            x = torch.zeros((1, self.H), dtype=torch.bfloat16, device=self.dev)
+            ids = torch.zeros((1, 1), dtype=torch.int32, device=self.dev)
+            self.forward_cached(k0, x, ids, torch.ones((1, 1), device=self.dev), max_fill=0)
+            torch.cuda.synchronize(self.dev)
+            self.done_seq = torch.zeros(0, dtype=torch.int32, device=self.dev)
+        return r
 
     # ---- prefill staging (moe_offload.py:305-462)
     def stage_layer(self, key, buf: int, stream) -> torch.Tensor:

@@ -400,3 +400,84 @@ def test_cache_prefetch(fused):
     for s in np.nonzero(sk >= 0)[0]:
         assert np.array_equal(slots[s, :src.blob], src.buf[sk[s] % nd]), f"slot {s}"
     assert bad == 0
+
+
+@pytest.mark.gpu
+def test_cache_copy_prefetch():
+    """Copy-engine prefetch (moe_offload.py:264-302): after each MoE call the next layer's predicted experts are
+    planned on the compute stream (slots claimed and pinned), the host worker copies them on its own stream, and the
+    next ensure commits the finished plan. Waiting for the worker between calls makes the sequence deterministic: every
+    plan and ensure decision equals the oracle's plan mode, the worker reports the plans and copies the records hold,
+    every slot holds its expert's blob, the final tables equal the oracle's, and every output equals the uncached one."""
+    import ctypes
+    import time
+    from exl3xpu import nvtier
+    L, E, H, I, K, nd, steps, P, S, mf = 2, 128, 128, 128, 3, 16, 30, 8, 60, 6
+    print("case cache copy-engine prefetch", flush=True)
+    store = nvtier.TierStore(H, I, K, E, S, n_layers=L)
+    keys = [f"model.layers.{li}.mlp" for li in range(L)]
+    for k in keys:
+        store.add_layer(k)
+    src = nvtier.SyntheticExpertSource(H, I, K, 83, n_distinct=nd)
+    for key in range(L * E):
+        ctypes.memmove(store.addr(key), src.buf[key % nd].ctypes.data, src.blob)
+    dev = torch.from_numpy(src.buf).cuda()
+    table = torch.tensor([dev[e % nd].data_ptr() for e in range(E)], dtype=torch.int64, device="cuda")
+    rng = np.random.default_rng(84)
+    pr = 1.0 / np.arange(1, E + 1) ** 1.2
+    pr /= pr.sum()
+    ids = np.stack([[rng.choice(E, P, replace=False, p=pr) for _ in range(L)] for _ in range(steps + 1)]).astype(np.int32)
+    w = rng.random(ids.shape, dtype=np.float32)
+    co = cache.CacheOracle(L, E, S, tier=False)
+    X = store.X
+    rl = cache.rec_len(P)
+    logbuf = torch.zeros(1 + 2 * steps * L * rl, dtype=torch.int32, device="cuda")
+    x = torch.randn(1, H, generator=torch.Generator().manual_seed(4)).to(torch.bfloat16).cuda()
+
+    def wait_worker():
+        torch.cuda.synchronize()
+        t0 = time.monotonic()
+        while not torch.equal(store.done_seq.cpu(), store._plan_seq.cpu()):
+            assert time.monotonic() - t0 < 10.0, "prefetch worker did not finish its copies"
+            time.sleep(0.0005)
+
+    store.start_copy_prefetch()
+    X.moe_set_decision_log(logbuf)
+    orecs, bad, planned, copied = [], 0, 0, 0
+    try:
+        for n in range(steps):
+            for li in range(L):
+                orecs.append(co.ensure(li, ids[n, li].copy(), w[n, li].copy()))
+                it = torch.from_numpy(ids[n, li]).view(1, P).cuda()
+                wt = torch.from_numpy(w[n, li]).view(1, P).cuda()
+                out = store.forward_cached(keys[li], x, it, wt)
+                ref = X.moe_forward(x, it, wt, table, I, K, E)
+                bad += int(not torch.equal(out, ref))
+                # the next call's layer and picks (true picks reversed: the cap of mf takes a different subset)
+                nn_, nli = (n, li + 1) if li + 1 < L else (n + 1, 0)
+                pred = ids[nn_, nli][::-1].copy()
+                r = co.plan(nli, pred.copy(), max_fill=mf)
+                orecs.append(r)
+                planned += int(r[2 + P] > 0)
+                copied += int(r[2 + P])
+                store.plan_prefetch(keys[nli], torch.from_numpy(pred).cuda(), max_fill=mf)
+                wait_worker()
+        torch.cuda.synchronize()
+    finally:
+        X.moe_set_decision_log(torch.zeros(0, dtype=torch.int32, device="cuda"))
+        counts = store.stop_copy_prefetch()
+    co.ensure(0, np.zeros(1, np.int32), np.ones(1, np.float32), max_fill=0)      # the stop's commit pass
+    lg = logbuf.cpu().numpy()
+    assert lg[0] == 2 * steps * L
+    recs = lg[1:].reshape(2 * steps * L, rl)
+    orecs = np.stack(orecs)
+    mism = np.nonzero((recs != orecs).any(axis=-1))[0]
+    assert mism.size == 0, f"first mismatch at call {mism[0]} ({'plan' if mism[0] % 2 else 'ensure'})"
+    assert list(counts) == [planned, copied] and copied > 0
+    assert (recs[1::2, 2 + P] <= mf).all() and (recs[0::2, 2 + P] < P).any()
+    sk = store.slot_key.cpu().numpy()
+    assert np.array_equal(sk, co.slot_key) and np.array_equal(store.slot_last.cpu().numpy(), co.slot_last)
+    slots = store.slots.cpu().numpy()
+    for s in np.nonzero(sk >= 0)[0]:
+        assert np.array_equal(slots[s, :src.blob], src.buf[sk[s] % nd]), f"slot {s}"
+    assert bad == 0

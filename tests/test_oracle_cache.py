@@ -214,3 +214,33 @@ def test_cache_oracle_prefetch_hand_case():
     assert r[0] == 2 and r[2 + 3] == 2 and r[3 + 3:3 + 5].tolist() == [0, 5]
     assert r[3 + 6:3 + 10].tolist() == [1, 1, 2, 2]          # (old key 1, slot 1), (old key 2, slot 2)
     assert co.slot_key.tolist() == [4, 0, 5, 3] and co.slot_last.tolist() == [2, 2, 2, 2] and co.tick[0] == 2
+
+
+def test_cache_oracle_plan_hand_case():
+    """Copy-engine plan mode (moe_prefetch_plan, a8:853-901, 1013-1038, 1127-1142) on a case derived by hand: claimed
+    slots are pinned (never victims, hits do not re-stamp them) until the next call commits them with the plan's
+    tick; at most 16 misses per plan."""
+    L, E, S = 1, 8, 4
+    co = cache.CacheOracle(L, E, S, tier=False)
+    co.ensure(0, np.array([0, 1], np.int32), np.ones(2, np.float32))           # T = 1: experts 0, 1 -> slots 0, 1
+    r = co.plan(0, np.array([2, 3], np.int32))                                  # T stays 1: 2, 3 -> slots 2, 3
+    assert r[0] == 1 and r[2 + 2] == 2 and r[3 + 2:3 + 4].tolist() == [2, 3]
+    assert co.slot_last.tolist() == [1, 1, 0x7FFFFFFF, 0x7FFFFFFF] and co.tick[0] == 1
+    # next decode call (T = 2): the plan is committed first (slots 2, 3 -> tick 1); 2 hits (stamped 2); 5 misses and
+    # takes the lowest slot among the eligible u = 2 (slots 0, 1, 3): slot 0, evicting expert 0
+    r = co.ensure(0, np.array([2, 5], np.int32), np.ones(2, np.float32))
+    assert r[0] == 2 and r[2 + 2] == 1 and r[3 + 2] == 5 and r[3 + 4:3 + 6].tolist() == [0, 0]
+    assert co.slot_last.tolist() == [2, 1, 2, 1] and co.slot_key.tolist() == [5, 1, 2, 3]
+    r = co.plan(0, np.array([4], np.int32))                                     # T = 2: 4 -> slot 1, pinned
+    assert r[2 + 1] == 1 and r[3 + 2 * 1 + 1] == 1 and co.slot_last[1] == 0x7FFFFFFF
+    # a second plan commits the first (slot 1 -> 2), so only slot 3 (last 1 < 2) is eligible: 6 -> slot 3
+    r = co.plan(0, np.array([6, 7], np.int32))
+    assert r[2 + 2] == 1 and r[3 + 2] == 6 and r[3 + 4:3 + 6].tolist() == [3, 3]
+    assert co.slot_last.tolist() == [2, 2, 2, 0x7FFFFFFF] and co.slot_key.tolist() == [5, 4, 2, 6]
+    # a prefetch call does not commit pending plans: slot 3 stays pinned and is not a victim
+    r = co.prefetch(0, np.array([7], np.int32))
+    assert r[2 + 1] == 0 and co.slot_last[3] == 0x7FFFFFFF
+    # the cap: a plan claims at most 16 slots whatever max_fill says
+    co2 = cache.CacheOracle(1, 64, 40, tier=False)
+    r = co2.plan(0, np.arange(30, dtype=np.int32), max_fill=30)
+    assert r[2 + 30] == 16 and int((co2.slot_last == 0x7FFFFFFF).sum()) == 16
