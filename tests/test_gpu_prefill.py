@@ -278,3 +278,54 @@ def test_tier_ensure_for_prefill():
         assert torch.equal(out, ref)
     finally:
         tier.close()
+
+
+def test_plugin_caller_sequence():
+    """The tier plugin's call sequence (plugin/sglang_plugin.tier.py:531-561 `apply`, 944-956 the host step after every
+    model step) over this API, tier mode: a 300-token prompt streamed through stage_forward, a 24-token prompt
+    (ensure_for_prefill, then the zero-copy forward), then decode steps through forward_cached (tier mask, RAM hits
+    written through), NvTierAsync.step after every model step. Every prompt output equals the all-resident output bit
+    for bit; every decode output equals the uncached forward on the true blobs with the post-mask picks."""
+    from exl3xpu import nvtier
+    H, I, K, E, S, L, topk, dsteps = 256, 128, 3, 32, 24, 3, 4, 40
+    print("case plugin caller sequence", flush=True)
+    store = nvtier.TierStore(H, I, K, E, S, n_layers=L)
+    keys = [f"model.layers.{li}.mlp" for li in range(L)]
+    for k in keys:
+        store.add_layer(k)
+    src = nvtier.SyntheticExpertSource(H, I, K, 23, n_distinct=L * E)
+    tier = nvtier.NvTierAsync(store, src, budget_records=40, latency=2)
+    blobs = torch.from_numpy(src.buf).cuda()
+    tables = [torch.tensor([blobs[li * E + e].data_ptr() for e in range(E)], dtype=torch.int64, device="cuda")
+              for li in range(L)]
+
+    def apply(li, x, it, wt, stage):            # the plugin's dispatch in tier mode
+        if x.shape[0] >= 3:
+            if stage and x.shape[0] >= 256:
+                return tier.stage_forward(store, keys[li], li, x, it, wt)
+            tier.ensure_for_prefill(li, it)
+            return store.forward(keys[li], x, it, wt)
+        store.prefill_reset()
+        return store.forward_cached(keys[li], x, it, wt)
+
+    bad, masked = [], 0
+    try:
+        steps = [(300, True, 90), (24, False, 91)] + [(1, False, 100 + n) for n in range(dsteps)]
+        for M, stage, seed in steps:
+            for li in range(L):
+                ids, w = synth.softmax_topk(seed * 7 + li, M, E, topk)
+                x = torch.from_numpy(exl3.bf16_to_f32(synth.activations(seed + li, M, H))).to(torch.bfloat16).cuda()
+                it, wt = torch.from_numpy(ids).cuda(), torch.from_numpy(w).cuda()
+                out = apply(li, x, it, wt, stage)
+                if M == 1:
+                    masked += int((wt == 0).sum().item())
+                ref = _ops().moe_forward(x, it, wt, tables[li], I, K, E)     # it / wt after the tier mask
+                torch.cuda.synchronize()
+                if not torch.equal(out, ref):
+                    bad.append((M, seed, li))
+            tier.step()                            # the host step hook after every model step
+        torch.cuda.synchronize()
+    finally:
+        tier.close()
+    assert not bad, f"outputs differ at (M, seed, layer) {bad[:4]}"
+    assert masked > 0                              # the decode steps exercised the tier mask
