@@ -167,9 +167,12 @@ hipError_t launch_align(const int32_t* ids, const float* w, int npairs, int topk
 
 // ---- xh pre-pass: input Hadamards as MFMA products with the +-1 matrix H128 ------------------------------------------
 // xh[s][pj][kb*128 + n] = fp16(sum_k H[n][k] * fp16(x[tok(s)][kb*128 + k] * suh_pj(e(s))[kb*128 + k]) / sqrt(128)).
-// Computed transposed (C^T = H * xt^T) with v_mfma_f32_32x32x16_f16: A = rows n of H (LDS table), B = 32 pair rows of
-// xt (built in registers from x and the pair's expert's suh), so each lane ends with 4 consecutive columns of one
-// pair row per accumulator group and stores them as 8 bytes. The fp32 sums differ from the butterfly order only in
+// Computed transposed (C^T = H * xt^T) with v_mfma_f32_32x32x16_f16: A = rows n of H, B = 32 pair rows of xt (built in
+// registers from x and the pair's expert's suh), so each lane ends with 4 consecutive columns of one pair row per
+// accumulator group. H[n][k] = (-1)^popc(n & k) splits over the bits of n and k: with n = 32 nb + n', k = 16 ks + k'
+// (n' < 32, k' < 16), popc(n & k) = popc(n' & (16 (ks & 1) + k')) + popc(nb & (ks >> 1)), so the A fragment of
+// (nb, ks) is one of two per-lane fragments, negated when popc(nb & (ks >> 1)) is odd: four fragments in registers
+// (built once per wave) instead of an H table in LDS. The fp32 sums differ from the butterfly order only in
 // rounding. Workgroup of 4 waves per (64 sorted pairs, projection): wave w takes the 32 rows 32 (w & 1) .. and the
 // 128-column blocks kb = (w >> 1), (w >> 1) + 2, ... The fp16 results of a block go through LDS ([pair][column]) so
 // that 16 lanes store one pair's 256-byte row segment with 16-byte stores.
@@ -198,9 +201,18 @@ __device__ __forceinline__ void ld_act8(const void* x, size_t i, float (&v)[8]) 
 }
 
 template <int DT>
-__device__ __forceinline__ void xh_blocks(const PrefillArgs& A, const half_t* hmat, half_t (*tbuf)[32 * kXhRow]) {
+__device__ __forceinline__ void xh_blocks(const PrefillArgs& A, half_t (*tbuf)[32 * kXhRow]) {
     const int H = A.g.H, nkb = H / 128;
     const int l = lane_id(), wv = threadIdx.x >> 6;
+    half8_t hf[2][2];                                            // [ks & 1][negated]: rows n' = l % 32, k' = 8 (l / 32) + j
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const bool neg = __popc((l & 31) & (b * 16 + (l >> 5) * 8 + j)) & 1;
+            hf[b][0][j] = neg ? (half_t)-1.0f : (half_t)1.0f;
+            hf[b][1][j] = neg ? (half_t)1.0f : (half_t)-1.0f;
+        }
     const int pj = blockIdx.x & 1, blk = blockIdx.x >> 1;
     // this lane's pair row (B operand column); lanes past the last pair read the last pair, so that no load is
     // conditional and the 16 loads of a block are in flight together (those rows are never stored)
@@ -225,7 +237,7 @@ __device__ __forceinline__ void xh_blocks(const PrefillArgs& A, const half_t* hm
             float16_t acc = float16_t{};
 #pragma unroll
             for (int ks = 0; ks < 8; ++ks) {
-                const half8_t ha = *(const half8_t*)(hmat + (nb * 32 + (l & 31)) * 128 + ks * 16 + (l >> 5) * 8);
+                const half8_t ha = hf[ks & 1][__popc(nb & (ks >> 1)) & 1];
                 acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(ha, bx[ks], acc, 0, 0, 0);
             }
 #pragma unroll
@@ -247,24 +259,12 @@ __device__ __forceinline__ void xh_blocks(const PrefillArgs& A, const half_t* hm
     }
 }
 
-__global__ void __launch_bounds__(64 * kXhWaves) prefill_xh_kernel(PrefillArgs A) {
-    __shared__ __align__(16) half_t hmat[128 * 128];             // H128, row n contiguous in k
+__global__ void __launch_bounds__(64 * kXhWaves) __attribute__((amdgpu_waves_per_eu(4))) prefill_xh_kernel(PrefillArgs A) {
     __shared__ __align__(16) half_t tbuf[kXhWaves][32 * kXhRow]; // per wave: [pair][column] of one block
-    // H128[n][k] = (-1)^popc(n & k); 8 consecutive k = k0 + j (k0 a multiple of 8) share the sign of n & k0, so each
-    // thread builds 8 entries from one parity and stores them with one 16-byte write
-    for (int i8 = threadIdx.x; i8 < 128 * 128 / 8; i8 += 64 * kXhWaves) {
-        const int n = i8 >> 4, k0 = (i8 & 15) * 8;
-        const int base = __popc(n & k0) & 1;
-        half8_t v;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) v[j] = ((base ^ __popc(n & j)) & 1) ? (half_t)-1.0f : (half_t)1.0f;
-        *(half8_t*)(hmat + n * 128 + k0) = v;
-    }
-    __syncthreads();
     // the block loop per activation dtype (no dtype branch between a block's loads)
-    if (A.x_dt == 1) xh_blocks<1>(A, hmat, tbuf);
-    else if (A.x_dt == 2) xh_blocks<2>(A, hmat, tbuf);
-    else xh_blocks<0>(A, hmat, tbuf);
+    if (A.x_dt == 1) xh_blocks<1>(A, tbuf);
+    else if (A.x_dt == 2) xh_blocks<2>(A, tbuf);
+    else xh_blocks<0>(A, tbuf);
 }
 
 // ---- LDS layouts of one K chunk ----------------------------------------------------------------------------------------
