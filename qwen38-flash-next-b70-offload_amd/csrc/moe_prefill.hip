@@ -84,9 +84,16 @@ __global__ void __launch_bounds__(1024) align_count_kernel(const int32_t* ids, i
 __global__ void __launch_bounds__(1024) align_scan_kernel(int nchunks, int E, int pad, int* chunk_cnt, AlignOut o) {
     __shared__ int sw[17];
     const int e = threadIdx.x;
+    constexpr int kB = 16;                        // chunk counts loaded together (clamped indices: no branch per load)
     int tot = 0;
     if (e < E)
-        for (int c = 0; c < nchunks; ++c) tot += chunk_cnt[(size_t)c * E + e];
+        for (int c0 = 0; c0 < nchunks; c0 += kB) {
+            int v[kB];
+#pragma unroll
+            for (int j = 0; j < kB; ++j) v[j] = chunk_cnt[(size_t)min(c0 + j, nchunks - 1) * E + e];
+#pragma unroll
+            for (int j = 0; j < kB; ++j) tot += c0 + j < nchunks ? v[j] : 0;
+        }
     int all;
     const int st = block_scan_1024(e < E ? tot : 0, sw, all);
     const int act = (e < E && tot > 0) ? 1 : 0;
@@ -102,12 +109,18 @@ __global__ void __launch_bounds__(1024) align_scan_kernel(int nchunks, int E, in
         o.act_pstart[ai] = pst;
     }
     if (e == 0) o.n_act[0] = nact;
-    if (e < E) {
+    if (e < E) {                                  // the counts become each chunk's first position of expert e
         int run = st;
-        for (int c = 0; c < nchunks; ++c) {
-            const int v = chunk_cnt[(size_t)c * E + e];
-            chunk_cnt[(size_t)c * E + e] = run;
-            run += v;
+        for (int c0 = 0; c0 < nchunks; c0 += kB) {
+            int v[kB];
+#pragma unroll
+            for (int j = 0; j < kB; ++j) v[j] = chunk_cnt[(size_t)min(c0 + j, nchunks - 1) * E + e];
+#pragma unroll
+            for (int j = 0; j < kB; ++j)
+                if (c0 + j < nchunks) {
+                    chunk_cnt[(size_t)(c0 + j) * E + e] = run;
+                    run += v[j];
+                }
         }
     }
 }
