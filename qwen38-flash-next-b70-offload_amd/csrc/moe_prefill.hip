@@ -226,7 +226,11 @@ __device__ __forceinline__ void xh_blocks(const PrefillArgs& A, half_t (*tbuf)[3
             hf[b][0][j] = neg ? (half_t)-1.0f : (half_t)1.0f;
             hf[b][1][j] = neg ? (half_t)1.0f : (half_t)-1.0f;
         }
-    const int pj = blockIdx.x & 1, blk = blockIdx.x >> 1;
+    // the two projections of a block of 64 pairs run on one XCD (blockIdx b and b + 8), so that the second can read the
+    // gathered x rows from that XCD's L2; the grid is rounded up to 16 workgroups
+    const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3;
+    const int pj = slot & 1, blk = (slot >> 1) * 8 + xcd;
+    if (blk * 64 >= A.npairs) return;
     // this lane's pair row (B operand column); lanes past the last pair read the last pair, so that no load is
     // conditional and the 16 loads of a block are in flight together (those rows are never stored)
     const int s = min(blk * 64 + (wv & 1) * 32 + (l & 31), A.npairs - 1);
@@ -681,7 +685,8 @@ hipError_t launch_prefill(PrefillArgs a, int E, void* ws, hipStream_t s) {
     a.pair_exp = o.pair_exp;
     hipError_t e = launch_align(a.ids, a.w, np, a.topk, E, 1, chunk, o, s);
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(prefill_xh_kernel, dim3((unsigned)(2 * ((np + 63) / 64))), dim3(64 * kXhWaves), 0, s, a);
+    hipLaunchKernelGGL(prefill_xh_kernel, dim3((unsigned)((2 * ((np + 63) / 64) + 15) / 16 * 16)), dim3(64 * kXhWaves), 0,
+                       s, a);
     const unsigned A8 = (unsigned)((A + 7) / 8 * 8);   // workgroups of an expert share blockIdx % 8
     const dim3 ggu(A8 * (unsigned)(I / 128)), gdn(A8 * (unsigned)(H / 256));
     switch (a.g.K) {
