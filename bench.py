@@ -12,8 +12,11 @@ roofline: the fused dequant-GEMV layer kernel (moe_layer_kernel, one moe_forward
 R x 48 calls captured in one HIP graph and timed with HIP events around its replay on the launch stream: algorithmic
 bytes per call = distinct experts x blob bytes (every byte of each routed expert blob is read once) / average call
 duration, against the MI355X HBM3E peak of 8 TB/s.
-cpu_baseline: the PyTorch CPU restatement of the same layer math (oracle/cpu_path.py), one config-0 layer timed and
-scaled to 48 layers.
+Untimed steps before the timed ones: --settle (default 1,000: the cache and RAM tier start empty and need about 1,000
+steps of the trace to reach their steady state) and then --warmup; the line reports masked picks, fills, evictions and
+dropped admissions per timed step, and the device status word (non-zero marks the line invalid).
+cpu_baseline: the PyTorch CPU restatement of the same math (oracle/cpu_path.py) on this host's cores: a real 48-layer
+bs=1 pass (value), the one-layer config-0 case and a single-thread layer.
 """
 from __future__ import annotations
 
@@ -43,32 +46,60 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def cpu_baseline(samples: int = 10):
+def _median_s(fn, warm: int, reps: int) -> float:
+    import numpy as np
+    for _ in range(warm):
+        fn()
+    ts = []
+    for _ in range(reps):
+        t = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t)
+    return float(np.median(ts))
+
+
+def cpu_baseline():
+    """The PyTorch CPU restatement of the path (oracle/cpu_path.py; the reference has no CPU path) on this host:
+    a real 48-layer decode pass at bs=1 (config-2 shapes, each layer its own Zipf routing and experts), the one-layer
+    config-0 case, and one layer on a single thread."""
     import numpy as np
     import torch
     from oracle import cpu_path, exl3, synth
-    n = min(16, len(os.sched_getaffinity(0)))
+    n = len(os.sched_getaffinity(0))
     torch.set_num_threads(n)
-    ids, w = synth.softmax_topk(20261201, 1, E, TOPK)
-    blobs = {int(e): torch.from_numpy(synth.expert_blob(20261201, int(e), H, I, K)) for e in ids[0]}
-    x = torch.from_numpy(exl3.bf16_to_f32(synth.activations(20261201, 1, H)))
+    seed = 20261201
+    distinct = [torch.from_numpy(synth.expert_blob(seed, i, H, I, K)) for i in range(64)]
     cp = cpu_path.CpuExperts(H, I, K)
-    for _ in range(3):
-        cp.layer(x, ids, w, blobs)
-    ts = []
-    for _ in range(samples):
-        t = time.perf_counter()
-        cp.layer(x, ids, w, blobs)
-        ts.append(time.perf_counter() - t)
-    t_layer = float(np.median(ts))
+    x = torch.from_numpy(exl3.bf16_to_f32(synth.activations(seed, 1, H)))
+    ids_t, w_t = synth.zipf_trace(seed, 1, L, E, TOPK)               # [1, L, 1, topk]
+    layers = [(ids_t[0, li], w_t[0, li], {int(e): distinct[(li * E + int(e)) % 64] for e in ids_t[0, li, 0]})
+              for li in range(L)]
+
+    def stack():
+        h = x
+        for ids, w, blobs in layers:          # the layers in order, each on the previous layer's output
+            h = cp.layer(h, ids, w, blobs).float()
+        return h
+    t_stack = _median_s(stack, 1, 3)
+    ids0, w0 = synth.softmax_topk(seed, 1, E, TOPK)
+    blobs0 = {int(e): distinct[int(e) % 64] for e in ids0[0]}
+    t_layer = _median_s(lambda: cp.layer(x, ids0, w0, blobs0), 3, 10)
+    torch.set_num_threads(1)
+    t_layer1 = _median_s(lambda: cp.layer(x, ids0, w0, blobs0), 1, 3)
+    torch.set_num_threads(n)
     model = ""
     try:
         model = next(l.split(":", 1)[1].strip() for l in open("/proc/cpuinfo") if l.startswith("model name"))
     except Exception:
         pass
-    return {"value": 1.0 / (L * t_layer), "unit": "tok/s", "cores": n, "kind": "port",
-            "sample": f"one config-0 MoE layer (bs=1, 10 experts: dequant + SwiGLU + combine) timed {samples}x after 3 "
-                      f"warm-ups, median {t_layer * 1e3:.1f} ms x 48 layers; torch {n} threads on {model}"}
+    return {"value": 1.0 / t_stack, "unit": "tok/s", "cores": n, "kind": "port",
+            "sample": f"one bs=1 decode token through 48 MoE layers (H 2048, I 512, 512 experts, top-10, K 3; Zipf "
+                      f"routing per layer, 64 distinct synthetic blobs): LUT dequant + SwiGLU GEMVs + combine per layer, "
+                      f"median of 3 passes after 1 warm-up = {t_stack:.3f} s; torch on {n} threads, {model}",
+            "cpu_model": model,
+            "config0_layer_ms": round(t_layer * 1e3, 2),
+            "single_thread": {"layer_ms": round(t_layer1 * 1e3, 1), "tok_s_48_layers": 1.0 / (L * t_layer1),
+                              "sample": "one config-0 layer on 1 thread, median of 3 after 1 warm-up, x 48 layers"}}
 
 
 PREFILL_TOKENS = 8192
@@ -131,8 +162,10 @@ def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=500)
-    ap.add_argument("--warmup", type=int, default=1000, help="untimed steps: the cache and RAM tier start empty and "
-                    "reach their steady state after about 1,000 steps of the Zipf trace")
+    ap.add_argument("--warmup", type=int, default=20, help="untimed steps right before the timed ones")
+    ap.add_argument("--settle", type=int, default=1000, help="untimed steps before the warm-up, whatever --warmup is: "
+                    "the HBM cache and the RAM tier start empty and reach their steady state after about 1,000 steps "
+                    "of the Zipf trace")
     ap.add_argument("--bs", type=int, default=1)
     ap.add_argument("--roofline-steps", type=int, default=20)
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -149,10 +182,11 @@ def main():
               "path); run with --gpus 1", file=sys.stderr)
         sys.exit(2)
 
+    import ctypes
+
     import numpy as np
     import torch
-    from exl3xpu import nvtier, synth
-    from exl3xpu.moe_offload import s64
+    from exl3xpu import capi, nvtier, synth
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
@@ -166,10 +200,10 @@ def main():
     src = nvtier.SyntheticExpertSource(H, I, K, SEED, n_distinct=64)
     tier = nvtier.NvTierAsync(store, src, budget_records=args.budget_records, latency=8)
     log(f"setup {time.perf_counter() - t0:.1f} s: slots {SLOTS} x {store.blob} B, pinned arena {store.size / 2**30:.1f} GiB")
-    steps, warm, bs = args.steps, args.warmup, args.bs
+    steps, warm, bs, settle = args.steps, args.warmup, args.bs, max(0, args.settle)
     if args.roofline_only:
-        steps, warm = 0, 0
-    ids_np, w_np = synth.zipf_trace(SEED, max(warm + steps, args.roofline_steps), L, E, TOPK, M=bs)
+        steps, warm, settle = 0, 0, 0
+    ids_np, w_np = synth.zipf_trace(SEED, max(settle + warm + steps, args.roofline_steps), L, E, TOPK, M=bs)
     ids_all = torch.from_numpy(ids_np).to(dev)
     w_all = torch.from_numpy(w_np).to(dev)
     xs = torch.randn(L, bs, H, generator=torch.Generator().manual_seed(SEED)).to(torch.bfloat16).to(dev)
@@ -207,23 +241,29 @@ def main():
             b.copy_(a)
         torch.cuda.synchronize()
         del a, b
-    for n in range(min(warm, 2)):
+    pre = settle + warm                        # untimed steps: settle (tier steady state), then warm-up
+    for n in range(min(pre, 2)):               # the first calls run eagerly (library set-up), then the graph
         decode_step(n)
     torch.cuda.synchronize()
     if not args.eager and not args.roofline_only:
         graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(graph, capture_error_mode="thread_local"):
             layers()
-    for n in range(min(warm, 2), warm):
+    t_settle = time.perf_counter()
+    for n in range(min(pre, 2), pre):
         decode_step(n)
     torch.cuda.synchronize()
+    if pre:
+        log(f"settle + warm-up: {pre} untimed steps in {time.perf_counter() - t_settle:.2f} s")
     st0 = dict(tier.stats)
     host_s.update(launch=0.0, tier_step=0.0)
     t1 = time.perf_counter()
-    for n in range(warm, warm + steps):
+    for n in range(pre, pre + steps):
         decode_step(n)
     torch.cuda.synchronize()
     el = time.perf_counter() - t1
+    status = (ctypes.c_int32 * 4)()
+    capi.check(capi.lib().exl3_device_status(status, torch.cuda.current_stream().cuda_stream), "device status")
     tok_s = steps * bs / el if steps else 0.0
     d = {k: tier.stats.get(k, 0) - st0.get(k, 0) for k in ("masked", "evicts", "nvme_reads", "admit_dropped", "wait_ms")}
     host_ms = {k: round(v / max(steps, 1) * 1e3, 4) for k, v in host_s.items()}
@@ -298,7 +338,14 @@ def main():
         "resident_decode_tok_s": round(resident_tok_s, 1),
         "per_step": {"masked": d["masked"] / sd, "fills": d["nvme_reads"] / sd, "evicts": d["evicts"] / sd,
                      "admit_dropped": d["admit_dropped"] / sd},
+        "untimed_steps": {"settle": settle, "warmup": warm},
+        "device_status": int(status[0]),
     }
+    if status[0]:
+        out["valid"] = False
+        out["invalid_reason"] = (f"{status[0]} bounded waits of the decode kernels timed out: outputs were computed "
+                                 "from incomplete data")
+        log(f"INVALID: device status {status[0]}")
     if not args.no_cpu_baseline and not args.roofline_only:
         out["cpu_baseline"] = cpu_baseline()
         log(f"cpu baseline {out['cpu_baseline']['value']:.4f} tok/s on {out['cpu_baseline']['cores']} threads")

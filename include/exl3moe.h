@@ -44,7 +44,8 @@ int64_t exl3_blob_bytes(int H, int I, int K);
 /* ---- process-wide configuration (a8:682-789) ---------------------------------------------------------------------- */
 
 /* moe_set_tier (a8:768-774): ram_res uint8 [L*E] (1 = RAM-tier copy valid), miss ring int32 [1 + cap]
- * ([0] = monotonic count), safe int32 [L]. ram_res == NULL turns the tier (masking) off. */
+ * ([0] = count of masked picks modulo 2^32; entry c at position 1 + (c mod 2^32) % cap), safe int32 [L].
+ * ram_res == NULL turns the tier (masking) off. */
 int exl3_set_tier(uint8_t* ram_res, int32_t* miss_ring, int64_t ring_numel, const int32_t* safe);
 /* moe_set_victims (a8:757): device int32 [1 + 2E] victim list, NULL = no victim write-back */
 int exl3_set_victims(int32_t* vict);
@@ -77,8 +78,9 @@ int exl3_set_decision_log(int32_t* buf, int64_t cap_records);
  * pointer of every pick; the prefill path otherwise: sorted routing, input Hadamards [M topk][2][H] fp16, abuf
  * [M topk][I] fp16, y [M topk][H] fp16). The decode kernel's cross-workgroup exchange is not in the workspace: the
  * library owns one zeroed device buffer per device and grows it when a call needs more (hipMalloc + hipMemset, after
- * a device synchronisation); a call that would grow it while its stream is being captured fails with
- * EXL3_EUNSUPPORTED, so run one call of the largest size before capturing. */
+ * a device synchronisation; the replaced buffer stays allocated, since graphs captured earlier still address it); a
+ * call that would grow it while its stream is being captured fails with EXL3_EUNSUPPORTED, so run one call of the
+ * largest size before capturing. */
 size_t exl3_moe_forward_workspace(int M, int H, int I, int topk, int n_experts);
 
 /* moe_forward (a8:1221-1225 -> moe_forward_impl a8:1263-1314): out[m] = sum_k w[m,k] * expert(ids[m,k])(x[m]).
@@ -155,7 +157,7 @@ int exl3_scatter_flags(uint8_t* flags, int64_t n_flags, const int32_t* packed, i
 /* The device side of one host tier step as one launch (replaces the snapshot .to("cpu") copies and the flag
  * index_copy_ of plugin/exl3xpu/nvtier.py:282-386 and 791-793): applies the diff as exl3_scatter_flags; mirrors the
  * miss ring (int32 [1 + ring_cap], [0] = count) into ring_mirror (same layout, device-mapped pinned): the entries at
- * positions [ring_from, count) (the last ring_cap of them at most) and the count; then copies src[k] -> dst[k]
+ * counts [ring_from, count) modulo 2^32 (the last ring_cap of them at most) and the count; then copies src[k] -> dst[k]
  * (nbytes[k] bytes, k < n_copies <= 4; dst device-mapped pinned host memory, both 16-byte aligned). ring may be NULL.
  * A flag the diff sets may be snapshotted before or after its update. */
 int exl3_tier_exchange(uint8_t* flags, int64_t n_flags, const int32_t* packed, int64_t n_diff, const int32_t* ring,
@@ -163,9 +165,14 @@ int exl3_tier_exchange(uint8_t* flags, int64_t n_flags, const int32_t* packed, i
                        void* const* dst, const int64_t* nbytes, int n_copies, void* stream);
 
 /* Device health flags (no reference counterpart): flags4[0] = bounded waits of the fused decode kernel that timed
- * out since load (0 in a healthy run; a timeout means an output was computed from an incomplete intermediate).
- * Synchronises `stream`. */
+ * out since load (0 in a healthy run; a timeout means an output was computed from an incomplete intermediate, so
+ * callers must treat a non-zero value as fatal). Synchronises `stream`. */
 int exl3_device_status(int32_t* flags4, void* stream);
+
+/* Device address (current device) of those four status words, 16-byte aligned, so that a caller can copy them
+ * without a synchronisation of its own: the host tier step adds them to the snapshot copies of exl3_tier_exchange
+ * and raises when flags4[0] != 0 (no reference counterpart). */
+int exl3_device_status_address(void** dev_ptr);
 
 /* Bit-exact dequantization (ReconstructKernel, exl3_esimd.h:869-936): PLANAR4 trellis words
  * [k_tiles][n_tiles][8K] -> fp16 bits [16 k_tiles][16 n_tiles] (W_inner, Hadamard domain). */
@@ -205,6 +212,21 @@ int exl3_host_free(void* p);
 int exl3_usm_kind(const void* p);
 /* memcpy_async (a8:1546-1549): async copy of raw bytes on `stream` */
 int exl3_memcpy_async(void* dst, const void* src, int64_t nbytes, void* stream);
+
+/* A batch of memcpy_async calls on one stream (replaces the Python loops of memcpy_async over expert runs in
+ * ExpertStore.make_resident / stage_layer, plugin/exl3xpu/moe_offload.py:173, 315-323, and NvTier._stage_forward,
+ * plugin/exl3xpu/nvtier.py:598-607). Every copy i must lie inside [dst_lo, dst_hi) and [src_lo, src_hi); the whole
+ * batch is checked first and nothing is enqueued when one copy is out of bounds (EXL3_EINVAL). */
+int exl3_copy_batch(void* const* dst, const void* const* src, const int64_t* nbytes, int64_t n, int64_t dst_lo,
+                    int64_t dst_hi, int64_t src_lo, int64_t src_hi, void* stream);
+
+/* Device tables of static placement in one launch (replaces the index_copy_ / index_fill_ sequences of
+ * ExpertStore.make_resident and evict, plugin/exl3xpu/moe_offload.py:178-184, 204-211). rec: device int64 [n][3] =
+ * (key, slot, ptr) on distinct keys and slots. slot >= 0: key -> slot (slot_key[slot] = key, slot_last[slot] = 0);
+ * slot < 0: key leaves slot -1 - slot (its slot_key and slot_last become -1). ptrs_all[key] = ptr, slot_of[key] =
+ * the new slot or -1. */
+int exl3_table_update(int64_t* ptrs_all, int32_t* slot_of, int32_t* slot_key, int32_t* slot_last, const int64_t* rec,
+                      int64_t n, void* stream);
 
 #ifdef __cplusplus
 }

@@ -166,8 +166,9 @@ static int ensure_impl(co_t *c, int layer, int32_t *ids, float *w, int P, int ma
         for (int i = 0; i < P; ++i) {
             int key = layer * E + ids[i];
             if (c->slot_of[key] < 0 && !c->ram_res[key]) {
-                int32_t cnt = c->ring[0]++;
-                c->ring[1 + (int)((uint32_t)cnt % (uint32_t)c->R)] = key;
+                uint32_t cnt = (uint32_t)c->ring[0];          /* the count wraps modulo 2^32 */
+                c->ring[0] = (int32_t)(cnt + 1u);
+                c->ring[1 + (int)(cnt % (uint32_t)c->R)] = key;
                 ids[i] = c->safe[layer];
                 w[i] = 0.0f;
                 c->stats_masked++;
@@ -291,14 +292,16 @@ int64_t co_host_step(co_t *c, int32_t *admit_out, int32_t *n_admit, int32_t *evi
     }
     c->n_done[slot_now] = 0;
     /* new misses with multiplicity (nvtier.py:765-775) */
-    int64_t cnt = (int64_t)ring[0], newm = cnt - c->ring_seen, cap = c->R;
+    /* the device count wraps modulo 2^32 (the reference's Python int does not; it never reaches 2^31 in its runs) */
+    uint32_t cnt = (uint32_t)ring[0];
+    int64_t newm = (int64_t)(uint32_t)(cnt - (uint32_t)c->ring_seen), cap = c->R;
     if (newm > cap) { c->stats_ring_overflow += newm - cap; newm = cap; }
     int64_t nwant = 0;
     int64_t *want = c->l_tmp;
     if (newm > 0) {
         int64_t *keys = c->l_tmp2;
         for (int64_t i = 0; i < newm; ++i) {
-            int64_t pos = ((cnt - newm + i) % cap + cap) % cap;
+            int64_t pos = (int64_t)((uint32_t)(cnt - (uint32_t)(newm - i)) % (uint32_t)cap);
             keys[i] = ring[1 + pos];
         }
         qsort(keys, (size_t)newm, 8, cmp_i64);
@@ -312,8 +315,7 @@ int64_t co_host_step(co_t *c, int32_t *admit_out, int32_t *n_admit, int32_t *evi
         g_cnt_for_sort = c->cnt_tmp;
         qsort(want, (size_t)nwant, 8, cmp_cnt_desc);
     }
-    c->ring_seen = cnt;
-    if (newm > 0) c->stats_masked += 0;
+    c->ring_seen = (int64_t)cnt;
     /* budget (nvtier.py:777-788) */
     int64_t inflight_n = 0, nres = 0;
     for (int i = 0; i < n; ++i) { inflight_n += c->inflight[i]; nres += res[i]; }

@@ -113,7 +113,8 @@ __device__ void ensure_wg(const EnsureArgs& A, EnsureShared& Z, int* done) {
 
     int pslot = -1;                              // wave 0: post-mask slot of pick `lane`
     if (wv == 0) {                               // tier mask, ascending pick order
-        int cnt = A.ram_res ? A.ring[0] : 0;
+        // the ring count is taken modulo 2^32 (it wraps after 2^32 masked picks; the host reads it the same way)
+        uint32_t cnt = A.ram_res ? (uint32_t)A.ring[0] : 0u;
         const int safe = A.ram_res ? A.safe[A.layer] : 0;
         const int safe_slot = A.ram_res ? A.slot_of[kb + safe] : -1;
         int T = 0;
@@ -128,8 +129,8 @@ __device__ void ensure_wg(const EnsureArgs& A, EnsureShared& Z, int* done) {
         const bool msk = A.ram_res && lane < P && so < 0 && !A.ram_res[kb + id];
         const uint64_t bal = __ballot(msk);
         if (msk) {
-            const int pos = cnt + __popcll(bal & ((1ull << lane) - 1ull));
-            A.ring[1 + (int)((uint32_t)pos % (uint32_t)A.ring_cap)] = kb + id;
+            const uint32_t pos = cnt + (uint32_t)__popcll(bal & ((1ull << lane) - 1ull));
+            A.ring[1 + (int)(pos % (uint32_t)A.ring_cap)] = kb + id;
             id = safe;
             so = safe_slot;
         }
@@ -144,9 +145,9 @@ __device__ void ensure_wg(const EnsureArgs& A, EnsureShared& Z, int* done) {
                 }
             st_agent_i32(A.pair_own + lane, own);
         }
-        cnt += __popcll(bal);
-        if (A.ram_res && lane == 0) A.ring[0] = cnt;
-        if (lane == 0) Z.sh[5] = cnt;
+        cnt += (uint32_t)__popcll(bal);
+        if (A.ram_res && lane == 0) A.ring[0] = (int32_t)cnt;
+        if (lane == 0) Z.sh[5] = (int)cnt;
         // no-miss call: the hit stamps are the only decisions (atomic max = "T unless pinned": every unpinned stamp
         // is an earlier tick, 0 or -1)
         const bool fast = __ballot(lane < P && pslot < 0) == 0ull;

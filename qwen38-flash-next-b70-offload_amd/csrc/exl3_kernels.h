@@ -94,6 +94,7 @@ struct PrefillArgs {
 // decode.hip
 hipError_t launch_moe_layer(int K, const DecodeArgs& a, hipStream_t s);
 int read_status(int* out, hipStream_t s);
+hipError_t status_address(void** p);
 hipError_t launch_dequant(int K, const uint32_t* tr, _Float16* out, int k_tiles, int n_tiles, hipStream_t s);
 // cache.hip
 hipError_t launch_ensure(const EnsureArgs& a, hipStream_t s);
@@ -101,6 +102,8 @@ hipError_t launch_ensure(const EnsureArgs& a, hipStream_t s);
 // (host_base[layer] + e * hstride) into its slot (slot_base + s * sstride, `copy_bytes` bytes) and repoint ptrs_all
 hipError_t launch_prefetch(const EnsureArgs& a, int64_t sstride, int64_t copy_bytes, hipStream_t s);
 hipError_t launch_scatter_flags(uint8_t* flags, int64_t n_flags, const int32_t* packed, int64_t n, hipStream_t s);
+hipError_t launch_table_update(int64_t* ptrs_all, int32_t* slot_of, int32_t* slot_key, int32_t* slot_last,
+                               const int64_t* rec, int64_t n, hipStream_t s);
 struct TierCopy { const uint8_t* src; uint8_t* dst; int64_t n; };   // n bytes, device -> pinned host
 struct TierCopies { TierCopy c[4]; int n; };
 struct TierRing { const int32_t* ring; int64_t cap, from; int32_t* mirror; };  // ring null: no mirroring

@@ -141,7 +141,7 @@ __global__ void __launch_bounds__(kEnsureThreads) ensure_kernel(EnsureArgs A) {
     int pslot = -1;
     if (wv == 0) {                                            // tier mask, ascending pick order
         const int kb = A.layer * E;
-        int cnt = A.ram_res ? A.ring[0] : 0;
+        uint32_t cnt = A.ram_res ? (uint32_t)A.ring[0] : 0u;      // modulo 2^32, as the host reads it
         const int safe = A.ram_res ? A.safe[A.layer] : 0;
         const int safe_slot = A.ram_res ? A.slot_of[kb + safe] : -1;
         const int64_t safe_ptr = A.ram_res && small ? A.ptrs_all[kb + safe] : 0;
@@ -161,8 +161,8 @@ __global__ void __launch_bounds__(kEnsureThreads) ensure_kernel(EnsureArgs A) {
             const bool msk = A.ram_res && i < P && so < 0 && !A.ram_res[kb + id];
             const uint64_t bal = __ballot(msk);
             if (msk) {
-                const int pos = cnt + __popcll(bal & ((1ull << lane) - 1ull));
-                A.ring[1 + (int)((uint32_t)pos % (uint32_t)A.ring_cap)] = kb + id;
+                const uint32_t pos = cnt + (uint32_t)__popcll(bal & ((1ull << lane) - 1ull));
+                A.ring[1 + (int)(pos % (uint32_t)A.ring_cap)] = kb + id;
                 id = safe;
                 so = safe_slot;
                 pptr = safe_ptr;
@@ -171,10 +171,10 @@ __global__ void __launch_bounds__(kEnsureThreads) ensure_kernel(EnsureArgs A) {
             }
             if (i < P) pid[i] = id;
             pslot = so;
-            cnt += __popcll(bal);
+            cnt += (uint32_t)__popcll(bal);
         }
-        if (A.ram_res && lane == 0) A.ring[0] = cnt;
-        if (lane == 0) sh[5] = cnt;
+        if (A.ram_res && lane == 0) A.ring[0] = (int32_t)cnt;
+        if (lane == 0) sh[5] = (int)cnt;
         // blob pointer of every post-mask pick (read by the GEMV workgroups). Assignments below never touch it: a
         // victim slot's owner is not a pick of this call (hits are stamped T, so their slots are not eligible), and
         // a miss keeps its host copy's pointer until the fill is committed at the end of the call.
@@ -489,6 +489,35 @@ hipError_t launch_scatter_flags(uint8_t* flags, int64_t n_flags, const int32_t* 
     return hipGetLastError();
 }
 
+// Residency records of static placement (make_resident / evict): record i = (key, slot, ptr) as three int64.
+// slot >= 0: the key now lives in that slot (slot_key[slot] = key, slot_last[slot] = 0: never used by a cached call
+// yet); slot < 0: the key left slot -1 - slot (slot_key and slot_last of that slot to -1). Either way
+// ptrs_all[key] = ptr and slot_of[key] = the new slot or -1. Records touch distinct keys and distinct slots.
+__global__ void table_update_kernel(int64_t* ptrs_all, int32_t* slot_of, int32_t* slot_key, int32_t* slot_last,
+                                    const int64_t* rec, int64_t n) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const int64_t key = rec[3 * i], slot = rec[3 * i + 1], ptr = rec[3 * i + 2];
+    ptrs_all[key] = ptr;
+    if (slot >= 0) {
+        slot_of[key] = (int32_t)slot;
+        slot_key[slot] = (int32_t)key;
+        slot_last[slot] = 0;
+    } else {
+        slot_of[key] = -1;
+        slot_key[-1 - slot] = -1;
+        slot_last[-1 - slot] = -1;
+    }
+}
+
+hipError_t launch_table_update(int64_t* ptrs_all, int32_t* slot_of, int32_t* slot_key, int32_t* slot_last,
+                               const int64_t* rec, int64_t n, hipStream_t s) {
+    if (n <= 0) return hipSuccess;
+    hipLaunchKernelGGL(table_update_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, ptrs_all, slot_of,
+                       slot_key, slot_last, rec, n);
+    return hipGetLastError();
+}
+
 // The whole device side of one host tier step in one launch: the flag diff of the step (as scatter_flags_kernel), the
 // miss-ring entries appended since position `from` (the count the host last read) into a pinned mirror of the ring,
 // with the count itself, and the snapshot copies of the device state into device-mapped pinned host buffers (16-byte
@@ -512,10 +541,11 @@ __global__ void __launch_bounds__(256) tier_exchange_kernel(uint8_t* flags, int6
         const int64_t key = p >> 1;
         if (p >= 0 && key < n_flags) flags[key] = (uint8_t)(p & 1);
     }
-    if (rg.ring) {
-        const int64_t cnt = rg.ring[0];
-        for (int64_t p = max(rg.from, cnt - rg.cap) + t; p < cnt; p += nt) {
-            const int64_t q = 1 + p % rg.cap;
+    if (rg.ring) {                               // the count and `from` are taken modulo 2^32
+        const uint32_t cnt = (uint32_t)rg.ring[0];
+        const int64_t n = min((int64_t)(uint32_t)(cnt - (uint32_t)rg.from), rg.cap);
+        for (int64_t i = t; i < n; i += nt) {
+            const int64_t q = 1 + (int64_t)((uint32_t)(cnt - (uint32_t)(n - i)) % (uint32_t)rg.cap);
             rg.mirror[q] = rg.ring[q];
         }
         if (t == 0) rg.mirror[0] = (int32_t)cnt;

@@ -210,10 +210,13 @@ static int64_t* pair_ptr_area(void* ws, int npairs, int H, int I) {
 
 // The decode kernel's cross-workgroup exchange buffer: library-owned, one per device, zeroed when (re)allocated so that
 // no word carries a live tag before the kernel writes it. It grows to the largest call seen; growing synchronizes the
-// device and cannot happen while the stream is being captured into a graph.
+// device and cannot happen while the stream is being captured into a graph. A replaced buffer is never freed: a graph
+// captured before the growth keeps its address in its kernel arguments and replays into it (the sizes double, so the
+// retired buffers together are at most the size of the current one).
 struct Exchange {
     uint64_t* p = nullptr;
     size_t words = 0;
+    std::vector<uint64_t*> retired;
 };
 static constexpr int kMaxDevices = 64;
 static std::mutex g_exch_mu;
@@ -244,7 +247,7 @@ static int exchange_buffer(size_t words, hipStream_t st, uint64_t** out) {
         (void)hipFree(p);
         return hip_fail(e, "exchange buffer: zero fill");
     }
-    if (x.p) (void)hipFree(x.p);
+    if (x.p) x.retired.push_back(x.p);
     x.p = p;
     x.words = n;
     *out = p;
@@ -620,7 +623,8 @@ int exl3_tier_exchange(uint8_t* flags, int64_t n_flags, const int32_t* packed, i
     if (n_diff < 0 || n_flags < 0 || n_diff > (int64_t)1 << 31 || n_copies < 0 || n_copies > 4)
         return fail(EXL3_EINVAL, "tier_exchange: n_diff=%lld n_copies=%d", (long long)n_diff, n_copies);
     if (n_diff && (!flags || !packed)) return fail(EXL3_EINVAL, "tier_exchange: null flags / diff");
-    if (ring && (!ring_mirror || ring_cap <= 0 || ring_from < 0))
+    // ring_from is a ring count (modulo 2^32, as the device keeps it): 0 <= ring_from < 2^32
+    if (ring && (!ring_mirror || ring_cap <= 0 || ring_cap > INT32_MAX || ring_from < 0 || ring_from > (int64_t)UINT32_MAX))
         return fail(EXL3_EINVAL, "tier_exchange: ring cap=%lld from=%lld", (long long)ring_cap, (long long)ring_from);
     const TierRing rg{ring, ring_cap, ring_from, ring_mirror};
     TierCopies cp{};
@@ -641,6 +645,12 @@ int exl3_device_status(int32_t* flags4, void* stream) {
     if (e != hipSuccess) return hip_fail(e, "device_status");
     e = hipStreamSynchronize((hipStream_t)stream);
     return e == hipSuccess ? EXL3_OK : hip_fail(e, "device_status sync");
+}
+
+int exl3_device_status_address(void** dev_ptr) {
+    if (!dev_ptr) return fail(EXL3_EINVAL, "device_status_address: null output");
+    const hipError_t e = status_address(dev_ptr);
+    return e == hipSuccess ? EXL3_OK : hip_fail(e, "device_status_address");
 }
 
 int exl3_dequant(const uint32_t* trellis, int k_tiles, int n_tiles, int K, uint16_t* out, void* stream) {
@@ -684,6 +694,31 @@ int exl3_usm_kind(const void* p) {
         case hipMemoryTypeManaged: return 3;
         default: return 0;
     }
+}
+
+int exl3_copy_batch(void* const* dst, const void* const* src, const int64_t* nbytes, int64_t n, int64_t dst_lo,
+                    int64_t dst_hi, int64_t src_lo, int64_t src_hi, void* stream) {
+    if (n < 0 || (n > 0 && (!dst || !src || !nbytes))) return fail(EXL3_EINVAL, "copy_batch: n=%lld", (long long)n);
+    // every range is checked against the caller's bounds before anything is enqueued: a batch is all or nothing
+    for (int64_t i = 0; i < n; ++i) {
+        const int64_t d = (int64_t)(uintptr_t)dst[i], s = (int64_t)(uintptr_t)src[i], b = nbytes[i];
+        if (b < 0 || (b > 0 && (d < dst_lo || d > dst_hi - b || s < src_lo || s > src_hi - b)))
+            return fail(EXL3_EINVAL, "copy_batch: copy %lld (%lld bytes) outside its bounds", (long long)i, (long long)b);
+    }
+    for (int64_t i = 0; i < n; ++i) {
+        if (!nbytes[i]) continue;
+        const hipError_t e = hipMemcpyAsync(dst[i], src[i], (size_t)nbytes[i], hipMemcpyDefault, (hipStream_t)stream);
+        if (e != hipSuccess) return hip_fail(e, "copy_batch: hipMemcpyAsync");
+    }
+    return EXL3_OK;
+}
+
+int exl3_table_update(int64_t* ptrs_all, int32_t* slot_of, int32_t* slot_key, int32_t* slot_last, const int64_t* rec,
+                      int64_t n, void* stream) {
+    if (n < 0 || (n > 0 && (!ptrs_all || !slot_of || !slot_key || !slot_last || !rec)))
+        return fail(EXL3_EINVAL, "table_update: n=%lld", (long long)n);
+    const hipError_t e = launch_table_update(ptrs_all, slot_of, slot_key, slot_last, rec, n, (hipStream_t)stream);
+    return e == hipSuccess ? EXL3_OK : hip_fail(e, "table_update");
 }
 
 int exl3_memcpy_async(void* dst, const void* src, int64_t nbytes, void* stream) {

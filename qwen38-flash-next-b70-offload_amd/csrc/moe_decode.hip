@@ -36,7 +36,9 @@ namespace exl3 {
 __device__ unsigned g_epoch;                 // call epoch (advanced by the last workgroup of each call; never ~0u)
 
 __device__ int g_cnt_all[4];          // [1] victim reads done, [2] fused ensure done
-__device__ int g_status[4];          // [0]: spin timeouts (should stay 0)
+// [0]: bounded waits that timed out since load (0 in a healthy run). 16-byte aligned: the host tier step copies the
+// four words into its pinned snapshot with 16-byte accesses.
+__device__ __align__(16) int g_status[4];
 
 constexpr int kSpinMax = 1 << 22;
 constexpr uint64_t kDownLoadDelay = 120;         // 1.2 us in s_memrealtime ticks
@@ -305,16 +307,17 @@ struct LayerShared {
     int last;
 };
 
-// bounded wait until *c >= target (one lane); a timeout is counted in g_status[0]
-__device__ __forceinline__ void wait_count(const int* c, int target) {
+// bounded wait until *c >= target (one lane); a timeout is counted in g_status[0] and returns false
+__device__ __forceinline__ bool wait_count(const int* c, int target) {
     int it = 0;
     while (__hip_atomic_load(c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target) {
         __builtin_amdgcn_s_sleep(1);
         if (++it > kSpinMax) {
             atomicAdd(&g_status[0], 1);
-            break;
+            return false;
         }
     }
+    return true;
 }
 
 // victim write-back (VictimCopyKernel, a8:1168-1189): workgroup (victim i, 64 KiB chunk c) copies its chunk of the
@@ -770,10 +773,9 @@ __device__ __forceinline__ void down_wg(const DecodeArgs& A, int blk, LayerShare
     // the last (row, block) of the layer: every other workgroup has consumed its inputs; advance the epoch and commit
     // the cache fills
     if (l == 0) {
-        if (A.n_vict_wg) {                       // every victim workgroup has counted itself: clear for the next call
-            wait_count(&g_cnt_all[1], A.n_vict_wg);
-            counter_reset(&g_cnt_all[1]);
-        }
+        // every victim workgroup has counted itself: clear for the next call. After a timed-out wait the count stays
+        // (the status word is non-zero and the host tier step raises), so no later call proceeds on a partial count.
+        if (A.n_vict_wg && wait_count(&g_cnt_all[1], A.n_vict_wg)) counter_reset(&g_cnt_all[1]);
         const unsigned ep = tag == ~0u ? 0u : tag;   // the next call's tag is never 0 (the zeroed buffer)
         __hip_atomic_store(&g_epoch, ep, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
@@ -863,6 +865,9 @@ hipError_t launch_moe_layer(int K, const DecodeArgs& a, hipStream_t s) {
 int read_status(int* out, hipStream_t s) {
     return (int)hipMemcpyFromSymbolAsync(out, HIP_SYMBOL(g_status), sizeof(int) * 4, 0, hipMemcpyDeviceToHost, s);
 }
+
+// device address of the status words on the current device (each device holds its own copy)
+hipError_t status_address(void** p) { return hipGetSymbolAddress(p, HIP_SYMBOL(g_status)); }
 
 hipError_t launch_dequant(int K, const uint32_t* tr, _Float16* out, int k_tiles, int n_tiles, hipStream_t s) {
     int ntw = K == 3 ? Geo<3>::NTW : (K == 2 ? Geo<2>::NTW : Geo<4>::NTW);

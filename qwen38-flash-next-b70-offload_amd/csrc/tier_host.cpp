@@ -53,12 +53,16 @@ extern "C" int exl3_admit_decide(exl3_admit_state* st, uint8_t* res, int64_t* ag
     if (n <= 0 || cap <= 0 || n_done < 0) return EXL3_EINVAL;
     for (int64_t i = 0; i < n_done; ++i)
         if (done[i] < 0 || done[i] >= n) return EXL3_EINVAL;
-    const int64_t cnt = ring[0];
-    int64_t newm = cnt - st->ring_seen;
+    if (cap > INT32_MAX) return EXL3_EINVAL;
+    // the device ring count wraps modulo 2^32: the entries since the last step are (cnt - ring_seen) mod 2^32, and entry
+    // c sits at position (c mod 2^32) % cap, the same formula the device uses when it writes
+    const uint32_t cnt = (uint32_t)ring[0];
+    int64_t newm = (int64_t)(uint32_t)(cnt - (uint32_t)st->ring_seen);
     const int64_t overflow = newm > cap ? newm - cap : 0;
     newm -= overflow;
+    auto pos_of = [cnt, newm, cap](int64_t i) { return (int64_t)((uint32_t)(cnt - (uint32_t)(newm - i)) % (uint32_t)cap); };
     for (int64_t i = 0; i < newm; ++i) {         // validate before touching the books
-        const int32_t key = ring[1 + (cnt - newm + i) % cap];
+        const int32_t key = ring[1 + pos_of(i)];
         if (key < 0 || key >= n) return EXL3_EINVAL;
     }
     Scratch& S = tls;
@@ -81,8 +85,7 @@ extern "C" int exl3_admit_decide(exl3_admit_state* st, uint8_t* res, int64_t* ag
     S.want.clear();
     if (newm > 0) {
         for (int64_t i = 0; i < newm; ++i) {
-            const int64_t pos = (cnt - newm + i) % cap;
-            const int64_t key = ring[1 + pos];
+            const int64_t key = ring[1 + pos_of(i)];
             if (S.count[key]++ == 0) S.touched.push_back(key);
         }
         for (int64_t key : S.touched)
@@ -93,7 +96,7 @@ extern "C" int exl3_admit_decide(exl3_admit_state* st, uint8_t* res, int64_t* ag
         for (int64_t t : S.touched) S.count[t] = 0;
         st->masked += newm;
     }
-    st->ring_seen = cnt;
+    st->ring_seen = (int64_t)cnt;                // in [0, 2^32)
     // 4
     int64_t n_res = 0, n_inf = 0;
     for (int64_t i = 0; i < n; ++i) {

@@ -48,6 +48,7 @@ SIGNATURES = {
     "exl3_moe_align": (c_i32, [c_p, c_p, c_i32, c_i32, c_i32, c_i32, c_p, c_p, c_p, c_sz, c_p]),
     "exl3_dequant": (c_i32, [c_p, c_i32, c_i32, c_i32, c_p, c_p]),
     "exl3_device_status": (c_i32, [c_p, c_p]),
+    "exl3_device_status_address": (c_i32, [c_p]),
     "exl3_scatter_flags": (c_i32, [c_p, c_i64, c_p, c_i64, c_p]),
     "exl3_tier_exchange": (c_i32, [c_p, c_i64, c_p, c_i64, c_p, c_i64, c_i64, c_p, c_p, c_p, c_p, c_i32, c_p]),
     "exl3_admit_decide": (c_i32, [c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_i64, c_p, c_p, c_p, c_p, c_p, c_p, c_p]),
@@ -55,6 +56,8 @@ SIGNATURES = {
     "exl3_host_free": (c_i32, [c_p]),
     "exl3_usm_kind": (c_i32, [c_p]),
     "exl3_memcpy_async": (c_i32, [c_p, c_p, c_i64, c_p]),
+    "exl3_copy_batch": (c_i32, [c_p, c_p, c_p, c_i64, c_i64, c_i64, c_i64, c_i64, c_p]),
+    "exl3_table_update": (c_i32, [c_p, c_p, c_p, c_p, c_p, c_i64, c_p]),
 }
 
 

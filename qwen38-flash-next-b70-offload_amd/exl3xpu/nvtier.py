@@ -1,87 +1,102 @@
-"""RAM expert tier for the MI355X device-managed expert cache (reference plugin/exl3xpu/nvtier.py).
+"""RAM expert tier below the device-managed HBM expert cache (the reference's plugin/exl3xpu/nvtier.py API).
 
-Tiers: HBM slots (device LRU, write-through on miss) -> RAM tier (one pinned, device-mapped host arena with a fixed
-address per expert, read zero-copy by the kernels) -> expert store (all experts; a pluggable fill source with a
-deterministic completion latency in host steps, standing in for the reference's O_DIRECT NVMe reads).
+Three tiers: HBM slots (device LRU, write-through on a miss) -> RAM records (one pinned, device-mapped host arena with
+a fixed address per expert, read zero-copy by the kernels) -> the expert store (every expert; a fill source: the
+packed on-disk expert file, or a seeded synthetic source with a deterministic completion latency in host steps).
 
-Device side (csrc/moe_cache.hip): picks whose expert is in neither HBM nor RAM are masked to (safe expert, weight 0) and
-logged to a miss ring; HBM victims whose RAM copy is not valid are written back to their RAM address and flagged.
-Host side (call step() after every decode step): consume the previous step's device snapshot, complete fills, admit the
-most-missed keys into free budget, evict RAM copies of HBM-resident experts first and then keys older than AGE steps,
-and upload the changed flags. The RAM arena is never unmapped, so an evicted key's bytes stay readable: the reference's
-punch/write-back race (its docs/results.md:164-172) cannot corrupt data here; "punch" is bookkeeping only.
+Device side (csrc/moe_cache.hip, csrc/exl3_ensure.cuh): a pick whose expert is in neither HBM nor RAM is masked to
+(the layer's safe expert, weight 0) and logged in a miss ring; an HBM victim whose RAM copy is not valid is written
+back to its record and flagged. Host side, after every decode step (NvTierAsync.step): consume the previous step's
+device snapshot, complete fills, admit the most-missed keys into free budget, evict RAM copies of HBM-resident
+experts first and then keys older than AGE steps, and upload the changed flags. The arena is never unmapped, so an
+evicted record's bytes stay readable until a fill overwrites them; eviction is bookkeeping only.
 """
 from __future__ import annotations
 
 import ctypes
+import json
 import logging
 import os
+import threading
 import time
 from concurrent.futures import ThreadPoolExecutor
 
 import numpy as np
 import torch
 
-from .moe_offload import ExpertStore, s64
+from .moe_offload import ExpertStore, _HostRecords, _Stager, s64
 
-MiB2 = 2 << 20
 log = logging.getLogger("exl3xpu")
+_REC_ALIGN = 4096
+
+
+def record_bytes(blob: int) -> int:
+    """Size of one expert record on disk and in the RAM arena: the blob rounded up to 4 KiB (direct I/O alignment)."""
+    return -(-int(blob) // _REC_ALIGN) * _REC_ALIGN
+
+
+def _env_int(name: str, default: int) -> int:
+    return int(os.environ.get(name, str(default)))
 
 
 class TierStore(ExpertStore):
-    """ExpertStore whose host copies live at fixed-stride addresses of one pinned arena (the reference uses a sparse
-    2 MiB-stride memfd, nvtier.py:22-53). stride defaults to the blob size rounded up to 4 KiB."""
+    """ExpertStore whose host records sit at fixed-stride addresses of one pinned arena: key li * E + e at
+    base + key * stride (the reference maps a sparse 2 MiB-stride memfd, nvtier.py:22-53). The stride defaults to the
+    blob rounded up to 4 KiB, the record size of the expert file. Ks: the bitrate of each layer in add_layer order
+    when layers differ; slots and records then take the largest blob."""
 
-    def __init__(self, H, I, K, E, n_slots, n_layers, stride=None, device=None, Ks=None):
-        """Ks: bitrate per layer (in add_layer order) when layers differ; slots and records take the largest blob."""
+    _own_host_arrays = False
+
+    def __init__(self, H, I, K, E, n_slots, n_layers, stride=None, device=None, Ks=None):  # noqa: E741
         self.Ks = [int(k) for k in Ks] if Ks is not None else None
         if self.Ks is not None and len(self.Ks) != n_layers:
             raise ValueError(f"TierStore: {len(self.Ks)} bitrates for {n_layers} layers")
         super().__init__(H, I, max(self.Ks) if self.Ks else K, E, n_slots, device=device, max_layers=n_layers)
         if self.Ks and len(set(self.Ks)) > 1:
             self.mixed_bitrates()
-        self.stride = int(stride) if stride else (self.blob + 4095) // 4096 * 4096
-        assert self.blob <= self.stride and self.stride % 16 == 0
+        self.stride = int(stride) if stride else record_bytes(self.blob)
+        if self.stride < self.blob or self.stride % 16:
+            raise ValueError(f"TierStore: stride {self.stride} must hold a blob ({self.blob} B), 16-byte multiple")
         self.L = n_layers
         self.size = n_layers * E * self.stride
         self.arena = self.X.host_alloc(self.size)
-        self.base = s64(self.arena.data_ptr())
-        self.X.moe_set_host_stride(self.stride)
+        self.base = self.arena.data_ptr()
+
+    def _host_stride(self) -> int:
+        return self.stride
+
+    def _new_records(self, li: int, blobs) -> _HostRecords:
+        span = self.E * self.stride
+        view = self.arena[li * span:(li + 1) * span].view(self.E, self.stride)[:, :self.blob]
+        if blobs is not None:
+            view.copy_(blobs)
+        return _HostRecords(self.base + li * span, self.stride, self.base, self.base + self.size, view)
 
     def add_layer(self, key, blobs=None):
-        li = len(self.layer_index)
-        if li >= self.L:
+        if len(self.layer_index) >= self.L:
             raise RuntimeError(f"TierStore: more than n_layers={self.L} MoE layers")
-        self.layer_index[key] = li
+        li = len(self.layer_index)
+        super().add_layer(key, blobs)
         if self.Ks:
             self.K_of[key] = self.Ks[li]
-        base = self.base + li * self.E * self.stride
-        self._host_ptr[key] = base + torch.arange(self.E, dtype=torch.int64) * self.stride
-        self.ptrs_all[li * self.E:(li + 1) * self.E].copy_(self._host_ptr[key])
-        self.host_base[li] = base
-        self.slot_of[key] = torch.full((self.E,), -1, dtype=torch.int32)
-        if blobs is not None:
-            for e in range(self.E):
-                self.arena[(li * self.E + e) * self.stride:(li * self.E + e) * self.stride + self.blob].copy_(blobs[e])
         return None
 
-    def addr(self, key: int) -> int:                       # key = li * E + e
-        return self.base + key * self.stride
+    def addr(self, key: int) -> int:
+        """Host record address of key = layer row * E + e."""
+        return self.base + int(key) * self.stride
 
-    def host_view(self, key):
-        li = self.layer_index[key]
-        return self.arena[li * self.E * self.stride:(li + 1) * self.E * self.stride].view(self.E, self.stride)[:, :self.blob]
 
+# ---- fill sources ---------------------------------------------------------------------------------------------------------
 
 class SyntheticExpertSource:
-    """Deterministic stand-in for the packed NVMe store (serve/pack_store.py): record r holds the blob of synthetic
-    expert r % n_distinct of workload `seed`; `read(r, dst)` copies it to a host address."""
+    """Seeded stand-in for the expert file: record r holds the blob of synthetic expert r % n_distinct of workload
+    `seed`; read(r, dst) copies it to a host address."""
 
-    def __init__(self, H, I, K, seed: int, n_distinct: int = 64):
+    def __init__(self, H, I, K, seed: int, n_distinct: int = 64):  # noqa: E741
         from .synth import expert_blob
-        self.blob = int(expert_blob(seed, 0, H, I, K).numel())
-        self.n = n_distinct
-        self.buf = np.stack([expert_blob(seed, i, H, I, K).numpy() for i in range(n_distinct)])
+        self.n = int(n_distinct)
+        self.buf = np.stack([expert_blob(seed, i, H, I, K).numpy() for i in range(self.n)])
+        self.blob = int(self.buf.shape[1])
         self.rec = self.blob
 
     def read(self, rec_index: int, dst: int) -> None:
@@ -93,8 +108,7 @@ class SyntheticExpertSource:
 
 
 class LayeredExpertSource:
-    """Fill source for a store whose layers differ in bitrate: record r = layer * E + e is read from sources[layer]
-    (a source of that layer's geometry)."""
+    """Fill source for a store whose layers differ in bitrate: record r = layer * E + e comes from sources[layer]."""
 
     def __init__(self, sources, E: int):
         self.sources, self.E = list(sources), int(E)
@@ -107,68 +121,193 @@ class LayeredExpertSource:
         return self.sources[rec_index // self.E].blob_of(rec_index)
 
 
+class ExpertFile:
+    """The packed expert store on disk (reference serve/pack_store.py:1-90, read by nvtier.py:96-112, 460-486):
+    record r = checkpoint layer * E + e, each `rec` = blob rounded up to 4 KiB bytes at offset r * rec, so every
+    record can be read with direct I/O into a 4 KiB-aligned buffer. meta (JSON beside the file, or a dict):
+    {"blob", "rec", "layers", "experts", "H", "I", "K"}.
+
+    read(r, dst) reads record r into host memory at dst. With O_DIRECT (default where the file system supports it)
+    the read goes straight into dst when dst is 4 KiB aligned and the kernel can pin it, else through an aligned
+    bounce buffer of this thread; buffered reads otherwise. Only the blob's bytes are written at dst."""
+
+    def __init__(self, path: str, meta=None, direct: bool | None = None):
+        if meta is None:
+            meta = os.path.splitext(path)[0] + ".json"
+        if isinstance(meta, (str, os.PathLike)):
+            with open(meta) as f:
+                meta = json.load(f)
+        self.meta = dict(meta)
+        self.blob, self.rec = int(meta["blob"]), int(meta["rec"])
+        if self.rec % _REC_ALIGN or self.rec < self.blob:
+            raise ValueError(f"ExpertFile: record size {self.rec} must be a 4 KiB multiple holding the blob")
+        self.path = path
+        want_direct = direct if direct is not None else _env_int("EXL3_NVTIER_DIRECT", 1) == 1
+        self.fd, self.direct = None, False
+        if want_direct and hasattr(os, "O_DIRECT"):
+            try:
+                self.fd = os.open(path, os.O_RDONLY | os.O_DIRECT)
+                self.direct = True
+            except OSError:
+                self.fd = None
+        if self.fd is None:
+            self.fd = os.open(path, os.O_RDONLY)
+        self._tls = threading.local()
+        self.reads = 0
+
+    def _bounce(self):
+        b = getattr(self._tls, "buf", None)
+        if b is None:
+            import mmap
+            b = mmap.mmap(-1, self.rec)                 # page-aligned anonymous memory
+            self._tls.buf = b
+            self._tls.addr = ctypes.addressof(ctypes.c_char.from_buffer(b))
+        return b, self._tls.addr
+
+    def read(self, rec_index: int, dst: int) -> None:
+        off = int(rec_index) * self.rec
+        if self.direct and dst % _REC_ALIGN == 0:
+            try:
+                n = os.preadv(self.fd, [(ctypes.c_char * self.rec).from_address(dst)], off)
+                if n == self.rec:
+                    self.reads += 1
+                    return
+            except OSError:
+                pass                                    # memory the kernel cannot pin for direct I/O: bounce
+        buf, addr = self._bounce()
+        n = os.preadv(self.fd, [buf], off)
+        if n != self.rec:
+            raise OSError(f"ExpertFile: short read of record {rec_index} ({n} of {self.rec} bytes)")
+        ctypes.memmove(dst, addr, self.blob)
+        self.reads += 1
+
+    def close(self) -> None:
+        if self.fd is not None:
+            os.close(self.fd)
+            self.fd = None
+
+
+def write_expert_file(path: str, source, n_layers: int, n_experts: int, H: int, I: int, K: int) -> dict:  # noqa: E741
+    """Write the expert file of `source` (records 0 .. n_layers * n_experts - 1) and its JSON meta; returns meta."""
+    rec = record_bytes(source.blob)
+    zero = bytes(rec - source.blob)
+    with open(path, "wb") as f:
+        for r in range(n_layers * n_experts):
+            f.write(np.ascontiguousarray(source.blob_of(r)).tobytes())
+            f.write(zero)
+    meta = {"blob": int(source.blob), "rec": rec, "layers": n_layers, "experts": n_experts, "H": H, "I": I, "K": K}
+    with open(os.path.splitext(path)[0] + ".json", "w") as f:
+        json.dump(meta, f)
+    return meta
+
+
+# ---- the tier ----------------------------------------------------------------------------------------------------------------
+
+class _TierDevice:
+    """The tier's device tensors (the reference's moe_set_tier / moe_set_victims globals, nvtier.py:69-87):
+    RAM flags, the miss ring, the safe expert per layer and the victim list; attached to the library while the tier
+    is open."""
+
+    def __init__(self, dev, n_keys: int, ring_cap: int, n_layers: int, n_experts: int, safe: int):
+        self.res = torch.zeros(n_keys, dtype=torch.uint8, device=dev)
+        self.ring = torch.zeros(1 + ring_cap, dtype=torch.int32, device=dev)
+        self.safe = torch.full((n_layers,), safe, dtype=torch.int32, device=dev)
+        self.vict = torch.zeros(1 + 2 * n_experts, dtype=torch.int32, device=dev)
+        self.dev = dev
+
+    def attach(self, X, victims: bool) -> None:
+        X.moe_set_tier(self.res, self.ring, self.safe)
+        X.moe_set_victims(self.vict if victims else torch.zeros(0, dtype=torch.int32, device=self.dev))
+
+    def detach(self, X) -> None:
+        none = torch.zeros(0, dtype=torch.int32, device=self.dev)
+        X.moe_set_tier(torch.zeros(0, dtype=torch.uint8, device=self.dev), none, none)
+        X.moe_set_victims(none)
+
+
+def _evict_order(over: int, classes, age: np.ndarray) -> np.ndarray:
+    """The `over` keys to evict: candidates of class 0 first, then class 1, ...; within a class by ascending age, ties
+    by ascending key. `classes` is a list of boolean masks over the keys."""
+    if over <= 0:
+        return np.zeros(0, dtype=np.int64)
+    keys, rank = [], []
+    for c, m in enumerate(classes):
+        k = np.nonzero(m)[0]
+        keys.append(k)
+        rank.append(np.full(k.size, c, dtype=np.int64))
+    keys, rank = np.concatenate(keys), np.concatenate(rank)
+    order = np.lexsort((keys, age[keys], rank))
+    return keys[order[:over]].astype(np.int64)
+
+
 class NvTier:
-    """Tier base: flags, miss ring, pinned safe expert per layer (nvtier.py:56-87).
-    source: object with read(rec_index, dst_addr) (an NVMe store reader or SyntheticExpertSource).
-    ram_budget: bytes (records = bytes // stride, like the reference) or, with budget_records, a record count."""
+    """RAM tier base (the reference's NvTier, nvtier.py:56-112): flags, miss ring, safe expert per layer (pinned in
+    RAM from the start), fills from the source into the arena, prefill-time fills (ensure_for_prefill), warm-up from
+    a routing prior (warm) and tier-mode prefill streaming (stage_forward).
+
+    source: a fill source with read(rec_index, dst) (ExpertFile, SyntheticExpertSource), or the path of an expert
+    file (meta: its JSON, default beside it). The RAM budget is ram_budget_bytes // stride records (the reference's
+    rule), or budget_records when given. ckpt_layer[li] is the checkpoint layer of store row li (record = that
+    layer * E + e)."""
 
     def __init__(self, store: TierStore, source, meta=None, ram_budget_bytes=2 << 30, ring_cap=1 << 16, safe=0,
                  dev=None, ckpt_layer=None, budget_records: int | None = None, latency: int = 8):
         self.st, self.E = store, store.E
-        self.src = source
-        self.L = len(ckpt_layer) if ckpt_layer is not None else store.L
-        self.ckpt = np.asarray(ckpt_layer if ckpt_layer is not None else range(self.L), dtype=np.int64)
-        self.dev = dev or store.dev
+        self.src = ExpertFile(source, meta) if isinstance(source, (str, os.PathLike)) else source
+        self.ckpt = np.asarray(ckpt_layer if ckpt_layer is not None else range(store.L), dtype=np.int64)
+        self.L = int(self.ckpt.size)
+        self.dev = torch.device(dev) if dev is not None else store.dev
         self.blob = store.blob
         self.budget = int(budget_records) if budget_records else max(1, int(ram_budget_bytes // store.stride))
         self.latency = max(1, int(latency))
         n = self.L * self.E
-        self.res_dev = torch.zeros(n, dtype=torch.uint8, device=self.dev)
-        self.ring = torch.zeros(1 + ring_cap, dtype=torch.int32, device=self.dev)
-        self.safe = torch.full((self.L,), safe, dtype=torch.int32, device=self.dev)
-        self.vict = torch.zeros(1 + 2 * self.E, dtype=torch.int32, device=self.dev)
+        self._d = _TierDevice(self.dev, n, int(ring_cap), self.L, self.E, int(safe))
+        self.res_dev, self.ring, self.safe, self.vict = self._d.res, self._d.ring, self._d.safe, self._d.vict
         self.res = np.zeros(n, dtype=np.uint8)
-        self.pinned = set(li * self.E + safe for li in range(self.L))
+        self.pinned = {li * self.E + int(safe) for li in range(self.L)}
         self.ring_seen = 0
         self.stats = dict(nvme_reads=0, nvme_ms=0.0, evicts=0, masked=0, steps=0, fill_ms=0.0, ring_overflow=0)
-        for k in sorted(self.pinned):
-            self._fill(k)
+        self._readers = None
+        self._streamer = None
+        self.fill_many(sorted(self.pinned))
         self.res_dev.copy_(torch.from_numpy(self.res))
-        X = store.X
-        X.moe_set_tier(self.res_dev, self.ring, self.safe)
-        if os.environ.get("EXL3_NVTIER_NO_VICTIM", "0") != "1":
-            X.moe_set_victims(self.vict)
-        else:
-            X.moe_set_victims(torch.zeros(0, dtype=torch.int32, device=self.dev))
+        self._d.attach(store.X, victims=_env_int("EXL3_NVTIER_NO_VICTIM", 0) != 1)
 
-    def close(self):
-        X = self.st.X
-        X.moe_set_tier(torch.zeros(0, dtype=torch.uint8, device=self.dev), torch.zeros(0, dtype=torch.int32, device=self.dev),
-                       torch.zeros(0, dtype=torch.int32, device=self.dev))
-        X.moe_set_victims(torch.zeros(0, dtype=torch.int32, device=self.dev))
-        X.moe_set_host_stride(0)
-        X.moe_set_slot_stride(0)
+    def close(self) -> None:
+        """Detach the tier from the library (no masking, no write-back afterwards) and stop the reader threads. The
+        store's strides are the store's and stay as they are."""
+        self._d.detach(self.st.X)
+        if self._readers is not None:
+            self._readers.shutdown(wait=True)
+            self._readers = None
 
+    # ---- records
     def rec_index(self, key: int) -> int:
         return int(self.ckpt[key // self.E]) * self.E + key % self.E
 
-    def _fill(self, key: int) -> None:
-        t = time.perf_counter()
+    def _pool(self) -> ThreadPoolExecutor:
+        if self._readers is None:
+            self._readers = ThreadPoolExecutor(_env_int("EXL3_NVTIER_FILL_THREADS", 16))
+        return self._readers
+
+    def _read(self, key: int) -> None:
         self.src.read(self.rec_index(key), self.st.addr(key))
-        self.res[key] = 1
-        self.stats["nvme_reads"] += 1
-        self.stats["nvme_ms"] += (time.perf_counter() - t) * 1e3
+
+    def _fill(self, key: int) -> None:
+        self.fill_many([key])
 
     def fill_many(self, keys) -> None:
+        """Read the records of `keys` into the arena (reader threads) and mark them RAM-resident (host books)."""
         keys = [int(k) for k in keys]
         if not keys:
             return
-        if not hasattr(self, "_pool"):
-            self._pool = ThreadPoolExecutor(int(os.environ.get("EXL3_NVTIER_FILL_THREADS", "16")))
         t = time.perf_counter()
-        list(self._pool.map(lambda k: self.src.read(self.rec_index(k), self.st.addr(k)), keys))
-        for k in keys:
-            self.res[k] = 1
+        if len(keys) < 4:
+            for k in keys:
+                self._read(k)
+        else:
+            list(self._pool().map(self._read, keys))
+        self.res[keys] = 1
         self.stats["nvme_reads"] += len(keys)
         self.stats["nvme_ms"] += (time.perf_counter() - t) * 1e3
 
@@ -176,133 +315,173 @@ class NvTier:
         return int(self.res.sum()) * self.st.stride
 
     def warm(self, keys_ckpt, max_bytes):
-        """Fill the RAM tier with the hottest experts (checkpoint keys, hottest first) up to max_bytes
-        (nvtier.py:492-509)."""
-        inv = {int(c): li for li, c in enumerate(self.ckpt)}
-        t = time.perf_counter()
-        cap = int(max_bytes // self.st.stride)
-        have = int(self.res.sum())
-        todo, seen = [], set()
-        for kc in keys_ckpt:
-            if have + len(todo) >= cap:
-                break
-            li = inv.get(int(kc) // self.E)
-            if li is None:
-                continue
-            k = li * self.E + int(kc) % self.E
-            if not self.res[k] and k not in seen:
-                todo.append(k)
-                seen.add(k)
+        """Fill the RAM tier with the hottest experts of a routing prior (checkpoint keys layer * E + e, hottest
+        first) until max_bytes of records are resident (reference nvtier.py:492-509); returns (filled, seconds)."""
+        t0 = time.perf_counter()
+        kc = np.asarray(list(keys_ckpt), dtype=np.int64)
+        row_of = np.full(int(self.ckpt.max()) + 1 if self.ckpt.size else 1, -1, dtype=np.int64)
+        row_of[self.ckpt] = np.arange(self.L)
+        lay = kc // self.E
+        known = (lay >= 0) & (lay < row_of.size)
+        rows = np.where(known, row_of[np.clip(lay, 0, row_of.size - 1)], -1)
+        keys = (rows * self.E + kc % self.E)[rows >= 0]
+        keys = keys[self.res[keys] == 0]
+        _, first = np.unique(keys, return_index=True)
+        keys = keys[np.sort(first)]                     # distinct, in prior order
+        room = max(0, int(max_bytes // self.st.stride) - int(self.res.sum()))
+        todo = keys[:room]
         self.fill_many(todo)
         if hasattr(self, "age"):
             self.age[todo] = 0
         self.res_dev.copy_(torch.from_numpy(self.res))
-        return len(todo), time.perf_counter() - t
+        return int(todo.size), time.perf_counter() - t0
 
-    # ---- tier-mode prefill streaming (nvtier.py:534-640) ------------------------------------------------------------
-    def stage_forward(self, store, key, li: int, x: torch.Tensor, ids: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
-        """Prefill-size MoE for layer `li` with its non-HBM experts streamed: reader threads copy the layer's records
-        from the fill source into a pinned host ring buffer (read-ahead of NB-1 layers, EXL3_NVTIER_STAGE_HOSTBUF,
-        default 4), a side stream copies them into one of two HBM staging buffers (runs of consecutive experts in one
-        copy), and the layer runs from the device table where(slot_of >= 0, slot, staging). The first layer of a
-        forward synchronises once and snapshots the HBM slot map; layers follow the checkpoint order."""
-        sg = getattr(self, "_sg", None) or self._stage_setup()
-        E, rec = self.E, sg["rec"]
-        pos = sg["pos"][li]
-        if pos == 0 or li not in sg["pending"]:
+    # ---- prefill
+    def ensure_for_prefill(self, li: int, ids) -> int:
+        """Make every expert of layer row li that `ids` routes to RAM-resident and flag it on the device, so that the
+        prefill kernels read it zero-copy (reference nvtier.py:389-457). The budget holds: over budget, evict first
+        the transient (prefill-only) fills, then RAM copies of HBM-resident experts, then the rest, each by ascending
+        age with ties by ascending key; never this layer's keys, pinned keys or fills in flight. Synchronous;
+        returns the number of records filled."""
+        n = self.L * self.E
+        if not hasattr(self, "transient"):
+            self.transient = np.zeros(n, dtype=bool)
+        ids_np = ids.reshape(-1).to("cpu", torch.int64).numpy() if torch.is_tensor(ids) else np.asarray(ids).reshape(-1)
+        keys = np.unique(ids_np) + li * self.E
+        miss = keys[self.res[keys] == 0]
+        inflight = getattr(self, "inflight", np.zeros(n, dtype=bool))
+        over = int(self.res.sum()) + int(inflight.sum()) + miss.size - self.budget
+        if miss.size and over > 0:
             torch.cuda.synchronize(self.dev)
-            sod = self.st.slot_of_dev[:self.L * E]
-            sg["snap_dev"] = sod.to(torch.int64)
-            sg["snap"] = sod.cpu().numpy()
-            for _, _, fs in sg["pending"].values():
-                for f in fs:
-                    f.result()
-            sg["pending"].clear()
-            for q in range(pos, min(pos + sg["NB"], len(sg["order"]))):
-                self._stage_kick(sg["order"][q])
-        hb, miss, futs = sg["pending"].pop(li)
+            back = (self.res_dev.cpu().numpy() == 1) & (self.res == 0)       # victims written back since the last step
+            self.res[back] = 1
+            age = getattr(self, "age", np.zeros(n, dtype=np.int64))
+            if hasattr(self, "age"):
+                age[back] = self.tick
+            ok = (self.res == 1) & ~inflight
+            ok[list(self.pinned)] = False
+            ok[keys] = False
+            vram = self.st.slot_of_dev[:n].cpu().numpy() >= 0
+            ev = _evict_order(over, [ok & self.transient, ok & ~self.transient & vram,
+                                     ok & ~self.transient & ~vram], age)
+            if ev.size:
+                self.res[ev] = 0
+                self.transient[ev] = False
+                self.res_dev.index_fill_(0, torch.from_numpy(ev).to(self.dev), 0)
+            self.stats["prefill_evicts"] = self.stats.get("prefill_evicts", 0) + int(ev.size)
+        self.fill_many(miss)
+        if miss.size:
+            if hasattr(self, "inflight"):
+                self.inflight[miss] = False
+            if hasattr(self, "age"):
+                self.age[miss] = self.tick
+            self.transient[miss] = True
+            self.res_dev.index_fill_(0, torch.from_numpy(miss.astype(np.int64)).to(self.dev), 1)
+        self.stats["prefill_fills"] = self.stats.get("prefill_fills", 0) + int(miss.size)
+        return int(miss.size)
+
+    def stage_forward(self, store, key, li: int, x: torch.Tensor, ids: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
+        """Prefill-size MoE for layer row li with its non-HBM experts streamed: reader threads read their records into
+        a pinned host ring (read-ahead of the following layers), the copy stream moves them into an HBM staging
+        buffer, and the layer runs on the table (HBM slot, else staging). The first layer of a forward synchronises
+        once and snapshots the slot map (reference nvtier.py:534-640)."""
+        if self._streamer is None:
+            self._streamer = _TierStreamer(self)
+        return self._streamer.run(store, key, li, x, ids, w)
+
+    # ---- reporting
+    def log_stats(self, logger=None, every=200):
+        """Every `every` host steps: per-step rates of masked picks, fills and evictions over the last period, the
+        host time per step and the RAM in use (reference nvtier.py:512-526)."""
+        steps = self.stats["steps"]
+        if not steps or steps % every:
+            return
+        prev = getattr(self, "_stats_mark", {})
+        d = {k: v - prev.get(k, 0) for k, v in self.stats.items() if isinstance(v, (int, float))}
+        per = max(1, int(d.get("steps", 0)))
+        (logger or log).info(
+            "exl3xpu tier: %d steps | per step: masked %.2f, fills %.2f, evictions %.2f, host %.3f ms (waiting %.3f) | "
+            "admissions dropped %d | RAM %.2f GiB of %.2f", per, d.get("masked", 0) / per, d.get("nvme_reads", 0) / per,
+            d.get("evicts", 0) / per, d.get("fill_ms", 0.0) / per, d.get("wait_ms", 0.0) / per,
+            int(d.get("admit_dropped", 0)), self.ram_bytes() / 2 ** 30, self.budget * self.st.stride / 2 ** 30)
+        self._stats_mark = dict(self.stats)
+
+
+class _TierStreamer:
+    """Tier-mode prefill streaming: per layer, the records of its non-HBM experts are read by the reader threads into
+    one of NB pinned host buffers (NB = EXL3_NVTIER_STAGE_HOSTBUF, default 4: NB - 1 layers of read-ahead), then the
+    copy stream moves them into one of the two HBM staging buffers. Layers run in checkpoint order; the first layer of
+    a forward (or a layer whose reads were not started) synchronises, snapshots the HBM slot map and restarts the
+    read-ahead."""
+
+    def __init__(self, tier: NvTier):
+        st = tier.st
+        self.tier, self.E, self.rec = tier, tier.E, st.stride
+        self.stager = _Stager(tier.dev, tier.E, self.rec)
+        self.nb = max(2, _env_int("EXL3_NVTIER_STAGE_HOSTBUF", 4))
+        self.host = [st.X.host_alloc(self.E * self.rec) for _ in range(self.nb)]
+        self.host_free = [None] * self.nb          # event of the copy that last read host buffer i
+        self.order = [int(li) for li in np.argsort(tier.ckpt, kind="stable")]
+        self.pos = {li: i for i, li in enumerate(self.order)}
+        self.pending = {}                          # layer row -> (host buffer, missing experts, futures)
+        self.next_host = 0
+        self.next_dev = 0
+        self.snap = None                           # host copy of the slot map at the start of the forward
+
+    def _kick(self, li: int) -> None:
+        hb = self.next_host
+        self.next_host = (hb + 1) % self.nb
+        if self.host_free[hb] is not None:
+            self.host_free[hb].synchronize()       # the copy that read this buffer NB - 1 layers ago is done
+            self.host_free[hb] = None
+        missing = np.nonzero(self.snap[li * self.E:(li + 1) * self.E] < 0)[0]
+        base, tier = self.host[hb].data_ptr(), self.tier
+        chunks = np.array_split(missing, min(8, max(1, missing.size)))
+
+        def read(part):
+            for e in part.tolist():
+                tier.src.read(tier.rec_index(li * self.E + e), base + e * self.rec)
+        self.pending[li] = (hb, missing, [tier._pool().submit(read, c) for c in chunks if c.size])
+
+    def _restart(self, pos: int) -> None:
+        torch.cuda.synchronize(self.tier.dev)
+        self.snap = self.tier.st.slot_of_dev[:self.tier.L * self.E].cpu().numpy()
+        for _, _, futs in self.pending.values():
+            for f in futs:
+                f.result()
+        self.pending.clear()
+        for q in range(pos, min(pos + self.nb, len(self.order))):
+            self._kick(self.order[q])
+
+    def run(self, store, key, li, x, ids, w):
+        pos = self.pos[li]
+        if pos == 0 or li not in self.pending:
+            self._restart(pos)
+        hb, missing, futs = self.pending.pop(li)
         for f in futs:
             f.result()
-        buf = sg["dbuf"]
-        sg["dbuf"] = 1 - buf
-        cur = torch.cuda.current_stream(self.dev)
-        dbase, hbase = s64(sg["dev"][buf].data_ptr()), s64(sg["host"][hb].data_ptr())
-        with torch.cuda.stream(sg["cs"]):
-            if sg["comp_ev"][buf] is not None:
-                sg["cs"].wait_event(sg["comp_ev"][buf])      # the layer that last read this staging buffer is done
-            m, i = miss.tolist(), 0
-            while i < len(m):
-                j = i
-                while j + 1 < len(m) and m[j + 1] == m[j] + 1:
-                    j += 1
-                self.st.X.memcpy_async(dbase + m[i] * rec, hbase + m[i] * rec, (j - i + 1) * rec)
-                i = j + 1
-            ev = torch.cuda.Event()
-            ev.record(sg["cs"])
-        sg["hfree"][hb] = ev
-        cur.wait_event(ev)
-        so = sg["snap_dev"][li * E:(li + 1) * E]
-        table = torch.where(so >= 0, self.st.slot_base + so.clamp_min(0) * self.st.blob, dbase + sg["ar"])
+        b = self.next_dev
+        self.next_dev ^= 1
+        base = self.host[hb].data_ptr()
+        src = base + np.arange(self.E, dtype=np.int64) * self.rec
+        ready = self.stager.fill(b, src, missing, base, base + self.E * self.rec)
+        self.host_free[hb] = ready
+        cs = torch.cuda.current_stream(self.tier.dev)
+        cs.wait_event(ready)
+        table = self.stager.table(b, self.snap[li * self.E:(li + 1) * self.E], store.slot_base, store.slot_stride)
         y = store.forward(key, x, ids, w, ptrs=table)
-        ce = torch.cuda.Event()
-        ce.record(cur)
-        sg["comp_ev"][buf] = ce
-        nq = pos + sg["NB"]
-        if nq < len(sg["order"]) and sg["order"][nq] not in sg["pending"]:
-            self._stage_kick(sg["order"][nq])
-        sg["bytes"] += len(miss) * rec
+        self.stager.release(b, cs)
+        self.tier.stats["stage_bytes"] = self.tier.stats.get("stage_bytes", 0) + int(missing.size) * self.rec
+        nq = pos + self.nb
+        if nq < len(self.order) and self.order[nq] not in self.pending:
+            self._kick(self.order[nq])
         return y
-
-    def _stage_setup(self):
-        E = self.E
-        rec = self.st.stride
-        NB = max(2, int(os.environ.get("EXL3_NVTIER_STAGE_HOSTBUF", "4")))
-        X = self.st.X
-        order = [int(li) for li in np.argsort(self.ckpt, kind="stable")]
-        sg = dict(rec=rec, NB=NB, dev=[torch.empty(E * rec, dtype=torch.uint8, device=self.dev) for _ in range(2)],
-                  host=[X.host_alloc(E * rec) for _ in range(NB)], cs=torch.cuda.Stream(self.dev),
-                  comp_ev=[None, None], hfree={}, pending={}, nexth=0, dbuf=0, order=order,
-                  pos={li: i for i, li in enumerate(order)}, snap=None, snap_dev=None, bytes=0,
-                  ar=torch.arange(E, dtype=torch.int64, device=self.dev) * rec,
-                  pool=ThreadPoolExecutor(int(os.environ.get("EXL3_NVTIER_FILL_THREADS", "16"))))
-        self._sg = sg
-        return sg
-
-    def _stage_kick(self, li: int) -> None:
-        """Start the reads of layer li's non-HBM experts into the next host ring buffer."""
-        sg, E, rec = self._sg, self.E, self._sg["rec"]
-        hb = sg["nexth"]
-        sg["nexth"] = (hb + 1) % sg["NB"]
-        ev = sg["hfree"].pop(hb, None)
-        if ev is not None:
-            ev.synchronize()                        # the copy that last read this host buffer is done
-        miss = np.nonzero(sg["snap"][li * E:(li + 1) * E] < 0)[0]
-        hp = s64(sg["host"][hb].data_ptr())
-        keys = [int(e) for e in miss]
-        per = max(1, -(-len(keys) // 8))
-
-        def rd(part):
-            for e in part:
-                self.src.read(self.rec_index(li * E + e), hp + e * rec)
-        sg["pending"][li] = (hb, miss, [sg["pool"].submit(rd, keys[i:i + per]) for i in range(0, len(keys), per)])
-
-    def log_stats(self, logger=None, every=200):
-        logger = logger or log
-        if self.stats["steps"] % every or not self.stats["steps"]:
-            return
-        b = getattr(self, "_last", None) or {k: 0 for k in self.stats}
-        d = {k: self.stats.get(k, 0) - b.get(k, 0) for k in self.stats}
-        n = max(1, d.get("steps", 0))
-        logger.info("exl3xpu: nvtier last %d steps: masked/step %.2f fills/step %.2f evicts/step %.1f host ms/step %.2f "
-                    "admit_dropped %d ram %.2f GB", n, d.get("masked", 0) / n, d.get("nvme_reads", 0) / n,
-                    d.get("evicts", 0) / n, d.get("fill_ms", 0) / n, d.get("admit_dropped", 0), self.ram_bytes() / 2 ** 30)
-        self._last = dict(self.stats)
 
 
 class NvTierFast(NvTier):
-    """Vectorised bookkeeping + background fills (nvtier.py:175-278): age, in-flight set, pinned mask; fills complete
-    `latency` host steps after admission (deterministic). The fills admitted by one host step are copied by a few
-    worker tasks (one future per chunk of keys), since each completes as a group."""
+    """Vectorised bookkeeping with background fills (the reference's NvTierFast, nvtier.py:175-278): per-key age,
+    in-flight and pinned masks; the fills admitted at host step n are read by worker tasks and become resident at
+    host step n + latency (a deterministic completion time in place of wall-clock NVMe reads)."""
 
     FILL_CHUNKS = 4
 
@@ -312,41 +491,31 @@ class NvTierFast(NvTier):
         self.age = np.zeros(n, dtype=np.int64)
         self.tick = 1
         self.pin_mask = np.zeros(n, dtype=bool)
-        self.pin_mask[list(self.pinned)] = True
+        self.pin_mask[sorted(self.pinned)] = True
         self.inflight = np.zeros(n, dtype=bool)
-        self._pending = {}                 # host step -> [(keys, future)]
+        self._due = {}                              # host step -> [(keys, future)]
         self._hstep = 0
-        self._pool = ThreadPoolExecutor(int(os.environ.get("EXL3_NVTIER_FILL_THREADS", "16")))
 
     def _read_keys(self, keys) -> None:
         for key in keys:
-            self.src.read(self.rec_index(key), self.st.addr(key))
+            self._read(key)
 
     def _queue_fills(self, keys, hs: int) -> None:
-        """fills admitted at host step hs: copied by workers, flagged resident at host step hs + latency"""
+        """Fills admitted at host step hs: read by workers, resident from host step hs + latency."""
         keys = [int(k) for k in keys]
         if not keys:
             return
-        per = -(-len(keys) // self.FILL_CHUNKS)
-        lst = self._pending.setdefault(hs + self.latency, [])
-        for i in range(0, len(keys), per):
-            part = keys[i:i + per]
-            lst.append((part, self._pool.submit(self._read_keys, part)))
+        due = self._due.setdefault(hs + self.latency, [])
+        for part in np.array_split(np.asarray(keys), min(self.FILL_CHUNKS, len(keys))):
+            due.append((part.tolist(), self._pool().submit(self._read_keys, part.tolist())))
         self.stats["nvme_reads"] += len(keys)
 
-    def _queue_fill(self, key: int, hs: int) -> None:
-        self._queue_fills([key], hs)
-
-    def _completed(self, hs: int):
+    def _completed(self, hs: int) -> list:
         done = []
-        for keys, fut in self._pending.pop(hs, []):
+        for keys, fut in self._due.pop(hs, []):
             fut.result()
             done.extend(keys)
         return done
-
-    def close(self):
-        self._pool.shutdown(wait=True)
-        super().close()
 
 
 class _AdmitState(ctypes.Structure):
@@ -360,8 +529,8 @@ def _ptr(a: np.ndarray) -> int:
 
 
 class AdmissionPolicy:
-    """Host bookkeeping of the admission-controlled tier step (_async_step_admit, nvtier.py:708-806); the decision
-    runs natively (exl3_admit_decide in libexl3moe.so) over the numpy books held here.
+    """Host books of the admission-controlled tier step (_async_step_admit, nvtier.py:708-806); the decision runs
+    natively (exl3_admit_decide in libexl3moe.so) over the numpy books held here.
 
     decide() consumes the device state of the PREVIOUS step (flags with the previous upload overlaid, miss ring, HBM
     slot map) plus the keys whose fills completed now, and returns (admitted keys, evicted keys, flag diff keys, flag
@@ -428,9 +597,9 @@ class NvTierAsync(NvTierFast):
 
     Per step on the stream: one exchange kernel (exl3_tier_exchange) that applies the step's (key, value) flag diff,
     read in place from a pinned double buffer, mirrors the miss-ring entries appended since the last snapshot into a
-    pinned ring mirror, and writes the snapshot of the RAM flags and the slot table into pinned double buffers; no
-    host allocation, no extra synchronisation. The host reads the mirror only between the wait for one exchange and
-    the launch of the next, so one mirror suffices."""
+    pinned ring mirror, and copies the RAM flags, the slot table and the device status words into pinned double
+    buffers; no host allocation, no extra synchronisation. A non-zero status (a bounded wait of a decode kernel timed
+    out, so an output was computed from incomplete data) raises RuntimeError at the next step."""
 
     def __init__(self, *a, **k):
         super().__init__(*a, **k)
@@ -439,31 +608,36 @@ class NvTierAsync(NvTierFast):
         n = self.L * self.E
         self._n = n
         X = self.st.X
-        # device-mapped pinned buffers: the exchange kernel writes the snapshots and reads the diffs in place
         self._h_res = [X.host_alloc(n) for _ in range(2)]
         self._h_ring = X.host_alloc(4 * self.ring.numel()).view(torch.int32)
         self._h_ring.zero_()
-        self._ring_from = 0                # ring count of the last snapshot read (the next exchange mirrors from it)
+        self._ring_from = 0                # ring count (mod 2^32) of the last snapshot read
         self._h_slot = [X.host_alloc(4 * n).view(torch.int32) for _ in range(2)]
+        self._h_status = [X.host_alloc(16).view(torch.int32) for _ in range(2)]
+        for t in self._h_status:
+            t.zero_()
         self._np_res = [t.numpy() for t in self._h_res]
         self._np_ring = self._h_ring.numpy()
         self._np_slot = [t.numpy() for t in self._h_slot]
-        self._h_diff = [X.host_alloc(4 * n).view(torch.int32) for _ in range(2)]   # device-mapped pinned
+        self._h_diff = [X.host_alloc(4 * n).view(torch.int32) for _ in range(2)]
         self._np_diff = [t.numpy() for t in self._h_diff]
         self._snap_ev = [torch.cuda.Event(), torch.cuda.Event()]
-        import ctypes
-        self._xargs = []                   # (src, dst, nbytes) ctypes arrays of the two snapshot copies per buffer
+        dev_status = ctypes.c_void_p()
+        capi.check(capi.lib().exl3_device_status_address(ctypes.byref(dev_status)), "device status address")
+        self._xargs = []                   # (src, dst, nbytes) ctypes arrays of the snapshot copies per buffer
         for b in range(2):
-            pairs = ((self.res_dev, self._h_res[b], n), (self.st.slot_of_dev, self._h_slot[b], 4 * n))
-            self._xargs.append(((ctypes.c_void_p * 2)(*[p[0].data_ptr() for p in pairs]),
-                                (ctypes.c_void_p * 2)(*[p[1].data_ptr() for p in pairs]),
-                                (ctypes.c_int64 * 2)(*[p[2] for p in pairs])))
+            copies = ((self.res_dev.data_ptr(), self._h_res[b].data_ptr(), n),
+                      (self.st.slot_of_dev.data_ptr(), self._h_slot[b].data_ptr(), 4 * n),
+                      (dev_status.value, self._h_status[b].data_ptr(), 16))
+            self._xargs.append(((ctypes.c_void_p * 3)(*[c[0] for c in copies]),
+                                (ctypes.c_void_p * 3)(*[c[1] for c in copies]),
+                                (ctypes.c_int64 * 3)(*[c[2] for c in copies])))
         self._have = [False, False]
         self._k = 0
         self._last_diff = None
         self._view = np.empty(n, dtype=np.uint8)
-        self.policy = AdmissionPolicy(n, self.pinned, self.budget, int(os.environ.get("EXL3_NVTIER_ADMIT_AGE", "4")),
-                                      int(os.environ.get("EXL3_NVTIER_ADMIT_QMAX", "256")), self.ring.numel() - 1)
+        self.policy = AdmissionPolicy(n, self.pinned, self.budget, _env_int("EXL3_NVTIER_ADMIT_AGE", 4),
+                                      _env_int("EXL3_NVTIER_ADMIT_QMAX", 256), self.ring.numel() - 1)
         self.policy.res[:] = self.res
         self.res = self.policy.res
         self.log_decisions = False
@@ -474,31 +648,33 @@ class NvTierAsync(NvTierFast):
         return np.nonzero(self.policy.inflight)[0]
 
     def step(self) -> int:
+        """The host step after a decode step; returns the number of masked picks it consumed."""
         t0 = time.perf_counter()
         pol = self.policy
         pol.tick += 1
         self.tick = pol.tick
         hs = self._hstep
         self._hstep += 1
-        n = self._n
         cur = torch.cuda.current_stream(self.dev)
-        L, sh = self._capi.lib(), cur.cuda_stream
-        k = self._k
-        self._k ^= 1
-        j = k ^ 1
+        k, j = self._k, self._k ^ 1
+        self._k = j
         n_diff = 0
         seen0 = pol.ring_seen
         if self._have[j]:
             tw = time.perf_counter()
             self._snap_ev[j].synchronize()
             self.stats["wait_ms"] = self.stats.get("wait_ms", 0.0) + (time.perf_counter() - tw) * 1e3
+            bad = int(self._h_status[j][0])
+            if bad:
+                raise RuntimeError(f"exl3xpu: {bad} bounded waits of the decode kernels timed out on the device "
+                                   "(outputs computed from incomplete data); the device state is not trustworthy")
             view = self._view
             np.copyto(view, self._np_res[j])
             if self._last_diff is not None:         # the flags uploaded with that snapshot
                 dk, dv = self._last_diff
                 view[dk] = dv
             adm, ev_keys, diff, vals = pol.decide(view, self._np_ring, self._np_slot[j], self._completed(hs))
-            self._ring_from = int(self._np_ring[0])
+            self._ring_from = int(self._np_ring[0]) & 0xFFFFFFFF
             self._queue_fills(adm, hs)
             if len(diff):
                 # buffer k was last read by the exchange of step n-2, which ran before the snapshot just waited for
@@ -517,68 +693,13 @@ class NvTierAsync(NvTierFast):
             self.decisions.append((np.zeros(0, np.int64), np.zeros(0, np.int64)))
         # this step's diff and the snapshot of the device state after decode step n, in one launch
         srcs, dsts, nbs = self._xargs[k]
-        self._capi.check(L.exl3_tier_exchange(self.res_dev.data_ptr(), n, self._h_diff[k].data_ptr(), n_diff,
+        L = self._capi.lib()
+        self._capi.check(L.exl3_tier_exchange(self.res_dev.data_ptr(), self._n, self._h_diff[k].data_ptr(), n_diff,
                                               self.ring.data_ptr(), self.ring.numel() - 1, self._ring_from,
-                                              self._h_ring.data_ptr(), srcs, dsts, nbs, 2, sh), "nvtier exchange")
+                                              self._h_ring.data_ptr(), srcs, dsts, nbs, 3, cur.cuda_stream),
+                         "nvtier exchange")
         self._snap_ev[k].record(cur)
         self._have[k] = True
         self.stats["steps"] += 1
         self.stats["fill_ms"] += (time.perf_counter() - t0) * 1e3
-        return int(max(0, pol.ring_seen - seen0))
-
-
-def _ensure_for_prefill(self, li, ids):
-    """Prefill: synchronously make every expert this layer's batch uses RAM-resident and flag it on the device, so
-    the prefill kernel can read it zero-copy (nvtier.py:389-457). Evicts, in order: prefill-only fills of other
-    layers, RAM copies of HBM-resident experts, the oldest; never this layer's keys, pinned keys or in-flight fills.
-    Ties by ascending key (stable sort)."""
-    n = self.L * self.E
-    if not hasattr(self, "transient"):
-        self.transient = np.zeros(n, dtype=bool)
-    keys = np.unique(ids.reshape(-1).to("cpu", torch.int64).numpy()) + li * self.E
-    miss = keys[self.res[keys] == 0]
-    if len(miss):
-        inflight = getattr(self, "inflight", np.zeros(n, dtype=bool))
-        over = int(self.res.sum()) + int(inflight.sum()) + len(miss) - self.budget
-        if over > 0:
-            torch.cuda.synchronize(self.dev)
-            res_d = self.res_dev.cpu().numpy()
-            newly = (res_d == 1) & (self.res == 0)
-            self.res[newly] = 1
-            if hasattr(self, "age"):
-                self.age[newly] = self.tick
-            age = getattr(self, "age", np.zeros(n, dtype=np.int64))
-            ok = (self.res == 1) & ~inflight
-            ok[list(self.pinned)] = False
-            ok[keys] = False
-            vram = self.st.slot_of_dev[:n].cpu().numpy() >= 0
-            ev = []
-            for m in (ok & self.transient, ok & ~self.transient & vram, ok & ~self.transient & ~vram):
-                if over <= 0:
-                    break
-                c = np.nonzero(m)[0]
-                c = c[np.argsort(age[c], kind="stable")[:over]]
-                ev.append(c)
-                over -= len(c)
-            ev = np.concatenate(ev) if ev else np.zeros(0, dtype=np.int64)
-            if len(ev):
-                self.res[ev] = 0
-                self.transient[ev] = False
-                self.res_dev.index_fill_(0, torch.from_numpy(ev.astype(np.int64)).to(self.dev), 0)
-            self.stats["prefill_evicts"] = self.stats.get("prefill_evicts", 0) + len(ev)
-    miss = [int(k) for k in miss]
-    self.fill_many(miss)
-    for k in miss:
-        if hasattr(self, "inflight"):
-            self.inflight[k] = False
-        if hasattr(self, "age"):
-            self.age[k] = self.tick
-        self.transient[k] = True
-    if miss:
-        idx = torch.tensor(miss, dtype=torch.int64).to(self.dev, non_blocking=True)
-        self.res_dev.index_fill_(0, idx, 1)
-    self.stats["prefill_fills"] = self.stats.get("prefill_fills", 0) + len(miss)
-    return len(miss)
-
-
-NvTier.ensure_for_prefill = _ensure_for_prefill
+        return int((pol.ring_seen - seen0) & 0xFFFFFFFF)

@@ -45,5 +45,25 @@ def main():
     print("written")
 
 
+def c4_top8():
+    """Config-4 expert shape (H 4096, I 1536, 128 experts) at top-8, bs=1, for K = 2, 3, 4: the oracle's outputs for
+    seeded inputs that the GPU test regenerates (blobs and activations from synth with seed 5000 + K). The oracle
+    needs about 5 s per expert at this shape, too slow to run inside a GPU test."""
+    H, I, E, topk = 4096, 1536, 128, 8
+    out = {}
+    for K in (2, 3, 4):
+        seed = 5000 + K
+        ids, w = synth.softmax_topk(seed, 1, E, topk)
+        x = synth.activations(seed, 1, H)
+        ews = {int(e): exl3.ExpertWeights(synth.expert_blob(seed, int(e), H, I, K), H, I, K) for e in ids[0]}
+        ob, of = exl3.moe_forward(x, ids, w, ews)
+        out.update({f"ids_{K}": ids, f"w_{K}": w, f"x_{K}": x, f"out_bf16_{K}": ob, f"out_f32_{K}": of})
+        print(f"c4 top-8 K={K} done", flush=True)
+    np.savez_compressed(os.path.join(HERE, "c4_top8.npz"), H=H, I=I, E=E, topk=topk, **out)
+
+
 if __name__ == "__main__":
-    main()
+    if "c4" in sys.argv[1:]:
+        c4_top8()
+    else:
+        main()

@@ -176,7 +176,6 @@ def test_cache_mixed_bitrates(H, I, steps):
         torch.cuda.synchronize()
     finally:
         X.moe_set_decision_log(torch.zeros(0, dtype=torch.int32, device="cuda"))
-        X.moe_set_slot_stride(0)
     lg = logbuf.cpu().numpy()
     assert lg[0] == steps * L
     recs = lg[1:].reshape(steps, L, rl)

@@ -92,3 +92,40 @@ def test_graph_replay_matches_eager(H, I):
     assert np.array_equal(rec_e, rec_g)
     assert [(a.tolist(), e.tolist()) for a, e in tier.decisions] == dec_e
     tier.close()
+
+
+def test_graph_replay_after_exchange_growth():
+    """A graph captured at bs=1 keeps the address of the decode exchange buffer in its kernel arguments. An eager call
+    large enough to grow that buffer afterwards (100 rows x top-10, 1,000 pairs) must leave the captured buffer
+    allocated: replays before and after the growth equal the eager bs=1 output bit for bit."""
+    from exl3xpu.moe_offload import ops
+    from oracle import exl3, synth
+    H, I, K, E, topk = 2048, 512, 3, 16, 10
+    print("case graph replay after exchange growth", flush=True)
+    blobs = torch.from_numpy(np.stack([synth.expert_blob(41, e, H, I, K) for e in range(E)])).cuda()
+    table = torch.tensor([blobs[e].data_ptr() for e in range(E)], dtype=torch.int64, device="cuda")
+    X = ops()
+
+    def inputs(M, seed):
+        ids, w = synth.softmax_topk(seed, M, E, topk)
+        x = torch.from_numpy(exl3.bf16_to_f32(synth.activations(seed, M, H))).to(torch.bfloat16).cuda()
+        return x, torch.from_numpy(ids).cuda(), torch.from_numpy(w).cuda()
+
+    x1, i1, w1 = inputs(1, 42)
+    ref = X.moe_forward(x1, i1, w1, table, I, K, E).clone()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, capture_error_mode="thread_local"):
+        out = X.moe_forward(x1, i1, w1, table, I, K, E)
+    graph.replay()
+    torch.cuda.synchronize()
+    assert torch.equal(out, ref)
+    xb, ib, wb = inputs(100, 43)
+    big = X.moe_forward(xb, ib, wb, table, I, K, E)
+    torch.cuda.synchronize()
+    assert torch.isfinite(big.float()).all()
+    for _ in range(3):
+        out.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref)

@@ -225,7 +225,7 @@ def test_tier_stage_forward_matches_resident():
         torch.cuda.synchronize()
         for n, (o, r) in enumerate(zip(outs, refs)):
             assert torch.equal(o, r), n
-        assert tier._sg["bytes"] == 2 * L * (E - 5) * store.stride     # every non-HBM expert, each pass
+        assert tier.stats["stage_bytes"] == 2 * L * (E - 5) * store.stride     # every non-HBM expert, each pass
     finally:
         tier.close()
 

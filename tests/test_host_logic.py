@@ -87,3 +87,92 @@ def test_admission_rejects_corrupt_snapshots():
     assert adm.tolist() == [5] and ev.size == 0 and dk.size == 0
     assert pol.inflight[5] and pol.stats["masked"] == 2
 
+
+
+@pytest.mark.parametrize("offset", [(1 << 31) - 40, (1 << 32) - 40])
+def test_admission_ring_count_wraps(offset):
+    """The device miss-ring count is kept modulo 2^32 (entry c at position (c mod 2^32) % cap). Feeding the policy
+    the oracle's snapshots with every count shifted by `offset` (crossing INT32_MAX, or 2^32 back to 0, within the
+    first steps) gives the decisions of the unshifted run."""
+    L, E, S, P, R = 6, 32, 40, 5, 256                  # R divides 2^32: a shift moves every entry by offset % R
+    budget, age, qmax, lat, steps = 45, 4, 12, 3, 120
+    ids, w = synth.zipf_trace(300, steps, L, E, P)
+    ids, w = ids[:, :, 0], w[:, :, 0]
+    A = cache.CacheOracle(L, E, S, ring_cap=R, budget=budget, age=age, qmax=qmax, latency=lat)
+    pols = [nvtier.AdmissionPolicy(L * E, [li * E for li in range(L)], budget, age, qmax, R) for _ in range(2)]
+    pols[1].ring_seen = offset
+    snaps, diffs, pending, crossed = [], [None, None], [{}, {}], False
+    for n in range(steps):
+        for li in range(L):
+            A.ensure(li, ids[n, li].copy(), w[n, li].copy())
+        for p in pols:
+            p.tick += 1
+        snaps.append((A.ram_res.copy(), A.ring.copy(), A.slot_of.astype(np.int32)))
+        A.host_step()
+        if len(snaps) < 2:
+            continue
+        view0, ring, slot_of = snaps[-2]
+        shifted = np.empty_like(ring)
+        cnt = (int(ring[0]) + offset) & 0xFFFFFFFF
+        shifted[0] = np.array(cnt, dtype=np.uint32).view(np.int32)
+        shifted[1:] = np.roll(ring[1:], offset % R)
+        crossed |= cnt < offset or cnt >= (1 << 31) > offset      # wrapped to 0, or negative as an int32
+        out = []
+        for i, (p, rg) in enumerate(zip(pols, (ring, shifted))):
+            view = view0.copy()
+            if diffs[i] is not None:
+                view[diffs[i][0]] = diffs[i][1]
+            adm, ev, dk, dv = p.decide(view, rg, slot_of, pending[i].pop(n, []))
+            pending[i].setdefault(n + lat, []).extend(adm.tolist())
+            diffs[i] = (dk, dv) if len(dk) else None
+            out.append((adm.tolist(), ev.tolist(), dk.tolist(), dv.tolist()))
+        assert out[0] == out[1], n
+        assert (pols[1].ring_seen - pols[0].ring_seen) & 0xFFFFFFFF == offset % (1 << 32)
+    assert crossed and pols[0].stats == pols[1].stats and pols[0].stats["masked"] > 40
+
+
+def test_plan_copies_merges_contiguous_runs():
+    """Staging copies: every missing record is covered exactly once, no copy spans a record that is not missing or a
+    gap between host records, and runs are maximal."""
+    rng = np.random.default_rng(7)
+    rec = 4096 * 3
+    for E, stride_gap in [(512, 0), (64, 4096), (33, 0)]:
+        src = (1 << 40) + np.arange(E, dtype=np.int64) * (rec + stride_gap)
+        src[E // 2:] += 8192 * 7                         # a break in host contiguity halfway
+        for _ in range(20):
+            missing = np.sort(rng.choice(E, rng.integers(0, E + 1), replace=False))
+            dst, srcs, nb = moe_offload.plan_copies(1 << 44, rec, src, missing)
+            covered = []
+            for d, s, n in zip(dst, srcs, nb):
+                assert n % rec == 0 and n > 0
+                e0 = (d - (1 << 44)) // rec
+                run = list(range(e0, e0 + n // rec))
+                covered += run
+                assert all(src[e] == s + (e - e0) * rec for e in run)        # host records contiguous along the run
+            assert covered == missing.tolist()
+            # maximal: two consecutive copies are not mergeable
+            for i in range(len(dst) - 1):
+                e_end = (dst[i] - (1 << 44)) // rec + nb[i] // rec
+                assert not (e_end == (dst[i + 1] - (1 << 44)) // rec and srcs[i] + nb[i] == srcs[i + 1])
+
+
+def test_evict_order_matches_sequential_classes():
+    """_evict_order (one lexsort over class, age, key) equals the eviction loop it replaces: classes in order, each
+    by a stable argsort of age over ascending keys, until `over` keys are taken (nvtier.py:414-419)."""
+    rng = np.random.default_rng(11)
+    for _ in range(200):
+        n = int(rng.integers(1, 300))
+        age = rng.integers(0, 6, n)
+        masks = [rng.random(n) < 0.3 for _ in range(3)]
+        masks[1] &= ~masks[0]
+        masks[2] &= ~(masks[0] | masks[1])
+        over = int(rng.integers(0, n + 2))
+        want, left = [], over
+        for m in masks:
+            if left <= 0:
+                break
+            c = np.nonzero(m)[0]
+            c = c[np.argsort(age[c], kind="stable")[:left]]
+            want += c.tolist()
+            left -= len(c)
+        assert nvtier._evict_order(over, masks, age).tolist() == want
