@@ -103,6 +103,24 @@ int exl3_moe_forward_cached(const void* x, int x_dtype, int64_t x_stride, int M,
                             int n_experts, void* out, int64_t out_stride, void* workspace, size_t workspace_bytes,
                             void* stream);
 
+/* The same call without any allocation (no reference counterpart: the reference always passes a workspace that
+ * torch allocates, a8:1229-1261). For callers that cannot allocate device memory: code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc. The decode scratch (the blob pointer of every pick and the
+ * cross-workgroup exchange words) comes from one static device array of EXL3_STATIC_SCRATCH_BYTES per device, held
+ * until the process ends; its address is looked up on the first call on a device and the array is cleared then (one
+ * fill kernel on `stream`). Limit: calls whose scratch exceeds the array (8 MiB: config-0 shapes up to 25 rows x
+ * top-10, config-4 shapes up to 7 rows x top-8) and calls that would take the uncached path (M >= prefill_min_m, or
+ * n_slots == 0) fail with EXL3_EUNSUPPORTED before anything is enqueued. Every call on one device shares the array
+ * and it keeps the last call's contents: calls that overlap on one device (other streams) race; stream-ordered calls
+ * are safe. Decisions and outputs are those of exl3_moe_forward_cached. */
+#define EXL3_STATIC_SCRATCH_BYTES ((size_t)8 << 20)
+int exl3_moe_forward_cached_static(const void* x, int x_dtype, int64_t x_stride, int M, int H, int32_t* topk_ids,
+                                   float* topk_w, int topk, int64_t* ptrs_all, int layer, int32_t* slot_of,
+                                   int32_t* slot_key, int32_t* slot_last, int32_t* tick, int n_slots,
+                                   const int64_t* host_base, int64_t slot_base, int64_t* fill_all, int32_t* fill_list,
+                                   int max_fill, int I, int K, int n_experts, void* out, int64_t out_stride,
+                                   void* stream);
+
 /* moe_prefetch (a8:1194-1222): claim slots for the (predicted) experts `ids` of layer `layer` with the ensure in
  * prefetch mode (launch_ensure a8:846-851: the tick is not advanced, so slots stamped by the last MoE call stay
  * protected; hits re-stamped, misses up to max_fill get exact-LRU slots older than the tick, old owners repointed to

@@ -258,7 +258,8 @@ static int forward_impl(const void* x, int x_dtype, int64_t x_stride, int M, int
                         int topk, const int64_t* ptrs, int I, int K, int E, void* out, int64_t out_stride, void* ws,
                         size_t ws_bytes, hipStream_t st, const int64_t* fill, int64_t* commit_ptrs, int64_t* commit_fill,
                         const int32_t* fill_list, const int64_t* pair_ptr, const VictimArgs* va = nullptr,
-                        int max_victims = 0, const EnsureArgs* fused_ens = nullptr, bool vict_inline = false) {
+                        int max_victims = 0, const EnsureArgs* fused_ens = nullptr, bool vict_inline = false,
+                        uint64_t* xb_given = nullptr) {
     if (!fill && use_prefill(M)) {
         if (H % 256) return fail(EXL3_EUNSUPPORTED, "moe prefill: H %% 256 == 0 required (H=%d)", H);
         if ((int64_t)M * topk > (1 << 28)) return fail(EXL3_EUNSUPPORTED, "moe prefill: %d x %d pairs", M, topk);
@@ -287,9 +288,11 @@ static int forward_impl(const void* x, int x_dtype, int64_t x_stride, int M, int
                     topk, kMaxPairs, kMaxRows);
     const size_t need = decode_workspace_bytes(npairs, H, I);
     if (!ws || ws_bytes < need) return fail(EXL3_EWORKSPACE, "moe_forward: workspace %zu < %zu bytes", ws_bytes, need);
-    uint64_t* xb = nullptr;
-    int rx = exchange_buffer(decode_exchange_words(npairs, H, I), st, &xb);
-    if (rx) return rx;
+    uint64_t* xb = xb_given;                      // the static scratch's exchange words, or the library buffer
+    if (!xb) {
+        const int rx = exchange_buffer(decode_exchange_words(npairs, H, I), st, &xb);
+        if (rx) return rx;
+    }
     DecodeArgs a{};
     a.x = x;
     a.x_dt = x_dtype;
@@ -490,12 +493,15 @@ int exl3_prefetch_worker_stop(int64_t* counts) {
     return EXL3_OK;
 }
 
-int exl3_moe_forward_cached(const void* x, int x_dtype, int64_t x_stride, int M, int H, int32_t* topk_ids,
-                            float* topk_w, int topk, int64_t* ptrs_all, int layer, int32_t* slot_of, int32_t* slot_key,
-                            int32_t* slot_last, int32_t* tick, int n_slots, const int64_t* host_base,
-                            int64_t slot_base, int64_t* fill_all, int32_t* fill_list, int max_fill, int I, int K,
-                            int n_experts, void* out, int64_t out_stride, void* workspace, size_t workspace_bytes,
-                            void* stream) {
+}  // extern "C"
+
+// moe_forward_cached with the decode scratch either from the caller's workspace and the library's exchange buffer
+// (xb == nullptr) or both from the static scratch (xb given: calls that fall back to another path are refused)
+static int cached_impl(const void* x, int x_dtype, int64_t x_stride, int M, int H, int32_t* topk_ids, float* topk_w,
+                       int topk, int64_t* ptrs_all, int layer, int32_t* slot_of, int32_t* slot_key, int32_t* slot_last,
+                       int32_t* tick, int n_slots, const int64_t* host_base, int64_t slot_base, int64_t* fill_all,
+                       int32_t* fill_list, int max_fill, int I, int K, int n_experts, void* out, int64_t out_stride,
+                       void* workspace, size_t workspace_bytes, void* stream, uint64_t* xb) {
     const int E = n_experts;
     if (M < 0 || topk <= 0 || layer < 0) return fail(EXL3_EINVAL, "moe_forward_cached: M=%d topk=%d layer=%d", M, topk, layer);
     if (x_dtype < EXL3_DT_F16 || x_dtype > EXL3_DT_F32) return fail(EXL3_EINVAL, "moe_forward_cached: x dtype");
@@ -504,9 +510,12 @@ int exl3_moe_forward_cached(const void* x, int x_dtype, int64_t x_stride, int M,
     if (M == 0) return EXL3_OK;
     hipStream_t st = (hipStream_t)stream;
     if (!ptrs_all) return fail(EXL3_EINVAL, "moe_forward_cached: null ptrs_all");
-    if (M >= g_cfg.prefill_min_m || n_slots == 0)
+    if (M >= g_cfg.prefill_min_m || n_slots == 0) {
+        if (xb) return fail(EXL3_EUNSUPPORTED, "moe_forward_cached_static: M=%d n_slots=%d takes the uncached path, "
+                            "which needs a workspace (use exl3_moe_forward_cached)", M, n_slots);
         return exl3_moe_forward(x, x_dtype, x_stride, M, H, topk_ids, topk_w, topk, ptrs_all + (int64_t)layer * E, I, K,
                                 E, out, out_stride, workspace, workspace_bytes, stream);
+    }
     if (!slot_of || !slot_key || !slot_last || !tick || !host_base || !fill_all || !fill_list)
         return fail(EXL3_EINVAL, "moe_forward_cached: null cache state");
     const BlobGeom g = blob_geom(H, I, K);
@@ -577,7 +586,79 @@ int exl3_moe_forward_cached(const void* x, int x_dtype, int64_t x_stride, int M,
     int64_t* fl = fill_all + (int64_t)layer * E;
     return forward_impl(x, x_dtype, x_stride, M, H, topk_ids, topk_w, topk, pl, I, K, E, out, out_stride, workspace,
                         workspace_bytes, st, fl, pl, fl, fill_list, ea.pair_ptr, &va, mv, fused ? &ea : nullptr,
-                        vict_inline);
+                        vict_inline, xb);
+}
+
+// ---- the entry point that allocates nothing ------------------------------------------------------------------------
+// Decode scratch in static device memory: the workspace (blob pointer of every pick, 256-aligned) followed by the
+// exchange words. Every device holds its own copy for the life of the process; its address on a device is looked up
+// once (hipGetSymbolAddress, that device current) and kept: host code never uses the array's name as an address.
+constexpr size_t kStaticScratchBytes = EXL3_STATIC_SCRATCH_BYTES;
+static __device__ __align__(256) uint8_t scratch[kStaticScratchBytes];
+static std::mutex g_scratch_mu;
+static uint8_t* g_scratch_ptr[kMaxDevices];
+
+__global__ void zero_fill_kernel(uint4* p, size_t n16) {
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n16; i += (size_t)gridDim.x * blockDim.x)
+        p[i] = make_uint4(0u, 0u, 0u, 0u);
+}
+
+// this device's scratch, set up on first use: its address, then one clear by a kernel on `st` (no memset node if the
+// first call is being captured; the exchange words only need to carry no live tag, which zero never is)
+static int static_scratch(hipStream_t st, uint8_t** out) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+    if (dev < 0 || dev >= kMaxDevices) return fail(EXL3_EUNSUPPORTED, "device %d >= %d", dev, kMaxDevices);
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p) return hip_fail(e, "static scratch: hipGetSymbolAddress");
+        hipLaunchKernelGGL(zero_fill_kernel, dim3(256), dim3(256), 0, st, (uint4*)p, kStaticScratchBytes / 16);
+        if ((e = hipGetLastError()) != hipSuccess) return hip_fail(e, "static scratch: clear");
+        g_scratch_ptr[dev] = (uint8_t*)p;
+    }
+    *out = g_scratch_ptr[dev];
+    return EXL3_OK;
+}
+
+extern "C" {
+
+int exl3_moe_forward_cached(const void* x, int x_dtype, int64_t x_stride, int M, int H, int32_t* topk_ids,
+                            float* topk_w, int topk, int64_t* ptrs_all, int layer, int32_t* slot_of, int32_t* slot_key,
+                            int32_t* slot_last, int32_t* tick, int n_slots, const int64_t* host_base,
+                            int64_t slot_base, int64_t* fill_all, int32_t* fill_list, int max_fill, int I, int K,
+                            int n_experts, void* out, int64_t out_stride, void* workspace, size_t workspace_bytes,
+                            void* stream) {
+    return cached_impl(x, x_dtype, x_stride, M, H, topk_ids, topk_w, topk, ptrs_all, layer, slot_of, slot_key,
+                       slot_last, tick, n_slots, host_base, slot_base, fill_all, fill_list, max_fill, I, K, n_experts,
+                       out, out_stride, workspace, workspace_bytes, stream, nullptr);
+}
+
+int exl3_moe_forward_cached_static(const void* x, int x_dtype, int64_t x_stride, int M, int H, int32_t* topk_ids,
+                                   float* topk_w, int topk, int64_t* ptrs_all, int layer, int32_t* slot_of,
+                                   int32_t* slot_key, int32_t* slot_last, int32_t* tick, int n_slots,
+                                   const int64_t* host_base, int64_t slot_base, int64_t* fill_all, int32_t* fill_list,
+                                   int max_fill, int I, int K, int n_experts, void* out, int64_t out_stride,
+                                   void* stream) {
+    if (M < 0 || topk <= 0 || H <= 0 || I <= 0) return fail(EXL3_EINVAL, "moe_forward_cached_static: M=%d topk=%d", M, topk);
+    if (M == 0)                                   // nothing to do; validated like any call, no scratch needed
+        return cached_impl(x, x_dtype, x_stride, 0, H, topk_ids, topk_w, topk, ptrs_all, layer, slot_of, slot_key,
+                           slot_last, tick, n_slots, host_base, slot_base, fill_all, fill_list, max_fill, I, K,
+                           n_experts, out, out_stride, nullptr, 0, stream, nullptr);
+    if ((int64_t)M * topk > kMaxPairs) return fail(EXL3_EUNSUPPORTED, "moe_forward_cached_static: %d picks > %d", M * topk, kMaxPairs);
+    const size_t ws = decode_workspace_bytes(M * topk, H, I);
+    const size_t need = ws + decode_exchange_words(M * topk, H, I) * 8;
+    if (need > kStaticScratchBytes)
+        return fail(EXL3_EUNSUPPORTED, "moe_forward_cached_static: the call needs %zu bytes of scratch, the static "
+                    "scratch holds %zu (fewer rows, or exl3_moe_forward_cached)", need, kStaticScratchBytes);
+    uint8_t* sp = nullptr;
+    const int r = static_scratch((hipStream_t)stream, &sp);
+    if (r) return r;
+    return cached_impl(x, x_dtype, x_stride, M, H, topk_ids, topk_w, topk, ptrs_all, layer, slot_of, slot_key,
+                       slot_last, tick, n_slots, host_base, slot_base, fill_all, fill_list, max_fill, I, K, n_experts,
+                       out, out_stride, sp, ws, stream, (uint64_t*)(sp + ws));
 }
 
 size_t exl3_moe_align_workspace(int M, int topk, int n_experts) {

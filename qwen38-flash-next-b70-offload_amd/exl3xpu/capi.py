@@ -37,6 +37,9 @@ SIGNATURES = {
     "exl3_moe_forward_cached": (c_i32, [c_p, c_i32, c_i64, c_i32, c_i32, c_p, c_p, c_i32, c_p, c_i32, c_p, c_p, c_p, c_p,
                                         c_i32, c_p, c_i64, c_p, c_p, c_i32, c_i32, c_i32, c_i32, c_p, c_i64, c_p, c_sz,
                                         c_p]),
+    "exl3_moe_forward_cached_static": (c_i32, [c_p, c_i32, c_i64, c_i32, c_i32, c_p, c_p, c_i32, c_p, c_i32, c_p, c_p,
+                                               c_p, c_p, c_i32, c_p, c_i64, c_p, c_p, c_i32, c_i32, c_i32, c_i32, c_p,
+                                               c_i64, c_p]),
     "exl3_moe_prefetch": (c_i32, [c_p, c_i32, c_p, c_i32, c_p, c_p, c_p, c_p, c_i32, c_p, c_i64, c_p, c_p, c_i32, c_i32,
                                   c_i64, c_p]),
     "exl3_moe_prefetch_plan": (c_i32, [c_p, c_i32, c_p, c_i32, c_p, c_p, c_p, c_p, c_i32, c_p, c_i64, c_p, c_p, c_p,
