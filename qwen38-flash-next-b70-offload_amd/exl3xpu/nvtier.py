@@ -90,7 +90,7 @@ class TierStore(ExpertStore):
 
 class SyntheticExpertSource:
     """Seeded stand-in for the expert file: record r holds the blob of synthetic expert r % n_distinct of workload
-    `seed`; read(r, dst) copies it to a host address."""
+    `seed`; read(r, dst, room) copies it to a host address (room: bytes writable at dst, at least the blob)."""
 
     def __init__(self, H, I, K, seed: int, n_distinct: int = 64):  # noqa: E741
         from .synth import expert_blob
@@ -99,7 +99,7 @@ class SyntheticExpertSource:
         self.blob = int(self.buf.shape[1])
         self.rec = self.blob
 
-    def read(self, rec_index: int, dst: int) -> None:
+    def read(self, rec_index: int, dst: int, room: int | None = None) -> None:
         src = self.buf[rec_index % self.n]
         ctypes.memmove(dst, src.ctypes.data, self.blob)
 
@@ -114,8 +114,8 @@ class LayeredExpertSource:
         self.sources, self.E = list(sources), int(E)
         self.blob = max(s.blob for s in self.sources)
 
-    def read(self, rec_index: int, dst: int) -> None:
-        self.sources[rec_index // self.E].read(rec_index, dst)
+    def read(self, rec_index: int, dst: int, room: int | None = None) -> None:
+        self.sources[rec_index // self.E].read(rec_index, dst, room)
 
     def blob_of(self, rec_index: int) -> np.ndarray:
         return self.sources[rec_index // self.E].blob_of(rec_index)
@@ -127,9 +127,10 @@ class ExpertFile:
     record can be read with direct I/O into a 4 KiB-aligned buffer. meta (JSON beside the file, or a dict):
     {"blob", "rec", "layers", "experts", "H", "I", "K"}.
 
-    read(r, dst) reads record r into host memory at dst. With O_DIRECT (default where the file system supports it)
-    the read goes straight into dst when dst is 4 KiB aligned and the kernel can pin it, else through an aligned
-    bounce buffer of this thread; buffered reads otherwise. Only the blob's bytes are written at dst."""
+    read(r, dst, room) reads record r into host memory at dst, where `room` bytes are writable (default: the blob).
+    With O_DIRECT (default where the file system supports it) the whole record goes straight into dst when dst is
+    4 KiB aligned, room holds the record and the kernel can pin the memory; otherwise it goes through an aligned
+    bounce buffer of this thread and only the blob's bytes are written at dst. Buffered reads without O_DIRECT."""
 
     def __init__(self, path: str, meta=None, direct: bool | None = None):
         if meta is None:
@@ -164,9 +165,9 @@ class ExpertFile:
             self._tls.addr = ctypes.addressof(ctypes.c_char.from_buffer(b))
         return b, self._tls.addr
 
-    def read(self, rec_index: int, dst: int) -> None:
+    def read(self, rec_index: int, dst: int, room: int | None = None) -> None:
         off = int(rec_index) * self.rec
-        if self.direct and dst % _REC_ALIGN == 0:
+        if self.direct and dst % _REC_ALIGN == 0 and room is not None and room >= self.rec:
             try:
                 n = os.preadv(self.fd, [(ctypes.c_char * self.rec).from_address(dst)], off)
                 if n == self.rec:
@@ -291,7 +292,7 @@ class NvTier:
         return self._readers
 
     def _read(self, key: int) -> None:
-        self.src.read(self.rec_index(key), self.st.addr(key))
+        self.src.read(self.rec_index(key), self.st.addr(key), self.st.stride)
 
     def _fill(self, key: int) -> None:
         self.fill_many([key])
@@ -440,7 +441,7 @@ class _TierStreamer:
 
         def read(part):
             for e in part.tolist():
-                tier.src.read(tier.rec_index(li * self.E + e), base + e * self.rec)
+                tier.src.read(tier.rec_index(li * self.E + e), base + e * self.rec, self.rec)
         self.pending[li] = (hb, missing, [tier._pool().submit(read, c) for c in chunks if c.size])
 
     def _restart(self, pos: int) -> None:
