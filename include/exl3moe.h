@@ -196,6 +196,32 @@ int exl3_device_status_address(void** dev_ptr);
  * [k_tiles][n_tiles][8K] -> fp16 bits [16 k_tiles][16 n_tiles] (W_inner, Hadamard domain). */
 int exl3_dequant(const uint32_t* trellis, int k_tiles, int n_tiles, int K, uint16_t* out, void* stream);
 
+/* ---- the dense EXL3 linear (exl3xpu_C.linear, experimental/n111-victim-ring/csrc/exl3_ops.sycl:651-757; the
+ * plugin's Exl3XpuLinearMethod.apply, plugin/sglang_plugin.tier.py:380-388) -------------------------------------
+ * out[M, n] = svh * H(sum_k xh[g][m][k] W[k][n]) / sqrt 128 with xh[g] = fp16(H(fp16(x * suh[g])) / sqrt 128), g the
+ * shard of output block n / 128 (shard_of_nb int32 [n/128]), W the mul1 codebook of the checkpoint trellis (int16
+ * [k/16][n/16][16K] read as little-endian uint32 words, natural order); suh fp16 [S][k], svh fp16 [n]; k, n multiples
+ * of 128. Codebook cb = 2 (mul1) with K = 2..6 is implemented, as the reference builds by default. */
+
+/* exl3_supported (exl3_ops.sycl:759-767): 1 when (K, cb) is implemented, else 0 */
+int exl3_linear_supported(int K, int cb);
+/* workspace bytes of exl3_linear_small (xh and the fp32 partial sums over K-slices of 512 rows) */
+size_t exl3_linear_workspace(int M, int k, int n, int S);
+/* the small-M path (exl3_gemm_small, exl3_ops.sycl:560-600): M <= 8 rows, x and out dtype EXL3_DT_* with row
+ * strides; three launches on `stream` (input Hadamards, fused dequant-GEMV into the partials, output Hadamard) */
+int exl3_linear_small(const void* x, int x_dtype, int64_t x_stride, int M, int k, int n, const void* trellis, int K,
+                      int cb, const void* suh, int S, const void* svh, const int32_t* shard_of_nb, void* out,
+                      int out_dtype, int64_t out_stride, void* workspace, size_t workspace_bytes, void* stream);
+/* exl3_had_in_rm (exl3_ops.sycl:602-608): xh fp16 [S][M][k] = fp16(H(fp16(x * suh[g])) / sqrt 128) */
+int exl3_had_in(const void* x, int x_dtype, int64_t x_stride, int M, int k, const void* suh, int S, void* xh,
+                void* stream);
+/* exl3_had_out_h (exl3_ops.sycl:610-616): out[M, n] = svh * H(y) / sqrt 128 for y fp16 [M][n] */
+int exl3_had_out(const void* y, int M, int n, const void* svh, void* out, int out_dtype, int64_t out_stride,
+                 void* stream);
+/* exl3_reconstruct (ReconstructKernel, exl3_esimd.h:869-936): w fp16 [k][n1 - n0] = the codebook weights of
+ * columns [n0, n1) (multiples of 16) of a natural-order trellis of k x n, bit-exact */
+int exl3_reconstruct(const void* trellis, int k, int n, int n0, int n1, int K, int cb, void* w, void* stream);
+
 /* ---- RAM-tier admission (host) ---------------------------------------------------------------------------------- */
 
 /* Books of the admission step besides the per-key arrays; the counters accumulate over calls. */

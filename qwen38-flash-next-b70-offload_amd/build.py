@@ -20,7 +20,7 @@ BUILD = os.path.join(HERE, "_build")
 ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 ARCH = "gfx950"
 
-HIP_SOURCES = ["moe_decode.hip", "moe_cache.hip", "moe_prefill.hip", "moe_capi.hip"]
+HIP_SOURCES = ["moe_decode.hip", "moe_cache.hip", "moe_prefill.hip", "linear.hip", "moe_capi.hip"]
 HOST_SOURCES = ["tier_host.cpp"]          # host-only C++ (g++)
 HIPCC_FLAGS = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}", "-Xclang", "-target-feature", "-Xclang",
                "-packed-fp32-ops", "-Wno-unused-command-line-argument"]

@@ -96,6 +96,13 @@ __device__ __forceinline__ size_t word_off(int r, int tiles_n, int tile, int p, 
     }
 }
 
+// word offset of (tile-row r, tile-col `tile`, period p, plane i) in the checkpoint's natural order: each tile's 8K
+// words in stream order, period p = words [p D, p D + D)
+template <int K>
+__device__ __forceinline__ size_t word_off_nat(int r, int tiles_n, int tile, int p, int i) {
+    return ((size_t)r * tiles_n + tile) * Geo<K>::W + p * Geo<K>::D + i;
+}
+
 // position of value u of period p inside the 16x16 tile
 template <int K>
 __host__ __device__ constexpr int val_row(int p, int u) {

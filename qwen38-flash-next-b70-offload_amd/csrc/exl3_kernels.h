@@ -91,6 +91,34 @@ struct PrefillArgs {
     BlobGeom g;
 };
 
+static inline size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
+
+// the dense EXL3 linear (linear.hip): out[M, n] = svh * H(sum_k xh[shard of n][m][k] W[k][n]) / sqrt 128
+constexpr int kLinMaxRows = 8;       // rows of the fused small-M path
+struct LinearArgs {
+    const void* x; int x_dt; int64_t x_stride;     // activations [M, k]
+    int M, k, n, S;                                // rows, input and output features, shards
+    const uint32_t* tr;                            // trellis words [k/16][n/16][8K], checkpoint (natural) order
+    const _Float16* suh;                           // [S][k]
+    const _Float16* svh;                           // [n]
+    const int32_t* shard_of_nb;                    // [n/128]
+    _Float16* xh;                                  // [S][M][k]
+    float* part;                                   // [P][M][n] partial sums over the K-slices
+    int P;                                         // K-slices (4 blocks of 128 rows each)
+};
+hipError_t launch_linear_had_in(const LinearArgs& a, hipStream_t s);
+hipError_t launch_linear_gemv(int K, const LinearArgs& a, hipStream_t s);   // needs a.xh from launch_linear_had_in
+// out = svh * H(sum of P parts) / sqrt 128; parts fp32 (y_half 0) or one fp16 matrix (y_half 1, P 1)
+hipError_t launch_linear_had_out(const void* parts, int y_half, int P, int M, int n, const _Float16* svh, void* out,
+                                 int out_dt, int64_t out_stride, hipStream_t s);
+// W[k][n1 - n0] fp16 (the codebook's weights) of tile-columns [n0/16, n1/16) of a natural-order trellis
+hipError_t launch_linear_reconstruct(int K, const uint32_t* tr, int k, int n, int n0, int n1, _Float16* w,
+                                     hipStream_t s);
+static inline int linear_kslices(int k) { return (k / 128 + 3) / 4; }
+static inline size_t linear_workspace_bytes(int M, int k, int n, int S) {
+    return align256((size_t)S * M * k * 2) + align256((size_t)linear_kslices(k) * M * n * 4);
+}
+
 // decode.hip
 hipError_t launch_moe_layer(int K, const DecodeArgs& a, hipStream_t s);
 int read_status(int* out, hipStream_t s);
@@ -120,7 +148,6 @@ hipError_t launch_prefill(PrefillArgs a, int E, void* ws, hipStream_t s);
 __host__ __device__ static inline int gu_kslices(int H) { return (H + 1023) / 1024; }
 
 // workspace of a decode call (bytes, 256-aligned parts): the blob pointer of every pick
-static inline size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
 static inline size_t decode_workspace_bytes(int npairs, int H, int I) {
     (void)H;
     (void)I;

@@ -1,0 +1,196 @@
+// The dense EXL3 linear on gfx950: out[M, n] = svh * H(sum_k xh[g(n)][m][k] W[k][n]) / sqrt 128, with
+// xh[g] = fp16(H(fp16(x * suh[g])) / sqrt 128) per shard g and W the mul1 codebook of a trellis in the checkpoint's
+// natural word order (reference: experimental/n111-victim-ring/csrc/exl3_ops.sycl:651-757; HadInKernel /
+// HadOutKernel, exl3_esimd.h:286-343; ReconstructKernel, exl3_esimd.h:869-936).
+//
+// Small M (<= kLinMaxRows): the input Hadamards, then the fused dequant-GEMV: a workgroup of 4 waves takes 4
+// consecutive 128-row blocks of one 64-column group, each wave one 8 x 4-tile block (the MoE gate/up wave GEMV on
+// natural-order words), every codebook value decoded once and multiplied into all M rows on the raw codebook integers
+// (sum w x = c1 sum h x + c2 sum x); the 4 waves are summed in LDS into one fp32 partial per K-slice, and the output
+// kernel sums the slices in order, then the output Hadamard x svh. Large M: the caller reconstructs fp16 W slices
+// (lin_reconstruct_kernel) for a library GEMM and runs the output kernel on its fp16 product.
+#include <hip/hip_runtime.h>
+
+#include "exl3_common.cuh"
+#include "exl3_gemv.cuh"
+#include "exl3_kernels.h"
+
+namespace exl3 {
+
+constexpr int kLinWaves = 4;
+
+// one wave per (shard g, row m, 128-block kb)
+__global__ void __launch_bounds__(256) lin_had_in_kernel(LinearArgs A) {
+    const int wave = blockIdx.x * 4 + (threadIdx.x >> 6), l = lane_id();
+    const int kbn = A.k / 128;
+    if (wave >= A.S * A.M * kbn) return;
+    const int kb = wave % kbn, m = (wave / kbn) % A.M, g = wave / (kbn * A.M);
+    const size_t xo = (size_t)m * A.x_stride + kb * 128 + 2 * l;
+    const half_t* su = A.suh + (size_t)g * A.k + kb * 128 + 2 * l;
+    float v0 = (float)(half_t)(ld_act(A.x, A.x_dt, xo) * (float)su[0]);
+    float v1 = (float)(half_t)(ld_act(A.x, A.x_dt, xo + 1) * (float)su[1]);
+    wave_fwht128(v0, v1);
+    *(half2_t*)(A.xh + ((size_t)g * A.M + m) * A.k + kb * 128 + 2 * l) =
+        half2_t{(half_t)(v0 * kRsqrt128), (half_t)(v1 * kRsqrt128)};
+}
+
+template <int K, int MR>
+__global__ void __launch_bounds__(64 * kLinWaves) lin_gemv_kernel(LinearArgs A) {
+    using GQ = Gemv4<K>;
+    __shared__ half2_t xq[kLinWaves][MR][64];
+    __shared__ float ssw[kLinWaves][MR];
+    __shared__ float red[kLinWaves][MR][64];
+    const int kbn = A.k / 128, P = A.P;
+    const int cg = blockIdx.x / P, ks = blockIdx.x % P;
+    const int wv = threadIdx.x >> 6, l = lane_id();
+    const int kb = ks * kLinWaves + wv;
+    const int g = A.shard_of_nb[cg >> 1];
+    // waves past the end of k add nothing; a shard index outside [0, S) leaves its columns at zero
+    const bool live = kb < kbn && (unsigned)g < (unsigned)A.S;
+    GQ gv;
+    if (live) gv.load_nat(A.tr, A.n / 16, kb * 8, cg * 4);
+#pragma unroll
+    for (int m = 0; m < MR; ++m) {               // the rows' xh of this 128-row block and their sums
+        half2_t v = half2_t{(half_t)0.f, (half_t)0.f};
+        if (live && m < A.M) v = *(const half2_t*)(A.xh + ((size_t)g * A.M + m) * A.k + kb * 128 + 2 * l);
+        xq[wv][m][l] = v;
+        const float s = wave_sum((float)v.x + (float)v.y);
+        if (l == 0) ssw[wv][m] = s;
+    }
+    float acc[MR][GQ::NCQ][2];
+#pragma unroll
+    for (int m = 0; m < MR; ++m)
+#pragma unroll
+        for (int q = 0; q < GQ::NCQ; ++q) acc[m][q][0] = acc[m][q][1] = 0.f;
+    if (live) gv.template compute_mr<MR>(&xq[wv][0][0], acc);     // the wave's own LDS rows: no barrier
+#pragma unroll
+    for (int m = 0; m < MR; ++m)
+#pragma unroll
+        for (int q = 0; q < GQ::NCQ; ++q) {
+            int c0;
+            if (GQ::reduce(acc[m][q], q, c0)) {
+                red[wv][m][c0] = acc[m][q][0];
+                red[wv][m][c0 + 8] = acc[m][q][1];
+            }
+        }
+    __syncthreads();
+    for (int i = threadIdx.x; i < MR * 64; i += 64 * kLinWaves) {
+        const int m = i >> 6, c = i & 63;
+        if (m >= A.M) continue;
+        float t = 0.f, xs = 0.f;                 // the 4 blocks in order
+#pragma unroll
+        for (int w = 0; w < kLinWaves; ++w) {
+            t += red[w][m][c];
+            xs += ssw[w][m];
+        }
+        A.part[((size_t)ks * A.M + m) * A.n + cg * 64 + c] = kC1 * t + kC2 * xs;
+    }
+}
+
+// one wave per (row m, 128-column block nb)
+template <typename TPart>
+__global__ void __launch_bounds__(256) lin_had_out_kernel(const TPart* part, int P, int M, int n, const half_t* svh,
+                                                          void* out, int out_dt, int64_t out_stride) {
+    const int wave = blockIdx.x * 4 + (threadIdx.x >> 6), l = lane_id();
+    const int nbn = n / 128;
+    if (wave >= M * nbn) return;
+    const int nb = wave % nbn, m = wave / nbn;
+    float v0 = 0.f, v1 = 0.f;
+    for (int p = 0; p < P; ++p) {                // the K-slices in order
+        const TPart* q = part + ((size_t)p * M + m) * n + nb * 128 + 2 * l;
+        v0 += (float)q[0];
+        v1 += (float)q[1];
+    }
+    wave_fwht128(v0, v1);
+    const half2_t sv = *(const half2_t*)(svh + nb * 128 + 2 * l);
+    const size_t o = (size_t)m * out_stride + nb * 128 + 2 * l;
+    st_act(out, out_dt, o, v0 * kRsqrt128 * (float)sv.x);
+    st_act(out, out_dt, o + 1, v1 * kRsqrt128 * (float)sv.y);
+}
+
+// one wave per (tile-row, strip of NTW tiles) of tile-columns [t0, t1): W[k][16 (t1 - t0)] fp16, bit-exact
+template <int K>
+__global__ void __launch_bounds__(256) lin_reconstruct_kernel(const uint32_t* __restrict__ tr, int k_tiles,
+                                                              int n_tiles, int t0, int t1, half_t* __restrict__ w) {
+    using GM = Geo<K>;
+    constexpr int G = GM::G, D = GM::D, NTW = GM::NTW;
+    const int nt = t1 - t0, strips = (nt + NTW - 1) / NTW;
+    const int wave = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (wave >= k_tiles * strips) return;
+    const int r = wave / strips, st = wave % strips;
+    const int l = lane_id(), p = l % G, j = l / G;
+    const int tl = st * NTW + j;
+    const bool ok = tl < nt;
+    uint32_t wd[D];
+#pragma unroll
+    for (int i = 0; i < D; ++i) wd[i] = ok ? tr[word_off_nat<K>(r, n_tiles, t0 + tl, p, i)] : 0u;
+    const uint32_t prev = (uint32_t)__shfl((int)wd[D - 1], j * G + ((p + G - 1) % G), 64);
+    if (!ok) return;
+    Period<K> P;
+    P.set(wd, prev);
+    const size_t ld = (size_t)nt * 16;
+    dequant_store<K, 0>(P, p, w + (size_t)r * 16 * ld + (size_t)tl * 16, ld);
+}
+
+// ---- launchers -----------------------------------------------------------------------------------------------------
+
+hipError_t launch_linear_had_in(const LinearArgs& a, hipStream_t s) {
+    const int waves = a.S * a.M * (a.k / 128);
+    hipLaunchKernelGGL(lin_had_in_kernel, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, s, a);
+    return hipGetLastError();
+}
+
+template <int K>
+static hipError_t gemv_rows(const LinearArgs& a, hipStream_t s) {
+    const dim3 grid((unsigned)((a.n / 64) * a.P)), block(64 * kLinWaves);
+    if (a.M <= 1) hipLaunchKernelGGL((lin_gemv_kernel<K, 1>), grid, block, 0, s, a);
+    else if (a.M <= 2) hipLaunchKernelGGL((lin_gemv_kernel<K, 2>), grid, block, 0, s, a);
+    else if (a.M <= 4) hipLaunchKernelGGL((lin_gemv_kernel<K, 4>), grid, block, 0, s, a);
+    else if (a.M <= kLinMaxRows) hipLaunchKernelGGL((lin_gemv_kernel<K, kLinMaxRows>), grid, block, 0, s, a);
+    else return hipErrorInvalidValue;
+    return hipGetLastError();
+}
+
+hipError_t launch_linear_gemv(int K, const LinearArgs& a, hipStream_t s) {
+    switch (K) {
+        case 2: return gemv_rows<2>(a, s);
+        case 3: return gemv_rows<3>(a, s);
+        case 4: return gemv_rows<4>(a, s);
+        case 5: return gemv_rows<5>(a, s);
+        case 6: return gemv_rows<6>(a, s);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+hipError_t launch_linear_had_out(const void* parts, int y_half, int P, int M, int n, const _Float16* svh, void* out,
+                                 int out_dt, int64_t out_stride, hipStream_t s) {
+    const int waves = M * (n / 128);
+    const dim3 grid((unsigned)((waves + 3) / 4));
+    if (y_half)
+        hipLaunchKernelGGL(lin_had_out_kernel<half_t>, grid, dim3(256), 0, s, (const half_t*)parts, P, M, n, svh, out,
+                           out_dt, out_stride);
+    else
+        hipLaunchKernelGGL(lin_had_out_kernel<float>, grid, dim3(256), 0, s, (const float*)parts, P, M, n, svh, out,
+                           out_dt, out_stride);
+    return hipGetLastError();
+}
+
+hipError_t launch_linear_reconstruct(int K, const uint32_t* tr, int k, int n, int n0, int n1, _Float16* w,
+                                     hipStream_t s) {
+    const int k_tiles = k / 16, n_tiles = n / 16, t0 = n0 / 16, t1 = n1 / 16;
+    auto launch = [&](auto kern, int ntw) {
+        const int waves = k_tiles * ((t1 - t0 + ntw - 1) / ntw);
+        hipLaunchKernelGGL(kern, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, s, tr, k_tiles, n_tiles, t0, t1, w);
+    };
+    switch (K) {
+        case 2: launch(lin_reconstruct_kernel<2>, Geo<2>::NTW); break;
+        case 3: launch(lin_reconstruct_kernel<3>, Geo<3>::NTW); break;
+        case 4: launch(lin_reconstruct_kernel<4>, Geo<4>::NTW); break;
+        case 5: launch(lin_reconstruct_kernel<5>, Geo<5>::NTW); break;
+        case 6: launch(lin_reconstruct_kernel<6>, Geo<6>::NTW); break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+}  // namespace exl3

@@ -743,6 +743,97 @@ int exl3_dequant(const uint32_t* trellis, int k_tiles, int n_tiles, int K, uint1
     return EXL3_OK;
 }
 
+// ---- the dense EXL3 linear ---------------------------------------------------------------------------------------
+
+int exl3_linear_supported(int K, int cb) { return cb == 2 && K >= 2 && K <= 6 ? 1 : 0; }
+
+size_t exl3_linear_workspace(int M, int k, int n, int S) {
+    if (M < 0 || k <= 0 || n <= 0 || S <= 0) return 0;
+    return linear_workspace_bytes(M, k, n, S);
+}
+
+static int linear_dims(const char* what, int M, int k, int n, int S) {
+    if (M < 0 || k <= 0 || n <= 0 || S <= 0 || k % 128 || n % 128)
+        return fail(EXL3_EINVAL, "%s: M=%d k=%d n=%d S=%d (k, n multiples of 128)", what, M, k, n, S);
+    return EXL3_OK;
+}
+
+int exl3_linear_small(const void* x, int x_dtype, int64_t x_stride, int M, int k, int n, const void* trellis, int K,
+                      int cb, const void* suh, int S, const void* svh, const int32_t* shard_of_nb, void* out,
+                      int out_dtype, int64_t out_stride, void* workspace, size_t workspace_bytes, void* stream) {
+    if (int r = linear_dims("linear_small", M, k, n, S)) return r;
+    if (!exl3_linear_supported(K, cb)) return fail(EXL3_EUNSUPPORTED, "linear_small: K=%d cb=%d", K, cb);
+    if (M > kLinMaxRows) return fail(EXL3_EUNSUPPORTED, "linear_small: M=%d > %d rows", M, kLinMaxRows);
+    if (x_dtype < EXL3_DT_F16 || x_dtype > EXL3_DT_F32 || out_dtype < EXL3_DT_F16 || out_dtype > EXL3_DT_F32)
+        return fail(EXL3_EINVAL, "linear_small: dtype");
+    if (M == 0) return EXL3_OK;
+    if (!x || !trellis || !suh || !svh || !shard_of_nb || !out) return fail(EXL3_EINVAL, "linear_small: null pointer");
+    if (x_stride < k || out_stride < n) return fail(EXL3_EINVAL, "linear_small: row strides");
+    const size_t need = linear_workspace_bytes(M, k, n, S);
+    if (!workspace || workspace_bytes < need)
+        return fail(EXL3_EWORKSPACE, "linear_small: workspace %zu < %zu bytes", workspace_bytes, need);
+    LinearArgs a{};
+    a.x = x;
+    a.x_dt = x_dtype;
+    a.x_stride = x_stride;
+    a.M = M;
+    a.k = k;
+    a.n = n;
+    a.S = S;
+    a.tr = (const uint32_t*)trellis;
+    a.suh = (const _Float16*)suh;
+    a.svh = (const _Float16*)svh;
+    a.shard_of_nb = shard_of_nb;
+    a.xh = (_Float16*)workspace;
+    a.part = (float*)((uint8_t*)workspace + align256((size_t)S * M * k * 2));
+    a.P = linear_kslices(k);
+    const hipStream_t st = (hipStream_t)stream;
+    hipError_t e = launch_linear_had_in(a, st);
+    if (e == hipSuccess) e = launch_linear_gemv(K, a, st);
+    if (e == hipSuccess) e = launch_linear_had_out(a.part, 0, a.P, M, n, a.svh, out, out_dtype, out_stride, st);
+    return e == hipSuccess ? EXL3_OK : hip_fail(e, "linear_small launch");
+}
+
+int exl3_had_in(const void* x, int x_dtype, int64_t x_stride, int M, int k, const void* suh, int S, void* xh,
+                void* stream) {
+    if (int r = linear_dims("had_in", M, k, 128, S)) return r;
+    if (x_dtype < EXL3_DT_F16 || x_dtype > EXL3_DT_F32) return fail(EXL3_EINVAL, "had_in: x dtype");
+    if (M == 0) return EXL3_OK;
+    if (!x || !suh || !xh || x_stride < k) return fail(EXL3_EINVAL, "had_in: bad arguments");
+    LinearArgs a{};
+    a.x = x;
+    a.x_dt = x_dtype;
+    a.x_stride = x_stride;
+    a.M = M;
+    a.k = k;
+    a.S = S;
+    a.suh = (const _Float16*)suh;
+    a.xh = (_Float16*)xh;
+    const hipError_t e = launch_linear_had_in(a, (hipStream_t)stream);
+    return e == hipSuccess ? EXL3_OK : hip_fail(e, "had_in launch");
+}
+
+int exl3_had_out(const void* y, int M, int n, const void* svh, void* out, int out_dtype, int64_t out_stride,
+                 void* stream) {
+    if (int r = linear_dims("had_out", M, 128, n, 1)) return r;
+    if (out_dtype < EXL3_DT_F16 || out_dtype > EXL3_DT_F32) return fail(EXL3_EINVAL, "had_out: out dtype");
+    if (M == 0) return EXL3_OK;
+    if (!y || !svh || !out || out_stride < n) return fail(EXL3_EINVAL, "had_out: bad arguments");
+    const hipError_t e = launch_linear_had_out(y, 1, 1, M, n, (const _Float16*)svh, out, out_dtype, out_stride,
+                                               (hipStream_t)stream);
+    return e == hipSuccess ? EXL3_OK : hip_fail(e, "had_out launch");
+}
+
+int exl3_reconstruct(const void* trellis, int k, int n, int n0, int n1, int K, int cb, void* w, void* stream) {
+    if (!exl3_linear_supported(K, cb)) return fail(EXL3_EUNSUPPORTED, "reconstruct: K=%d cb=%d", K, cb);
+    if (k <= 0 || n <= 0 || k % 16 || n % 16 || n0 < 0 || n1 > n || n0 >= n1 || n0 % 16 || n1 % 16)
+        return fail(EXL3_EINVAL, "reconstruct: k=%d n=%d columns [%d, %d)", k, n, n0, n1);
+    if (!trellis || !w) return fail(EXL3_EINVAL, "reconstruct: null pointer");
+    const hipError_t e = launch_linear_reconstruct(K, (const uint32_t*)trellis, k, n, n0, n1, (_Float16*)w,
+                                                   (hipStream_t)stream);
+    return e == hipSuccess ? EXL3_OK : hip_fail(e, "reconstruct launch");
+}
+
 void* exl3_host_alloc(int64_t nbytes) {
     void* p = nullptr;
     if (nbytes <= 0) {

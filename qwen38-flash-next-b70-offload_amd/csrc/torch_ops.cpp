@@ -6,6 +6,8 @@
 #include <torch/all.h>
 #include <torch/library.h>
 
+#include <algorithm>
+
 #include "../../include/exl3moe.h"
 
 namespace {
@@ -219,7 +221,135 @@ at::Tensor dequant(at::Tensor trellis, int64_t k_tiles, int64_t n_tiles, int64_t
     return out;
 }
 
+// ---- torch.ops.exl3xpu_C: the dense EXL3 linear (experimental/n111-victim-ring/csrc/exl3_ops.sycl:639-781, 784-815)
+
+void linear_checks(const at::Tensor& trellis, const at::Tensor& suh, const at::Tensor& svh, const at::Tensor& sonb,
+                   int64_t k, int64_t K, int64_t cb) {
+    TORCH_CHECK(exl3_linear_supported((int)K, (int)cb), "exl3xpu_C.linear: K=", K, " cb=", cb, " not built");
+    TORCH_CHECK(trellis.is_cuda() && trellis.is_contiguous() && trellis.dim() == 3 && trellis.size(0) * 16 == k &&
+                    trellis.size(2) == 16 * K,
+                "exl3xpu_C.linear: trellis [k/16, n/16, 16K] contiguous on the device");
+    TORCH_CHECK(suh.scalar_type() == at::kHalf && suh.is_contiguous() && suh.dim() == 2 && suh.size(1) == k,
+                "exl3xpu_C.linear: suh fp16 [S, k]");
+    TORCH_CHECK(svh.scalar_type() == at::kHalf && svh.is_contiguous() && svh.size(0) == trellis.size(1) * 16,
+                "exl3xpu_C.linear: svh fp16 [n]");
+    TORCH_CHECK(sonb.scalar_type() == at::kInt && sonb.is_contiguous() && sonb.numel() * 128 == svh.size(0),
+                "exl3xpu_C.linear: shard_of_nb int32 [n / 128]");
+}
+
+void gemm_small(at::Tensor x2, at::Tensor trellis, at::Tensor suh, at::Tensor svh, at::Tensor shard_of_nb, at::Tensor out,
+                int64_t K, int64_t cb) {
+    const int64_t M = x2.size(0), k = x2.size(1), n = svh.size(0);
+    linear_checks(trellis, suh, svh, shard_of_nb, k, K, cb);
+    TORCH_CHECK(x2.stride(1) == 1 && out.dim() == 2 && out.size(0) == M && out.size(1) == n && out.stride(1) == 1,
+                "exl3_gemm_small: x [M, k], out [M, n] with unit column strides");
+    const size_t ws_bytes = exl3_linear_workspace((int)M, (int)k, (int)n, (int)suh.size(0));
+    auto ws = at::empty({(int64_t)ws_bytes}, x2.options().dtype(at::kByte));
+    check(exl3_linear_small(x2.data_ptr(), dtype_code(x2), x2.stride(0), (int)M, (int)k, (int)n, trellis.data_ptr(),
+                            (int)K, (int)cb, suh.data_ptr(), (int)suh.size(0), svh.data_ptr(),
+                            shard_of_nb.data_ptr<int>(), out.data_ptr(), dtype_code(out), out.stride(0), ws.data_ptr(),
+                            ws_bytes, cur_stream(x2)),
+          "exl3xpu_C.exl3_gemm_small");
+}
+
+void had_in_rm(at::Tensor x, at::Tensor suh, at::Tensor xh) {
+    TORCH_CHECK(x.dim() == 2 && x.stride(1) == 1, "exl3_had_in_rm: x [M, k]");
+    TORCH_CHECK(xh.scalar_type() == at::kHalf && xh.is_contiguous() && xh.dim() == 3 && xh.size(1) == x.size(0) &&
+                    xh.size(2) == x.size(1) && suh.scalar_type() == at::kHalf && suh.dim() == 2 &&
+                    suh.size(0) == xh.size(0) && suh.is_contiguous(),
+                "exl3_had_in_rm: xh fp16 [S, M, k], suh fp16 [S, k]");
+    check(exl3_had_in(x.data_ptr(), dtype_code(x), x.stride(0), (int)x.size(0), (int)x.size(1), suh.data_ptr(),
+                      (int)suh.size(0), xh.data_ptr(), cur_stream(x)),
+          "exl3xpu_C.exl3_had_in_rm");
+}
+
+void had_out_h(at::Tensor y, at::Tensor svh, at::Tensor out) {
+    TORCH_CHECK(y.scalar_type() == at::kHalf && y.is_contiguous() && y.sizes() == out.sizes() && y.dim() == 2 &&
+                    out.stride(1) == 1 && svh.scalar_type() == at::kHalf && svh.numel() == y.size(1),
+                "exl3_had_out_h: y fp16 [M, n] contiguous, out [M, n], svh fp16 [n]");
+    check(exl3_had_out(y.data_ptr(), (int)y.size(0), (int)y.size(1), svh.data_ptr(), out.data_ptr(), dtype_code(out),
+                       out.stride(0), cur_stream(y)),
+          "exl3xpu_C.exl3_had_out_h");
+}
+
+void reconstruct(at::Tensor trellis, at::Tensor w, int64_t n0, int64_t K, int64_t cb) {
+    TORCH_CHECK(trellis.is_cuda() && trellis.is_contiguous() && trellis.dim() == 3, "exl3_reconstruct: trellis");
+    TORCH_CHECK(w.scalar_type() == at::kHalf && w.is_contiguous() && w.dim() == 2 && w.size(0) == trellis.size(0) * 16,
+                "exl3_reconstruct: w fp16 [k, width] contiguous");
+    check(exl3_reconstruct(trellis.data_ptr(), (int)w.size(0), (int)trellis.size(1) * 16, (int)n0,
+                           (int)(n0 + w.size(1)), (int)K, (int)cb, w.data_ptr(), cur_stream(w)),
+          "exl3xpu_C.exl3_reconstruct");
+}
+
+// exl3_linear (exl3_ops.sycl:651-757): M <= small_m_max (at most 8 rows here) -> the fused path; otherwise the input
+// Hadamards, per shard group the reconstructed fp16 weights in slices of slice_n columns times xh[g] (a library
+// GEMM, fp16 output), then the output Hadamard
+at::Tensor linear(at::Tensor x, at::Tensor trellis, at::Tensor suh, at::Tensor svh, at::Tensor shard_of_nb,
+                  at::IntArrayRef group_bounds, int64_t K, int64_t cb, int64_t small_m_max, int64_t slice_n) {
+    auto shape = x.sizes().vec();
+    const int64_t k = shape.back(), n = svh.size(0);
+    auto x2 = x.reshape({-1, k});
+    if (!x2.is_contiguous()) x2 = x2.contiguous();
+    const int64_t M = x2.size(0);
+    shape.back() = n;
+    auto out = at::empty({M, n}, x.options());
+    if (M == 0) return out.view(shape);
+    linear_checks(trellis, suh, svh, shard_of_nb, k, K, cb);
+    if (M <= std::min<int64_t>(small_m_max, 8)) {
+        gemm_small(x2, trellis, suh, svh, shard_of_nb, out, K, cb);
+        return out.view(shape);
+    }
+    const int64_t S = suh.size(0);
+    TORCH_CHECK((int64_t)group_bounds.size() == S + 1 && group_bounds[0] == 0 && group_bounds[S] == n,
+                "exl3xpu_C.linear: group_bounds [0, ..., n] with one group per suh row");
+    auto xh = at::empty({S, M, k}, x.options().dtype(at::kHalf));
+    had_in_rm(x2, suh, xh);
+    auto y = at::empty({M, n}, x.options().dtype(at::kHalf));
+    const int64_t step = slice_n > 0 ? std::max<int64_t>(16, slice_n / 16 * 16) : n;
+    // one reconstructed slice at a time, from the caching allocator (stream-ordered reuse across slices and calls)
+    auto wbuf = at::empty({k * std::min(step, n)}, x.options().dtype(at::kHalf));
+    for (int64_t g = 0; g < S; ++g) {
+        const int64_t g0 = group_bounds[g], g1 = group_bounds[g + 1];
+        TORCH_CHECK(g0 <= g1 && g1 <= n, "exl3xpu_C.linear: group_bounds not ascending");
+        for (int64_t n0 = g0; n0 < g1; n0 += step) {
+            const int64_t n1 = std::min(n0 + step, g1);
+            auto w = wbuf.narrow(0, 0, k * (n1 - n0)).view({k, n1 - n0});
+            reconstruct(trellis, w, n0, K, cb);
+            auto ys = y.narrow(1, n0, n1 - n0);
+            at::matmul_out(ys, xh[g], w);
+        }
+    }
+    had_out_h(y, svh, out);
+    return out.view(shape);
+}
+
+at::Tensor linear_meta(at::Tensor x, at::Tensor trellis, at::Tensor suh, at::Tensor svh, at::Tensor shard_of_nb,
+                       at::IntArrayRef group_bounds, int64_t K, int64_t cb, int64_t small_m_max, int64_t slice_n) {
+    auto shape = x.sizes().vec();
+    shape.back() = svh.size(0);
+    return at::empty(shape, x.options());
+}
+
+bool linear_supported(int64_t K, int64_t cb) { return exl3_linear_supported((int)K, (int)cb) != 0; }
+
 }  // namespace
+
+TORCH_LIBRARY(exl3xpu_C, m) {
+    m.def("linear(Tensor x, Tensor trellis, Tensor suh, Tensor svh, Tensor shard_of_nb, int[] group_bounds, int K, "
+          "int cb, int small_m_max, int slice_n) -> Tensor");
+    m.impl("linear", c10::DispatchKey::CUDA, &linear);
+    m.impl("linear", c10::DispatchKey::Meta, &linear_meta);
+    m.def("exl3_gemm_small(Tensor x, Tensor trellis, Tensor suh, Tensor svh, Tensor shard_of_nb, Tensor(a!) out, "
+          "int K, int cb) -> ()");
+    m.impl("exl3_gemm_small", c10::DispatchKey::CUDA, &gemm_small);
+    m.def("exl3_supported(int K, int cb) -> bool", &linear_supported);
+    m.def("exl3_had_in_rm(Tensor x, Tensor suh, Tensor(a!) xh) -> ()");
+    m.impl("exl3_had_in_rm", c10::DispatchKey::CUDA, &had_in_rm);
+    m.def("exl3_had_out_h(Tensor y, Tensor svh, Tensor(a!) out) -> ()");
+    m.impl("exl3_had_out_h", c10::DispatchKey::CUDA, &had_out_h);
+    m.def("exl3_reconstruct(Tensor trellis, Tensor(a!) w, int n0, int K, int cb) -> ()");
+    m.impl("exl3_reconstruct", c10::DispatchKey::CUDA, &reconstruct);
+}
 
 TORCH_LIBRARY(exl3xpu_moe, m) {
     m.def("moe_forward(Tensor x, Tensor topk_ids, Tensor topk_w, Tensor ptrs, int I, int K, int n_experts) -> Tensor");

@@ -254,7 +254,8 @@ class NvTier:
     def __init__(self, store: TierStore, source, meta=None, ram_budget_bytes=2 << 30, ring_cap=1 << 16, safe=0,
                  dev=None, ckpt_layer=None, budget_records: int | None = None, latency: int = 8):
         self.st, self.E = store, store.E
-        self.src = ExpertFile(source, meta) if isinstance(source, (str, os.PathLike)) else source
+        self._own_src = isinstance(source, (str, os.PathLike))   # a file opened here is closed by close()
+        self.src = ExpertFile(source, meta) if self._own_src else source
         self.ckpt = np.asarray(ckpt_layer if ckpt_layer is not None else range(store.L), dtype=np.int64)
         self.L = int(self.ckpt.size)
         self.dev = torch.device(dev) if dev is not None else store.dev
@@ -275,12 +276,14 @@ class NvTier:
         self._d.attach(store.X, victims=_env_int("EXL3_NVTIER_NO_VICTIM", 0) != 1)
 
     def close(self) -> None:
-        """Detach the tier from the library (no masking, no write-back afterwards) and stop the reader threads. The
-        store's strides are the store's and stay as they are."""
+        """Detach the tier from the library (no masking, no write-back afterwards), stop the reader threads and close
+        an expert file the tier opened from a path. The store's strides are the store's and stay as they are."""
         self._d.detach(self.st.X)
         if self._readers is not None:
             self._readers.shutdown(wait=True)
             self._readers = None
+        if self._own_src:
+            self.src.close()
 
     # ---- records
     def rec_index(self, key: int) -> int:

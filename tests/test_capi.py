@@ -47,3 +47,23 @@ def test_setters():
     assert L.exl3_set_host_stride(0) == 0
     assert L.exl3_set_tier(None, None, 0, None) == 0
     assert L.exl3_set_pair_max_m(4) == 0 and L.exl3_set_prefill_min_m(256) == 0
+
+
+def test_linear_entry_points_validate_without_a_gpu():
+    L = capi.lib()
+    assert [L.exl3_linear_supported(k, 2) for k in range(1, 8)] == [0, 1, 1, 1, 1, 1, 0]
+    assert L.exl3_linear_supported(3, 1) == 0
+    # xh fp16 [S, M, k] + fp32 parts [ceil(k / 512), M, n], each 256-byte aligned
+    assert L.exl3_linear_workspace(1, 2048, 4096, 1) == 4096 + 4 * 4096 * 4
+    assert L.exl3_linear_workspace(8, 2048, 4608, 3) == 3 * 8 * 2048 * 2 + 4 * 8 * 4608 * 4
+    assert L.exl3_linear_small(None, 0, 0, 1, 100, 256, None, 3, 2, None, 1, None, None, None, 0, 0, None, 0,
+                               None) == 1                       # k not a multiple of 128
+    assert L.exl3_linear_small(None, 0, 0, 9, 128, 256, None, 3, 2, None, 1, None, None, None, 0, 0, None, 0,
+                               None) == 2                       # more rows than the fused path takes
+    assert L.exl3_linear_small(None, 0, 0, 1, 128, 256, None, 7, 2, None, 1, None, None, None, 0, 0, None, 0,
+                               None) == 2                       # K outside 2..6
+    assert L.exl3_linear_small(None, 0, 0, 0, 128, 256, None, 3, 2, None, 1, None, None, None, 0, 0, None, 0,
+                               None) == 0                       # no rows: nothing to do
+    assert L.exl3_reconstruct(None, 128, 256, 16, 8, 3, 2, None, None) == 1
+    assert L.exl3_had_in(None, 0, 0, 0, 256, None, 1, None, None) == 0
+    assert L.exl3_had_out(None, 1, 100, None, None, 0, 100, None) == 1

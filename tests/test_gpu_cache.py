@@ -480,3 +480,39 @@ def test_cache_copy_prefetch():
     for s in np.nonzero(sk >= 0)[0]:
         assert np.array_equal(slots[s, :src.blob], src.buf[sk[s] % nd]), f"slot {s}"
     assert bad == 0
+
+
+def test_tier_fills_from_expert_file(tmp_path):
+    """The RAM tier filled from a packed expert file (write_expert_file, read back through ExpertFile: O_DIRECT where
+    the file system allows it) instead of the seeded source: the same trace as test_cache_multirow_tier, with every
+    device record and host decision equal to the oracle's and every output equal to the plain forward on the true
+    blobs."""
+    from exl3xpu import nvtier
+    L, E, S, M, TK, steps, H, I, K = 6, 128, 150, 4, 10, 60, 128, 128, 3
+    ids, w = synth.zipf_trace(20261203, steps, L, E, TK, M=M)
+    ids = np.ascontiguousarray(ids.reshape(steps, L, M * TK))
+    w = np.ascontiguousarray(w.reshape(steps, L, M * TK))
+    co = cache.CacheOracle(L, E, S, ring_cap=1 << 12, budget=160, age=4, qmax=64, latency=3)
+    orecs, olog = co.run(ids, w)
+    src = nvtier.SyntheticExpertSource(H, I, K, 11, n_distinct=16)
+    path = str(tmp_path / "experts.bin")
+    nvtier.write_expert_file(path, src, L, E, H, I, K)
+    store = nvtier.TierStore(H, I, K, E, S, n_layers=L)
+    for li in range(L):
+        store.add_layer(f"model.layers.{li}.mlp")
+    tier = nvtier.NvTierAsync(store, path, ring_cap=1 << 12, budget_records=160, latency=3)
+    tier.policy.admit_age, tier.policy.admit_qmax = 4, 64
+    tier.log_decisions = True
+    print(f"case tier fills from expert file (direct I/O {tier.src.direct})", flush=True)
+    blobs = torch.from_numpy(src.buf).cuda()
+    ref_ptr = torch.tensor([blobs[r % src.n].data_ptr() for r in range(L * E)], dtype=torch.int64, device="cuda")
+    try:
+        recs, bad = _run(store, tier, ids, w, H, check_out_every=1, ref_ptr=ref_ptr, M=M)
+    finally:
+        tier.close()
+    mism = np.nonzero((recs != orecs).any(axis=-1))
+    assert mism[0].size == 0, f"first mismatch at step/layer {mism[0][0]}/{mism[1][0]}"
+    for n, ((a1, e1), (a2, e2)) in enumerate(zip(tier.decisions, olog)):
+        assert a1.tolist() == a2.tolist() and e1.tolist() == e2.tolist(), n
+    assert bad == 0
+    assert tier.src.reads > 0 and recs[:, :, 2 + M * TK].sum() > 0

@@ -1,0 +1,145 @@
+"""GPU parity of the dense EXL3 linear (torch.ops.exl3xpu_C.linear and its C-ABI) against oracle/linear.py.
+
+Outputs: rel-L2 <= 2e-3 after the same final rounding to the output dtype on both sides; the large-M path is compared
+with the oracle's "large" variant (the fp16 GEMM output rounded before the output Hadamard). The reconstructed
+weights are bit-exact."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import exl3, linear as olin, synth
+
+pytestmark = pytest.mark.gpu
+TOL = 2e-3
+
+
+def _rel(a, b):
+    a = np.asarray(a, np.float64)
+    b = np.asarray(b, np.float64)
+    return float(np.linalg.norm(a - b) / np.linalg.norm(b))
+
+
+def _group(ck):
+    from exl3xpu.linear import FusedGroup
+    tr = torch.from_numpy(ck["trellis"])
+    b = ck["bounds"]
+    shards = [(tr[:, b[g] // 16:b[g + 1] // 16].contiguous(), torch.from_numpy(ck["suh"][g]),
+               torch.from_numpy(ck["svh"][b[g]:b[g + 1]])) for g in range(len(b) - 1)]
+    return FusedGroup(shards, "cuda")
+
+
+def _x(seed, M, k, dtype):
+    xf = exl3.bf16_to_f32(synth.activations(seed, M, k))
+    if dtype == torch.float16:
+        xf = xf.astype(np.float16).astype(np.float32)
+    return xf, torch.from_numpy(xf).to("cuda", dtype)
+
+
+def _round(ref, dtype):
+    return torch.from_numpy(ref.astype(np.float32)).to(dtype).float().numpy()
+
+
+@pytest.mark.parametrize("K", [2, 3, 4, 5, 6])
+@pytest.mark.parametrize("M", [1, 2, 3, 8])
+def test_linear_small_vs_oracle(K, M):
+    print(f"case linear small K={K} M={M}", flush=True)
+    ck = olin.checkpoint(100 + K, 512, [256, 128, 128], K)         # three shards of one fused q/k/v-style group
+    g = _group(ck)
+    for dtype in (torch.bfloat16, torch.float16):
+        xf, x = _x(7 * M + K, M, 512, dtype)
+        y = g(x)
+        torch.cuda.synchronize()
+        assert y.dtype == dtype and tuple(y.shape) == (M, 512)
+        r = _rel(y.float().cpu().numpy(), _round(olin.linear(xf, ck, "small"), dtype))
+        assert r < TOL, (dtype, r)
+
+
+@pytest.mark.parametrize("K,M,slice_n", [(3, 9, 4096), (3, 300, 128), (4, 64, 192), (2, 33, 0), (6, 17, 256)])
+def test_linear_large_vs_oracle(K, M, slice_n):
+    """Above 8 rows: the input Hadamards, reconstructed fp16 weight slices (slice_n columns, 0 = whole groups) times xh
+    of each shard group in the library GEMM, then the output Hadamard."""
+    print(f"case linear large K={K} M={M} slice={slice_n}", flush=True)
+    ck = olin.checkpoint(200 + K, 384, [256, 384, 128], K)
+    g = _group(ck)
+    xf, x = _x(11 + M, M, 384, torch.bfloat16)
+    y = g(x, slice_n=slice_n)
+    torch.cuda.synchronize()
+    r = _rel(y.float().cpu().numpy(), _round(olin.linear(xf, ck, "large"), torch.bfloat16))
+    assert r < TOL, r
+
+
+def test_linear_small_threshold_and_shapes():
+    """small_m_max picks the path (both agree with the oracle), batch dimensions are kept, bias is added, M = 0 is an
+    empty result."""
+    ck = olin.checkpoint(31, 256, [256], 3)
+    g = _group(ck)
+    xf, x = _x(5, 6, 256, torch.float16)
+    ref = olin.linear(xf, ck, "small")
+    y_small = g(x.view(2, 3, 256), small_m_max=8)
+    y_large = g(x.view(2, 3, 256), small_m_max=1)
+    bias = torch.full((256,), 0.5, device="cuda", dtype=torch.float16)
+    y_bias = g(x, bias=bias)
+    torch.cuda.synchronize()
+    assert tuple(y_small.shape) == (2, 3, 256)
+    assert _rel(y_small.reshape(6, 256).float().cpu().numpy(), _round(ref, torch.float16)) < TOL
+    assert _rel(y_large.reshape(6, 256).float().cpu().numpy(), _round(olin.linear(xf, ck, "large"), torch.float16)) < TOL
+    assert torch.allclose(y_bias.float(), y_small.reshape(6, 256).float() + 0.5, atol=2e-3)
+    assert tuple(g(x[:0]).shape) == (0, 256)
+
+
+@pytest.mark.parametrize("K", [2, 3, 5])
+def test_reconstruct_bitexact(K):
+    """exl3_reconstruct of a column range == the oracle's decode of the same tiles, bit for bit."""
+    from exl3xpu.linear import C
+    print(f"case reconstruct K={K}", flush=True)
+    ck = olin.checkpoint(300 + K, 256, [512], K)
+    ref = olin.weight(ck["trellis"], K).view(np.uint16)
+    tr = torch.from_numpy(ck["trellis"]).cuda()
+    for n0, n1 in ((0, 512), (16, 48), (128, 400)):
+        w = torch.empty((256, n1 - n0), dtype=torch.float16, device="cuda")
+        C().exl3_reconstruct(tr, w, n0, K, 2)
+        torch.cuda.synchronize()
+        assert np.array_equal(w.cpu().numpy().view(np.uint16), ref[:, n0:n1]), (n0, n1)
+
+
+def test_had_in_had_out_vs_oracle():
+    """exl3_had_in_rm: xh within one fp16 ulp of the oracle (butterfly order aside, equal almost everywhere);
+    exl3_had_out_h: svh * H(y) / sqrt 128 within fp32 rounding."""
+    from exl3xpu.linear import C
+    ck = olin.checkpoint(41, 256, [128, 128], 3)
+    xf, x = _x(3, 5, 256, torch.bfloat16)
+    ref = olin.had_in(xf, ck["suh"])
+    xh = torch.empty((2, 5, 256), dtype=torch.float16, device="cuda")
+    C().exl3_had_in_rm(x, torch.from_numpy(ck["suh"]).cuda(), xh)
+    y = torch.from_numpy(np.random.default_rng(2).standard_normal((5, 256)).astype(np.float16)).cuda()
+    out = torch.empty((5, 256), dtype=torch.float32, device="cuda")
+    C().exl3_had_out_h(y, torch.from_numpy(ck["svh"]).cuda(), out)
+    torch.cuda.synchronize()
+    got = xh.cpu().numpy()
+    assert np.mean(got == ref) > 0.99
+    assert np.max(np.abs(got.astype(np.float32) - ref.astype(np.float32))) <= np.max(np.abs(ref)) * 2.0 ** -10
+    want = exl3.had_blocks(y.cpu().numpy().astype(np.float32)) * exl3.RSQRT128 * ck["svh"].astype(np.float32)
+    assert np.allclose(out.cpu().numpy(), want, rtol=1e-5, atol=1e-6)
+
+
+def test_linear_small_capi_fp32_out():
+    """exl3_linear_small through the C-ABI: fp32 output with a row stride, the caller's workspace."""
+    from exl3xpu import capi
+    L = capi.lib()
+    ck = olin.checkpoint(51, 1024, [512, 256], 4)
+    M, k, n, S = 4, 1024, 768, 2
+    xf, x = _x(8, M, k, torch.bfloat16)
+    tr = torch.from_numpy(ck["trellis"]).cuda()
+    suh = torch.from_numpy(ck["suh"]).cuda()
+    svh = torch.from_numpy(ck["svh"]).cuda()
+    sonb = torch.from_numpy(ck["shard_of_nb"]).cuda()
+    out = torch.zeros((M, n + 64), dtype=torch.float32, device="cuda")
+    ws_bytes = L.exl3_linear_workspace(M, k, n, S)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device="cuda")
+    capi.check(L.exl3_linear_small(x.data_ptr(), 1, k, M, k, n, tr.data_ptr(), 4, 2, suh.data_ptr(), S,
+                                   svh.data_ptr(), sonb.data_ptr(), out.data_ptr(), 2, n + 64, ws.data_ptr(),
+                                   ws_bytes, capi.stream_handle()), "linear_small")
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    assert _rel(got[:, :n], olin.linear(xf, ck, "small")) < TOL
+    assert not got[:, n:].any()                                   # nothing written past n in the padded rows
