@@ -158,6 +158,112 @@ def run_prefill(args, dev):
     print(json.dumps(out), flush=True)
 
 
+# the dense projections of one decoder layer as fused groups (input size k, output widths of the shards)
+LINEAR_GROUPS = ((2048, (2048, 2048, 4096, 4096)), (4096, (2048,)), (2048, (512, 512)), (512, (2048,)))
+LINEAR_PREFILL_M = 1024
+
+
+def run_linear(args, dev):
+    """Dense-linear leg: torch.ops.exl3xpu_C.linear over the dense projections of 48 decoder layers (per layer the fused
+    groups 2048 -> 12,288 of 4 shards, 4096 -> 2048, 2048 -> 1024 of 2 shards and 512 -> 2048; EXL3 K=3, seeded random
+    trellis, bs=1 bf16 activations): 192 calls per token captured in one HIP graph and timed with HIP events around its
+    replays. value = tokens per second of those calls; roofline = trellis bytes per token / time per token against the
+    8 TB/s HBM peak (each call's three kernels included). The same groups at 1,024 rows (the reconstruct + fp16 GEMM
+    path) give the prefill figure. cpu_baseline: oracle/cpu_path.CpuLinear (decode through the codebook table on every
+    call, fp32 matmuls) on one layer's groups at bs=1 on this host's cores, x 48 layers."""
+    import numpy as np
+    import torch
+    from exl3xpu.linear import FusedGroup
+
+    g = torch.Generator(device=dev).manual_seed(SEED + 7)
+    sign = lambda n, scale: (torch.where(torch.rand(n, device=dev, generator=g) < 0.5, -1.0, 1.0) * scale).half()
+    layers = []
+    for _ in range(L):
+        grp = []
+        for k, widths in LINEAR_GROUPS:
+            shards = [(torch.randint(-32768, 32768, (k // 16, w // 16, 16 * K), dtype=torch.int16, device=dev,
+                                     generator=g), sign(k, 1.0), sign(w, 0.02)) for w in widths]
+            grp.append(FusedGroup(shards, dev))
+        layers.append(grp)
+    tr_bytes = sum(fg.trellis.numel() * 2 for fg in layers[0]) * L
+    bs = args.bs
+    xin = [torch.randn(bs, k, device=dev, generator=g).to(torch.bfloat16) for k, _ in LINEAR_GROUPS]
+
+    def token():
+        for grp in layers:
+            for fg, x in zip(grp, xin):
+                fg(x)
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(3):
+            token()
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        token()
+    steps, warm = max(1, min(args.steps, 200)), max(1, args.warmup)
+    for _ in range(warm):
+        graph.replay()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    ev0.record()
+    for _ in range(steps):
+        graph.replay()
+    ev1.record()
+    torch.cuda.synchronize()
+    t_tok = ev0.elapsed_time(ev1) / steps * 1e-3
+    gbs = tr_bytes / t_tok / 1e9
+
+    # the large-M path: one layer's groups at 1,024 rows, eager
+    Mp = LINEAR_PREFILL_M
+    xp = [torch.randn(Mp, k, device=dev, generator=g).to(torch.bfloat16) for k, _ in LINEAR_GROUPS]
+    flops = sum(2.0 * Mp * fg.k * fg.n for fg in layers[0])
+
+    def prefill_layer(li):
+        for fg, x in zip(layers[li], xp):
+            fg(x)
+    for li in range(3):
+        prefill_layer(li)
+    torch.cuda.synchronize()
+    ev0.record()
+    for li in range(L):
+        prefill_layer(li)
+    ev1.record()
+    torch.cuda.synchronize()
+    t_pf = ev0.elapsed_time(ev1) / L * 1e-3
+    out = {
+        "metric": "dense EXL3 linear decode tok/s bs=1 (48 layers of fused projections, EXL3 3bpw); % of HBM peak",
+        "value": round(1.0 / t_tok, 1), "unit": "tok/s", "n_gpus": 1, "steps": steps, "warmup": warm,
+        "ms_per_step": round(t_tok * 1e3, 4), "higher_is_better": True, "dtype": "bf16 in/out, fp32 accumulate",
+        "data": "synthetic", "vs_baseline": None,
+        "config": {"workload": "dense projections of one decode token through 48 layers: per layer 2048->12288 (4 "
+                               "shards), 4096->2048, 2048->1024 (2 shards), 512->2048; EXL3 K=3; bs=%d" % bs,
+                   "calls_per_token": L * len(LINEAR_GROUPS), "trellis_bytes_per_token": tr_bytes},
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK, 4), "traffic": None},
+        "prefill_1024_rows": {"ms_per_layer": round(t_pf * 1e3, 4), "tflops": round(flops / t_pf / 1e12, 1),
+                              "frac_fp16_mfma": round(flops / t_pf / 1e12 / MFMA_PEAK_F16, 4)},
+    }
+    log(f"dense linear: {t_tok * 1e6:.1f} us per token ({t_tok * 1e6 / (L * len(LINEAR_GROUPS)):.2f} us per call), "
+        f"{gbs:.0f} GB/s of trellis ({gbs / HBM_PEAK * 100:.1f} % of HBM peak); 1,024 rows: {t_pf * 1e3:.3f} ms per "
+        f"layer = {flops / t_pf / 1e12:.0f} TFLOP/s")
+    if not args.no_cpu_baseline:
+        from oracle import cpu_path
+        n = len(os.sched_getaffinity(0))
+        torch.set_num_threads(n)
+        cl = cpu_path.CpuLinear(K)
+        cpu_groups = [(fg.trellis.cpu(), fg.suh.cpu(), fg.svh.cpu(), fg.bounds) for fg in layers[0]]
+        xc = [x.float().cpu() for x in xin]
+        t_cpu = _median_s(lambda: [cl(x, *gr) for gr, x in zip(cpu_groups, xc)], 1, 3)
+        out["cpu_baseline"] = {"value": round(1.0 / (L * t_cpu), 3), "unit": "tok/s", "cores": n, "kind": "port",
+                               "sample": f"one layer's four groups at bs={bs} (trellis decode through the codebook "
+                                         f"table + fp32 matmuls, torch on {n} threads), median of 3 after 1 warm-up = "
+                                         f"{t_cpu:.3f} s, x 48 layers"}
+    print(json.dumps(out), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -172,6 +278,7 @@ def main():
     ap.add_argument("--budget-records", type=int, default=BUDGET)
     ap.add_argument("--eager", action="store_true", help="launch the 48 layer calls eagerly instead of a HIP graph")
     ap.add_argument("--prefill", action="store_true", help="the prefill leg (8,192-token chunk, staged) instead of decode")
+    ap.add_argument("--linear", action="store_true", help="the dense EXL3 linear leg instead of MoE decode")
     ap.add_argument("--prefill-staged", action="store_true", help="(disabled) the staged prefill variant")
     ap.add_argument("--roofline-only", action="store_true",
                     help="counter runs: only the HBM-resident layer calls, after 3 device copies of 256 MiB (the "
@@ -192,6 +299,8 @@ def main():
     torch.cuda.set_device(dev)
     if args.prefill:
         return run_prefill(args, dev)
+    if args.linear:
+        return run_linear(args, dev)
     t0 = time.perf_counter()
     store = nvtier.TierStore(H, I, K, E, SLOTS, n_layers=L, device=dev)
     keys = [f"model.layers.{li}.mlp" for li in range(L)]

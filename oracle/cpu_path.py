@@ -39,10 +39,10 @@ class CpuExperts:
             h = np.block([[h, h], [h, -h]])
         return h
 
-    def _decode(self, words_planar: torch.Tensor, kt: int, nt: int) -> torch.Tensor:
+    def _decode(self, words_planar: torch.Tensor, kt: int, nt: int, planar: bool = True) -> torch.Tensor:
         K, D, G = self.K, self.D, self.G
         w = words_planar.view(kt, nt, 8 * K).to(torch.int64) & 0xFFFFFFFF
-        if D > 1:      # PLANAR4 -> natural: [row, group, plane, tile, g] -> [row, tile, g, plane]
+        if planar and D > 1:      # PLANAR4 -> natural: [row, group, plane, tile, g] -> [row, tile, g, plane]
             w = w.view(kt, nt // 4, D, 4, G).permute(0, 1, 3, 4, 2).reshape(kt, nt, 8 * K)
         B = w[..., self.i1]
         A = w[..., self.i0]
@@ -86,3 +86,23 @@ class CpuExperts:
             for k in range(len(ids[m])):
                 out[m] += self.pair(x[m], blobs[int(ids[m][k])], float(w[m][k]))
         return out.to(torch.bfloat16)
+
+
+class CpuLinear(CpuExperts):
+    """The dense EXL3 linear (experimental/n111-victim-ring/csrc/exl3_ops.sycl:651-757) on the CPU: the checkpoint
+    trellis (natural word order) decoded through the codebook table on every call, then the input Hadamards per shard,
+    fp32 matmuls of each shard's columns, and the output Hadamard x svh."""
+
+    def __init__(self, K):
+        super().__init__(128, 128, K)
+
+    def __call__(self, x: torch.Tensor, trellis: torch.Tensor, suh: torch.Tensor, svh: torch.Tensor, bounds):
+        """x fp32 [M, k]; trellis int16 [k/16, n/16, 16K]; suh fp16 [S, k]; svh fp16 [n]; bounds [0, ..., n]."""
+        kt, nt = trellis.shape[:2]
+        W = self._decode(trellis.contiguous().view(torch.int32), kt, nt, planar=False)
+        r = float(exl3.RSQRT128)
+        y = torch.empty(x.shape[0], nt * 16)
+        for g in range(len(bounds) - 1):
+            xh = (self.had((x * suh[g].float()).half().float()) * r).half().float()
+            y[:, bounds[g]:bounds[g + 1]] = xh @ W[:, bounds[g]:bounds[g + 1]]
+        return self.had(y) * r * svh.float()

@@ -102,12 +102,14 @@ struct LinearArgs {
     const _Float16* suh;                           // [S][k]
     const _Float16* svh;                           // [n]
     const int32_t* shard_of_nb;                    // [n/128]
-    _Float16* xh;                                  // [S][M][k]
+    _Float16* xh;                                  // [S][M][k] (the large-M path's input Hadamards)
     float* part;                                   // [P][M][n] partial sums over the K-slices
+    int* cnt;                                      // [n/128] arrival counters: zero on entry, left zero
     int P;                                         // K-slices (4 blocks of 128 rows each)
 };
 hipError_t launch_linear_had_in(const LinearArgs& a, hipStream_t s);
-hipError_t launch_linear_gemv(int K, const LinearArgs& a, hipStream_t s);   // needs a.xh from launch_linear_had_in
+// the fused small-M linear (M <= kLinMaxRows): input Hadamards, dequant-GEMV and output Hadamard in one launch
+hipError_t launch_linear_small(int K, const LinearArgs& a, void* out, int out_dt, int64_t out_stride, hipStream_t s);
 // out = svh * H(sum of P parts) / sqrt 128; parts fp32 (y_half 0) or one fp16 matrix (y_half 1, P 1)
 hipError_t launch_linear_had_out(const void* parts, int y_half, int P, int M, int n, const _Float16* svh, void* out,
                                  int out_dt, int64_t out_stride, hipStream_t s);
@@ -115,8 +117,10 @@ hipError_t launch_linear_had_out(const void* parts, int y_half, int P, int M, in
 hipError_t launch_linear_reconstruct(int K, const uint32_t* tr, int k, int n, int n0, int n1, _Float16* w,
                                      hipStream_t s);
 static inline int linear_kslices(int k) { return (k / 128 + 3) / 4; }
-static inline size_t linear_workspace_bytes(int M, int k, int n, int S) {
-    return align256((size_t)S * M * k * 2) + align256((size_t)linear_kslices(k) * M * n * 4);
+// small-M workspace: the arrival counters [n/128] int32, then the partial sums [P][M][n] fp32
+static inline size_t linear_counter_bytes(int n) { return align256((size_t)(n / 128) * 4); }
+static inline size_t linear_workspace_bytes(int M, int k, int n) {
+    return linear_counter_bytes(n) + align256((size_t)linear_kslices(k) * M * n * 4);
 }
 
 // decode.hip

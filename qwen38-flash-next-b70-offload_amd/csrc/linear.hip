@@ -3,12 +3,13 @@
 // natural word order (reference: experimental/n111-victim-ring/csrc/exl3_ops.sycl:651-757; HadInKernel /
 // HadOutKernel, exl3_esimd.h:286-343; ReconstructKernel, exl3_esimd.h:869-936).
 //
-// Small M (<= kLinMaxRows): the input Hadamards, then the fused dequant-GEMV: a workgroup of 4 waves takes 4
-// consecutive 128-row blocks of one 64-column group, each wave one 8 x 4-tile block (the MoE gate/up wave GEMV on
-// natural-order words), every codebook value decoded once and multiplied into all M rows on the raw codebook integers
-// (sum w x = c1 sum h x + c2 sum x); the 4 waves are summed in LDS into one fp32 partial per K-slice, and the output
-// kernel sums the slices in order, then the output Hadamard x svh. Large M: the caller reconstructs fp16 W slices
-// (lin_reconstruct_kernel) for a library GEMM and runs the output kernel on its fp16 product.
+// Small M (<= kLinMaxRows), one launch: a workgroup of 4 waves takes 4 consecutive 128-row blocks of one 64-column
+// group; each wave computes the input Hadamards of its own block for every row in registers, then runs the 8 x 4-tile
+// dequant-GEMV (the MoE gate/up wave GEMV on natural-order words), every codebook value decoded once and multiplied
+// into all M rows on the raw codebook integers (sum w x = c1 sum h x + c2 sum x). The 4 waves are summed in LDS into
+// one fp32 partial per K-slice; the last of the 2P workgroups of a 128-column block to arrive (an atomic counter that
+// it resets) sums the P partials in slice order and applies the output Hadamard x svh. Large M: the input-Hadamard
+// kernel, fp16 W slices (lin_reconstruct_kernel) for a library GEMM, then the output kernel on its fp16 product.
 #include <hip/hip_runtime.h>
 
 #include "exl3_common.cuh"
@@ -34,25 +35,65 @@ __global__ void __launch_bounds__(256) lin_had_in_kernel(LinearArgs A) {
         half2_t{(half_t)(v0 * kRsqrt128), (half_t)(v1 * kRsqrt128)};
 }
 
+// s0, s1 = sum over i < n, in index order, of the float pair at p + i * stride (8-byte aligned); agent-scope loads,
+// 16 pairs per round trip
+__device__ __forceinline__ void sum2_agent(const float* p, int n, size_t stride, float& s0, float& s1) {
+    s0 = s1 = 0.f;
+    for (int i = 0; i < n; i += 16) {
+        uint64_t v[16];
+#pragma unroll
+        for (int j = 0; j < 16; ++j)
+            v[j] = i + j < n ? __hip_atomic_load((const uint64_t*)(p + (size_t)(i + j) * stride), __ATOMIC_RELAXED,
+                                                 __HIP_MEMORY_SCOPE_AGENT)
+                             : 0u;
+#pragma unroll
+        for (int j = 0; j < 16; ++j)
+            if (i + j < n) {
+                s0 += __uint_as_float((uint32_t)v[j]);
+                s1 += __uint_as_float((uint32_t)(v[j] >> 32));
+            }
+    }
+}
+
 template <int K, int MR>
-__global__ void __launch_bounds__(64 * kLinWaves) lin_gemv_kernel(LinearArgs A) {
+__global__ void __launch_bounds__(64 * kLinWaves) lin_small_kernel(LinearArgs A, void* out, int out_dt,
+                                                                  int64_t out_stride) {
     using GQ = Gemv4<K>;
     __shared__ half2_t xq[kLinWaves][MR][64];
     __shared__ float ssw[kLinWaves][MR];
     __shared__ float red[kLinWaves][MR][64];
+    __shared__ int last;
     const int kbn = A.k / 128, P = A.P;
-    const int cg = blockIdx.x / P, ks = blockIdx.x % P;
+    const int cg = blockIdx.x / P, ks = blockIdx.x % P, nb = cg >> 1;
     const int wv = threadIdx.x >> 6, l = lane_id();
     const int kb = ks * kLinWaves + wv;
-    const int g = A.shard_of_nb[cg >> 1];
-    // waves past the end of k add nothing; a shard index outside [0, S) leaves its columns at zero
-    const bool live = kb < kbn && (unsigned)g < (unsigned)A.S;
+    const bool in_k = kb < kbn;                  // waves past the end of k add nothing
+    // the loads that depend on nothing go first: the weights, the activations and the block's shard index
     GQ gv;
-    if (live) gv.load_nat(A.tr, A.n / 16, kb * 8, cg * 4);
+    if (in_k) gv.load_nat(A.tr, A.n / 16, kb * 8, cg * 4);
+    float xv[MR][2];
 #pragma unroll
-    for (int m = 0; m < MR; ++m) {               // the rows' xh of this 128-row block and their sums
-        half2_t v = half2_t{(half_t)0.f, (half_t)0.f};
-        if (live && m < A.M) v = *(const half2_t*)(A.xh + ((size_t)g * A.M + m) * A.k + kb * 128 + 2 * l);
+    for (int m = 0; m < MR; ++m) {
+        xv[m][0] = xv[m][1] = 0.f;
+        if (in_k && m < A.M) {
+            const size_t xo = (size_t)m * A.x_stride + kb * 128 + 2 * l;
+            xv[m][0] = ld_act(A.x, A.x_dt, xo);
+            xv[m][1] = ld_act(A.x, A.x_dt, xo + 1);
+        }
+    }
+    const int g = A.shard_of_nb[nb];
+    const bool live = in_k && (unsigned)g < (unsigned)A.S;   // a shard index outside [0, S) leaves its columns zero
+    half2_t su = half2_t{(half_t)0.f, (half_t)0.f};
+    if (live) su = *(const half2_t*)(A.suh + (size_t)g * A.k + kb * 128 + 2 * l);
+#pragma unroll
+    for (int m = 0; m < MR; ++m) {               // xh = fp16(H(fp16(x su)) / sqrt 128) of this block, and its sum
+        float v0 = 0.f, v1 = 0.f;
+        if (live && m < A.M) {
+            v0 = (float)(half_t)(xv[m][0] * (float)su.x);
+            v1 = (float)(half_t)(xv[m][1] * (float)su.y);
+        }
+        wave_fwht128(v0, v1);
+        const half2_t v = half2_t{(half_t)(v0 * kRsqrt128), (half_t)(v1 * kRsqrt128)};
         xq[wv][m][l] = v;
         const float s = wave_sum((float)v.x + (float)v.y);
         if (l == 0) ssw[wv][m] = s;
@@ -83,7 +124,26 @@ __global__ void __launch_bounds__(64 * kLinWaves) lin_gemv_kernel(LinearArgs A) 
             t += red[w][m][c];
             xs += ssw[w][m];
         }
-        A.part[((size_t)ks * A.M + m) * A.n + cg * 64 + c] = kC1 * t + kC2 * xs;
+        st_agent(A.part + ((size_t)ks * A.M + m) * A.n + cg * 64 + c, kC1 * t + kC2 * xs);
+    }
+    wait_stores();
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        last = counter_add(A.cnt + nb, 1) == 2 * P - 1;
+        if (last) counter_reset(A.cnt + nb);     // every arrival of this block is in: ready for the next call
+    }
+    __syncthreads();
+    if (!last) return;
+    // the block's output rows: the P partials in slice order, then the output Hadamard x svh (one wave per row)
+    const half2_t sv = *(const half2_t*)(A.svh + nb * 128 + 2 * l);
+    for (int m = wv; m < A.M; m += kLinWaves) {
+        const float* q = A.part + (size_t)m * A.n + nb * 128 + 2 * l;
+        float v0, v1;
+        sum2_agent(q, P, (size_t)A.M * A.n, v0, v1);
+        wave_fwht128(v0, v1);
+        const size_t o = (size_t)m * out_stride + nb * 128 + 2 * l;
+        st_act(out, out_dt, o, v0 * kRsqrt128 * (float)sv.x);
+        st_act(out, out_dt, o + 1, v1 * kRsqrt128 * (float)sv.y);
     }
 }
 
@@ -141,23 +201,24 @@ hipError_t launch_linear_had_in(const LinearArgs& a, hipStream_t s) {
 }
 
 template <int K>
-static hipError_t gemv_rows(const LinearArgs& a, hipStream_t s) {
+static hipError_t small_rows(const LinearArgs& a, void* out, int out_dt, int64_t out_stride, hipStream_t s) {
     const dim3 grid((unsigned)((a.n / 64) * a.P)), block(64 * kLinWaves);
-    if (a.M <= 1) hipLaunchKernelGGL((lin_gemv_kernel<K, 1>), grid, block, 0, s, a);
-    else if (a.M <= 2) hipLaunchKernelGGL((lin_gemv_kernel<K, 2>), grid, block, 0, s, a);
-    else if (a.M <= 4) hipLaunchKernelGGL((lin_gemv_kernel<K, 4>), grid, block, 0, s, a);
-    else if (a.M <= kLinMaxRows) hipLaunchKernelGGL((lin_gemv_kernel<K, kLinMaxRows>), grid, block, 0, s, a);
+    if (a.M <= 1) hipLaunchKernelGGL((lin_small_kernel<K, 1>), grid, block, 0, s, a, out, out_dt, out_stride);
+    else if (a.M <= 2) hipLaunchKernelGGL((lin_small_kernel<K, 2>), grid, block, 0, s, a, out, out_dt, out_stride);
+    else if (a.M <= 4) hipLaunchKernelGGL((lin_small_kernel<K, 4>), grid, block, 0, s, a, out, out_dt, out_stride);
+    else if (a.M <= kLinMaxRows)
+        hipLaunchKernelGGL((lin_small_kernel<K, kLinMaxRows>), grid, block, 0, s, a, out, out_dt, out_stride);
     else return hipErrorInvalidValue;
     return hipGetLastError();
 }
 
-hipError_t launch_linear_gemv(int K, const LinearArgs& a, hipStream_t s) {
+hipError_t launch_linear_small(int K, const LinearArgs& a, void* out, int out_dt, int64_t out_stride, hipStream_t s) {
     switch (K) {
-        case 2: return gemv_rows<2>(a, s);
-        case 3: return gemv_rows<3>(a, s);
-        case 4: return gemv_rows<4>(a, s);
-        case 5: return gemv_rows<5>(a, s);
-        case 6: return gemv_rows<6>(a, s);
+        case 2: return small_rows<2>(a, out, out_dt, out_stride, s);
+        case 3: return small_rows<3>(a, out, out_dt, out_stride, s);
+        case 4: return small_rows<4>(a, out, out_dt, out_stride, s);
+        case 5: return small_rows<5>(a, out, out_dt, out_stride, s);
+        case 6: return small_rows<6>(a, out, out_dt, out_stride, s);
         default: return hipErrorInvalidValue;
     }
 }

@@ -747,9 +747,9 @@ int exl3_dequant(const uint32_t* trellis, int k_tiles, int n_tiles, int K, uint1
 
 int exl3_linear_supported(int K, int cb) { return cb == 2 && K >= 2 && K <= 6 ? 1 : 0; }
 
-size_t exl3_linear_workspace(int M, int k, int n, int S) {
-    if (M < 0 || k <= 0 || n <= 0 || S <= 0) return 0;
-    return linear_workspace_bytes(M, k, n, S);
+size_t exl3_linear_workspace(int M, int k, int n) {
+    if (M < 0 || k <= 0 || n <= 0) return 0;
+    return linear_workspace_bytes(M, k, n);
 }
 
 static int linear_dims(const char* what, int M, int k, int n, int S) {
@@ -769,7 +769,7 @@ int exl3_linear_small(const void* x, int x_dtype, int64_t x_stride, int M, int k
     if (M == 0) return EXL3_OK;
     if (!x || !trellis || !suh || !svh || !shard_of_nb || !out) return fail(EXL3_EINVAL, "linear_small: null pointer");
     if (x_stride < k || out_stride < n) return fail(EXL3_EINVAL, "linear_small: row strides");
-    const size_t need = linear_workspace_bytes(M, k, n, S);
+    const size_t need = linear_workspace_bytes(M, k, n);
     if (!workspace || workspace_bytes < need)
         return fail(EXL3_EWORKSPACE, "linear_small: workspace %zu < %zu bytes", workspace_bytes, need);
     LinearArgs a{};
@@ -784,13 +784,10 @@ int exl3_linear_small(const void* x, int x_dtype, int64_t x_stride, int M, int k
     a.suh = (const _Float16*)suh;
     a.svh = (const _Float16*)svh;
     a.shard_of_nb = shard_of_nb;
-    a.xh = (_Float16*)workspace;
-    a.part = (float*)((uint8_t*)workspace + align256((size_t)S * M * k * 2));
+    a.cnt = (int*)workspace;
+    a.part = (float*)((uint8_t*)workspace + linear_counter_bytes(n));
     a.P = linear_kslices(k);
-    const hipStream_t st = (hipStream_t)stream;
-    hipError_t e = launch_linear_had_in(a, st);
-    if (e == hipSuccess) e = launch_linear_gemv(K, a, st);
-    if (e == hipSuccess) e = launch_linear_had_out(a.part, 0, a.P, M, n, a.svh, out, out_dtype, out_stride, st);
+    const hipError_t e = launch_linear_small(K, a, out, out_dtype, out_stride, (hipStream_t)stream);
     return e == hipSuccess ? EXL3_OK : hip_fail(e, "linear_small launch");
 }
 

@@ -7,6 +7,9 @@
 #include <torch/library.h>
 
 #include <algorithm>
+#include <map>
+#include <mutex>
+#include <vector>
 
 #include "../../include/exl3moe.h"
 
@@ -237,14 +240,31 @@ void linear_checks(const at::Tensor& trellis, const at::Tensor& suh, const at::T
                 "exl3xpu_C.linear: shard_of_nb int32 [n / 128]");
 }
 
+// The small-M workspace of one (device, stream): zeroed at allocation (every call leaves its counters zero) and shared
+// by the calls on that stream, which run in order. Sized for 8 rows; a larger one replaces it when a call needs more,
+// and the replaced buffers are kept, since a captured HIP graph may still hold their addresses.
+at::Tensor& small_workspace(const at::Tensor& x, size_t bytes) {
+    static std::mutex mu;
+    static auto* cache = new std::map<std::pair<int, void*>, at::Tensor>();
+    static auto* retired = new std::vector<at::Tensor>();
+    std::lock_guard<std::mutex> lock(mu);
+    auto& t = (*cache)[{(int)x.device().index(), cur_stream(x)}];
+    if (!t.defined() || (size_t)t.numel() < bytes) {
+        if (t.defined()) retired->push_back(t);
+        t = at::zeros({(int64_t)bytes}, x.options().dtype(at::kByte));
+    }
+    return t;
+}
+
 void gemm_small(at::Tensor x2, at::Tensor trellis, at::Tensor suh, at::Tensor svh, at::Tensor shard_of_nb, at::Tensor out,
                 int64_t K, int64_t cb) {
     const int64_t M = x2.size(0), k = x2.size(1), n = svh.size(0);
     linear_checks(trellis, suh, svh, shard_of_nb, k, K, cb);
     TORCH_CHECK(x2.stride(1) == 1 && out.dim() == 2 && out.size(0) == M && out.size(1) == n && out.stride(1) == 1,
                 "exl3_gemm_small: x [M, k], out [M, n] with unit column strides");
-    const size_t ws_bytes = exl3_linear_workspace((int)M, (int)k, (int)n, (int)suh.size(0));
-    auto ws = at::empty({(int64_t)ws_bytes}, x2.options().dtype(at::kByte));
+    TORCH_CHECK(M <= 8, "exl3_gemm_small: at most 8 rows, got ", M);
+    const size_t ws_bytes = exl3_linear_workspace(8, (int)k, (int)n);
+    auto& ws = small_workspace(x2, ws_bytes);
     check(exl3_linear_small(x2.data_ptr(), dtype_code(x2), x2.stride(0), (int)M, (int)k, (int)n, trellis.data_ptr(),
                             (int)K, (int)cb, suh.data_ptr(), (int)suh.size(0), svh.data_ptr(),
                             shard_of_nb.data_ptr<int>(), out.data_ptr(), dtype_code(out), out.stride(0), ws.data_ptr(),

@@ -62,7 +62,7 @@ SIGNATURES = {
     "exl3_copy_batch": (c_i32, [c_p, c_p, c_p, c_i64, c_i64, c_i64, c_i64, c_i64, c_p]),
     "exl3_table_update": (c_i32, [c_p, c_p, c_p, c_p, c_p, c_i64, c_p]),
     "exl3_linear_supported": (c_i32, [c_i32, c_i32]),
-    "exl3_linear_workspace": (c_sz, [c_i32, c_i32, c_i32, c_i32]),
+    "exl3_linear_workspace": (c_sz, [c_i32, c_i32, c_i32]),
     "exl3_linear_small": (c_i32, [c_p, c_i32, c_i64, c_i32, c_i32, c_i32, c_p, c_i32, c_i32, c_p, c_i32, c_p, c_p, c_p,
                                   c_i32, c_i64, c_p, c_sz, c_p]),
     "exl3_had_in": (c_i32, [c_p, c_i32, c_i64, c_i32, c_i32, c_p, c_i32, c_p, c_p]),

@@ -123,23 +123,50 @@ def test_had_in_had_out_vs_oracle():
 
 
 def test_linear_small_capi_fp32_out():
-    """exl3_linear_small through the C-ABI: fp32 output with a row stride, the caller's workspace."""
+    """exl3_linear_small through the C-ABI: fp32 output with a row stride, the caller's zeroed workspace used by two
+    calls in a row (4 rows, then 2), its counters left zero after each."""
     from exl3xpu import capi
     L = capi.lib()
     ck = olin.checkpoint(51, 1024, [512, 256], 4)
-    M, k, n, S = 4, 1024, 768, 2
-    xf, x = _x(8, M, k, torch.bfloat16)
+    k, n, S = 1024, 768, 2
     tr = torch.from_numpy(ck["trellis"]).cuda()
     suh = torch.from_numpy(ck["suh"]).cuda()
     svh = torch.from_numpy(ck["svh"]).cuda()
     sonb = torch.from_numpy(ck["shard_of_nb"]).cuda()
-    out = torch.zeros((M, n + 64), dtype=torch.float32, device="cuda")
-    ws_bytes = L.exl3_linear_workspace(M, k, n, S)
-    ws = torch.empty(ws_bytes, dtype=torch.uint8, device="cuda")
-    capi.check(L.exl3_linear_small(x.data_ptr(), 1, k, M, k, n, tr.data_ptr(), 4, 2, suh.data_ptr(), S,
-                                   svh.data_ptr(), sonb.data_ptr(), out.data_ptr(), 2, n + 64, ws.data_ptr(),
-                                   ws_bytes, capi.stream_handle()), "linear_small")
-    torch.cuda.synchronize()
-    got = out.cpu().numpy()
-    assert _rel(got[:, :n], olin.linear(xf, ck, "small")) < TOL
-    assert not got[:, n:].any()                                   # nothing written past n in the padded rows
+    ws_bytes = L.exl3_linear_workspace(4, k, n)
+    ws = torch.zeros(ws_bytes, dtype=torch.uint8, device="cuda")
+    for M, seed in ((4, 8), (2, 9)):
+        xf, x = _x(seed, M, k, torch.bfloat16)
+        out = torch.zeros((M, n + 64), dtype=torch.float32, device="cuda")
+        capi.check(L.exl3_linear_small(x.data_ptr(), 1, k, M, k, n, tr.data_ptr(), 4, 2, suh.data_ptr(), S,
+                                       svh.data_ptr(), sonb.data_ptr(), out.data_ptr(), 2, n + 64, ws.data_ptr(),
+                                       ws_bytes, capi.stream_handle()), "linear_small")
+        torch.cuda.synchronize()
+        got = out.cpu().numpy()
+        assert _rel(got[:, :n], olin.linear(xf, ck, "small")) < TOL, M
+        assert not got[:, n:].any()                               # nothing written past n in the padded rows
+        assert not ws[:n // 128 * 4].any()                        # every arrival counter back at zero
+
+
+def test_linear_small_in_graph_replays():
+    """The fused small path captured in a HIP graph (the shared per-stream workspace and its counters) and replayed
+    several times with new inputs and eager calls in between: every replay equals the eager result bit for bit."""
+    ck = olin.checkpoint(71, 512, [256, 256], 3)
+    g = _group(ck)
+    xs = [_x(80 + i, 1, 512, torch.bfloat16)[1] for i in range(4)]
+    x_static = xs[0].clone()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        g(x_static)
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        y_static = g(x_static)
+    for x in xs:
+        want = g(x)                                               # eager, on the current stream
+        torch.cuda.synchronize()
+        x_static.copy_(x)
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(y_static, want)

@@ -56,3 +56,15 @@ def test_linear_meta_shape_and_support():
     assert tuple(y.shape) == (2, 3, 768) and y.dtype == torch.bfloat16
     assert [c.exl3_supported(k, 2) for k in range(1, 8)] == [False, True, True, True, True, True, False]
     assert not c.exl3_supported(3, 1)
+
+
+@pytest.mark.parametrize("K", [2, 4, 6])
+def test_cpu_linear_baseline_matches_oracle(K):
+    """The torch CPU linear that bench.py times as its CPU baseline computes what oracle/linear.py computes."""
+    from oracle import cpu_path, exl3, synth
+    ck = olin.checkpoint(60 + K, 256, [128, 256], K)
+    xf = exl3.bf16_to_f32(synth.activations(61 + K, 2, 256))
+    y = cpu_path.CpuLinear(K)(torch.from_numpy(xf), torch.from_numpy(ck["trellis"]), torch.from_numpy(ck["suh"]),
+                              torch.from_numpy(ck["svh"]), ck["bounds"]).numpy()
+    ref = olin.linear(xf, ck)
+    assert np.linalg.norm(y - ref) / np.linalg.norm(ref) < 1e-5
