@@ -286,10 +286,14 @@ __global__ void __launch_bounds__(64 * kXhWaves) __attribute__((amdgpu_waves_per
 
 // ---- LDS layouts of one K chunk ----------------------------------------------------------------------------------------
 // B: tile j of tile-row kt at kt * kBRow + j * kTileB, column c of the tile at 32 c, its k-half h (k = 8 h .. 8 h + 7)
-// in the 16-byte slot h ^ (c >> 3) ^ (j & 1). The 16 lanes of a B-fragment read (16 columns of one tile) and the 16 lanes
-// of a decoder store (8 periods of two neighbouring tiles) each cover 16 distinct slots of the 64 banks.
+// in the 16-byte slot h ^ (j & 1). On gfx950 a ds_read_b128 serves the 8-lane blocks (0, 3), (1, 2), (4, 7) and (5, 6)
+// of a wave together, and a block of 8 consecutive columns at 32-byte spacing covers the even or the odd 16-byte bank
+// groups of a 256-byte row, as its slot parity says. In a B-fragment read the block of lanes 8 b .. 8 b + 7 holds tile
+// b >> 1 & 1, k-half b >> 2 and columns 8 (b & 1) .. + 7, so its parity is (b >> 2) ^ (b >> 1 & 1), which differs in
+// each of those pairs of blocks: one pass per 16 lanes (a parity that also flipped with c >> 3 made every pair collide,
+// half the read rate). A decoder store's 8-lane blocks alternate tiles, hence parities.
 __device__ __forceinline__ int b_slot(int tile, int c, int h) {
-    return tile * kTileB + c * 32 + ((h ^ (c >> 3) ^ (tile & 1)) << 4);
+    return tile * kTileB + c * 32 + ((h ^ (tile & 1)) << 4);
 }
 // A: row r of the chunk at r * kARow, its 16-byte piece j (k = 8 j .. 8 j + 7) in slot j ^ ((r >> 1) & 7): 16 rows of one
 // piece (an A-fragment read) and 2 rows of 8 pieces (a staging store) each hit 16 distinct slots.
@@ -371,8 +375,8 @@ struct ChunkDecoder {
             const int sw = (tile & 1) << 4;
             *(hv_t*)(tb + (0 ^ sw)) = o[j][0];
             *(hv_t*)(tb + (16 ^ sw)) = o[j][1];
-            *(hv_t*)(tb + 8 * 32 + (16 ^ sw)) = o[j][2];
-            *(hv_t*)(tb + 8 * 32 + (0 ^ sw)) = o[j][3];
+            *(hv_t*)(tb + 8 * 32 + (0 ^ sw)) = o[j][2];
+            *(hv_t*)(tb + 8 * 32 + (16 ^ sw)) = o[j][3];
         }
     }
 
@@ -389,8 +393,8 @@ struct ChunkDecoder {
             const int sw = (tile & 1) << 4;
             *(hv_t*)(tb + (0 ^ sw)) = slot_vals<0, 0>(P[j], es);
             *(hv_t*)(tb + (16 ^ sw)) = slot_vals<0, 1>(P[j], es);
-            *(hv_t*)(tb + 8 * 32 + (16 ^ sw)) = slot_vals<1, 0>(P[j], es);
-            *(hv_t*)(tb + 8 * 32 + (0 ^ sw)) = slot_vals<1, 1>(P[j], es);
+            *(hv_t*)(tb + 8 * 32 + (0 ^ sw)) = slot_vals<1, 0>(P[j], es);
+            *(hv_t*)(tb + 8 * 32 + (16 ^ sw)) = slot_vals<1, 1>(P[j], es);
         }
     }
 };
