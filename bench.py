@@ -158,6 +158,93 @@ def run_prefill(args, dev):
     print(json.dumps(out), flush=True)
 
 
+def run_prefill_tiered(args, dev):
+    """Prefill leg through the tier (config 3's PCIe-inclusive figure): 8,192 tokens through 48 MoE layers (H 2048,
+    I 512, 512 experts, top-10 softmax routing per layer, K=3) with the 8,000-slot HBM cache seeded (166-167 random
+    experts of each layer resident) and every other expert read by the prefill kernels straight from its record in
+    the pinned RAM-tier arena over PCIe, each byte once per 192-row pass: the plugin's ensure_for_prefill + zero-copy
+    route (plugin/sglang_plugin.tier.py:531-561, nvtier.py:389-457) at full size, here with every record already in
+    the arena. The staged route (copy stream into HBM staging buffers) stays disabled. Before timing, one layer's
+    zero-copy output is checked bit for bit against the same layer on HBM copies of the same blobs."""
+    import numpy as np
+    import torch
+    from exl3xpu import nvtier
+    from exl3xpu.moe_offload import ops
+
+    X = ops()
+    t0 = time.perf_counter()
+    store = nvtier.TierStore(H, I, K, E, SLOTS, n_layers=L, device=dev)
+    src = nvtier.SyntheticExpertSource(H, I, K, SEED, n_distinct=64)
+    blobs = torch.from_numpy(src.buf[np.arange(E) % src.n])
+    keys = [f"model.layers.{li}.mlp" for li in range(L)]
+    for k in keys:
+        store.add_layer(k, blobs)
+    del blobs
+    rng = np.random.default_rng(SEED + 5)
+    for li, k in enumerate(keys):
+        store.make_resident(k, rng.choice(E, SLOTS // L + (1 if li < SLOTS % L else 0), replace=False))
+    torch.cuda.synchronize()
+    log(f"prefill-tiered setup {time.perf_counter() - t0:.1f} s: {store.resident_count()} resident keys, pinned arena "
+        f"{store.size / 2**30:.1f} GiB")
+    g = torch.Generator(device=dev).manual_seed(SEED + 6)
+    M, R = PREFILL_TOKENS, 4
+    xs = [torch.randn(M, H, generator=g, device=dev).to(torch.bfloat16) for _ in range(R)]
+    ids_l, w_l, host_bytes = [], [], 0
+    for li in range(L):
+        p = torch.softmax(torch.randn(M, E, generator=g, device=dev), dim=-1)
+        w, i = torch.topk(p, TOPK, dim=-1)
+        ids_l.append(i.to(torch.int32).contiguous())
+        w_l.append((w / w.sum(-1, keepdim=True)).contiguous())
+        used = torch.unique(i).cpu().numpy()
+        host_bytes += int((store.slot_of[keys[li]].numpy()[used] < 0).sum()) * store.blob
+    # zero-copy == HBM-resident, bit for bit, on layer 0
+    dblobs = torch.from_numpy(src.buf).to(dev)
+    table = torch.tensor([dblobs[e % src.n].data_ptr() for e in range(E)], dtype=torch.int64, device=dev)
+    y_zc = store.forward(keys[0], xs[0], ids_l[0], w_l[0])
+    y_res = X.moe_forward(xs[0], ids_l[0], w_l[0], table, I, K, E)
+    torch.cuda.synchronize()
+    same = bool(torch.equal(y_zc, y_res))
+    log(f"zero-copy layer output equals the HBM-resident one: {same}")
+    if not same:
+        raise SystemExit("bench.py --prefill-tiered: zero-copy output differs from the HBM-resident output")
+
+    def chunk(resident):
+        for li, k in enumerate(keys):
+            if resident:
+                X.moe_forward(xs[li % R], ids_l[li], w_l[li], table, I, K, E)
+            else:
+                store.forward(k, xs[li % R], ids_l[li], w_l[li])
+
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    times = {}
+    for resident in (False, True):
+        chunk(resident)
+        torch.cuda.synchronize()
+        ev0.record()
+        chunk(resident)
+        ev1.record()
+        torch.cuda.synchronize()
+        times[resident] = ev0.elapsed_time(ev1) * 1e-3
+    t, t_res = times[False], times[True]
+    out = {
+        "metric": "MoE prefill tok/s through the tier (8,192 tokens x 48 layers x 512E top-10, EXL3 3bpw; 8,000 HBM "
+                  "slots, other experts read zero-copy from the pinned RAM tier)",
+        "value": round(M / t, 1), "unit": "tok/s", "n_gpus": 1, "higher_is_better": True,
+        "ms_per_chunk": round(t * 1e3, 2), "ms_per_layer": round(t / L * 1e3, 3),
+        "pcie_read_gb_s": round(host_bytes / t / 1e9, 2), "host_bytes_per_chunk": host_bytes,
+        "resident_ms_per_chunk": round(t_res * 1e3, 2),
+        "pcie_time_share": round(1.0 - t_res / t, 3),
+        "config": {"workload": "prefill chunk of 8,192 tokens through 48 MoE layers x 512 experts (H 2048, I 512), "
+                               "top-10, EXL3 K=3; 8,000 HBM-resident experts, the rest read over PCIe from the pinned "
+                               "RAM tier (every record present)", "tokens": M, "layers": L, "slots": SLOTS},
+        "dtype": "bf16 activations, f16 MFMA, fp32 accumulate", "data": "synthetic",
+    }
+    log(f"prefill through the tier: {t * 1e3:.1f} ms per 8,192-token chunk = {M / t:.0f} tok/s; "
+        f"{host_bytes / 1e9:.2f} GB read over PCIe = {host_bytes / t / 1e9:.1f} GB/s; all-resident "
+        f"{t_res * 1e3:.1f} ms")
+    print(json.dumps(out), flush=True)
+
+
 # the dense projections of one decoder layer as fused groups (input size k, output widths of the shards)
 LINEAR_GROUPS = ((2048, (2048, 2048, 4096, 4096)), (4096, (2048,)), (2048, (512, 512)), (512, (2048,)))
 LINEAR_PREFILL_M = 1024
@@ -279,6 +366,8 @@ def main():
     ap.add_argument("--eager", action="store_true", help="launch the 48 layer calls eagerly instead of a HIP graph")
     ap.add_argument("--prefill", action="store_true", help="the prefill leg (8,192-token chunk, staged) instead of decode")
     ap.add_argument("--linear", action="store_true", help="the dense EXL3 linear leg instead of MoE decode")
+    ap.add_argument("--prefill-tiered", action="store_true",
+                    help="the prefill leg through the tier (8,000 HBM slots, zero-copy RAM-tier reads)")
     ap.add_argument("--prefill-staged", action="store_true", help="(disabled) the staged prefill variant")
     ap.add_argument("--roofline-only", action="store_true",
                     help="counter runs: only the HBM-resident layer calls, after 3 device copies of 256 MiB (the "
@@ -301,6 +390,8 @@ def main():
         return run_prefill(args, dev)
     if args.linear:
         return run_linear(args, dev)
+    if args.prefill_tiered:
+        return run_prefill_tiered(args, dev)
     t0 = time.perf_counter()
     store = nvtier.TierStore(H, I, K, E, SLOTS, n_layers=L, device=dev)
     keys = [f"model.layers.{li}.mlp" for li in range(L)]

@@ -280,6 +280,34 @@ def test_tier_ensure_for_prefill():
         tier.close()
 
 
+def test_prefill_zero_copy_config0_shapes():
+    """The prefill kernels at the config-0 expert shape (H 2048, I 512, 512 experts, top-10) on a table that mixes HBM
+    slots (100 experts) and records of the pinned RAM-tier arena read over PCIe (the other 412, all routed to by
+    2,048 tokens): the same bits as a table of HBM copies of the same blobs."""
+    from exl3xpu import nvtier
+    H, I, K, E, M, topk = 2048, 512, 3, 512, 2048, 10
+    print("case prefill zero-copy config-0 shapes", flush=True)
+    store = nvtier.TierStore(H, I, K, E, 100, n_layers=2)
+    src = nvtier.SyntheticExpertSource(H, I, K, 23, n_distinct=32)
+    blobs = torch.from_numpy(src.buf[np.arange(E) % src.n])
+    keys = ["model.layers.0.mlp", "model.layers.1.mlp"]
+    for k in keys:
+        store.add_layer(k, blobs)
+    resident = np.random.default_rng(5).choice(E, 100, replace=False)
+    store.make_resident(keys[0], resident)
+    ids, w = synth.softmax_topk(83, M, E, topk)
+    assert len(np.unique(ids)) == E
+    it, wt = torch.from_numpy(ids).cuda(), torch.from_numpy(w).cuda()
+    x = torch.from_numpy(exl3.bf16_to_f32(synth.activations(84, M, H))).to(torch.bfloat16).cuda()
+    out = store.forward(keys[0], x, it, wt)
+    dblobs = torch.from_numpy(src.buf).cuda()
+    ref_t = torch.tensor([dblobs[e % src.n].data_ptr() for e in range(E)], dtype=torch.int64, device="cuda")
+    ref = _ops().moe_forward(x, it, wt, ref_t, I, K, E)
+    torch.cuda.synchronize()
+    assert int((store.slot_of[keys[0]] >= 0).sum()) == 100
+    assert torch.equal(out, ref)
+
+
 def test_plugin_caller_sequence():
     """The tier plugin's call sequence (plugin/sglang_plugin.tier.py:531-561 `apply`, 944-956 the host step after every
     model step) over this API, tier mode: a 300-token prompt streamed through stage_forward, a 24-token prompt
