@@ -54,6 +54,37 @@ def test_linear_small_vs_oracle(K, M):
         assert r < TOL, (dtype, r)
 
 
+@pytest.mark.parametrize("k,widths,K,M", [(2048, [1024, 1024], 3, 1), (4096, [512], 3, 3), (640, [384, 256], 5, 2),
+                                          (128, [256], 4, 8), (2048, [256, 256, 512, 512], 2, 4)])
+def test_linear_small_k_slices(k, widths, K, M):
+    """The fused path over 1 to 8 K-slices of 512 rows, with a last slice that is partly past the end of k (640, 128:
+    those waves add nothing), several shards: the last workgroup of every 128-column block sums the slices in order."""
+    print(f"case linear small k={k} widths={widths} K={K} M={M}", flush=True)
+    ck = olin.checkpoint(400 + k + K, k, widths, K)
+    g = _group(ck)
+    xf, x = _x(k + M, M, k, torch.bfloat16)
+    y = g(x)
+    torch.cuda.synchronize()
+    r = _rel(y.float().cpu().numpy(), _round(olin.linear(xf, ck, "small"), torch.bfloat16))
+    assert r < TOL, r
+
+
+def test_linear_out_of_range_shard_gives_zero_columns():
+    """A shard index outside [0, S) in shard_of_nb is never dereferenced: that block's columns come out zero and the
+    other blocks are unchanged."""
+    from exl3xpu.linear import C
+    ck = olin.checkpoint(77, 256, [256, 256], 3)
+    g = _group(ck)
+    xf, x = _x(78, 2, 256, torch.bfloat16)
+    good = g(x)
+    bad_map = g.shard_of_nb.clone()
+    bad_map[1] = 7
+    y = C().linear(x, g.trellis, g.suh, g.svh, bad_map, g.bounds, g.K, g.cb, 8, 4096)
+    torch.cuda.synchronize()
+    assert not y[:, 128:256].float().any()
+    assert torch.equal(y[:, :128], good[:, :128]) and torch.equal(y[:, 256:], good[:, 256:])
+
+
 @pytest.mark.parametrize("K,M,slice_n", [(3, 9, 4096), (3, 300, 128), (4, 64, 192), (2, 33, 0), (6, 17, 256)])
 def test_linear_large_vs_oracle(K, M, slice_n):
     """Above 8 rows: the input Hadamards, reconstructed fp16 weight slices (slice_n columns, 0 = whole groups) times xh
