@@ -20,6 +20,79 @@ namespace exl3 {
 
 constexpr int kLinWaves = 4;
 
+typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
+typedef float float4_t __attribute__((ext_vector_type(4)));
+
+// The 8 x 4-tile wave GEMV with the multiply-adds on the matrix cores (v_mfma_f32_16x16x16_f16), for the bitrates
+// whose trellis period is 2 columns x 16 rows of a tile (V = 32: K = 3, 5). A pass covers 4 tile-rows x 2 tile-columns:
+// lane l decodes period l & 7 of tile-row 4 (ps & 1) + (l >> 4), tile-column 2 (ps >> 1) + ((l >> 3) & 1), so the 16
+// lanes of MFMA k-group q = l >> 4 share one tile-row and each lane's period holds the 4-row slices (rows 4 i .. 4 i + 3)
+// of its two columns p and p + 8 that the B operand needs. The B values are the raw codebook integers h (exact in fp16,
+// two packed per register); A = the rows' xh over the same 4-row slices (zero for rows past MR); the raw-h affine is
+// applied to the column sums as in the VALU version. VALU per weight: bfe, mul, sad and half a pack, for any MR.
+template <int K>
+struct GemvMfma {
+    static constexpr int D = Geo<K>::D;
+    static_assert(Geo<K>::V == 32 && Geo<K>::G == 8, "the MFMA layout needs periods of 2 columns x 16 rows");
+    uint32_t wd[4][D];
+
+    __device__ __forceinline__ void load_nat(const uint32_t* tr, int tiles_n, int rt0, int ct0) {
+        const int l = lane_id(), q = l >> 4, c = (l >> 3) & 1, p = l & 7;
+#pragma unroll
+        for (int ps = 0; ps < 4; ++ps)
+#pragma unroll
+            for (int i = 0; i < D; ++i)
+                wd[ps][i] = __builtin_nontemporal_load(
+                    as_global(tr) + word_off_nat<K>(rt0 + 4 * (ps & 1) + q, tiles_n, ct0 + 2 * (ps >> 1) + c, p, i));
+    }
+
+    // raw h of values u and u + 1 packed into one register (h of u in the low half)
+    template <int u>
+    __device__ __forceinline__ static uint32_t pair(const Period<K>& P) {
+        return cb_raw(P.template state<u>()) | (cb_raw(P.template state<u + 1>()) << 16);
+    }
+    template <int i, int h>
+    __device__ __forceinline__ static half4_t bop(const Period<K>& P) {
+        constexpr int u0 = 2 * (i >> 1) + 4 * h + 16 * (i & 1);      // rows 4 i .. 4 i + 3 of column p + 8 h
+        const uint32_t w0 = pair<u0>(P), w1 = pair<u0 + 8>(P);
+        typedef uint32_t u2_t __attribute__((ext_vector_type(2)));
+        return __builtin_bit_cast(half4_t, u2_t{w0, w1});
+    }
+    template <int MR, int i>
+    __device__ __forceinline__ static void step(const Period<K>& P, const half2_t* xq, int xrow, float4_t (&acc)[2]) {
+        const int m = lane_id() & 15;
+        half4_t a = half4_t{(half_t)0.f, (half_t)0.f, (half_t)0.f, (half_t)0.f};
+        if (m < MR) a = *(const half4_t*)(xq + m * 64 + (xrow + 4 * i) / 2);
+        acc[0] = __builtin_amdgcn_mfma_f32_16x16x16f16(a, bop<i, 0>(P), acc[0], 0, 0, 0);
+        acc[1] = __builtin_amdgcn_mfma_f32_16x16x16f16(a, bop<i, 1>(P), acc[1], 0, 0, 0);
+    }
+
+    // xq = [MR][64] half2 (the wave's 128-row block of each row); acc[pair of tile-columns][h]: D[m][n] with lane l
+    // holding rows m = 4 (l >> 4) .. + 3 of column n = l & 15 (tile-column (n >> 3) & 1 of the pair, column n & 7 + 8 h)
+    template <int MR>
+    __device__ __forceinline__ void compute(const half2_t* xq, float4_t (&acc)[2][2]) const {
+        const int l = lane_id(), q = l >> 4;
+        const int src = (l & ~7) | ((l + 7) & 7);
+#pragma unroll
+        for (int ps = 0; ps < 4; ++ps) {
+            const uint32_t prev = (uint32_t)__shfl((int)wd[ps][D - 1], src, 64);
+            Period<K> P;
+            P.set(wd[ps], prev);
+            const int xrow = 16 * (4 * (ps & 1) + q);
+            step<MR, 0>(P, xq, xrow, acc[ps >> 1]);
+            step<MR, 1>(P, xq, xrow, acc[ps >> 1]);
+            step<MR, 2>(P, xq, xrow, acc[ps >> 1]);
+            step<MR, 3>(P, xq, xrow, acc[ps >> 1]);
+        }
+    }
+};
+// MFMA from 4 rows on (at 1 and 2 rows the VALU multiply-adds cost less than the MFMA path's operand handling:
+// 7.7 / 8.8 us against 8.2 / 8.9 us per call at bs 1 / 2 on the 48-layer dense workload; 10.2 / 13.5 against
+// 10.8 / 15.8 at bs 4 / 8)
+template <int K, int MR> constexpr bool kLinMfma = Geo<K>::V == 32 && Geo<K>::G == 8 && MR >= 4;
+template <int K, bool M> struct LinGemvSel { using type = Gemv4<K>; };
+template <int K> struct LinGemvSel<K, true> { using type = GemvMfma<K>; };
+
 // one wave per (shard g, row m, 128-block kb)
 __global__ void __launch_bounds__(256) lin_had_in_kernel(LinearArgs A) {
     const int wave = blockIdx.x * 4 + (threadIdx.x >> 6), l = lane_id();
@@ -58,7 +131,7 @@ __device__ __forceinline__ void sum2_agent(const float* p, int n, size_t stride,
 template <int K, int MR>
 __global__ void __launch_bounds__(64 * kLinWaves) lin_small_kernel(LinearArgs A, void* out, int out_dt,
                                                                   int64_t out_stride) {
-    using GQ = Gemv4<K>;
+    using GQ = typename LinGemvSel<K, kLinMfma<K, MR>>::type;
     __shared__ half2_t xq[kLinWaves][MR][64];
     __shared__ float ssw[kLinWaves][MR];
     __shared__ float red[kLinWaves][MR][64];
@@ -98,22 +171,38 @@ __global__ void __launch_bounds__(64 * kLinWaves) lin_small_kernel(LinearArgs A,
         const float s = wave_sum((float)v.x + (float)v.y);
         if (l == 0) ssw[wv][m] = s;
     }
-    float acc[MR][GQ::NCQ][2];
+    if constexpr (kLinMfma<K, MR>) {
+        float4_t acc[2][2];
 #pragma unroll
-    for (int m = 0; m < MR; ++m)
+        for (int c = 0; c < 2; ++c)
+            acc[c][0] = acc[c][1] = float4_t{0.f, 0.f, 0.f, 0.f};
+        if (live) gv.template compute<MR>(&xq[wv][0][0], acc);      // the wave's own LDS rows: no barrier
+        const int n = l & 15, q4 = 4 * (l >> 4);
 #pragma unroll
-        for (int q = 0; q < GQ::NCQ; ++q) acc[m][q][0] = acc[m][q][1] = 0.f;
-    if (live) gv.template compute_mr<MR>(&xq[wv][0][0], acc);     // the wave's own LDS rows: no barrier
+        for (int c = 0; c < 2; ++c)
 #pragma unroll
-    for (int m = 0; m < MR; ++m)
+            for (int h = 0; h < 2; ++h)
 #pragma unroll
-        for (int q = 0; q < GQ::NCQ; ++q) {
-            int c0;
-            if (GQ::reduce(acc[m][q], q, c0)) {
-                red[wv][m][c0] = acc[m][q][0];
-                red[wv][m][c0 + 8] = acc[m][q][1];
+                for (int v = 0; v < 4; ++v)
+                    if (q4 + v < MR) red[wv][q4 + v][16 * (2 * c + ((n >> 3) & 1)) + 8 * h + (n & 7)] = acc[c][h][v];
+    } else {
+        float acc[MR][GQ::NCQ][2];
+#pragma unroll
+        for (int m = 0; m < MR; ++m)
+#pragma unroll
+            for (int q = 0; q < GQ::NCQ; ++q) acc[m][q][0] = acc[m][q][1] = 0.f;
+        if (live) gv.template compute_mr<MR>(&xq[wv][0][0], acc);     // the wave's own LDS rows: no barrier
+#pragma unroll
+        for (int m = 0; m < MR; ++m)
+#pragma unroll
+            for (int q = 0; q < GQ::NCQ; ++q) {
+                int c0;
+                if (GQ::reduce(acc[m][q], q, c0)) {
+                    red[wv][m][c0] = acc[m][q][0];
+                    red[wv][m][c0 + 8] = acc[m][q][1];
+                }
             }
-        }
+    }
     __syncthreads();
     for (int i = threadIdx.x; i < MR * 64; i += 64 * kLinWaves) {
         const int m = i >> 6, c = i & 63;
