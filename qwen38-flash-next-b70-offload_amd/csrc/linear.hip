@@ -20,14 +20,14 @@ namespace exl3 {
 
 constexpr int kLinWaves = 4;
 
-typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef float float4_t __attribute__((ext_vector_type(4)));
 
-// The 8 x 4-tile wave GEMV with the multiply-adds on the matrix cores (v_mfma_f32_16x16x16_f16), for the bitrates
-// whose trellis period is 2 columns x 16 rows of a tile (V = 32: K = 3, 5). A pass covers 4 tile-rows x 2 tile-columns:
-// lane l decodes period l & 7 of tile-row 4 (ps & 1) + (l >> 4), tile-column 2 (ps >> 1) + ((l >> 3) & 1), so the 16
-// lanes of MFMA k-group q = l >> 4 share one tile-row and each lane's period holds the 4-row slices (rows 4 i .. 4 i + 3)
-// of its two columns p and p + 8 that the B operand needs. The B values are the raw codebook integers h (exact in fp16,
+// The 8 x 4-tile wave GEMV with the multiply-adds on the matrix cores (v_mfma_f32_16x16x32_f16, the full-rate shape
+// on gfx950), for the bitrates whose trellis period is 2 columns x 16 rows of a tile (V = 32: K = 3, 5). A pass covers
+// 4 tile-rows x 2 tile-columns: lane l decodes period l & 7 of tile-row 4 (ps & 1) + (l >> 4), tile-column
+// 2 (ps >> 1) + ((l >> 3) & 1), so the 16 lanes of MFMA k-group q = l >> 4 share one tile-row and each lane's period
+// holds the 8-row halves (rows 8 i .. 8 i + 7) of its two columns p and p + 8 that the B operand needs. The B values are the raw codebook integers h (exact in fp16,
 // two packed per register); A = the rows' xh over the same 4-row slices (zero for rows past MR); the raw-h affine is
 // applied to the column sums as in the VALU version. VALU per weight: bfe, mul, sad and half a pack, for any MR.
 template <int K>
@@ -51,20 +51,20 @@ struct GemvMfma {
     __device__ __forceinline__ static uint32_t pair(const Period<K>& P) {
         return cb_raw(P.template state<u>()) | (cb_raw(P.template state<u + 1>()) << 16);
     }
+    // rows 8 i .. 8 i + 7 of column p + 8 h: u = 2 i + 4 h + {0, 1, 8, 9, 16, 17, 24, 25} in row order
     template <int i, int h>
-    __device__ __forceinline__ static half4_t bop(const Period<K>& P) {
-        constexpr int u0 = 2 * (i >> 1) + 4 * h + 16 * (i & 1);      // rows 4 i .. 4 i + 3 of column p + 8 h
-        const uint32_t w0 = pair<u0>(P), w1 = pair<u0 + 8>(P);
-        typedef uint32_t u2_t __attribute__((ext_vector_type(2)));
-        return __builtin_bit_cast(half4_t, u2_t{w0, w1});
+    __device__ __forceinline__ static half8_t bop(const Period<K>& P) {
+        constexpr int u0 = 2 * i + 4 * h;
+        typedef uint32_t u4_t __attribute__((ext_vector_type(4)));
+        return __builtin_bit_cast(half8_t, u4_t{pair<u0>(P), pair<u0 + 8>(P), pair<u0 + 16>(P), pair<u0 + 24>(P)});
     }
     template <int MR, int i>
     __device__ __forceinline__ static void step(const Period<K>& P, const half2_t* xq, int xrow, float4_t (&acc)[2]) {
         const int m = lane_id() & 15;
-        half4_t a = half4_t{(half_t)0.f, (half_t)0.f, (half_t)0.f, (half_t)0.f};
-        if (m < MR) a = *(const half4_t*)(xq + m * 64 + (xrow + 4 * i) / 2);
-        acc[0] = __builtin_amdgcn_mfma_f32_16x16x16f16(a, bop<i, 0>(P), acc[0], 0, 0, 0);
-        acc[1] = __builtin_amdgcn_mfma_f32_16x16x16f16(a, bop<i, 1>(P), acc[1], 0, 0, 0);
+        half8_t a = half8_t{};
+        if (m < MR) a = *(const half8_t*)(xq + m * 64 + (xrow + 8 * i) / 2);
+        acc[0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bop<i, 0>(P), acc[0], 0, 0, 0);
+        acc[1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bop<i, 1>(P), acc[1], 0, 0, 0);
     }
 
     // xq = [MR][64] half2 (the wave's 128-row block of each row); acc[pair of tile-columns][h]: D[m][n] with lane l
@@ -81,8 +81,6 @@ struct GemvMfma {
             const int xrow = 16 * (4 * (ps & 1) + q);
             step<MR, 0>(P, xq, xrow, acc[ps >> 1]);
             step<MR, 1>(P, xq, xrow, acc[ps >> 1]);
-            step<MR, 2>(P, xq, xrow, acc[ps >> 1]);
-            step<MR, 3>(P, xq, xrow, acc[ps >> 1]);
         }
     }
 };
