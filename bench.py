@@ -366,6 +366,8 @@ def main():
     ap.add_argument("--eager", action="store_true", help="launch the 48 layer calls eagerly instead of a HIP graph")
     ap.add_argument("--prefill", action="store_true", help="the prefill leg (8,192-token chunk, staged) instead of decode")
     ap.add_argument("--linear", action="store_true", help="the dense EXL3 linear leg instead of MoE decode")
+    ap.add_argument("--bookkeeping", action="store_true",
+                    help="config 1: the cache and tier decisions on 128 x 128 experts over the 4,000-step trace")
     ap.add_argument("--prefill-tiered", action="store_true",
                     help="the prefill leg through the tier (8,000 HBM slots, zero-copy RAM-tier reads)")
     ap.add_argument("--prefill-staged", action="store_true", help="(disabled) the staged prefill variant")
@@ -393,11 +395,16 @@ def main():
     if args.prefill_tiered:
         return run_prefill_tiered(args, dev)
     t0 = time.perf_counter()
-    store = nvtier.TierStore(H, I, K, E, SLOTS, n_layers=L, device=dev)
+    # config 1 (--bookkeeping): the same cache and tier on 128 x 128 experts, so that a layer call is the fused ensure
+    # plus a 64 KB GEMV; the 4,000-step trace from an empty cache, no warm-up
+    Hm, Im = (128, 128) if args.bookkeeping else (H, I)
+    if args.bookkeeping:             # the trace's first two steps run eagerly (library set-up), the other 3,998 timed
+        args.steps, args.warmup, args.settle = 3998, 0, 2
+    store = nvtier.TierStore(Hm, Im, K, E, SLOTS, n_layers=L, device=dev)
     keys = [f"model.layers.{li}.mlp" for li in range(L)]
     for k in keys:
         store.add_layer(k)
-    src = nvtier.SyntheticExpertSource(H, I, K, SEED, n_distinct=64)
+    src = nvtier.SyntheticExpertSource(Hm, Im, K, SEED, n_distinct=64)
     tier = nvtier.NvTierAsync(store, src, budget_records=args.budget_records, latency=8)
     log(f"setup {time.perf_counter() - t0:.1f} s: slots {SLOTS} x {store.blob} B, pinned arena {store.size / 2**30:.1f} GiB")
     steps, warm, bs, settle = args.steps, args.warmup, args.bs, max(0, args.settle)
@@ -406,7 +413,7 @@ def main():
     ids_np, w_np = synth.zipf_trace(SEED, max(settle + warm + steps, args.roofline_steps), L, E, TOPK, M=bs)
     ids_all = torch.from_numpy(ids_np).to(dev)
     w_all = torch.from_numpy(w_np).to(dev)
-    xs = torch.randn(L, bs, H, generator=torch.Generator().manual_seed(SEED)).to(torch.bfloat16).to(dev)
+    xs = torch.randn(L, bs, Hm, generator=torch.Generator().manual_seed(SEED)).to(torch.bfloat16).to(dev)
 
     ids_s = torch.empty(L, bs, TOPK, dtype=torch.int32, device=dev)     # static graph inputs
     w_s = torch.empty(L, bs, TOPK, dtype=torch.float32, device=dev)
@@ -422,13 +429,19 @@ def main():
 
     graph = None
     host_s = {"launch": 0.0, "tier_step": 0.0}
+    gpu_ev = []                                 # (start, end) events around each timed step's launch (bookkeeping)
 
     def decode_step(n):
         t = time.perf_counter()
+        if args.bookkeeping and n >= settle + warm:
+            gpu_ev.append((torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)))
+            gpu_ev[-1][0].record()
         if graph is None:
             layers()
         else:
             graph.replay()
+        if gpu_ev and n >= settle + warm:
+            gpu_ev[-1][1].record()
         t2 = time.perf_counter()
         tier.step()
         host_s["launch"] += t2 - t
@@ -471,6 +484,31 @@ def main():
     sd = max(steps, 1)
     log(f"decode ({'eager' if graph is None else 'graph'}) {steps} steps in {el:.3f} s: {tok_s:.1f} tok/s; per step masked {d['masked'] / sd:.1f} "
         f"fills {d['nvme_reads'] / sd:.2f} evicts {d['evicts'] / sd:.2f}; host ms per step {host_ms}")
+
+    if args.bookkeeping:
+        gpu_ms = float(np.median([a.elapsed_time(b) for a, b in gpu_ev]))
+        dec_s = steps * L * bs * TOPK / el
+        out = {
+            "metric": "expert-cache bookkeeping: device ensure per layer call and host tier step (48L x 512E, 8,000 "
+                      "slots, 4,000-step Zipf trace)",
+            "value": round(dec_s, 1), "unit": "cache decisions/s", "n_gpus": 1, "steps": steps,
+            "higher_is_better": True, "data": "synthetic: seeded Zipf(1.1) trace, 128 x 128 EXL3 K=3 experts",
+            "us_per_layer_call": round(gpu_ms * 1e3 / L, 3), "gpu_ms_per_step": round(gpu_ms, 4),
+            "ms_per_step": round(el / sd * 1e3, 4), "host_ms_per_step": host_ms,
+            "per_step": {"masked": d["masked"] / sd, "fills": d["nvme_reads"] / sd, "evicts": d["evicts"] / sd,
+                         "admit_dropped": d["admit_dropped"] / sd},
+            "config": {"workload": "config 1: 48 layers x 512 experts, top-10 Zipf(1.1) trace of 4,000 steps from an "
+                                   "empty cache (the first 2 eager and untimed), 8,000 HBM slots, 1,075-record RAM tier, AGE 4 / QMAX 256, 8-step fill "
+                                   "latency; one forward_cached call per layer (HIP graph) + the host tier step",
+                       "layers": L, "experts": E, "topk": TOPK, "hbm_slots": SLOTS,
+                       "ram_budget_records": args.budget_records},
+            "device_status": int(status[0]),
+        }
+        log(f"bookkeeping: {gpu_ms * 1e3 / L:.2f} us per layer call (median step {gpu_ms:.3f} ms on the GPU), host tier "
+            f"step {host_ms['tier_step'] - host_ms['tier_wait']:.3f} ms of work; {dec_s:.0f} decisions/s")
+        tier.close()
+        print(json.dumps(out), flush=True)
+        return
 
     # ---- roofline: dequant-GEMV on HBM-resident experts, distinct slots per (step, layer) call
     X = store.X
