@@ -37,8 +37,13 @@ constexpr int kARow = 64 * 2;                   // one A row of a K chunk (64 fp
 constexpr int kAProj = kPfRows * kARow;         // A of one projection and K chunk: 24 KB
 // double-buffered B and A (gate/up: both projections); the fp32 epilogue tile [64][256] reuses the B buffers
 constexpr int pf_lds(int nproj) { return 2 * (kBChunk + nproj * kAProj); }
-static_assert(2 * kBChunk >= 64 * 256 * 4, "epilogue tile must fit the B buffers");
+// the fp32 epilogue tile [64 rows][256 columns] at a row stride of 260 floats: the 16-byte row reads of the epilogues
+// (16 lanes per row, 4 rows per wave) then fall on disjoint bank groups in each pair of 8-lane blocks that
+// ds_read_b128 serves together (at 256 the pairs (0, 3), (1, 2), ... collide)
+constexpr int kEpRow = 260;
+// (the tile reaches past the B buffers into the A buffers, both idle between the last chunk and the next pass)
 static_assert(pf_lds(2) <= 160 * 1024, "gate/up buffers exceed the LDS of a CU");
+static_assert(64 * kEpRow * 4 <= pf_lds(1), "the epilogue tile must fit the LDS of both GEMM kernels");
 
 // ---- block scan helpers (1,024 threads) ---------------------------------------------------------------------------
 __device__ __forceinline__ int wave_incl_scan(int v) {
@@ -503,7 +508,7 @@ __device__ __forceinline__ void stash_acc(const float16_t (&acc)[2], float* ep) 
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
             const int row = rpar * 32 + (i & 3) + 8 * (i >> 2) + 4 * (l >> 5);
-            ep[row * 256 + q * 64 + cb * 32 + (l & 31)] = acc[cb][i];
+            ep[row * kEpRow + q * 64 + cb * 32 + (l & 31)] = acc[cb][i];
         }
 }
 
@@ -549,7 +554,7 @@ __global__ void __launch_bounds__(kPfThreads) prefill_gateup_kernel(PrefillArgs 
             // cross-lane butterflies) but not stored
             for (int r4 = wv * 4; r4 < 64; r4 += 4 * kPfWaves) {
                 const int rr = r4 + (l >> 4), row = m * 64 + rr;
-                const float* er = ep + rr * 256 + (l & 15) * 8;
+                const float* er = ep + rr * kEpRow + (l & 15) * 8;
                 float g[8], u[8], av[8];
 #pragma unroll
                 for (int j = 0; j < 8; ++j) {
@@ -562,7 +567,8 @@ __global__ void __launch_bounds__(kPfThreads) prefill_gateup_kernel(PrefillArgs 
                 for (int j = 0; j < 8; ++j) {
                     const float gj = (float)(half_t)(g[j] * kRsqrt128 * (float)hg[j]);
                     const float uj = (float)(half_t)(u[j] * kRsqrt128 * (float)hu[j]);
-                    const float aj = (float)(half_t)(gj / (1.0f + expf(-gj)) * uj);
+                    // SiLU with the hardware exp and reciprocal (about 1 ulp in fp32 each, then rounded to fp16)
+                    const float aj = (float)(half_t)(gj * __frcp_rn(1.0f + __expf(-gj)) * uj);
                     av[j] = (float)(half_t)(aj * (float)hd[j]);
                 }
                 row_fwht128(av);
@@ -615,7 +621,7 @@ __global__ void __launch_bounds__(kPfThreads) prefill_down_kernel(PrefillArgs A)
 #pragma unroll
             for (int i = 0; i < kPass; ++i) {
                 const int rr = 2 * (wv + kPfWaves * i) + (l >> 5), row = m * 64 + rr;
-                const float* er = ep + rr * 256 + hb * 128 + (l & 15) * 8;
+                const float* er = ep + rr * kEpRow + hb * 128 + (l & 15) * 8;
                 float v[8];
 #pragma unroll
                 for (int j = 0; j < 8; ++j) v[j] = er[j];
