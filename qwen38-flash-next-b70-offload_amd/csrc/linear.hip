@@ -126,18 +126,14 @@ __device__ __forceinline__ void sum2_agent(const float* p, int n, size_t stride,
     }
 }
 
+// One wave's share: the weights of 128-row block kb x 64-column group cg (loads issued first), the input Hadamards of
+// that block for every row into xqw [MR][64] (their sums into sswv [MR]), the dequant-GEMV, and the wave's 64 column
+// sums per row into redw [MR][64]
 template <int K, int MR>
-__global__ void __launch_bounds__(64 * kLinWaves) lin_small_kernel(LinearArgs A, void* out, int out_dt,
-                                                                  int64_t out_stride) {
+__device__ __forceinline__ void lin_wave(const LinearArgs& A, int kb, int cg, int nb, half2_t (*xqw)[64], float* sswv,
+                                         float (*redw)[64]) {
     using GQ = typename LinGemvSel<K, kLinMfma<K, MR>>::type;
-    __shared__ half2_t xq[kLinWaves][MR][64];
-    __shared__ float ssw[kLinWaves][MR];
-    __shared__ float red[kLinWaves][MR][64];
-    __shared__ int last;
-    const int kbn = A.k / 128, P = A.P;
-    const int cg = blockIdx.x / P, ks = blockIdx.x % P, nb = cg >> 1;
-    const int wv = threadIdx.x >> 6, l = lane_id();
-    const int kb = ks * kLinWaves + wv;
+    const int kbn = A.k / 128, l = lane_id();
     const bool in_k = kb < kbn;                  // waves past the end of k add nothing
     // the loads that depend on nothing go first: the weights, the activations and the block's shard index
     GQ gv;
@@ -165,16 +161,16 @@ __global__ void __launch_bounds__(64 * kLinWaves) lin_small_kernel(LinearArgs A,
         }
         wave_fwht128(v0, v1);
         const half2_t v = half2_t{(half_t)(v0 * kRsqrt128), (half_t)(v1 * kRsqrt128)};
-        xq[wv][m][l] = v;
+        xqw[m][l] = v;
         const float s = wave_sum((float)v.x + (float)v.y);
-        if (l == 0) ssw[wv][m] = s;
+        if (l == 0) sswv[m] = s;
     }
     if constexpr (kLinMfma<K, MR>) {
         float4_t acc[2][2];
 #pragma unroll
         for (int c = 0; c < 2; ++c)
             acc[c][0] = acc[c][1] = float4_t{0.f, 0.f, 0.f, 0.f};
-        if (live) gv.template compute<MR>(&xq[wv][0][0], acc);      // the wave's own LDS rows: no barrier
+        if (live) gv.template compute<MR>(&xqw[0][0], acc);      // the wave's own LDS rows: no barrier
         const int n = l & 15, q4 = 4 * (l >> 4);
 #pragma unroll
         for (int c = 0; c < 2; ++c)
@@ -182,25 +178,38 @@ __global__ void __launch_bounds__(64 * kLinWaves) lin_small_kernel(LinearArgs A,
             for (int h = 0; h < 2; ++h)
 #pragma unroll
                 for (int v = 0; v < 4; ++v)
-                    if (q4 + v < MR) red[wv][q4 + v][16 * (2 * c + ((n >> 3) & 1)) + 8 * h + (n & 7)] = acc[c][h][v];
+                    if (q4 + v < MR) redw[q4 + v][16 * (2 * c + ((n >> 3) & 1)) + 8 * h + (n & 7)] = acc[c][h][v];
     } else {
         float acc[MR][GQ::NCQ][2];
 #pragma unroll
         for (int m = 0; m < MR; ++m)
 #pragma unroll
             for (int q = 0; q < GQ::NCQ; ++q) acc[m][q][0] = acc[m][q][1] = 0.f;
-        if (live) gv.template compute_mr<MR>(&xq[wv][0][0], acc);     // the wave's own LDS rows: no barrier
+        if (live) gv.template compute_mr<MR>(&xqw[0][0], acc);     // the wave's own LDS rows: no barrier
 #pragma unroll
         for (int m = 0; m < MR; ++m)
 #pragma unroll
             for (int q = 0; q < GQ::NCQ; ++q) {
                 int c0;
                 if (GQ::reduce(acc[m][q], q, c0)) {
-                    red[wv][m][c0] = acc[m][q][0];
-                    red[wv][m][c0 + 8] = acc[m][q][1];
+                    redw[m][c0] = acc[m][q][0];
+                    redw[m][c0 + 8] = acc[m][q][1];
                 }
             }
     }
+}
+
+template <int K, int MR>
+__global__ void __launch_bounds__(64 * kLinWaves) lin_small_kernel(LinearArgs A, void* out, int out_dt,
+                                                                  int64_t out_stride) {
+    __shared__ half2_t xq[kLinWaves][MR][64];
+    __shared__ float ssw[kLinWaves][MR];
+    __shared__ float red[kLinWaves][MR][64];
+    __shared__ int last;
+    const int P = A.P;
+    const int cg = blockIdx.x / P, ks = blockIdx.x % P, nb = cg >> 1;
+    const int wv = threadIdx.x >> 6, l = lane_id();
+    lin_wave<K, MR>(A, ks * kLinWaves + wv, cg, nb, xq[wv], ssw[wv], red[wv]);
     __syncthreads();
     for (int i = threadIdx.x; i < MR * 64; i += 64 * kLinWaves) {
         const int m = i >> 6, c = i & 63;
@@ -279,6 +288,43 @@ __global__ void __launch_bounds__(256) lin_reconstruct_kernel(const uint32_t* __
     dequant_store<K, 0>(P, p, w + (size_t)r * 16 * ld + (size_t)tl * 16, ld);
 }
 
+// k <= 512 (one K-slice): a workgroup of 8 waves takes both 64-column groups of a 128-column block (waves 0-3 the
+// first, 4-7 the second, one 128-row block each), sums the slice in LDS and applies the output Hadamard itself: no
+// partials in global memory and no arrival counter. Same sums in the same order as lin_small_kernel with P = 1.
+constexpr int kLin1Waves = 8;
+template <int K, int MR>
+__global__ void __launch_bounds__(64 * kLin1Waves) lin_small1_kernel(LinearArgs A, void* out, int out_dt,
+                                                                    int64_t out_stride) {
+    __shared__ half2_t xq[kLin1Waves][MR][64];
+    __shared__ float ssw[kLin1Waves][MR];
+    __shared__ float red[kLin1Waves][MR][64];
+    __shared__ float yb[MR][128];
+    const int nb = blockIdx.x;
+    const int wv = threadIdx.x >> 6, l = lane_id();
+    lin_wave<K, MR>(A, wv & 3, 2 * nb + (wv >> 2), nb, xq[wv], ssw[wv], red[wv]);
+    __syncthreads();
+    for (int i = threadIdx.x; i < MR * 128; i += 64 * kLin1Waves) {
+        const int m = i >> 7, c = i & 127, w0 = (c >> 6) * 4;
+        if (m >= A.M) continue;
+        float t = 0.f, xs = 0.f;                 // the 4 blocks in order
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+            t += red[w0 + w][m][c & 63];
+            xs += ssw[w][m];
+        }
+        yb[m][c] = 0.f + (kC1 * t + kC2 * xs);
+    }
+    __syncthreads();
+    const half2_t sv = *(const half2_t*)(A.svh + nb * 128 + 2 * l);
+    for (int m = wv; m < A.M; m += kLin1Waves) {
+        float v0 = yb[m][2 * l], v1 = yb[m][2 * l + 1];
+        wave_fwht128(v0, v1);
+        const size_t o = (size_t)m * out_stride + nb * 128 + 2 * l;
+        st_act(out, out_dt, o, v0 * kRsqrt128 * (float)sv.x);
+        st_act(out, out_dt, o + 1, v1 * kRsqrt128 * (float)sv.y);
+    }
+}
+
 // ---- launchers -----------------------------------------------------------------------------------------------------
 
 hipError_t launch_linear_had_in(const LinearArgs& a, hipStream_t s) {
@@ -289,6 +335,18 @@ hipError_t launch_linear_had_in(const LinearArgs& a, hipStream_t s) {
 
 template <int K>
 static hipError_t small_rows(const LinearArgs& a, void* out, int out_dt, int64_t out_stride, hipStream_t s) {
+    if (a.P == 1) {
+        const dim3 grid1((unsigned)(a.n / 128)), block1(64 * kLin1Waves);
+        if (a.M <= 1) hipLaunchKernelGGL((lin_small1_kernel<K, 1>), grid1, block1, 0, s, a, out, out_dt, out_stride);
+        else if (a.M <= 2)
+            hipLaunchKernelGGL((lin_small1_kernel<K, 2>), grid1, block1, 0, s, a, out, out_dt, out_stride);
+        else if (a.M <= 4)
+            hipLaunchKernelGGL((lin_small1_kernel<K, 4>), grid1, block1, 0, s, a, out, out_dt, out_stride);
+        else if (a.M <= kLinMaxRows)
+            hipLaunchKernelGGL((lin_small1_kernel<K, kLinMaxRows>), grid1, block1, 0, s, a, out, out_dt, out_stride);
+        else return hipErrorInvalidValue;
+        return hipGetLastError();
+    }
     const dim3 grid((unsigned)((a.n / 64) * a.P)), block(64 * kLinWaves);
     if (a.M <= 1) hipLaunchKernelGGL((lin_small_kernel<K, 1>), grid, block, 0, s, a, out, out_dt, out_stride);
     else if (a.M <= 2) hipLaunchKernelGGL((lin_small_kernel<K, 2>), grid, block, 0, s, a, out, out_dt, out_stride);
