@@ -19,6 +19,7 @@
 #include "exl3_kernels.h"
 
 #include <algorithm>
+#include <type_traits>
 #include <utility>
 
 namespace exl3 {
@@ -456,22 +457,37 @@ __device__ __forceinline__ void gemm_core(const uint32_t* tr, int tiles_n, int n
     // this lane's B-fragment offsets (columns 64 q + l % 32 and + 32, k-half l / 32)
     const int n = q * 64 + (l & 31);
     const int boff0 = b_slot(n >> 4, n & 15, l >> 5), boff1 = b_slot((n + 32) >> 4, n & 15, l >> 5);
-    auto mfma = [&](int cur) {
+    // the wave's live row blocks j < nj (rb = rpar + 2 j < nrb), as a compile-time count: no branch per block, so the
+    // fragment reads of a K step go out together
+    const int nj = (nrb - rpar + 1) >> 1;
+    auto mfma_n = [&](auto NJ, int cur) {
+        constexpr int kNj = decltype(NJ)::value;
         const uint8_t* bb = b0 + cur * kBChunk;
         const uint8_t* ab = a0 + cur * (NPROJ * kAProj) + proj * kAProj;
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) {
+            // all fragment reads of the K step first (the fence keeps them ahead of the MFMAs)
             const half8_t f0 = *(const half8_t*)(bb + ks * kBRow + boff0);
             const half8_t f1 = *(const half8_t*)(bb + ks * kBRow + boff1);
+            half8_t fa[kNj];
 #pragma unroll
-            for (int j = 0; j < kPfRb; ++j) {
-                const int rb = rpar + 2 * j;
-                if (rb < nrb) {
-                    const half8_t fa = *(const half8_t*)(ab + a_slot(rb * 32 + (l & 31), 2 * ks + (l >> 5)));
-                    acc[j][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa, f0, acc[j][0], 0, 0, 0);
-                    acc[j][1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa, f1, acc[j][1], 0, 0, 0);
-                }
+            for (int j = 0; j < kNj; ++j)
+                fa[j] = *(const half8_t*)(ab + a_slot((rpar + 2 * j) * 32 + (l & 31), 2 * ks + (l >> 5)));
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int j = 0; j < kNj; ++j) {
+                acc[j][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[j], f0, acc[j][0], 0, 0, 0);
+                acc[j][1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[j], f1, acc[j][1], 0, 0, 0);
             }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+    auto mfma = [&](int cur) {
+        switch (nj) {
+            case 3: mfma_n(std::integral_constant<int, 3>{}, cur); break;
+            case 2: mfma_n(std::integral_constant<int, 2>{}, cur); break;
+            case 1: mfma_n(std::integral_constant<int, 1>{}, cur); break;
+            default: break;
         }
     };
     auto produce = [&](int c) {                   // chunk c + 1 into its buffers, loads of chunk c + 2
