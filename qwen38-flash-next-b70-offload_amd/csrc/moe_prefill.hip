@@ -654,16 +654,34 @@ __global__ void __launch_bounds__(kPfThreads) prefill_down_kernel(PrefillArgs A)
     }
 }
 
-// out[m][h] = sum over k (in order) of y[pair_of[m topk + k]][h]; 8 columns per thread
+// out[m][h] = sum over k (in order) of y[pair_of[m topk + k]][h]; 8 columns per thread. Up to kCombMax picks: all
+// pick positions, then all rows' loads go out before the sum (a loop would wait for each position and each row in
+// turn); more picks take the loop.
+constexpr int kCombMax = 16;
 __global__ void __launch_bounds__(256) prefill_combine_kernel(PrefillArgs A) {
-    const int m = blockIdx.x, H = A.g.H;
+    const int m = blockIdx.x, H = A.g.H, topk = A.topk;
     for (int h0 = threadIdx.x * 8; h0 < H; h0 += 256 * 8) {
         float acc[8] = {};
-        for (int k = 0; k < A.topk; ++k) {
-            const int pos = A.pair_of[m * A.topk + k];
-            const half8_t v = *(const half8_t*)(A.y + (size_t)pos * H + h0);
+        if (topk <= kCombMax) {
+            // without a branch per pick (picks past topk repeat the last one and are not summed)
+            int pos[kCombMax];
 #pragma unroll
-            for (int j = 0; j < 8; ++j) acc[j] += (float)v[j];
+            for (int k = 0; k < kCombMax; ++k) pos[k] = A.pair_of[m * topk + min(k, topk - 1)];
+            half8_t v[kCombMax];
+#pragma unroll
+            for (int k = 0; k < kCombMax; ++k) v[k] = *(const half8_t*)(A.y + (size_t)pos[k] * H + h0);
+#pragma unroll
+            for (int k = 0; k < kCombMax; ++k)
+                if (k < topk)
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) acc[j] += (float)v[k][j];
+        } else {
+            for (int k = 0; k < topk; ++k) {
+                const int pos = A.pair_of[m * topk + k];
+                const half8_t v = *(const half8_t*)(A.y + (size_t)pos * H + h0);
+#pragma unroll
+                for (int j = 0; j < 8; ++j) acc[j] += (float)v[j];
+            }
         }
         const size_t oo = (size_t)m * A.out_stride + h0;
 #pragma unroll
