@@ -9,7 +9,7 @@
 //
 // Codebook mul1 (exl3_esimd.h:40-68): x = s * 0x83DCD12D mod 2^32, h = 1024 + bytesum(x) (its bit pattern is
 // 0x6400 + bytesum as fp16, exact), w = RNE_fp16(h * c1 + c2). On gfx950 v_mul_lo_u32 is full rate, so the decode is
-// bfe + mul + sad (+ the consumer's FMA).
+// bfe + mul + sad, and two values that share an activation pair go through one v_dot2_f32_f16.
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -47,6 +47,15 @@ __device__ __forceinline__ uint32_t cb_raw(uint32_t s) {
 }
 __device__ __forceinline__ half_t cb_h(uint32_t s) {
     return __builtin_bit_cast(half_t, (uint16_t)cb_raw(s));
+}
+// h of states s0 and s1 as one packed fp16 pair (s0 in the low half) in two instructions after the multiplies:
+// v_sad_u8 adds bytesum(s0 * mul1) to 0x6400 in both halves (at most 0x67FC, no carry into the high half), then
+// v_sad_hi_u8 adds bytesum(s1 * mul1) << 16
+__device__ __forceinline__ uint32_t cb_raw2(uint32_t s0, uint32_t s1) {
+    return __builtin_amdgcn_sad_hi_u8(s1 * kMul1, 0u, __builtin_amdgcn_sad_u8(s0 * kMul1, 0u, 0x64006400u));
+}
+__device__ __forceinline__ half2_t cb_h2(uint32_t s0, uint32_t s1) {
+    return __builtin_bit_cast(half2_t, cb_raw2(s0, s1));
 }
 // bit-exact codebook value: h * c1 + c2 is exact in fp32 (22 significant bits), one rounding to fp16 (RNE)
 __device__ __forceinline__ half_t cb_w(uint32_t s) {

@@ -5,30 +5,28 @@
 
 namespace exl3 {
 
-// one period of one tile-row: xv[a][qq] holds activation rows (8a + 2q, 8a + 2q + 1), q = (qb + qq) & 3
+// one period of one tile-row: xv[a][qq] holds activation rows (8a + 2q, 8a + 2q + 1), q = (qb + qq) & 3. Values u and
+// u + 1 (u even) are the rows of one activation pair in the same column, so one v_dot2_f32_f16 takes both.
 template <int K, int NQ, int u>
 __device__ __forceinline__ void accum_period(const Period<K>& P, const half2_t (&xv)[2][NQ], float (&acc)[2]) {
     if constexpr (u < Geo<K>::V) {
-        const half_t h = cb_h(P.template state<u>());
-        const half2_t xp = xv[(u >> 1) & 1][u >> 3];
-        const half_t xs = (u & 1) ? xp.y : xp.x;
-        acc[(u >> 2) & 1] = __builtin_fmaf((float)h, (float)xs, acc[(u >> 2) & 1]);
-        accum_period<K, NQ, u + 1>(P, xv, acc);
+        static_assert(u % 2 == 0 && Geo<K>::V % 2 == 0, "values are taken in pairs");
+        const half2_t h = cb_h2(P.template state<u>(), P.template state<u + 1>());
+        acc[(u >> 2) & 1] = __builtin_amdgcn_fdot2(h, xv[(u >> 1) & 1][u >> 3], acc[(u >> 2) & 1], false);
+        accum_period<K, NQ, u + 2>(P, xv, acc);
     }
 }
 
-// the same for MR activation rows at once: each codebook value is decoded once and multiplied into every row
+// the same for MR activation rows at once: each pair of codebook values is decoded once and multiplied into every row
 template <int K, int NQ, int MR, int u>
 __device__ __forceinline__ void accum_period_mr(const Period<K>& P, const half2_t (&xv)[MR][2][NQ],
                                                 float (&acc)[MR][2]) {
     if constexpr (u < Geo<K>::V) {
-        const float h = (float)cb_h(P.template state<u>());
+        const half2_t h = cb_h2(P.template state<u>(), P.template state<u + 1>());
 #pragma unroll
-        for (int m = 0; m < MR; ++m) {
-            const half2_t xp = xv[m][(u >> 1) & 1][u >> 3];
-            acc[m][(u >> 2) & 1] = __builtin_fmaf(h, (float)((u & 1) ? xp.y : xp.x), acc[m][(u >> 2) & 1]);
-        }
-        accum_period_mr<K, NQ, MR, u + 1>(P, xv, acc);
+        for (int m = 0; m < MR; ++m)
+            acc[m][(u >> 2) & 1] = __builtin_amdgcn_fdot2(h, xv[m][(u >> 1) & 1][u >> 3], acc[m][(u >> 2) & 1], false);
+        accum_period_mr<K, NQ, MR, u + 2>(P, xv, acc);
     }
 }
 

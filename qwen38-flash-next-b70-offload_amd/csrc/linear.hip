@@ -29,7 +29,8 @@ typedef float float4_t __attribute__((ext_vector_type(4)));
 // 2 (ps >> 1) + ((l >> 3) & 1), so the 16 lanes of MFMA k-group q = l >> 4 share one tile-row and each lane's period
 // holds the 8-row halves (rows 8 i .. 8 i + 7) of its two columns p and p + 8 that the B operand needs. The B values are the raw codebook integers h (exact in fp16,
 // two packed per register); A = the rows' xh over the same 4-row slices (zero for rows past MR); the raw-h affine is
-// applied to the column sums as in the VALU version. VALU per weight: bfe, mul, sad and half a pack, for any MR.
+// applied to the column sums as in the VALU version. VALU per weight: bfe, mul and sad (v_sad_hi_u8 packs the pair),
+// for any MR.
 template <int K>
 struct GemvMfma {
     static constexpr int D = Geo<K>::D;
@@ -49,7 +50,7 @@ struct GemvMfma {
     // raw h of values u and u + 1 packed into one register (h of u in the low half)
     template <int u>
     __device__ __forceinline__ static uint32_t pair(const Period<K>& P) {
-        return cb_raw(P.template state<u>()) | (cb_raw(P.template state<u + 1>()) << 16);
+        return cb_raw2(P.template state<u>(), P.template state<u + 1>());
     }
     // rows 8 i .. 8 i + 7 of column p + 8 h: u = 2 i + 4 h + {0, 1, 8, 9, 16, 17, 24, 25} in row order
     template <int i, int h>
