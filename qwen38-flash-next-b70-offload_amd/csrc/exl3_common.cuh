@@ -61,6 +61,12 @@ __device__ __forceinline__ half2_t cb_h2(uint32_t s0, uint32_t s1) {
 __device__ __forceinline__ half_t cb_w(uint32_t s) {
     return (half_t)__builtin_fmaf((float)cb_h(s), kC1, kC2);
 }
+// the same for states s0 and s1 (s0 in the low half) in one v_pk_fma_f16: c1 and c2 are fp16 values and the fused
+// multiply-add rounds the exact h * c1 + c2 once (RNE), so each half equals cb_w (no result is subnormal: |w| > 1e-3)
+__device__ __forceinline__ half2_t cb_w2(uint32_t s0, uint32_t s1) {
+    return __builtin_elementwise_fma(cb_h2(s0, s1), half2_t{(half_t)kC1, (half_t)kC1},
+                                     half2_t{(half_t)kC2, (half_t)kC2});
+}
 
 // ---- trellis state extraction -----------------------------------------------------------------------------------------
 // Period-relative stream bits: [-32, 0) = previous period's last word, [32j, 32j+32) = word j of the period.

@@ -30,12 +30,15 @@ __device__ __forceinline__ void accum_period_mr(const Period<K>& P, const half2_
     }
 }
 
-// bit-exact store of one period's values (row/col of value u depend on the period for K != 3)
+// bit-exact store of one period's values (row/col of value u depend on the period for K != 3), decoded in pairs as
+// the prefill decoder does, so that the exhaustive dequant checks cover both halves of cb_w2
 template <int K, int u>
 __device__ __forceinline__ void dequant_store(const Period<K>& P, int p, _Float16* o, size_t n_out) {
     if constexpr (u < Geo<K>::V) {
-        o[(size_t)val_row<K>(p, u) * n_out + val_col<K>(p, u)] = cb_w(P.template state<u>());
-        dequant_store<K, u + 1>(P, p, o, n_out);
+        const half2_t w = cb_w2(P.template state<u>(), P.template state<u + 1>());
+        o[(size_t)val_row<K>(p, u) * n_out + val_col<K>(p, u)] = w.x;
+        o[(size_t)val_row<K>(p, u + 1) * n_out + val_col<K>(p, u + 1)] = w.y;
+        dequant_store<K, u + 2>(P, p, o, n_out);
     }
 }
 

@@ -337,11 +337,15 @@ struct ChunkDecoder {
         }
     }
 
-    // slot (column 8 ci + (V p >> 5), k-half kh): values u = 8 (e >> 1) + 4 ci + 2 kh + (e & 1), e = 0 .. E - 1
+    // slot (column 8 ci + (V p >> 5), k-half kh): values u = 8 (e >> 1) + 4 ci + 2 kh + (e & 1), e = 0 .. E - 1; the
+    // values e = 2 f and 2 f + 1 are states u and u + 1, decoded as one pair
     typedef _Float16 hv_t __attribute__((ext_vector_type(E)));
-    template <int ci, int kh, int... e>
-    __device__ __forceinline__ static hv_t slot_vals(const Period<K>& P, std::integer_sequence<int, e...>) {
-        return hv_t{cb_w(P.template state<((e >> 1) << 3) | (ci << 2) | (kh << 1) | (e & 1)>())...};
+    typedef uint32_t hp_t __attribute__((ext_vector_type(E / 2)));
+    template <int ci, int kh, int... f>
+    __device__ __forceinline__ static hv_t slot_vals(const Period<K>& P, std::integer_sequence<int, f...>) {
+        return __builtin_bit_cast(
+            hv_t, hp_t{__builtin_bit_cast(uint32_t, cb_w2(P.template state<(f << 3) | (ci << 2) | (kh << 1)>(),
+                                                          P.template state<(f << 3) | (ci << 2) | (kh << 1) | 1>()))...});
     }
 
     // this thread's periods of the chunk (the previous word of each comes from the neighbouring lane)
@@ -358,7 +362,7 @@ struct ChunkDecoder {
     // slot s (= 2 ci + kh) of every period: a quarter of the chunk's values of this thread
     template <int s>
     __device__ __forceinline__ static void slot(const Period<K> (&P)[PER], hv_t (&o)[PER][4]) {
-        constexpr auto es = std::make_integer_sequence<int, E>{};
+        constexpr auto es = std::make_integer_sequence<int, E / 2>{};
 #pragma unroll
         for (int j = 0; j < PER; ++j) o[j][s] = slot_vals<(s >> 1), (s & 1)>(P[j], es);
     }
@@ -390,7 +394,7 @@ struct ChunkDecoder {
     __device__ __forceinline__ void decode_store(uint8_t* buf) const {
         Period<K> P[PER];
         prep(P);
-        constexpr auto es = std::make_integer_sequence<int, E>{};
+        constexpr auto es = std::make_integer_sequence<int, E / 2>{};
 #pragma unroll
         for (int j = 0; j < PER; ++j) {
             const int q = threadIdx.x + j * kPfThreads;
