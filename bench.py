@@ -38,7 +38,7 @@ HBM_PEAK = 8000.0   # GB/s, MI355X HBM3E
 # HBM counters of one resident moe_layer_kernel<3> call at this workload (KiB per dispatch, rocprofv3 --pmc FETCH_SIZE
 # and --pmc WRITE_SIZE over bench.py --roofline-only) and the factor that maps each counter to the bytes of a plain
 # 256 MiB device copy in the same runs; re-measured whenever the kernel changes.
-PMC_KIB = {"fetch": 7223.0, "write": 467.0}
+PMC_KIB = {"fetch": 7211.0, "write": 467.0}
 PMC_SCALE = {"fetch": 262144 / 131087.2, "write": 1.0}
 
 

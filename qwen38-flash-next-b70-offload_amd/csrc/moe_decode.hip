@@ -3,8 +3,8 @@
 //
 //   gate/up WGs (ids 0 .. n_gu-1), one per (pair, projection, PLANAR4 group of 4 tile-columns = 64 columns of I,
 //     1024-row slice of H): issue their trellis-word loads first, then the input Hadamard of x*suh (one 128-row block
-//     per wave), the trellis GEMV (one period per lane: bfe + mul + sad + fma_mix per weight) with an in-WG reduction,
-//     and publish the 64 column sums (fp32) of the slice for the pair.
+//     per wave), the trellis GEMV (one period per lane: bfe + mul + sad per weight, one v_dot2_f32_f16 per two) with an
+//     in-WG reduction, and publish the 64 column sums (fp32) of the slice for the pair.
 //   down WGs (ids n_gu ..), one per (pair, 128-column block of H) over the whole K = I: issue their word loads, wait
 //     (bounded) for the pair's gate/up sums, run the gate/up epilogue of the pair themselves (output Hadamards * svh,
 //     SiLU(g)*u, *suh_d, down-input Hadamard -> the down input in LDS, fp16), GEMV with an in-WG reduction, epilogue
@@ -25,7 +25,8 @@
 // keeps fp16 partials per tile-row); the fp16 rounding points of the epilogues are the reference's.
 //
 // The codebook affine w = c1*h + c2 is applied to the dot product: sum_k w_k x_k = c1 sum_k h_k x_k + c2 sum_k x_k,
-// with h the exact fp16 1024 + bytesum, so the inner loop is bfe, mul, sad and one mixed-precision FMA per weight.
+// with h the exact fp16 1024 + bytesum, so the inner loop is bfe, mul and sad per weight and one v_dot2_f32_f16 per
+// two weights (the two h of a dot product packed by v_sad_hi_u8).
 #include "exl3_common.cuh"
 #include "exl3_gemv.cuh"
 #include "exl3_ensure.cuh"
