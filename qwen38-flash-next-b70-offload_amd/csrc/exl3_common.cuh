@@ -206,6 +206,72 @@ __device__ __forceinline__ void row_fwht128(float (&v)[8]) {
     }
 }
 
+// row_fwht128 up to a sign per lane, in fewer instructions: each cross-lane butterfly is v + s p with the lane's sign
+// s, so the partner p is the multiplicand and its DPP move folds into the v_fmac_f32 (the compiler does not fold a DPP
+// move into v_fmac_f32, so the stages are written as such). The upper lane of a pair then holds v - p = -(p - v)
+// (exactly: rounding to nearest is symmetric), and the two lanes of every later pair carry the same accumulated sign,
+// so the result is exactly row_sign() times row_fwht128's. Callers fold row_sign() into the scale they multiply by.
+__device__ __forceinline__ float row_sign() {
+    return (__builtin_popcount(lane_id() & 15) & 1) ? -1.0f : 1.0f;
+}
+__device__ __forceinline__ void row_fwht128_signed(float (&v)[8]) {
+#pragma unroll
+    for (int h = 1; h < 8; h <<= 1)
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+            if (!(j & h)) {
+                const float a = v[j], b = v[j + h];
+                v[j] = a + b;
+                v[j + h] = a - b;
+            }
+    const int l = lane_id();
+    const float s1 = (l & 1) ? -1.0f : 1.0f, s2 = (l & 2) ? -1.0f : 1.0f;
+    const float s4 = (l & 4) ? -1.0f : 1.0f, s8 = (l & 8) ? -1.0f : 1.0f;
+    // v[j] += s * v[j] of lane l ^ m. Each block starts with s_nop 1: a DPP source must be written by a VALU at least
+    // two wait states before it is read, whatever the compiler placed before the block; inside a block every DPP
+    // source was written at least seven instructions earlier.
+#define EXL3_FMAC8(CTRL, S)                                                                                      \
+    asm("s_nop 1\n\t"                                                                                          \
+        "v_fmac_f32_dpp %0, %0, %8 " CTRL " row_mask:0xf bank_mask:0xf\n\t"                                    \
+        "v_fmac_f32_dpp %1, %1, %8 " CTRL " row_mask:0xf bank_mask:0xf\n\t"                                    \
+        "v_fmac_f32_dpp %2, %2, %8 " CTRL " row_mask:0xf bank_mask:0xf\n\t"                                    \
+        "v_fmac_f32_dpp %3, %3, %8 " CTRL " row_mask:0xf bank_mask:0xf\n\t"                                    \
+        "v_fmac_f32_dpp %4, %4, %8 " CTRL " row_mask:0xf bank_mask:0xf\n\t"                                    \
+        "v_fmac_f32_dpp %5, %5, %8 " CTRL " row_mask:0xf bank_mask:0xf\n\t"                                    \
+        "v_fmac_f32_dpp %6, %6, %8 " CTRL " row_mask:0xf bank_mask:0xf\n\t"                                    \
+        "v_fmac_f32_dpp %7, %7, %8 " CTRL " row_mask:0xf bank_mask:0xf"                                          \
+        : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]), "+v"(v[4]), "+v"(v[5]), "+v"(v[6]), "+v"(v[7])          \
+        : "v"(S))
+    EXL3_FMAC8("quad_perm:[1,0,3,2]", s1);                                                      // xor 1
+    EXL3_FMAC8("quad_perm:[2,3,0,1]", s2);                                                      // xor 2
+    {   // xor 4: the half-row mirror (lane ^ 7) as its own move, then quad_perm [3,2,1,0] (^ 3) in the multiply-add
+        float h[8];
+        asm("s_nop 1\n\t"
+            "v_mov_b32_dpp %0, %8 row_half_mirror row_mask:0xf bank_mask:0xf\n\t"
+            "v_mov_b32_dpp %1, %9 row_half_mirror row_mask:0xf bank_mask:0xf\n\t"
+            "v_mov_b32_dpp %2, %10 row_half_mirror row_mask:0xf bank_mask:0xf\n\t"
+            "v_mov_b32_dpp %3, %11 row_half_mirror row_mask:0xf bank_mask:0xf\n\t"
+            "v_mov_b32_dpp %4, %12 row_half_mirror row_mask:0xf bank_mask:0xf\n\t"
+            "v_mov_b32_dpp %5, %13 row_half_mirror row_mask:0xf bank_mask:0xf\n\t"
+            "v_mov_b32_dpp %6, %14 row_half_mirror row_mask:0xf bank_mask:0xf\n\t"
+            "v_mov_b32_dpp %7, %15 row_half_mirror row_mask:0xf bank_mask:0xf\n\t"
+            "s_nop 1\n\t"
+            "v_fmac_f32_dpp %8, %0, %16 quad_perm:[3,2,1,0] row_mask:0xf bank_mask:0xf\n\t"
+            "v_fmac_f32_dpp %9, %1, %16 quad_perm:[3,2,1,0] row_mask:0xf bank_mask:0xf\n\t"
+            "v_fmac_f32_dpp %10, %2, %16 quad_perm:[3,2,1,0] row_mask:0xf bank_mask:0xf\n\t"
+            "v_fmac_f32_dpp %11, %3, %16 quad_perm:[3,2,1,0] row_mask:0xf bank_mask:0xf\n\t"
+            "v_fmac_f32_dpp %12, %4, %16 quad_perm:[3,2,1,0] row_mask:0xf bank_mask:0xf\n\t"
+            "v_fmac_f32_dpp %13, %5, %16 quad_perm:[3,2,1,0] row_mask:0xf bank_mask:0xf\n\t"
+            "v_fmac_f32_dpp %14, %6, %16 quad_perm:[3,2,1,0] row_mask:0xf bank_mask:0xf\n\t"
+            "v_fmac_f32_dpp %15, %7, %16 quad_perm:[3,2,1,0] row_mask:0xf bank_mask:0xf"
+            : "=&v"(h[0]), "=&v"(h[1]), "=&v"(h[2]), "=&v"(h[3]), "=&v"(h[4]), "=&v"(h[5]), "=&v"(h[6]), "=&v"(h[7]),
+              "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]), "+v"(v[4]), "+v"(v[5]), "+v"(v[6]), "+v"(v[7])
+            : "v"(s4));
+    }
+    EXL3_FMAC8("row_ror:8", s8);                                                                // xor 8
+#undef EXL3_FMAC8
+}
+
 __device__ __forceinline__ float bf16_to_f32(bf16_bits b) { return __uint_as_float((uint32_t)b << 16); }
 __device__ __forceinline__ bf16_bits f32_to_bf16(float f) {
     uint32_t u = __float_as_uint(f);

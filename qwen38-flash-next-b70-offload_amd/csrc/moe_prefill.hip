@@ -646,8 +646,10 @@ __global__ void __launch_bounds__(kPfThreads) prefill_down_kernel(PrefillArgs A)
                 float v[8];
 #pragma unroll
                 for (int j = 0; j < 8; ++j) v[j] = er[j];
-                row_fwht128(v);
-                const float sc = kRsqrt128 * pw[i];
+                // the DPP-folded transform (fewer VALU instructions; the gate/up epilogue, with three transforms per
+                // row, measured slower with it and keeps row_fwht128)
+                row_fwht128_signed(v);
+                const float sc = row_sign() * kRsqrt128 * pw[i];
                 half8_t o;
 #pragma unroll
                 for (int j = 0; j < 8; ++j) o[j] = (half_t)(v[j] * sc * (float)hs[j]);
