@@ -167,6 +167,9 @@ __device__ __forceinline__ float wave_sum(float v) {
 // In-wave unnormalised Sylvester Walsh-Hadamard of 128 values, lane l holding x[2l] (v0) and x[2l+1] (v1).
 // Butterflies in the order of exl3_esimd.h:210-220 (h = 1, 2, ..., 64), lower element a + b, upper a - b: the fp32
 // results are identical to the sequential restatement.
+// Each cross-lane butterfly is one FMA with the lane's sign s (+1 lower, -1 upper), no select: v s + p inside a row
+// (v + p, p - v), and across rows the permlane swap's own pair (r0, r1), which is (own, partner) in the lower half and
+// (partner, own) in the upper, as r0 + s r1. Each result is the same single rounding of the same two operands.
 __device__ __forceinline__ void wave_fwht128(float& v0, float& v1) {
     {
         float a = v0 + v1, b = v0 - v1;
@@ -175,11 +178,24 @@ __device__ __forceinline__ void wave_fwht128(float& v0, float& v1) {
     }
     const int l = lane_id();
 #pragma unroll
-    for (int m = 1; m < 64; m <<= 1) {
-        float p0 = lane_xor(v0, m), p1 = lane_xor(v1, m);
-        bool up = (l & m) != 0;
-        v0 = up ? p0 - v0 : v0 + p0;
-        v1 = up ? p1 - v1 : v1 + p1;
+    for (int m = 1; m < 16; m <<= 1) {
+        const float sg = (l & m) ? -1.0f : 1.0f;
+        v0 = __builtin_fmaf(v0, sg, lane_xor(v0, m));
+        v1 = __builtin_fmaf(v1, sg, lane_xor(v1, m));
+    }
+    {
+        const float sg = (l & 16) ? -1.0f : 1.0f;
+        const auto r0 = __builtin_amdgcn_permlane16_swap(__float_as_uint(v0), __float_as_uint(v0), false, false);
+        const auto r1 = __builtin_amdgcn_permlane16_swap(__float_as_uint(v1), __float_as_uint(v1), false, false);
+        v0 = __builtin_fmaf(__uint_as_float(r0[1]), sg, __uint_as_float(r0[0]));
+        v1 = __builtin_fmaf(__uint_as_float(r1[1]), sg, __uint_as_float(r1[0]));
+    }
+    {
+        const float sg = (l & 32) ? -1.0f : 1.0f;
+        const auto r0 = __builtin_amdgcn_permlane32_swap(__float_as_uint(v0), __float_as_uint(v0), false, false);
+        const auto r1 = __builtin_amdgcn_permlane32_swap(__float_as_uint(v1), __float_as_uint(v1), false, false);
+        v0 = __builtin_fmaf(__uint_as_float(r0[1]), sg, __uint_as_float(r0[0]));
+        v1 = __builtin_fmaf(__uint_as_float(r1[1]), sg, __uint_as_float(r1[0]));
     }
 }
 
