@@ -424,13 +424,19 @@ template <int NPROJ>
 struct AStage {
     static constexpr int NL = NPROJ * kPfRows / 64;          // 16-byte loads per lane per chunk (8 rows x 128 B each)
     uint4 v[NL];
+    // rows at or past `rows` read as zero through the buffer descriptor's range (num_records = rows * lda halfs: row
+    // rows - 1 of the last projection still lies inside it, row `rows` of the first does not), so the loads carry no
+    // branch per row
     __device__ __forceinline__ void load(const half_t* a, size_t lda, size_t proj_off, int rows, int k0) {
         const int l = lane_id(), wv = threadIdx.x >> 6;
+        const auto rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<half_t*>(a), (short)0, rows * (int)lda * 2,
+                                                            0x00020000);
 #pragma unroll
         for (int i = 0; i < NL; ++i) {
             const int g = wv + 8 * i, pj = g / (kPfRows / 8), r = (g % (kPfRows / 8)) * 8 + (l >> 3);
-            v[i] = r < rows ? *(const uint4*)(a + pj * proj_off + (size_t)r * lda + k0 + (l & 7) * 8)
-                            : make_uint4(0, 0, 0, 0);
+            const int off = (pj * (int)proj_off + r * (int)lda + k0 + (l & 7) * 8) * 2;
+            const auto t = __builtin_amdgcn_raw_buffer_load_b128(rsrc, off, 0, 0);
+            v[i] = make_uint4(t[0], t[1], t[2], t[3]);
         }
     }
     __device__ __forceinline__ void store(uint8_t* buf, int nrb) const {
