@@ -474,6 +474,31 @@ __device__ __forceinline__ void gemm_core(const uint32_t* tr, int tiles_n, int n
         constexpr int kNj = decltype(NJ)::value;
         const uint8_t* bb = b0 + cur * kBChunk;
         const uint8_t* ab = a0 + cur * (NPROJ * kAProj) + proj * kAProj;
+        if constexpr (NPROJ == 1 && K <= 3) {
+            // down at K <= 3 (VGPRs to spare; K = 4 would spill): the fragments of K step ks + 1 are read before the MFMAs of step ks, so each
+            // step's MFMAs wait only for reads issued one step earlier
+            half8_t fb[2][2], fa[2][kNj];
+            auto rd = [&](int ks, int st) {
+                fb[st][0] = *(const half8_t*)(bb + ks * kBRow + boff0);
+                fb[st][1] = *(const half8_t*)(bb + ks * kBRow + boff1);
+#pragma unroll
+                for (int j = 0; j < kNj; ++j)
+                    fa[st][j] = *(const half8_t*)(ab + a_slot((rpar + 2 * j) * 32 + (l & 31), 2 * ks + (l >> 5)));
+            };
+            rd(0, 0);
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks) {
+                if (ks + 1 < 4) rd(ks + 1, (ks + 1) & 1);
+                __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                for (int j = 0; j < kNj; ++j) {
+                    acc[j][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[ks & 1][j], fb[ks & 1][0], acc[j][0], 0, 0, 0);
+                    acc[j][1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[ks & 1][j], fb[ks & 1][1], acc[j][1], 0, 0, 0);
+                }
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            return;
+        }
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) {
             // all fragment reads of the K step first (the fence keeps them ahead of the MFMAs)
