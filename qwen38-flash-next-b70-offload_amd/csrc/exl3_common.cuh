@@ -227,6 +227,7 @@ __device__ __forceinline__ void row_fwht128(float (&v)[8]) {
 // move into v_fmac_f32, so the stages are written as such). The upper lane of a pair then holds v - p = -(p - v)
 // (exactly: rounding to nearest is symmetric), and the two lanes of every later pair carry the same accumulated sign,
 // so the result is exactly row_sign() times row_fwht128's. Callers fold row_sign() into the scale they multiply by.
+// The whole wave must be active (DPP reads the partner lane unconditionally).
 __device__ __forceinline__ float row_sign() {
     return (__builtin_popcount(lane_id() & 15) & 1) ? -1.0f : 1.0f;
 }

@@ -424,9 +424,9 @@ template <int NPROJ>
 struct AStage {
     static constexpr int NL = NPROJ * kPfRows / 64;          // 16-byte loads per lane per chunk (8 rows x 128 B each)
     uint4 v[NL];
-    // rows at or past `rows` read as zero through the buffer descriptor's range (num_records = rows * lda halfs: row
-    // rows - 1 of the last projection still lies inside it, row `rows` of the first does not), so the loads carry no
-    // branch per row
+    // rows at or past `rows` read as zero through the buffer descriptor's range (num_records = rows * lda halfs, in
+    // bytes: row rows - 1 of the last projection still lies inside it, row `rows` of the first does not), so the loads
+    // carry no branch per row and nothing past the pass's rows is read
     __device__ __forceinline__ void load(const half_t* a, size_t lda, size_t proj_off, int rows, int k0) {
         const int l = lane_id(), wv = threadIdx.x >> 6;
         const auto rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<half_t*>(a), (short)0, rows * (int)lda * 2,
@@ -475,8 +475,8 @@ __device__ __forceinline__ void gemm_core(const uint32_t* tr, int tiles_n, int n
         const uint8_t* bb = b0 + cur * kBChunk;
         const uint8_t* ab = a0 + cur * (NPROJ * kAProj) + proj * kAProj;
         if constexpr (NPROJ == 1 && K <= 3) {
-            // down at K <= 3 (VGPRs to spare; K = 4 would spill): the fragments of K step ks + 1 are read before the MFMAs of step ks, so each
-            // step's MFMAs wait only for reads issued one step earlier
+            // down at K <= 3 (VGPRs to spare; K = 4 would spill): the fragments of K step ks + 1 are read before the
+            // MFMAs of step ks, so each step's MFMAs wait only for reads issued one step earlier
             half8_t fb[2][2], fa[2][kNj];
             auto rd = [&](int ks, int st) {
                 fb[st][0] = *(const half8_t*)(bb + ks * kBRow + boff0);
