@@ -518,12 +518,15 @@ __device__ __forceinline__ void gemm_core(const uint32_t* tr, int tiles_n, int n
         }
     };
     auto mfma = [&](int cur) {
+        // the multiplying wave issues ahead of the producing wave of its SIMD while its MFMAs last
+        __builtin_amdgcn_s_setprio(1);
         switch (nj) {
             case 3: mfma_n(std::integral_constant<int, 3>{}, cur); break;
             case 2: mfma_n(std::integral_constant<int, 2>{}, cur); break;
             case 1: mfma_n(std::integral_constant<int, 1>{}, cur); break;
             default: break;
         }
+        __builtin_amdgcn_s_setprio(0);
     };
     auto produce = [&](int c) {                   // chunk c + 1 into its buffers, loads of chunk c + 2
         if (c + 1 < nchunks) {
