@@ -615,21 +615,22 @@ __global__ void __launch_bounds__(kPfThreads) prefill_gateup_kernel(PrefillArgs 
                     g[j] = er[j];
                     u[j] = er[128 + j];
                 }
-                row_fwht128(g);
-                row_fwht128(u);
+                row_fwht128_signed(g);
+                row_fwht128_signed(u);
+                const float rs = row_sign() * kRsqrt128;
 #pragma unroll
                 for (int j = 0; j < 8; ++j) {
-                    const float gj = (float)(half_t)(g[j] * kRsqrt128 * (float)hg[j]);
-                    const float uj = (float)(half_t)(u[j] * kRsqrt128 * (float)hu[j]);
+                    const float gj = (float)(half_t)(g[j] * rs * (float)hg[j]);
+                    const float uj = (float)(half_t)(u[j] * rs * (float)hu[j]);
                     // SiLU with the hardware exp and reciprocal (v_exp_f32, v_rcp_f32: about 1 ulp in fp32 each,
                     // then rounded to fp16)
                     const float aj = (float)(half_t)(gj * __builtin_amdgcn_rcpf(1.0f + __expf(-gj)) * uj);
                     av[j] = (float)(half_t)(aj * (float)hd[j]);
                 }
-                row_fwht128(av);
+                row_fwht128_signed(av);
                 half8_t o;
 #pragma unroll
-                for (int j = 0; j < 8; ++j) o[j] = (half_t)(av[j] * kRsqrt128);
+                for (int j = 0; j < 8; ++j) o[j] = (half_t)(av[j] * rs);
                 if (row < rows) *(half8_t*)(A.abuf + (size_t)(s0 + r0 + row) * I + cb8) = o;
             }
             __syncthreads();
@@ -680,9 +681,7 @@ __global__ void __launch_bounds__(kPfThreads) prefill_down_kernel(PrefillArgs A)
                 float v[8];
 #pragma unroll
                 for (int j = 0; j < 8; ++j) v[j] = er[j];
-                // the DPP-folded transform (fewer VALU instructions; the gate/up epilogue, with three transforms per
-                // row, measured slower with it and keeps row_fwht128)
-                row_fwht128_signed(v);
+                row_fwht128_signed(v);                       // the DPP-folded transform, as in the gate/up epilogue
                 const float sc = row_sign() * kRsqrt128 * pw[i];
                 half8_t o;
 #pragma unroll
