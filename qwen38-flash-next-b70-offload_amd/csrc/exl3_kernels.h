@@ -75,6 +75,8 @@ struct AlignOut {
     int* act_expert; int* act_start; int* act_cnt; int* act_pstart; int* n_act;   // [A], [A], [A], [A], [1]
     int* pair_tok; int* pair_of; float* pair_w;                                    // [npairs] each
     int* pair_exp;                                                                  // expert of each sorted pair or null
+    // the active experts again in GEMM dispatch order (descending 32-row block count, ties by ascending id), or null
+    int* ord_expert; int* ord_start; int* ord_cnt;                                  // [A] each
 };
 
 struct PrefillArgs {
@@ -82,7 +84,7 @@ struct PrefillArgs {
     const int32_t* ids; const float* w;            // [M * topk]
     int M, topk, npairs;
     const int64_t* ptrs;                           // per-layer blob pointer table [E]
-    const int* act_expert; const int* act_start; const int* act_cnt; const int* n_act;
+    const int* ord_expert; const int* ord_start; const int* ord_cnt; const int* n_act;   // GEMM dispatch order
     const int* pair_tok; const float* pair_w; const int* pair_of; const int* pair_exp;
     _Float16* xh;                                  // [npairs (sorted)][2][H] input Hadamards (gate, up)
     _Float16* abuf;                                // [npairs (sorted)][I]

@@ -115,6 +115,46 @@ __global__ void __launch_bounds__(1024) align_scan_kernel(int nchunks, int E, in
         o.act_pstart[ai] = pst;
     }
     if (e == 0) o.n_act[0] = nact;
+    if (o.ord_expert) {
+        // the GEMM dispatch order: active experts by descending key = 32-row blocks (capped at 255; two passes rank
+        // above one), ties by ascending id. Position = experts with a larger key + lower ids with the same key: ranks
+        // inside a wave from ballots, per-(wave, key) counts turned into offsets.
+        __shared__ int wk[16 * 256];
+        const int l = lane_id(), wv = threadIdx.x >> 6;
+        const int key = act ? min((tot + 31) >> 5, 255) : -1;
+        for (int i = threadIdx.x; i < 16 * 256; i += 1024) wk[i] = 0;
+        __syncthreads();
+        uint64_t todo = __ballot(key >= 0);
+        int rk = 0;
+        while (todo) {
+            const int leader = __builtin_ctzll(todo);
+            const int kv = __shfl(key, leader, 64);
+            const uint64_t m = __ballot(key == kv);
+            if (key == kv) rk = __popcll(m & ((1ull << l) - 1));
+            if (l == leader) wk[wv * 256 + kv] = __popcll(m);
+            todo &= ~m;
+        }
+        __syncthreads();
+        const int kt = 255 - (int)threadIdx.x;    // threads 0..255 own the keys in descending order
+        int ck = 0;
+        if (kt >= 0)
+            for (int w = 0; w < 16; ++w) ck += wk[w * 256 + kt];
+        int nsort;
+        const int above = block_scan_1024(kt >= 0 ? ck : 0, sw, nsort);
+        if (kt >= 0)
+            for (int w = 0, run = above; w < 16; ++w) {
+                const int c = wk[w * 256 + kt];
+                wk[w * 256 + kt] = run;
+                run += c;
+            }
+        __syncthreads();
+        if (key >= 0) {
+            const int pos = wk[wv * 256 + key] + rk;
+            o.ord_expert[pos] = e;
+            o.ord_start[pos] = st;
+            o.ord_cnt[pos] = tot;
+        }
+    }
     if (e < E) {                                  // the counts become each chunk's first position of expert e
         int run = st;
         for (int c0 = 0; c0 < nchunks; c0 += kB) {
@@ -566,8 +606,10 @@ __device__ __forceinline__ void stash_acc(const float16_t (&acc)[2], float* ep) 
         }
 }
 
-// workgroup -> (active expert a, column block): the nblk workgroups of an expert share blockIdx % 8, i.e. one XCD and
-// its L2, which serves the expert's A rows to all of them
+// workgroup -> (position a of the dispatch order, column block): the nblk workgroups of an expert share blockIdx % 8,
+// i.e. one XCD and its L2, which serves the expert's A rows to all of them. Workgroups are dispatched in blockIdx
+// order, so the experts with the most rows (two passes first) start first, dealt round-robin over the XCDs, and the
+// last workgroups of the launch are the shortest.
 __device__ __forceinline__ void pf_block(int nblk, int& a, int& blk) {
     const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3;
     a = (slot / nblk) * 8 + xcd;
@@ -581,7 +623,7 @@ __global__ void __launch_bounds__(kPfThreads) prefill_gateup_kernel(PrefillArgs 
     int a, nb;
     pf_block(nbn, a, nb);
     if (a >= A.n_act[0]) return;
-    const int e = A.act_expert[a], s0 = A.act_start[a], cnt = A.act_cnt[a];
+    const int e = A.ord_expert[a], s0 = A.ord_start[a], cnt = A.ord_cnt[a];
     const uint8_t* base = (const uint8_t*)A.ptrs[e];
     const int wv = threadIdx.x >> 6, l = lane_id();
     const int tiles_n = 2 * I / 16;
@@ -645,7 +687,7 @@ __global__ void __launch_bounds__(kPfThreads) prefill_down_kernel(PrefillArgs A)
     int a, nt;
     pf_block(ntn, a, nt);
     if (a >= A.n_act[0]) return;
-    const int e = A.act_expert[a], s0 = A.act_start[a], cnt = A.act_cnt[a];
+    const int e = A.ord_expert[a], s0 = A.ord_start[a], cnt = A.ord_cnt[a];
     const uint8_t* base = (const uint8_t*)A.ptrs[e];
     const int wv = threadIdx.x >> 6, l = lane_id();
     const int tiles_n = H / 16;
@@ -735,7 +777,7 @@ size_t align_scratch_bytes(int npairs, int E) {
 size_t prefill_workspace_bytes(int M, int H, int I, int topk, int E) {
     const size_t np = (size_t)M * topk, A = std::min<size_t>(np, (size_t)E);
     const size_t nch = (np + kAlignChunk - 1) / kAlignChunk;
-    return align256((4 * A + 1) * 4) + 3 * align256(np * 4) + align256(np * 4) + align256(nch * E * 4) +
+    return align256((7 * A + 1) * 4) + 3 * align256(np * 4) + align256(np * 4) + align256(nch * E * 4) +
            align256(np * 2 * H * 2) + align256(np * I * 2) + align256(np * H * 2);
 }
 
@@ -745,12 +787,15 @@ hipError_t launch_prefill(PrefillArgs a, int E, void* ws, hipStream_t s) {
     uint8_t* p = (uint8_t*)ws;
     auto take = [&p](size_t n) { uint8_t* q = p; p += align256(n); return q; };
     AlignOut o;
-    int* act = (int*)take((4 * A + 1) * 4);
+    int* act = (int*)take((7 * A + 1) * 4);
     o.act_expert = act;
     o.act_start = act + A;
     o.act_cnt = act + 2 * A;
     o.act_pstart = act + 3 * A;
     o.n_act = act + 4 * A;
+    o.ord_expert = act + 4 * A + 1;
+    o.ord_start = o.ord_expert + A;
+    o.ord_cnt = o.ord_start + A;
     o.pair_tok = (int*)take((size_t)np * 4);
     o.pair_of = (int*)take((size_t)np * 4);
     o.pair_exp = (int*)take((size_t)np * 4);
@@ -759,9 +804,9 @@ hipError_t launch_prefill(PrefillArgs a, int E, void* ws, hipStream_t s) {
     a.xh = (half_t*)take((size_t)np * 2 * H * 2);
     a.abuf = (half_t*)take((size_t)np * I * 2);
     a.y = (half_t*)take((size_t)np * H * 2);
-    a.act_expert = o.act_expert;
-    a.act_start = o.act_start;
-    a.act_cnt = o.act_cnt;
+    a.ord_expert = o.ord_expert;
+    a.ord_start = o.ord_start;
+    a.ord_cnt = o.ord_cnt;
     a.n_act = o.n_act;
     a.pair_tok = o.pair_tok;
     a.pair_w = o.pair_w;
