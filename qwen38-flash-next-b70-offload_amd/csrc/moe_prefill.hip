@@ -739,23 +739,31 @@ __global__ void __launch_bounds__(kPfThreads) prefill_down_kernel(PrefillArgs A)
 // pick positions, then all rows' loads go out before the sum (a loop would wait for each position and each row in
 // turn); more picks take the loop.
 constexpr int kCombMax = 16;
+// the picks' rows of one token, 8 columns, loaded together (picks past topk repeat the last one and are not summed)
+template <int KM>
+__device__ __forceinline__ void comb_rows(const PrefillArgs& A, int m, int topk, int H, int h0, float (&acc)[8]) {
+    int pos[KM];
+#pragma unroll
+    for (int k = 0; k < KM; ++k) pos[k] = A.pair_of[m * topk + min(k, topk - 1)];
+    half8_t v[KM];
+#pragma unroll
+    for (int k = 0; k < KM; ++k) v[k] = *(const half8_t*)(A.y + (size_t)pos[k] * H + h0);
+#pragma unroll
+    for (int k = 0; k < KM; ++k)
+        if (k < topk)
+#pragma unroll
+            for (int j = 0; j < 8; ++j) acc[j] += (float)v[k][j];
+}
 __global__ void __launch_bounds__(256) prefill_combine_kernel(PrefillArgs A) {
     const int m = blockIdx.x, H = A.g.H, topk = A.topk;
+    // one 16-byte store per 8 outputs when the row start allows it (16-bit outputs, 8-aligned offsets)
+    const bool vec = A.x_dt != 2 && (A.out_stride & 7) == 0 && ((uintptr_t)A.out & 15) == 0;
     for (int h0 = threadIdx.x * 8; h0 < H; h0 += 256 * 8) {
         float acc[8] = {};
-        if (topk <= kCombMax) {
-            // without a branch per pick (picks past topk repeat the last one and are not summed)
-            int pos[kCombMax];
-#pragma unroll
-            for (int k = 0; k < kCombMax; ++k) pos[k] = A.pair_of[m * topk + min(k, topk - 1)];
-            half8_t v[kCombMax];
-#pragma unroll
-            for (int k = 0; k < kCombMax; ++k) v[k] = *(const half8_t*)(A.y + (size_t)pos[k] * H + h0);
-#pragma unroll
-            for (int k = 0; k < kCombMax; ++k)
-                if (k < topk)
-#pragma unroll
-                    for (int j = 0; j < 8; ++j) acc[j] += (float)v[k][j];
+        if (topk <= 10) {
+            comb_rows<10>(A, m, topk, H, h0, acc);
+        } else if (topk <= kCombMax) {
+            comb_rows<kCombMax>(A, m, topk, H, h0, acc);
         } else {
             for (int k = 0; k < topk; ++k) {
                 const int pos = A.pair_of[m * topk + k];
@@ -765,8 +773,18 @@ __global__ void __launch_bounds__(256) prefill_combine_kernel(PrefillArgs A) {
             }
         }
         const size_t oo = (size_t)m * A.out_stride + h0;
+        if (vec) {
+            uint32_t w[4];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) st_act(A.out, A.x_dt, oo + j, acc[j]);
+            for (int j = 0; j < 4; ++j)
+                w[j] = A.x_dt == 1 ? (uint32_t)f32_to_bf16(acc[2 * j]) | ((uint32_t)f32_to_bf16(acc[2 * j + 1]) << 16)
+                                   : (uint32_t)__builtin_bit_cast(uint16_t, (half_t)acc[2 * j]) |
+                                         ((uint32_t)__builtin_bit_cast(uint16_t, (half_t)acc[2 * j + 1]) << 16);
+            *(uint4*)((uint16_t*)A.out + oo) = make_uint4(w[0], w[1], w[2], w[3]);
+        } else {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) st_act(A.out, A.x_dt, oo + j, acc[j]);
+        }
     }
 }
 
