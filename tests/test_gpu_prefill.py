@@ -130,6 +130,25 @@ def test_prefill_expert_with_more_than_256_rows():
     _check_vs_oracle(256, 256, 3, 2, 300, 2, 7100, 1)
 
 
+def test_prefill_fp16_activations():
+    """fp16 activations and output (the combine's 16-byte stores of fp16 values) against the oracle's fp32 result; the
+    synthetic bf16 inputs are exact in fp16, so the difference is the prefill's own rounding."""
+    print("case prefill fp16 activations", flush=True)
+    H, I, K, E, M, topk, seed = 2048, 512, 3, 32, 256, 4, 7400
+    x, ids, w, blobs, table, keep = _case(H, I, K, E, M, topk, seed)
+    ews = {e: exl3.ExpertWeights(b, H, I, K) for e, b in blobs.items()}
+    _, of = exl3.moe_forward(x, ids, w, ews, variant="prefill")
+    xs = torch.from_numpy(exl3.bf16_to_f32(x)).cuda().half()
+    with _PrefillFrom(256):
+        out = _ops().moe_forward(xs, torch.from_numpy(ids).cuda(), torch.from_numpy(w).cuda(), table, I, K, E)
+        torch.cuda.synchronize()
+    assert out.dtype == torch.float16
+    got = out.float().cpu().numpy()
+    r = rel_l2(got, of)
+    print(f"prefill fp16 rel-L2 {r:.2e}", flush=True)
+    assert np.isfinite(got).all() and r <= TOL
+
+
 @pytest.mark.parametrize("K", [2, 3, 4])
 def test_prefill_large_expert_shapes(K):
     """H 4096 / I 1536 (12 column blocks of I, 16 column tiles of H), each bitrate."""
