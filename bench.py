@@ -58,10 +58,15 @@ def _median_s(fn, warm: int, reps: int) -> float:
     return float(np.median(ts))
 
 
+CPU_WARM, CPU_REPS = 3, 10          # untimed passes, then the median of this many timed passes (every CPU figure)
+CPU_SAMPLE_LAYERS = 24               # layers per timed decode pass: half of the 48 (about 1.4 s per pass on 16 threads)
+
+
 def cpu_baseline():
     """The PyTorch CPU restatement of the path (oracle/cpu_path.py; the reference has no CPU path) on this host:
-    a real 48-layer decode pass at bs=1 (config-2 shapes, each layer its own Zipf routing and experts), the one-layer
-    config-0 case, and one layer on a single thread."""
+    a bs=1 decode pass through the first CPU_SAMPLE_LAYERS of the 48 layers (config-2 shapes, each layer its own Zipf
+    routing and experts, each on the previous layer's output), scaled to 48 layers; the one-layer config-0 case; and
+    one layer on a single thread. Each is the median of CPU_REPS timed runs after CPU_WARM untimed ones."""
     import numpy as np
     import torch
     from oracle import cpu_path, exl3, synth
@@ -77,15 +82,15 @@ def cpu_baseline():
 
     def stack():
         h = x
-        for ids, w, blobs in layers:          # the layers in order, each on the previous layer's output
+        for ids, w, blobs in layers[:CPU_SAMPLE_LAYERS]:     # in order, each on the previous layer's output
             h = cp.layer(h, ids, w, blobs).float()
         return h
-    t_stack = _median_s(stack, 1, 3)
+    t_stack = _median_s(stack, CPU_WARM, CPU_REPS) * L / CPU_SAMPLE_LAYERS
     ids0, w0 = synth.softmax_topk(seed, 1, E, TOPK)
     blobs0 = {int(e): distinct[int(e) % 64] for e in ids0[0]}
-    t_layer = _median_s(lambda: cp.layer(x, ids0, w0, blobs0), 3, 10)
+    t_layer = _median_s(lambda: cp.layer(x, ids0, w0, blobs0), CPU_WARM, CPU_REPS)
     torch.set_num_threads(1)
-    t_layer1 = _median_s(lambda: cp.layer(x, ids0, w0, blobs0), 1, 3)
+    t_layer1 = _median_s(lambda: cp.layer(x, ids0, w0, blobs0), CPU_WARM, CPU_REPS)
     torch.set_num_threads(n)
     model = ""
     try:
@@ -93,13 +98,16 @@ def cpu_baseline():
     except Exception:
         pass
     return {"value": 1.0 / t_stack, "unit": "tok/s", "cores": n, "kind": "port",
-            "sample": f"one bs=1 decode token through 48 MoE layers (H 2048, I 512, 512 experts, top-10, K 3; Zipf "
-                      f"routing per layer, 64 distinct synthetic blobs): LUT dequant + SwiGLU GEMVs + combine per layer, "
-                      f"median of 3 passes after 1 warm-up = {t_stack:.3f} s; torch on {n} threads, {model}",
+            "sample": f"one bs=1 decode token through the first {CPU_SAMPLE_LAYERS} of the 48 MoE layers (H 2048, "
+                      f"I 512, 512 experts, top-10, K 3; Zipf routing per layer, 64 distinct synthetic blobs): LUT "
+                      f"dequant + SwiGLU GEMVs + combine per layer, median of {CPU_REPS} passes after {CPU_WARM} "
+                      f"untimed ones, x {L / CPU_SAMPLE_LAYERS:g} = {t_stack:.3f} s per token; torch on {n} threads, "
+                      f"{model}",
             "cpu_model": model,
             "config0_layer_ms": round(t_layer * 1e3, 2),
             "single_thread": {"layer_ms": round(t_layer1 * 1e3, 1), "tok_s_48_layers": 1.0 / (L * t_layer1),
-                              "sample": "one config-0 layer on 1 thread, median of 3 after 1 warm-up, x 48 layers"}}
+                              "sample": f"one config-0 layer on 1 thread, median of {CPU_REPS} after {CPU_WARM} "
+                                        f"untimed runs, x 48 layers"}}
 
 
 PREFILL_TOKENS = 8192
@@ -350,11 +358,11 @@ def run_linear(args, dev):
         cl = cpu_path.CpuLinear(K)
         cpu_groups = [(fg.trellis.cpu(), fg.suh.cpu(), fg.svh.cpu(), fg.bounds) for fg in layers[0]]
         xc = [x.float().cpu() for x in xin]
-        t_cpu = _median_s(lambda: [cl(x, *gr) for gr, x in zip(cpu_groups, xc)], 1, 3)
+        t_cpu = _median_s(lambda: [cl(x, *gr) for gr, x in zip(cpu_groups, xc)], CPU_WARM, CPU_REPS)
         out["cpu_baseline"] = {"value": round(1.0 / (L * t_cpu), 3), "unit": "tok/s", "cores": n, "kind": "port",
                                "sample": f"one layer's four groups at bs={bs} (trellis decode through the codebook "
-                                         f"table + fp32 matmuls, torch on {n} threads), median of 3 after 1 warm-up = "
-                                         f"{t_cpu:.3f} s, x 48 layers"}
+                                         f"table + fp32 matmuls, torch on {n} threads), median of {CPU_REPS} after "
+                                         f"{CPU_WARM} untimed runs = {t_cpu:.3f} s, x 48 layers"}
     print(json.dumps(out), flush=True)
 
 

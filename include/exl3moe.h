@@ -44,7 +44,8 @@ int64_t exl3_blob_bytes(int H, int I, int K);
 /* ---- process-wide configuration (a8:682-789) ---------------------------------------------------------------------- */
 
 /* moe_set_tier (a8:768-774): ram_res uint8 [L*E] (1 = RAM-tier copy valid), miss ring int32 [1 + cap]
- * ([0] = count of masked picks modulo 2^32; entry c at position 1 + (c mod 2^32) % cap), safe int32 [L].
+ * ([0] = count of masked picks modulo 2^32; entry c at position 1 + (c mod 2^32) % cap, cap a power of two so that
+ * positions stay continuous across the wrap of the count; EXL3_EINVAL otherwise), safe int32 [L].
  * ram_res == NULL turns the tier (masking) off. */
 int exl3_set_tier(uint8_t* ram_res, int32_t* miss_ring, int64_t ring_numel, const int32_t* safe);
 /* moe_set_victims (a8:757): device int32 [1 + 2E] victim list, NULL = no victim write-back */
@@ -176,7 +177,8 @@ int exl3_scatter_flags(uint8_t* flags, int64_t n_flags, const int32_t* packed, i
  * index_copy_ of plugin/exl3xpu/nvtier.py:282-386 and 791-793): applies the diff as exl3_scatter_flags; mirrors the
  * miss ring (int32 [1 + ring_cap], [0] = count) into ring_mirror (same layout, device-mapped pinned): the entries at
  * counts [ring_from, count) modulo 2^32 (the last ring_cap of them at most) and the count; then copies src[k] -> dst[k]
- * (nbytes[k] bytes, k < n_copies <= 4; dst device-mapped pinned host memory, both 16-byte aligned). ring may be NULL.
+ * (nbytes[k] bytes, k < n_copies <= 4; dst device-mapped pinned host memory, both 16-byte aligned). ring may be NULL;
+ * ring_cap is a power of two (as exl3_set_tier requires).
  * A flag the diff sets may be snapshotted before or after its update. */
 int exl3_tier_exchange(uint8_t* flags, int64_t n_flags, const int32_t* packed, int64_t n_diff, const int32_t* ring,
                        int64_t ring_cap, int64_t ring_from, int32_t* ring_mirror, const void* const* src,
@@ -191,6 +193,13 @@ int exl3_device_status(int32_t* flags4, void* stream);
  * without a synchronisation of its own: the host tier step adds them to the snapshot copies of exl3_tier_exchange
  * and raises when flags4[0] != 0 (no reference counterpart). */
 int exl3_device_status_address(void** dev_ptr);
+
+/* Mirror of flags4[0] in host memory (no reference counterpart): host_word points into pinned host memory
+ * (exl3_host_alloc) and is raised by one, with a system-scope atomic, by every bounded wait that times out on the
+ * current device, from then on (NULL: no mirror). A caller notices a timeout by reading that word, with no copy and
+ * no synchronisation, so graph-captured decode loops stay sync-free; the ExpertStore wrappers raise RuntimeError at
+ * their next call when it moved. Synchronous (sets a device symbol); call it outside graph capture. */
+int exl3_set_status_mirror(int32_t* host_word);
 
 /* Bit-exact dequantization (ReconstructKernel, exl3_esimd.h:869-936): PLANAR4 trellis words
  * [k_tiles][n_tiles][8K] -> fp16 bits [16 k_tiles][16 n_tiles] (W_inner, Hadamard domain). */

@@ -289,6 +289,17 @@ __device__ __forceinline__ void row_fwht128_signed(float (&v)[8]) {
 #undef EXL3_FMAC8
 }
 
+// SiLU(g) * u as both expert paths (decode and prefill) compute it, so that one token gets the same fp16 act from
+// either: g * rcp(1 + exp(-g)) * u on the hardware exp and reciprocal (__expf is v_exp_f32 of the fp32 product
+// -g * log2(e); v_exp_f32 and v_rcp_f32 are each within about 1 ulp in fp32). The reference evaluates
+// g / (1 + exp(-g)) * u under -ffast-math SYCL (kernels/moe-a8/exl3_moe.a8.sycl:250). Over every finite fp16 g, with
+// any 1-ulp error of the exp and the reciprocal, SiLU(g) stays within 4e-6 relative of the exact value (most of it
+// the fp32 rounding of -g * log2(e) at large |g|), and its fp16 rounding is at most one fp16 ulp from the exact
+// value's; tests/test_oracle_exl3.py checks both bounds.
+__device__ __forceinline__ float silu_mul(float g, float u) {
+    return g * __builtin_amdgcn_rcpf(1.0f + __expf(-g)) * u;
+}
+
 __device__ __forceinline__ float bf16_to_f32(bf16_bits b) { return __uint_as_float((uint32_t)b << 16); }
 __device__ __forceinline__ bf16_bits f32_to_bf16(float f) {
     uint32_t u = __float_as_uint(f);

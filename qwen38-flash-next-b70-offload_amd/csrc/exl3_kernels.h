@@ -93,7 +93,7 @@ struct PrefillArgs {
     BlobGeom g;
 };
 
-static inline size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
+constexpr size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
 
 // the dense EXL3 linear (linear.hip): out[M, n] = svh * H(sum_k xh[shard of n][m][k] W[k][n]) / sqrt 128
 constexpr int kLinMaxRows = 8;       // rows of the fused small-M path
@@ -129,12 +129,16 @@ static inline size_t linear_workspace_bytes(int M, int k, int n) {
 hipError_t launch_moe_layer(int K, const DecodeArgs& a, hipStream_t s);
 int read_status(int* out, hipStream_t s);
 hipError_t status_address(void** p);
+hipError_t set_status_mirror(int* host_word);
 hipError_t launch_dequant(int K, const uint32_t* tr, _Float16* out, int k_tiles, int n_tiles, hipStream_t s);
 // cache.hip
 hipError_t launch_ensure(const EnsureArgs& a, hipStream_t s);
 // prefetch (moe_prefetch a8:1194-1222): ensure in prefetch mode, then copy every assigned expert from its host record
 // (host_base[layer] + e * hstride) into its slot (slot_base + s * sstride, `copy_bytes` bytes) and repoint ptrs_all
 hipError_t launch_prefetch(const EnsureArgs& a, int64_t sstride, int64_t copy_bytes, hipStream_t s);
+// the copies and the commit of a cached call outside the decode kernel, after its ensure (a: the ensure's arguments;
+// blob: bytes of the layer's blob; max_n: an upper bound of the call's fills)
+hipError_t launch_cached_fills(const EnsureArgs& a, int64_t blob, int max_n, uint8_t* ram_res, hipStream_t s);
 hipError_t launch_scatter_flags(uint8_t* flags, int64_t n_flags, const int32_t* packed, int64_t n, hipStream_t s);
 hipError_t launch_table_update(int64_t* ptrs_all, int32_t* slot_of, int32_t* slot_key, int32_t* slot_last,
                                const int64_t* rec, int64_t n, hipStream_t s);
@@ -154,7 +158,7 @@ hipError_t launch_prefill(PrefillArgs a, int E, void* ws, hipStream_t s);
 __host__ __device__ static inline int gu_kslices(int H) { return (H + 1023) / 1024; }
 
 // workspace of a decode call (bytes, 256-aligned parts): the blob pointer of every pick
-static inline size_t decode_workspace_bytes(int npairs, int H, int I) {
+constexpr size_t decode_workspace_bytes(int npairs, int H, int I) {
     (void)H;
     (void)I;
     return align256((size_t)npairs * 8);

@@ -474,6 +474,67 @@ hipError_t launch_prefetch(const EnsureArgs& a, int64_t sstride, int64_t copy_by
     return hipGetLastError();
 }
 
+// ---- cached calls larger than the decode kernel takes --------------------------------------------------------------
+// A cached call with more picks (or rows) than the fused decode kernel takes, below prefill_min_m, runs the ensure over
+// all its picks (one launch, the decode-mode decisions), then these three kernels, then the prefill kernels over the
+// committed table: victim write-back (each victim with a write-back key copies its slot to that key's host record and
+// flags it RAM-resident; a8:1168-1189), the fills (each assigned miss copied from the host record its table entry
+// still names into its new slot), and the commit (ptrs_all = fill_all, fill_all = 0; a8:371-395). The reference
+// reads such misses zero-copy and writes them through inside its align-path GEMV (a8:1239, 1277-1314): the decisions,
+// the final cache state and the slot bytes are the same, and the outputs too (the same blob bytes are read).
+// Workgroup (i, chunk) copies 64 KiB of the i-th entry with 16-byte accesses; entries past the call's count return.
+__device__ __forceinline__ void copy_chunk(const uint8_t* src, uint8_t* dst, int64_t bytes, int ch) {
+    const int64_t b1 = min(bytes, (int64_t)(ch + 1) * kPrefetchChunk);
+    for (int64_t o = (int64_t)ch * kPrefetchChunk + threadIdx.x * 16; o < b1; o += 256 * 16)
+        *(uint4*)(dst + o) = *(const uint4*)(src + o);
+}
+
+__global__ void __launch_bounds__(256) cached_victim_kernel(const int32_t* vict, const int64_t* host_base,
+                                                            int64_t hstride, int E, int64_t slot_base, int64_t sstride,
+                                                            uint8_t* ram_res, int chunks) {
+    const int mi = blockIdx.x / chunks, ch = blockIdx.x % chunks;
+    if (mi >= vict[0]) return;
+    const int old = vict[1 + 2 * mi], s = vict[2 + 2 * mi];
+    if (old < 0) return;                                       // no write-back (empty slot, or a valid RAM copy)
+    if (ram_res && ch == 0 && threadIdx.x == 0) ram_res[old] = 1;
+    copy_chunk((const uint8_t*)(slot_base + (int64_t)s * sstride),
+               (uint8_t*)(host_base[old / E] + (int64_t)(old % E) * hstride), sstride, ch);
+}
+
+__global__ void __launch_bounds__(256) cached_fill_kernel(const int32_t* fill_list, const int64_t* ptrs_all,
+                                                          const int64_t* fill_all, int layer, int E, int64_t bytes,
+                                                          int chunks) {
+    const int mi = blockIdx.x / chunks, ch = blockIdx.x % chunks;
+    if (mi >= fill_list[0]) return;
+    const int64_t key = (int64_t)layer * E + fill_list[1 + mi];
+    copy_chunk((const uint8_t*)ptrs_all[key], (uint8_t*)fill_all[key], bytes, ch);
+}
+
+__global__ void __launch_bounds__(256) cached_commit_kernel(const int32_t* fill_list, int64_t* ptrs_all,
+                                                            int64_t* fill_all, int layer, int E) {
+    const int n = fill_list[0];
+    for (int mi = threadIdx.x; mi < n; mi += 256) {
+        const int64_t key = (int64_t)layer * E + fill_list[1 + mi];
+        ptrs_all[key] = fill_all[key];
+        fill_all[key] = 0;
+    }
+}
+
+hipError_t launch_cached_fills(const EnsureArgs& a, int64_t blob, int max_n, uint8_t* ram_res, hipStream_t s) {
+    if (max_n <= 0) return hipSuccess;
+    if (a.vict) {
+        const int vchunks = (int)((a.blob + kPrefetchChunk - 1) / kPrefetchChunk);     // whole slots (a.blob: stride)
+        hipLaunchKernelGGL(cached_victim_kernel, dim3((unsigned)(max_n * vchunks)), dim3(256), 0, s, a.vict,
+                           a.host_base, a.hstride, a.E, a.slot_base, a.blob, ram_res, vchunks);
+    }
+    const int chunks = (int)((blob + kPrefetchChunk - 1) / kPrefetchChunk);
+    hipLaunchKernelGGL(cached_fill_kernel, dim3((unsigned)(max_n * chunks)), dim3(256), 0, s, a.fill_list, a.ptrs_all,
+                       a.fill_all, a.layer, a.E, blob, chunks);
+    hipLaunchKernelGGL(cached_commit_kernel, dim3(1), dim3(256), 0, s, a.fill_list, a.ptrs_all, a.fill_all, a.layer,
+                       a.E);
+    return hipGetLastError();
+}
+
 // flag upload of the host tier step: packed[i] = key << 1 | value, read in place (pinned host memory is device-mapped)
 __global__ void scatter_flags_kernel(uint8_t* flags, int64_t n_flags, const int32_t* packed, int64_t n) {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;

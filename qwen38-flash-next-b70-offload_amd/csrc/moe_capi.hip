@@ -132,6 +132,11 @@ int exl3_set_tier(uint8_t* ram_res, int32_t* miss_ring, int64_t ring_numel, cons
         return EXL3_OK;
     }
     if (!miss_ring || ring_numel < 2 || !safe) return fail(EXL3_EINVAL, "moe_set_tier: ring [1 + cap] and safe [L] required");
+    // entry c sits at 1 + (c mod 2^32) % cap: with a power-of-two cap the position is continuous across the 2^32 wrap
+    // of the count (any other cap maps counts on either side of the wrap to the same entry)
+    const int64_t cap = ring_numel - 1;
+    if (cap > INT32_MAX || (cap & (cap - 1)))
+        return fail(EXL3_EINVAL, "moe_set_tier: ring capacity %lld must be a power of two <= 2^30", (long long)cap);
     g_cfg.ram_res = ram_res;
     g_cfg.ring = miss_ring;
     g_cfg.ring_cap = (int)(ring_numel - 1);
@@ -193,12 +198,16 @@ int exl3_set_decision_log(int32_t* buf, int64_t cap_records) {
     return EXL3_OK;
 }
 
-static bool use_prefill(int M) { return M >= g_cfg.prefill_min_m; }
+// the prefill kernels serve a call from prefill_min_m rows on, and also below it when the call has more picks or rows
+// than the fused decode kernel takes (the reference's align path covers pair_max_m < M < prefill_min_m, a8:1277-1314;
+// the prefill kernels here are exact from M = 1 on)
+static bool exceeds_decode(int M, int topk) { return (int64_t)M * topk > kMaxPairs || M > kMaxRows; }
+static bool use_prefill(int M, int topk) { return M >= g_cfg.prefill_min_m || exceeds_decode(M, topk); }
 
 size_t exl3_moe_forward_workspace(int M, int H, int I, int topk, int n_experts) {
     if (M <= 0 || topk <= 0 || H <= 0 || I <= 0) return 0;
     const int E = std::min(std::max(n_experts, 1), kMaxExperts);
-    return use_prefill(M) ? prefill_workspace_bytes(M, H, I, topk, E) : decode_workspace_bytes(M * topk, H, I);
+    return use_prefill(M, topk) ? prefill_workspace_bytes(M, H, I, topk, E) : decode_workspace_bytes(M * topk, H, I);
 }
 
 static int64_t* pair_ptr_area(void* ws, int npairs, int H, int I) {
@@ -260,7 +269,7 @@ static int forward_impl(const void* x, int x_dtype, int64_t x_stride, int M, int
                         const int32_t* fill_list, const int64_t* pair_ptr, const VictimArgs* va = nullptr,
                         int max_victims = 0, const EnsureArgs* fused_ens = nullptr, bool vict_inline = false,
                         uint64_t* xb_given = nullptr) {
-    if (!fill && use_prefill(M)) {
+    if (!fill && use_prefill(M, topk)) {
         if (H % 256) return fail(EXL3_EUNSUPPORTED, "moe prefill: H %% 256 == 0 required (H=%d)", H);
         if ((int64_t)M * topk > (1 << 28)) return fail(EXL3_EUNSUPPORTED, "moe prefill: %d x %d pairs", M, topk);
         const size_t need = prefill_workspace_bytes(M, H, I, topk, E);
@@ -520,7 +529,9 @@ static int cached_impl(const void* x, int x_dtype, int64_t x_stride, int M, int 
         return fail(EXL3_EINVAL, "moe_forward_cached: null cache state");
     const BlobGeom g = blob_geom(H, I, K);
     const int P = M * topk;
-    if (P > kMaxPairs) return fail(EXL3_EUNSUPPORTED, "moe_forward_cached: %d picks > %d", P, kMaxPairs);
+    if (exceeds_decode(M, topk) && xb)
+        return fail(EXL3_EUNSUPPORTED, "moe_forward_cached_static: %d x %d picks take the prefill kernels, which need "
+                    "a workspace (use exl3_moe_forward_cached)", M, topk);
     EnsureArgs ea{};
     ea.ids = topk_ids;
     ea.w = topk_w;
@@ -549,6 +560,24 @@ static int cached_impl(const void* x, int x_dtype, int64_t x_stride, int M, int 
     ea.vict = g_cfg.vict;
     ea.log = g_cfg.log;
     ea.log_cap = g_cfg.log_cap;
+    if (exceeds_decode(M, topk)) {
+        // more picks than the decode kernel takes: one ensure over all of them, victim write-back, fill copies and
+        // the commit, then the prefill kernels over the committed table (the caller's ids and w carry the tier mask)
+        if (H % 256) return fail(EXL3_EUNSUPPORTED, "moe_forward_cached: %d picks need the prefill kernels (H %% 256)", P);
+        const size_t need = prefill_workspace_bytes(M, H, I, topk, E);
+        if (!workspace || workspace_bytes < need)
+            return fail(EXL3_EWORKSPACE, "moe_forward_cached: workspace %zu < %zu bytes", workspace_bytes, need);
+        ea.pend = g_cfg.n_layers > 0 ? g_cfg.pend : nullptr;   // commit finished copy-engine plans first
+        ea.done_seq = g_cfg.done_seq;
+        ea.n_layers = g_cfg.n_layers;
+        hipError_t e = launch_ensure(ea, st);
+        if (e == hipErrorInvalidValue) return fail(EXL3_EUNSUPPORTED, "moe_forward_cached: ensure state does not fit in LDS");
+        if (e != hipSuccess) return hip_fail(e, "ensure launch");
+        e = launch_cached_fills(ea, g.blob, std::min(std::min(ea.max_fill, E), P), g_cfg.ram_res, st);
+        if (e != hipSuccess) return hip_fail(e, "cached fills launch");
+        return forward_impl(x, x_dtype, x_stride, M, H, topk_ids, topk_w, topk, ptrs_all + (int64_t)layer * E, I, K, E,
+                            out, out_stride, workspace, workspace_bytes, st, nullptr, nullptr, nullptr, nullptr, nullptr);
+    }
     const size_t need = decode_workspace_bytes(P, H, I);
     if (!workspace || workspace_bytes < need)
         return fail(EXL3_EWORKSPACE, "moe_forward_cached: workspace %zu < %zu bytes", workspace_bytes, need);
@@ -590,10 +619,17 @@ static int cached_impl(const void* x, int x_dtype, int64_t x_stride, int M, int 
 }
 
 // ---- the entry point that allocates nothing ------------------------------------------------------------------------
-// Decode scratch in static device memory: the workspace (blob pointer of every pick, 256-aligned) followed by the
-// exchange words. Every device holds its own copy for the life of the process; its address on a device is looked up
-// once (hipGetSymbolAddress, that device current) and kept: host code never uses the array's name as an address.
+// Decode scratch in static device memory: a pointer area sized for the largest call (the blob pointer or the
+// first-pick flag of every pick, kMaxPairs entries), then the exchange words. Both start at fixed offsets whatever
+// the call's size: the exchange words are validated only by their tag (call epoch + 1 in the high half), so they
+// must never share an address with pointers or flags of an earlier call, whose high halves could pass as a tag.
+// Every device holds its own copy for the life of the process; its address on a device is looked up once
+// (hipGetSymbolAddress, that device current) and kept: host code never uses the array's name as an address.
 constexpr size_t kStaticScratchBytes = EXL3_STATIC_SCRATCH_BYTES;
+constexpr size_t kStaticPtrBytes = align256((size_t)kMaxPairs * 8);      // offset of the exchange words
+static_assert(decode_workspace_bytes(kMaxPairs, 0, 0) <= kStaticPtrBytes,
+              "the pointer area of the static scratch must hold the workspace of the largest decode call");
+static_assert(kStaticPtrBytes % 256 == 0 && kStaticPtrBytes < kStaticScratchBytes, "static scratch layout");
 static __device__ __align__(256) uint8_t scratch[kStaticScratchBytes];
 static std::mutex g_scratch_mu;
 static uint8_t* g_scratch_ptr[kMaxDevices];
@@ -649,7 +685,8 @@ int exl3_moe_forward_cached_static(const void* x, int x_dtype, int64_t x_stride,
                            n_experts, out, out_stride, nullptr, 0, stream, nullptr);
     if ((int64_t)M * topk > kMaxPairs) return fail(EXL3_EUNSUPPORTED, "moe_forward_cached_static: %d picks > %d", M * topk, kMaxPairs);
     const size_t ws = decode_workspace_bytes(M * topk, H, I);
-    const size_t need = ws + decode_exchange_words(M * topk, H, I) * 8;
+    if (ws > kStaticPtrBytes) return fail(EXL3_EUNSUPPORTED, "moe_forward_cached_static: pointer area");
+    const size_t need = kStaticPtrBytes + decode_exchange_words(M * topk, H, I) * 8;
     if (need > kStaticScratchBytes)
         return fail(EXL3_EUNSUPPORTED, "moe_forward_cached_static: the call needs %zu bytes of scratch, the static "
                     "scratch holds %zu (fewer rows, or exl3_moe_forward_cached)", need, kStaticScratchBytes);
@@ -658,7 +695,7 @@ int exl3_moe_forward_cached_static(const void* x, int x_dtype, int64_t x_stride,
     if (r) return r;
     return cached_impl(x, x_dtype, x_stride, M, H, topk_ids, topk_w, topk, ptrs_all, layer, slot_of, slot_key,
                        slot_last, tick, n_slots, host_base, slot_base, fill_all, fill_list, max_fill, I, K, n_experts,
-                       out, out_stride, sp, ws, stream, (uint64_t*)(sp + ws));
+                       out, out_stride, sp, ws, stream, (uint64_t*)(sp + kStaticPtrBytes));
 }
 
 size_t exl3_moe_align_workspace(int M, int topk, int n_experts) {
@@ -704,9 +741,12 @@ int exl3_tier_exchange(uint8_t* flags, int64_t n_flags, const int32_t* packed, i
     if (n_diff < 0 || n_flags < 0 || n_diff > (int64_t)1 << 31 || n_copies < 0 || n_copies > 4)
         return fail(EXL3_EINVAL, "tier_exchange: n_diff=%lld n_copies=%d", (long long)n_diff, n_copies);
     if (n_diff && (!flags || !packed)) return fail(EXL3_EINVAL, "tier_exchange: null flags / diff");
-    // ring_from is a ring count (modulo 2^32, as the device keeps it): 0 <= ring_from < 2^32
-    if (ring && (!ring_mirror || ring_cap <= 0 || ring_cap > INT32_MAX || ring_from < 0 || ring_from > (int64_t)UINT32_MAX))
-        return fail(EXL3_EINVAL, "tier_exchange: ring cap=%lld from=%lld", (long long)ring_cap, (long long)ring_from);
+    // ring_from is a ring count (modulo 2^32, as the device keeps it): 0 <= ring_from < 2^32; the capacity is a power
+    // of two, as exl3_set_tier requires, so that positions stay continuous across the wrap of the count
+    if (ring && (!ring_mirror || ring_cap <= 0 || ring_cap > INT32_MAX || (ring_cap & (ring_cap - 1)) || ring_from < 0 ||
+                 ring_from > (int64_t)UINT32_MAX))
+        return fail(EXL3_EINVAL, "tier_exchange: ring cap=%lld (a power of two) from=%lld", (long long)ring_cap,
+                    (long long)ring_from);
     const TierRing rg{ring, ring_cap, ring_from, ring_mirror};
     TierCopies cp{};
     for (int k = 0; k < n_copies; ++k) {
@@ -726,6 +766,11 @@ int exl3_device_status(int32_t* flags4, void* stream) {
     if (e != hipSuccess) return hip_fail(e, "device_status");
     e = hipStreamSynchronize((hipStream_t)stream);
     return e == hipSuccess ? EXL3_OK : hip_fail(e, "device_status sync");
+}
+
+int exl3_set_status_mirror(int32_t* host_word) {
+    const hipError_t e = set_status_mirror((int*)host_word);
+    return e == hipSuccess ? EXL3_OK : hip_fail(e, "set_status_mirror");
 }
 
 int exl3_device_status_address(void** dev_ptr) {

@@ -41,6 +41,9 @@ __device__ int g_cnt_all[4];          // [1] victim reads done, [2] fused ensure
 // [0]: bounded waits that timed out since load (0 in a healthy run). 16-byte aligned: the host tier step copies the
 // four words into its pinned snapshot with 16-byte accesses.
 __device__ __align__(16) int g_status[4];
+// optional mirror of g_status[0] in pinned host memory (null: none), raised with a system-scope atomic by the wave
+// whose wait timed out, so that a host caller can notice a timeout by reading host memory, without a copy or a sync
+__device__ int* g_status_host;
 
 constexpr int kSpinMax = 1 << 22;
 constexpr uint64_t kDownLoadDelay = 120;         // 1.2 us in s_memrealtime ticks
@@ -58,9 +61,14 @@ __device__ __forceinline__ unsigned call_tag() {
     return __hip_atomic_load(&g_epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u;
 }
 // bounded-spin bookkeeping shared by the polls: true once the budget is spent (counted in g_status[0])
+__device__ __forceinline__ void count_timeout() {
+    atomicAdd(&g_status[0], 1);
+    int* h = g_status_host;
+    if (h) __hip_atomic_fetch_add(h, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
 __device__ __forceinline__ bool spin_out(int& it) {
     if (++it > kSpinMax) {
-        if (lane_id() == 0) atomicAdd(&g_status[0], 1);
+        if (lane_id() == 0) count_timeout();
         return true;
     }
     __builtin_amdgcn_s_sleep(1);
@@ -202,7 +210,7 @@ __device__ __forceinline__ bool wait_count(const int* c, int target) {
     while (__hip_atomic_load(c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target) {
         __builtin_amdgcn_s_sleep(1);
         if (++it > kSpinMax) {
-            atomicAdd(&g_status[0], 1);
+            count_timeout();
             return false;
         }
     }
@@ -544,8 +552,8 @@ __device__ __forceinline__ void down_wg(const DecodeArgs& A, int blk, LayerShare
             g1 = (float)(half_t)(g1 * kRsqrt128 * (float)e_g.y);
             u0 = (float)(half_t)(u0 * kRsqrt128 * (float)e_u.x);
             u1 = (float)(half_t)(u1 * kRsqrt128 * (float)e_u.y);
-            float a0 = (float)(half_t)(g0 / (1.0f + expf(-g0)) * u0);
-            float a1 = (float)(half_t)(g1 / (1.0f + expf(-g1)) * u1);
+            float a0 = (float)(half_t)silu_mul(g0, u0);
+            float a1 = (float)(half_t)silu_mul(g1, u1);
             a0 = (float)(half_t)(a0 * (float)e_d.x);
             a1 = (float)(half_t)(a1 * (float)e_d.y);
             wave_fwht128(a0, a1);
@@ -757,6 +765,11 @@ int read_status(int* out, hipStream_t s) {
 
 // device address of the status words on the current device (each device holds its own copy)
 hipError_t status_address(void** p) { return hipGetSymbolAddress(p, HIP_SYMBOL(g_status)); }
+
+// the host mirror of the timeout count on the current device (a synchronous copy of the pointer into the symbol)
+hipError_t set_status_mirror(int* host_word) {
+    return hipMemcpyToSymbol(HIP_SYMBOL(g_status_host), &host_word, sizeof(host_word), 0, hipMemcpyHostToDevice);
+}
 
 hipError_t launch_dequant(int K, const uint32_t* tr, _Float16* out, int k_tiles, int n_tiles, hipStream_t s) {
     int ntw = K == 3 ? Geo<3>::NTW : (K == 2 ? Geo<2>::NTW : Geo<4>::NTW);

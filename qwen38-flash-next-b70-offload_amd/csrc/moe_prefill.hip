@@ -664,9 +664,7 @@ __global__ void __launch_bounds__(kPfThreads) prefill_gateup_kernel(PrefillArgs 
                 for (int j = 0; j < 8; ++j) {
                     const float gj = (float)(half_t)(g[j] * rs * (float)hg[j]);
                     const float uj = (float)(half_t)(u[j] * rs * (float)hu[j]);
-                    // SiLU with the hardware exp and reciprocal (v_exp_f32, v_rcp_f32: about 1 ulp in fp32 each,
-                    // then rounded to fp16)
-                    const float aj = (float)(half_t)(gj * __builtin_amdgcn_rcpf(1.0f + __expf(-gj)) * uj);
+                    const float aj = (float)(half_t)silu_mul(gj, uj);
                     av[j] = (float)(half_t)(aj * (float)hd[j]);
                 }
                 row_fwht128_signed(av);

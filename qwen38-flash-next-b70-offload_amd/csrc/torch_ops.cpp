@@ -9,6 +9,7 @@
 #include <algorithm>
 #include <map>
 #include <mutex>
+#include <tuple>
 #include <vector>
 
 #include "../../include/exl3moe.h"
@@ -240,15 +241,26 @@ void linear_checks(const at::Tensor& trellis, const at::Tensor& suh, const at::T
                 "exl3xpu_C.linear: shard_of_nb int32 [n / 128]");
 }
 
-// The small-M workspace of one (device, stream): zeroed at allocation (every call leaves its counters zero) and shared
-// by the calls on that stream, which run in order. Sized for 8 rows; a larger one replaces it when a call needs more,
-// and the replaced buffers are kept, since a captured HIP graph may still hold their addresses.
+// The small-M workspace. Its arrival counters must be zero when a call starts; every call leaves them zero.
+// Eager calls on one (device, stream) share one buffer, zeroed when it is allocated, and run in stream order. A call
+// made while its stream is being captured into a HIP graph gets a buffer of that capture alone (keyed by the capture
+// id), allocated and zeroed inside the capture: the zero fill (a fill kernel, not a memset node) is then a node of
+// that graph, so each replay starts from zero whatever ran on the buffer of another graph or of eager calls, and
+// graphs captured one after another on the same stream can be replayed in any order. Sized for 8 rows; a larger one
+// replaces it when a call needs more. Buffers are kept until the process ends: a captured graph holds their
+// addresses.
 at::Tensor& small_workspace(const at::Tensor& x, size_t bytes) {
     static std::mutex mu;
-    static auto* cache = new std::map<std::pair<int, void*>, at::Tensor>();
+    static auto* cache = new std::map<std::tuple<int, void*, unsigned long long>, at::Tensor>();
     static auto* retired = new std::vector<at::Tensor>();
+    void* st = cur_stream(x);
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    unsigned long long cid = 0;
+    TORCH_CHECK(hipStreamGetCaptureInfo((hipStream_t)st, &cs, &cid) == hipSuccess, "exl3_gemm_small: capture status");
+    if (cs != hipStreamCaptureStatusActive) cid = 0;            // eager: the stream's own buffer
+    else if (cid == 0) cid = ~0ull;                             // (capture ids start at 1; keep 0 for eager calls)
     std::lock_guard<std::mutex> lock(mu);
-    auto& t = (*cache)[{(int)x.device().index(), cur_stream(x)}];
+    auto& t = (*cache)[{(int)x.device().index(), st, cid}];
     if (!t.defined() || (size_t)t.numel() < bytes) {
         if (t.defined()) retired->push_back(t);
         t = at::zeros({(int64_t)bytes}, x.options().dtype(at::kByte));

@@ -52,6 +52,7 @@ SIGNATURES = {
     "exl3_dequant": (c_i32, [c_p, c_i32, c_i32, c_i32, c_p, c_p]),
     "exl3_device_status": (c_i32, [c_p, c_p]),
     "exl3_device_status_address": (c_i32, [c_p]),
+    "exl3_set_status_mirror": (c_i32, [c_p]),
     "exl3_scatter_flags": (c_i32, [c_p, c_i64, c_p, c_i64, c_p]),
     "exl3_tier_exchange": (c_i32, [c_p, c_i64, c_p, c_i64, c_p, c_i64, c_i64, c_p, c_p, c_p, c_p, c_i32, c_p]),
     "exl3_admit_decide": (c_i32, [c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_i64, c_p, c_p, c_p, c_p, c_p, c_p, c_p]),

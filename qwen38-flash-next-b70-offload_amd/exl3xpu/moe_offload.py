@@ -17,6 +17,8 @@ current stream unless a stream is given, and nothing synchronises the host unles
   store.stage_layer(key, buf, stream)                     prefill: stage the layer's non-HBM experts into HBM
   store.forward_prefill_staged(key, x, topk_ids, topk_w)  prefill with the next layer staged on a copy stream
   store.slot_of[key]                                      host mirror of the layer's slot map (int32 [E], -1 = host)
+  store.check_device_status()                             raise if a decode kernel's bounded wait timed out (also
+                                                          done by forward / forward_cached / prefetch)
 
 Expert blob (blob_bytes(H, I, K) bytes; 1,195,008 for H 2048, I 512, K 3), the reference's format:
   gate|up trellis u32 [H/16][2I/16][8K] | down trellis u32 [I/16][H/16][8K] | fp16 suh_g[H] suh_u[H] svh_g[I] svh_u[I]
@@ -26,6 +28,7 @@ from __future__ import annotations
 
 import ctypes
 import heapq
+import logging
 import os
 import re
 import threading
@@ -34,7 +37,8 @@ from dataclasses import dataclass
 import numpy as np
 import torch
 
-__all__ = ["ops", "s64", "planar4", "pack_expert", "plan_copies", "BlobLayout", "ExpertStore", "STAGE_VERIFIED_BYTES"]
+__all__ = ["ops", "s64", "planar4", "pack_expert", "plan_copies", "BlobLayout", "ExpertStore", "STAGE_VERIFIED_BYTES",
+           "staging_fits"]
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 _ops_lock = threading.Lock()
@@ -45,8 +49,25 @@ _X_SHAPED_OPS = ("moe_forward", "moe_forward_cached")
 # Staged prefill (copy-stream streaming into HBM staging buffers) has been verified on the GPU with staging buffers of
 # up to this many bytes per layer. A full-size run (8,192 tokens x 48 layers, 512 experts of 1.2 MB) ended in a GPU
 # memory fault whose cause has not been found (a CPU replay of that sequence found every copy, table entry and stream
-# order in bounds), so larger staging raises instead of running.
+# order in bounds), so larger staging is never enqueued: the staged entry points serve such layers through the
+# zero-copy route instead (the prefill kernels read non-HBM experts straight from their pinned host records; the
+# same blob bytes, so the same output bits), and _Stager itself refuses larger buffers.
 STAGE_VERIFIED_BYTES = 2 << 20
+
+log = logging.getLogger("exl3xpu")
+_route_logged = set()
+
+
+def staging_fits(n_experts: int, rec: int) -> bool:
+    """True when a layer's staging buffer (n_experts records of rec bytes) is within the GPU-verified size."""
+    return int(n_experts) * int(rec) <= STAGE_VERIFIED_BYTES
+
+
+def _log_zero_copy_route(what: str, nbytes: int) -> None:
+    if what not in _route_logged:
+        _route_logged.add(what)
+        log.warning("exl3xpu: %s: staging buffer of %d B is above the verified %d B; the layer runs zero-copy from "
+                    "the pinned host records instead (same output)", what, nbytes, STAGE_VERIFIED_BYTES)
 
 
 def ops():
@@ -189,6 +210,47 @@ def _stream_handle(stream) -> int:
     return int(stream.cuda_stream)
 
 
+# ---- device health ---------------------------------------------------------------------------------------------------------
+
+class _StatusWatch:
+    """Watches the host mirror of the decode kernels' timeout count (exl3_set_status_mirror): a word of pinned host
+    memory that the device raises whenever a bounded wait gives up, so that an output was computed from incomplete
+    data. check() reads that word (host memory: no copy, no synchronisation, nothing enqueued) and raises
+    RuntimeError when it moved since the previous check."""
+
+    def __init__(self, word):
+        self.word = word                                # int32 CPU view of the mirror, [>= 1]
+        self.seen = int(word[0])
+
+    def check(self, what: str = "exl3xpu") -> None:
+        v = int(self.word[0])
+        if v != self.seen:
+            n, self.seen = v - self.seen, v
+            raise RuntimeError(f"{what}: {n} bounded waits of the decode kernels timed out on the device since the "
+                               "last check (an output was computed from incomplete data); the device state is not "
+                               "trustworthy")
+
+
+_mirror_lock = threading.Lock()
+_mirrors: dict = {}
+
+
+def _status_mirror(dev) -> torch.Tensor:
+    """The pinned timeout-count mirror of `dev`, set up (and registered with the library) on first use."""
+    idx = torch.device(dev).index
+    idx = torch.cuda.current_device() if idx is None else idx
+    with _mirror_lock:
+        t = _mirrors.get(idx)
+        if t is None:
+            t = ops().host_alloc(16).view(torch.int32)
+            t.zero_()
+            capi = _capi()
+            with torch.cuda.device(idx):
+                capi.check(capi.lib().exl3_set_status_mirror(t.data_ptr()), "status mirror")
+            _mirrors[idx] = t
+    return t
+
+
 # ---- HBM slots -----------------------------------------------------------------------------------------------------------
 
 class _SlotPool:
@@ -269,7 +331,7 @@ class _Stager:
     bounds-checked by the library before anything is enqueued."""
 
     def __init__(self, dev, E: int, rec: int):
-        if E * rec > STAGE_VERIFIED_BYTES:
+        if not staging_fits(E, rec):
             raise RuntimeError(
                 f"exl3xpu: staged prefill with {E} x {rec} B staging buffers is disabled: a full-size staged run "
                 f"faulted the GPU and its cause has not been found; staging has been verified up to "
@@ -434,6 +496,7 @@ class ExpertStore:
         self.pf_slot = torch.zeros(self.E, dtype=torch.int32, device=d)
         self.pend = torch.zeros(self.max_layers * 35, dtype=torch.int32, device=d)
         self.done_seq = torch.zeros(0, dtype=torch.int32, device=d)
+        self._watch = _StatusWatch(_status_mirror(d))
 
     # ---- geometry and strides
     def _host_stride(self) -> int:
@@ -573,7 +636,13 @@ class ExpertStore:
         w = topk_w if topk_w.dtype == torch.float32 and topk_w.is_contiguous() else topk_w.contiguous().to(torch.float32)
         return ids, w
 
+    def check_device_status(self) -> None:
+        """Raise RuntimeError if a bounded wait of a decode kernel timed out on this store's device since the last
+        check. Reads host memory only. forward, forward_cached and prefetch run it before enqueueing anything."""
+        self._watch.check("exl3xpu")
+
     def forward(self, key, x: torch.Tensor, topk_ids: torch.Tensor, topk_w: torch.Tensor, ptrs=None) -> torch.Tensor:
+        self._watch.check("exl3xpu.forward")
         ids, w = self._routing(topk_ids, topk_w)
         return self.X.moe_forward(x, ids, w, self.ptrs(key) if ptrs is None else ptrs, self.I, self.k_of(key), self.E)
 
@@ -583,6 +652,7 @@ class ExpertStore:
         and are written through into their new slot, committed at the end of the call (no host sync; graph-safe).
         With the RAM tier on, masked picks are rewritten in topk_ids / topk_w when those are int32 / fp32
         contiguous (else in the converted copies)."""
+        self._watch.check("exl3xpu.forward_cached")
         ids, w = self._routing(topk_ids, topk_w)
         self._mirror_stale = True
         self._bind_strides()
@@ -598,6 +668,7 @@ class ExpertStore:
         previous MoE call, and make the compute stream wait for it before the next."""
         if not self.n_slots:
             return
+        self._watch.check("exl3xpu.prefetch")
         flat = self._ids32(ids)
         self._mirror_stale = True
         self._bind_strides()
@@ -659,7 +730,12 @@ class ExpertStore:
     def stage_layer(self, key, buf: int, stream) -> torch.Tensor:
         """Copy every non-resident expert of `key` into staging buffer `buf` (0 or 1) on `stream`; returns the
         pointer table (slots for residents, staging otherwise) to pass to forward(ptrs=...) once `stream` has been
-        waited on. Uses the host mirror of the slot map (refreshed from the device after cached calls)."""
+        waited on. Uses the host mirror of the slot map (refreshed from the device after cached calls). A staging
+        buffer above STAGE_VERIFIED_BYTES is not used: the returned table is then the layer's own (HBM slot, else the
+        pinned host record, read zero-copy), with nothing enqueued on `stream`."""
+        if not staging_fits(self.E, self._records_stride()):
+            _log_zero_copy_route("stage_layer", self.E * self._records_stride())
+            return self.ptrs(key).clone()
         if self._pipeline is None:
             self._pipeline = _PrefillPipeline(self)
         stg = self._pipeline.stager
@@ -679,7 +755,12 @@ class ExpertStore:
     def forward_prefill_staged(self, key, x: torch.Tensor, topk_ids: torch.Tensor,
                                topk_w: torch.Tensor) -> torch.Tensor:
         """Prefill-size MoE for `key` from a staging buffer: its non-resident experts were copied on the copy stream
-        (normally while the previous layer computed); the next layer is staged into the other buffer now."""
+        (normally while the previous layer computed); the next layer is staged into the other buffer now. With a
+        staging buffer above STAGE_VERIFIED_BYTES the layer runs on its own table instead (HBM slot, else the pinned
+        host record, read zero-copy by the prefill kernels): the same blob bytes, so the same output."""
+        if not staging_fits(self.E, self._records_stride()):
+            _log_zero_copy_route("forward_prefill_staged", self.E * self._records_stride())
+            return self.forward(key, x, topk_ids, topk_w)
         if self._pipeline is None:
             self._pipeline = _PrefillPipeline(self)
         return self._pipeline.run(key, x, topk_ids, topk_w)

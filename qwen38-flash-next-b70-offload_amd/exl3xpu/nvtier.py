@@ -24,7 +24,7 @@ from concurrent.futures import ThreadPoolExecutor
 import numpy as np
 import torch
 
-from .moe_offload import ExpertStore, _HostRecords, _Stager, s64
+from .moe_offload import ExpertStore, _HostRecords, _Stager, _log_zero_copy_route, s64, staging_fits
 
 log = logging.getLogger("exl3xpu")
 _REC_ALIGN = 4096
@@ -388,7 +388,13 @@ class NvTier:
         """Prefill-size MoE for layer row li with its non-HBM experts streamed: reader threads read their records into
         a pinned host ring (read-ahead of the following layers), the copy stream moves them into an HBM staging
         buffer, and the layer runs on the table (HBM slot, else staging). The first layer of a forward synchronises
-        once and snapshots the slot map (reference nvtier.py:534-640)."""
+        once and snapshots the slot map (reference nvtier.py:534-640). A staging buffer above STAGE_VERIFIED_BYTES
+        is not used: the layer's experts are made RAM-resident (ensure_for_prefill) and the prefill kernels read the
+        non-HBM ones zero-copy from their records, which gives the same output."""
+        if not staging_fits(self.E, store.stride):
+            _log_zero_copy_route("NvTier.stage_forward", self.E * store.stride)
+            self.ensure_for_prefill(li, ids)
+            return store.forward(key, x, ids, w)
         if self._streamer is None:
             self._streamer = _TierStreamer(self)
         return self._streamer.run(store, key, li, x, ids, w)

@@ -288,7 +288,7 @@ def test_tier_exchange():
     c_src = (ctypes.c_void_p * 2)(*[t.data_ptr() for t in srcs])
     c_dst = (ctypes.c_void_p * 2)(*[t.data_ptr() for t in dsts])
     c_n = (ctypes.c_int64 * 2)(*sizes)
-    cap = 1000
+    cap = 1024                                            # a power of two (required)
     ring = torch.randint(0, n, (1 + cap,), generator=g, dtype=torch.int32)
     mirror = X.host_alloc(4 * (1 + cap)).view(torch.int32)
     mirror.fill_(-7)
@@ -309,10 +309,10 @@ def test_tier_exchange():
     m, r = mirror.numpy(), ring.numpy()
     assert m[0] == 700 and np.array_equal(m[1 + 650:1 + 700], r[1 + 650:1 + 700])
     assert (m[1:1 + 650] == -7).all() and (m[1 + 700:] == -7).all()
-    rc, _ = run(0, 1300, 900)                             # wraps: positions 900..999, then 0..299
+    rc, _ = run(0, 1300, 900)                             # wraps: positions 900..1023, then 0..275
     assert rc == 0 and m[0] == 1300
-    assert np.array_equal(m[1 + 900:], r[1 + 900:]) and np.array_equal(m[1:1 + 300], r[1:1 + 300])
-    assert (m[1 + 300:1 + 650] == -7).all()
+    assert np.array_equal(m[1 + 900:], r[1 + 900:]) and np.array_equal(m[1:1 + 276], r[1:1 + 276])
+    assert (m[1 + 276:1 + 650] == -7).all()
     mirror.fill_(-7)
     rc, _ = run(0, 5000, 100)                             # more than cap since `from`: the last cap entries
     assert rc == 0 and m[0] == 5000 and np.array_equal(m[1:], r[1:])
@@ -323,6 +323,10 @@ def test_tier_exchange():
     assert np.array_equal(flags.cpu().numpy(), want)
     bad = (ctypes.c_void_p * 1)(srcs[1].data_ptr() + 4)
     assert run(0, 5000, 5000, nc=1, src=bad)[0] != 0
+    # a capacity that is not a power of two is refused before anything is enqueued
+    rd = ring.cuda()
+    assert L.exl3_tier_exchange(flags.data_ptr(), n, diff.data_ptr(), 0, rd.data_ptr(), cap - 24, 0, mirror.data_ptr(),
+                                c_src, c_dst, c_n, 0, st) != 0
 
 
 @pytest.mark.gpu
@@ -516,3 +520,33 @@ def test_tier_fills_from_expert_file(tmp_path):
         assert a1.tolist() == a2.tolist() and e1.tolist() == e2.tolist(), n
     assert bad == 0
     assert tier.src.reads > 0 and recs[:, :, 2 + M * TK].sum() > 0
+
+
+@pytest.mark.parametrize("M", [150, 255])
+def test_cache_midsize_rows(M):
+    """Cached calls between the decode kernel's limit (1,024 picks) and prefill_min_m (256): M = 150 and 255 rows x
+    top-10 at the config-0 shapes (H 2048, I 512, 512 experts), 2 layers, 300 slots, a 600-record RAM tier, Zipf
+    routing (reference: the cached op over the align path, kernels/moe-a8/exl3_moe.a8.sycl:1239, 1277-1314). One
+    ensure takes all 1,500 / 2,550 picks; victims are written back, fills copied and committed, and the prefill
+    kernels read the committed table. Every device record and host decision equals the oracle's (one reference
+    ensure per call, Appendix A.1 of the contract), and every output equals the uncached forward on the true blobs
+    with the post-mask picks, bit for bit."""
+    L, E, S, TK, steps = 2, 512, 300, 10, 8
+    print(f"case cache mid-size rows M={M}", flush=True)
+    ids, w = synth.zipf_trace(20261210 + M, steps, L, E, TK, M=M)
+    ids = np.ascontiguousarray(ids.reshape(steps, L, M * TK))
+    w = np.ascontiguousarray(w.reshape(steps, L, M * TK))
+    co = cache.CacheOracle(L, E, S, ring_cap=1 << 12, budget=600, age=4, qmax=256, latency=2)
+    orecs, olog = co.run(ids, w)
+    store, tier, blobs, ref_ptr = _setup(L, E, S, 2048, 512, 3, 600, 256, 4, 2, 1 << 12, 19)
+    recs, bad = _run(store, tier, ids, w, 2048, check_out_every=1, ref_ptr=ref_ptr, M=M)
+    mism = np.nonzero((recs != orecs).any(axis=-1))
+    assert mism[0].size == 0, f"first mismatch at step/layer {mism[0][0]}/{mism[1][0]}"
+    for n, ((a1, e1), (a2, e2)) in enumerate(zip(tier.decisions, olog)):
+        assert a1.tolist() == a2.tolist() and e1.tolist() == e2.tolist(), n
+    assert bad == 0
+    P = M * TK
+    assert recs[:, :, 1].max() > 0 and recs[:, :, 2 + P].sum() > 0       # masked picks and fills happened
+    wb = recs[:, :, 3 + 2 * P:3 + 4 * P:2]
+    assert (wb >= 0).any()                                                 # and victims were written back
+    tier.close()

@@ -201,3 +201,33 @@ def test_linear_small_in_graph_replays():
         graph.replay()
         torch.cuda.synchronize()
         assert torch.equal(y_static, want)
+
+
+def test_linear_small_two_graphs_on_one_capture_stream():
+    """Two graphs captured one after another on torch's default capture stream, with no call on that stream before the
+    first capture, replayed second-first and then alternately with eager calls in between: every replay equals the
+    eager result bit for bit. Each capture zeroes the arrival counters of a workspace of its own inside the graph, so
+    a replay never depends on which graph (or eager call) ran before it."""
+    print("case linear small two graphs on one capture stream", flush=True)
+    ck = olin.checkpoint(72, 512, [256, 256], 3)
+    g = _group(ck)
+    xs = [_x(90 + i, 1, 512, torch.bfloat16)[1] for i in range(3)]
+    xa, xb = xs[0].clone(), xs[1].clone()
+    ga, gb = torch.cuda.CUDAGraph(), torch.cuda.CUDAGraph()
+    with torch.cuda.graph(ga):
+        ya = g(xa)
+    with torch.cuda.graph(gb):
+        yb = g(xb)
+    torch.cuda.synchronize()
+    want_a, want_b, want_c = g(xs[0]), g(xs[1]), g(xs[2])         # eager, on the current stream
+    torch.cuda.synchronize()
+    for rep in range(3):
+        gb.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(yb, want_b), rep
+        ga.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(ya, want_a), rep
+        yc = g(xs[2])
+        torch.cuda.synchronize()
+        assert torch.equal(yc, want_c), rep

@@ -327,24 +327,23 @@ def test_prefill_zero_copy_config0_shapes():
     assert torch.equal(out, ref)
 
 
-def test_plugin_caller_sequence():
+def _plugin_sequence(H, I, K, E, S, L, topk, dsteps, budget, n_distinct, prompts, seed):
     """The tier plugin's call sequence (plugin/sglang_plugin.tier.py:531-561 `apply`, 944-956 the host step after every
-    model step) over this API, tier mode: a 300-token prompt streamed through stage_forward, a 24-token prompt
-    (ensure_for_prefill, then the zero-copy forward), then decode steps through forward_cached (tier mask, RAM hits
-    written through), NvTierAsync.step after every model step. Every prompt output equals the all-resident output bit
-    for bit; every decode output equals the uncached forward on the true blobs with the post-mask picks."""
+    model step) over this API, tier mode: the prompts of `prompts` ((tokens, staged?) pairs; staged prompts of at
+    least 256 tokens go through stage_forward, the others through ensure_for_prefill and the zero-copy forward), then
+    decode steps through forward_cached (tier mask, RAM hits written through), NvTierAsync.step after every model
+    step. Every prompt output equals the all-resident output bit for bit; every decode output equals the uncached
+    forward on the true blobs with the post-mask picks."""
     from exl3xpu import nvtier
-    H, I, K, E, S, L, topk, dsteps = 256, 128, 3, 32, 24, 3, 4, 40
-    print("case plugin caller sequence", flush=True)
     store = nvtier.TierStore(H, I, K, E, S, n_layers=L)
     keys = [f"model.layers.{li}.mlp" for li in range(L)]
     for k in keys:
         store.add_layer(k)
-    src = nvtier.SyntheticExpertSource(H, I, K, 23, n_distinct=L * E)
-    tier = nvtier.NvTierAsync(store, src, budget_records=40, latency=2)
+    src = nvtier.SyntheticExpertSource(H, I, K, seed, n_distinct=n_distinct)
+    tier = nvtier.NvTierAsync(store, src, budget_records=budget, latency=2)
     blobs = torch.from_numpy(src.buf).cuda()
-    tables = [torch.tensor([blobs[li * E + e].data_ptr() for e in range(E)], dtype=torch.int64, device="cuda")
-              for li in range(L)]
+    tables = [torch.tensor([blobs[(li * E + e) % n_distinct].data_ptr() for e in range(E)], dtype=torch.int64,
+                           device="cuda") for li in range(L)]
 
     def apply(li, x, it, wt, stage):            # the plugin's dispatch in tier mode
         if x.shape[0] >= 3:
@@ -357,11 +356,12 @@ def test_plugin_caller_sequence():
 
     bad, masked = [], 0
     try:
-        steps = [(300, True, 90), (24, False, 91)] + [(1, False, 100 + n) for n in range(dsteps)]
-        for M, stage, seed in steps:
+        steps = [(M, st, seed * 10 + 90 + n) for n, (M, st) in enumerate(prompts)]
+        steps += [(1, False, seed * 10 + 100 + n) for n in range(dsteps)]
+        for M, stage, sd in steps:
             for li in range(L):
-                ids, w = synth.softmax_topk(seed * 7 + li, M, E, topk)
-                x = torch.from_numpy(exl3.bf16_to_f32(synth.activations(seed + li, M, H))).to(torch.bfloat16).cuda()
+                ids, w = synth.softmax_topk(sd * 7 + li, M, E, topk)
+                x = torch.from_numpy(exl3.bf16_to_f32(synth.activations(sd + li, M, H))).to(torch.bfloat16).cuda()
                 it, wt = torch.from_numpy(ids).cuda(), torch.from_numpy(w).cuda()
                 out = apply(li, x, it, wt, stage)
                 if M == 1:
@@ -369,10 +369,51 @@ def test_plugin_caller_sequence():
                 ref = _ops().moe_forward(x, it, wt, tables[li], I, K, E)     # it / wt after the tier mask
                 torch.cuda.synchronize()
                 if not torch.equal(out, ref):
-                    bad.append((M, seed, li))
+                    bad.append((M, sd, li))
             tier.step()                            # the host step hook after every model step
         torch.cuda.synchronize()
     finally:
         tier.close()
     assert not bad, f"outputs differ at (M, seed, layer) {bad[:4]}"
     assert masked > 0                              # the decode steps exercised the tier mask
+
+
+def test_plugin_caller_sequence():
+    """The plugin's tier-mode call sequence at small expert shapes (H 256, I 128, 32 experts, top-4): a 300-token
+    prompt streamed through stage_forward (staging buffers within the verified size), a 24-token prompt, 40 decode
+    steps."""
+    print("case plugin caller sequence", flush=True)
+    _plugin_sequence(256, 128, 3, 32, 24, 3, 4, 40, 40, 3 * 32, [(300, True), (24, False)], 23)
+
+
+def test_plugin_caller_sequence_config0_shapes():
+    """The same sequence at the config-0 expert shapes (H 2048, I 512, 512 experts of 1.2 MB, top-10; 2 layers, 300
+    HBM slots, a 700-record RAM tier): the 300-token prompt through stage_forward needs a 612 MB staging buffer, above
+    the verified size, so it takes the zero-copy route (ensure_for_prefill, then the prefill kernels read the non-HBM
+    experts from their pinned records); its output equals the all-resident output bit for bit, as do the 24-token
+    prompt's and the decode steps'."""
+    from exl3xpu.moe_offload import staging_fits
+    print("case plugin caller sequence config-0 shapes", flush=True)
+    assert not staging_fits(512, 1196032)
+    _plugin_sequence(2048, 512, 3, 512, 300, 2, 10, 12, 700, 64, [(300, True), (24, False)], 29)
+
+
+@pytest.mark.parametrize("M", [150, 255])
+def test_midsize_rows_uncached_vs_oracle(M):
+    """Uncached calls with more picks than the decode kernel takes (1,500 and 2,550 at top-10) below prefill_min_m
+    (256, unchanged) run the prefill kernels (the reference's align path, kernels/moe-a8/exl3_moe.a8.sycl:1277-1314):
+    config-0 shapes, against the oracle's prefill rounding points within rel-L2 2e-3 (16 distinct blobs over the 512
+    experts keep the oracle to seconds)."""
+    H, I, K, E, TK, nd = 2048, 512, 3, 512, 10, 16
+    print(f"case mid-size rows uncached M={M}", flush=True)
+    ids, w = synth.softmax_topk(700 + M, M, E, TK)
+    made = [synth.expert_blob(31, j, H, I, K) for j in range(nd)]
+    dev = torch.from_numpy(np.stack(made)).cuda()
+    table = torch.tensor([dev[e % nd].data_ptr() for e in range(E)], dtype=torch.int64, device="cuda")
+    x = synth.activations(800 + M, M, H)
+    gb = _run(x, ids, w, table, I, K, E)
+    ews = [exl3.ExpertWeights(b, H, I, K) for b in made]
+    ob, _ = exl3.moe_forward(x, ids, w, lambda e: ews[e % nd], variant="prefill")
+    r = rel_l2(gb, exl3.bf16_to_f32(ob))
+    print(f"mid-size M={M}: rel-L2 bf16 {r:.2e}", flush=True)
+    assert np.isfinite(gb).all() and r <= TOL

@@ -176,3 +176,59 @@ def test_evict_order_matches_sequential_classes():
             want += c.tolist()
             left -= len(c)
         assert nvtier._evict_order(over, masks, age).tolist() == want
+
+
+def test_staged_prefill_routes_zero_copy_above_limit():
+    """Above STAGE_VERIFIED_BYTES per staging buffer (every real expert count: 512 records of 1,196,032 B need 612
+    MB), the staged entry points never build a stager: ExpertStore.forward_prefill_staged runs forward() on the
+    layer's own table, stage_layer returns that table, and NvTier.stage_forward makes the batch RAM-resident
+    (ensure_for_prefill) and then runs forward(); nothing is staged. At or below the limit they stage."""
+    import torch
+    from exl3xpu import moe_offload, nvtier
+    assert moe_offload.staging_fits(16, 131072) and not moe_offload.staging_fits(16, 131073)
+    assert not moe_offload.staging_fits(512, 1196032)
+    calls = []
+    st = moe_offload.ExpertStore.__new__(moe_offload.ExpertStore)
+    st.E, st.slot_stride, st._pipeline = 512, 1196032, None
+    st.forward = lambda key, x, ids, w, ptrs=None: calls.append(("forward", key, ptrs)) or "y"
+    st.ptrs = lambda key: torch.arange(4)
+    assert st.forward_prefill_staged("k0", None, None, None) == "y"
+    assert calls == [("forward", "k0", None)] and st._pipeline is None
+    assert torch.equal(st.stage_layer("k0", 0, None), torch.arange(4)) and st._pipeline is None
+    calls.clear()
+    tier = nvtier.NvTier.__new__(nvtier.NvTier)
+    tier.E, tier._streamer = 512, None
+    tier.ensure_for_prefill = lambda li, ids: calls.append(("ensure", li, ids))
+
+    class _Store:
+        stride = 1196032
+
+        def forward(self, key, x, ids, w):
+            calls.append(("forward", key))
+            return "y"
+    assert tier.stage_forward(_Store(), "k3", 3, "x", "ids", "w") == "y"
+    assert calls == [("ensure", 3, "ids"), ("forward", "k3")] and tier._streamer is None
+
+
+def test_status_watch_raises_when_the_mirror_moves():
+    """The ExpertStore wrappers read the host mirror of the device timeout count (pinned host memory that a timed-out
+    bounded wait raises) before enqueueing anything, and raise RuntimeError once per change of it; forward,
+    forward_cached and prefetch all check, and the failed call enqueues nothing."""
+    from exl3xpu.moe_offload import ExpertStore, _StatusWatch
+    word = np.zeros(4, dtype=np.int32)
+    w = _StatusWatch(word)
+    w.check()
+    word[0] = 3
+    with pytest.raises(RuntimeError, match="3 bounded waits"):
+        w.check()
+    w.check()                                            # reported once
+    st = ExpertStore.__new__(ExpertStore)
+    st._watch, st.n_slots = _StatusWatch(word), 4
+    st._routing = lambda *a: pytest.fail("enqueued after a timeout")
+    st._ids32 = st._routing
+    for n, call in enumerate((lambda: st.forward_cached("k", None, None, None), lambda: st.forward("k", None, None, None),
+                              lambda: st.prefetch("k", None), st.check_device_status)):
+        word[0] = 4 + n
+        with pytest.raises(RuntimeError, match="1 bounded waits"):
+            call()
+    st.check_device_status()

@@ -186,3 +186,41 @@ def test_align_stable_counting_sort():
     assert np.array_equal(np.sort(a["act_expert"]), np.unique(ids))
     assert np.array_equal(ids.reshape(-1)[order][a["pair_of"]], ids.reshape(-1))
     assert a["n_blk"] == sum(-(-c // 8) for c in np.bincount(ids.reshape(-1)) if c)
+
+
+def _f32_nudge(x, k):
+    """x (float32 array) moved by k in {-1, 0, 1} ulps."""
+    if k == 0:
+        return x
+    return np.nextafter(x, np.float32(np.inf) if k > 0 else np.float32(-np.inf)).astype(np.float32)
+
+
+def test_silu_device_formula_bound():
+    """The SiLU of both expert kernels (silu_mul, csrc/exl3_common.cuh): g * rcp(1 + exp2(fp32(-g * log2e_f32))) with
+    v_exp_f32 and v_rcp_f32 each within one fp32 ulp. For every finite fp16 g and every combination of those ulp
+    errors, the fp32 SiLU stays within 4e-6 relative of g / (1 + exp(-g)) in float64 (results below 1e-30 in
+    magnitude: both below 1e-30), and its fp16 rounding is at most one fp16 ulp from that of the exact value. A
+    formula with exp(+g), or a lost factor g, fails both bounds by orders of magnitude."""
+    g16 = np.arange(65536, dtype=np.uint16).view(np.float16)
+    g16 = g16[np.isfinite(g16)]
+    g32, g = g16.astype(np.float32), g16.astype(np.float64)
+    with np.errstate(over="ignore"):
+        exact = g / (1.0 + np.exp(-g))
+        e32 = np.exp2(((-g32) * np.float32(float.fromhex("0x1.715476p+0"))).astype(np.float64)).astype(np.float32)
+
+    def order(h):                      # fp16 values -> integers in value order (one step = one fp16 ulp)
+        b = h.view(np.int16).astype(np.int32)
+        return np.where(b < 0, -(b & 0x7FFF), b)
+    big = np.abs(exact) > 1e-30
+    worst_rel, worst_ulp = 0.0, 0
+    for de in (-1, 0, 1):
+        d = np.float32(1) + _f32_nudge(e32, de)
+        with np.errstate(divide="ignore", over="ignore"):
+            r = (1.0 / d.astype(np.float64)).astype(np.float32)
+        for dr in (-1, 0, 1):
+            s = g32 * _f32_nudge(r, dr)
+            rel = np.abs(s[big].astype(np.float64) - exact[big]) / np.abs(exact[big])
+            worst_rel = max(worst_rel, float(rel.max()))
+            assert (np.abs(s[~big]) <= 1e-30).all()
+            worst_ulp = max(worst_ulp, int(np.abs(order(s.astype(np.float16)) - order(exact.astype(np.float16))).max()))
+    assert worst_rel <= 4e-6 and worst_ulp <= 1, (worst_rel, worst_ulp)
