@@ -9,10 +9,10 @@
 //     (bounded) for the pair's gate/up sums, run the gate/up epilogue of the pair themselves (output Hadamards * svh,
 //     SiLU(g)*u, *suh_d, down-input Hadamard -> the down input in LDS, fp16), GEMV with an in-WG reduction, epilogue
 //     (output Hadamard * w * svh_d) -> y (fp32). The WG of the last pick of a row (the combiner of that row and block)
-//     waits with all its waves for the other picks' y and sums the top-k y's in k order into out; the combiner of the
-//     last (row, block) also checks that every other gate/up and down workgroup has consumed its inputs (each raises
-//     a started word once it has), then commits the expert-cache fills (ptrs[e] = fill[e]; fill[e] = 0) and advances
-//     the call epoch.
+//     loads the other picks' y with its wave 0 alone (no LDS round, no barrier) and sums the top-k y's in k order into
+//     out; in the combiner of the last (row, block) the other waves meanwhile check that every other gate/up and down
+//     workgroup has consumed its inputs (each raises a started word once it has), then wave 0 commits the
+//     expert-cache fills (ptrs[e] = fill[e]; fill[e] = 0) and advances the call epoch.
 // Every value handed from one workgroup to another is a tagged word (tag = call epoch + 1 in the high half, the fp32
 // value in the low half) written with one 64-bit agent-scope store into a library-owned zeroed buffer: a consumer polls
 // the data itself, so no producer waits for its stores and no counter is shared (same-address atomics serialize at
@@ -177,7 +177,7 @@ struct Gemv8 {
 
 constexpr int kWaves = 8;                    // waves per workgroup (both kinds)
 constexpr int kThreads = 64 * kWaves;
-constexpr int kCombRound = 2 * kWaves;       // picks whose y a combiner loads per round (two per wave)
+constexpr int kCombPicks = 10;               // other picks' y a combiner's wave 0 loads per round
 
 struct GateUpShared {
     half2_t xq[kWaves][64];                  // per wave: Hadamard-transformed x * suh of its 128-row block
@@ -185,7 +185,6 @@ struct GateUpShared {
 };
 struct DownShared {
     half2_t xd[kMaxI / 2];                   // the pair's down input (fp16), [I/2]
-    float yc[kCombRound][128];               // combiner: the other picks' y of its block, one round of picks
     // the last workgroup of a call with the ensure inside: the commit, victim and mask-rewrite inputs, loaded early
     int fin_nf, fin_nv;
     int fin_ef[kEnsMaxP];                    // filled experts
@@ -330,16 +329,25 @@ __device__ __forceinline__ void gateup_wg(const DecodeArgs& A, int blk, LayerSha
     const int hb = ks * 8 + wv;
     const bool live = hb < nhb;
     const int tiles_n = 2 * I / 16, ct0 = pj * (I / 16) + cg * 4, rt0 = hb * 8;
+    // x and suh of this wave's block first, so that its input Hadamard need not wait for the weight words
+    float xa0 = 0.f, xa1 = 0.f;
+    half_t sa0 = 0, sa1 = 0;
+    if (live) {
+        const half_t* suh = (const half_t*)(base + (pj ? A.g.off_suh_u : A.g.off_suh_g));
+        const int k0 = hb * 128 + 2 * l;
+        const size_t xo = (size_t)m * A.x_stride + k0;
+        xa0 = ld_act(A.x, A.x_dt, xo);
+        xa1 = ld_act(A.x, A.x_dt, xo + 1);
+        sa0 = suh[k0];
+        sa1 = suh[k0 + 1];
+    }
     GQ g;
     if (live) g.load((const uint32_t*)base, tiles_n, rt0, ct0);
     const unsigned tag = wv == 0 ? call_tag() : 0u;
     float ssum = 0.f;
     if (live) {                                  // input Hadamard of x * suh over this wave's block
-        const half_t* suh = (const half_t*)(base + (pj ? A.g.off_suh_u : A.g.off_suh_g));
-        const int k0 = hb * 128 + 2 * l;
-        const size_t xo = (size_t)m * A.x_stride + k0;
-        float v0 = (float)(half_t)(ld_act(A.x, A.x_dt, xo) * (float)suh[k0]);
-        float v1 = (float)(half_t)(ld_act(A.x, A.x_dt, xo + 1) * (float)suh[k0 + 1]);
+        float v0 = (float)(half_t)(xa0 * (float)sa0);
+        float v1 = (float)(half_t)(xa1 * (float)sa1);
         wave_fwht128(v0, v1);
         const half_t h0 = (half_t)(v0 * kRsqrt128), h1 = (half_t)(v1 * kRsqrt128);
         S.u.gu.xq[wv][l] = half2_t{h0, h1};
@@ -600,7 +608,9 @@ __device__ __forceinline__ void down_wg(const DecodeArgs& A, int blk, LayerShare
     __syncthreads();
     const int k = a % A.topk;
     const bool comb = k == A.topk - 1;           // combiner of (row m, block nb): the row's last pick, highest id
-    if (wv != 0 && !comb) return;
+    const int nfin = A.M * nbn, me = m * nbn + nb;
+    const bool fin = comb && me == nfin - 1;     // the last combiner of the call also commits
+    if (wv != 0 && !fin) return;
     const int c = nb * 128 + 2 * l;
     float v0 = 0.f, v1 = 0.f;
     uint64_t* yb = A.xy + (size_t)(m * A.topk) * H + c;
@@ -614,59 +624,54 @@ __device__ __forceinline__ void down_wg(const DecodeArgs& A, int blk, LayerShare
         const float sc = kRsqrt128 * wgt;
         v0 = v0 * sc * (float)sc_d.x;
         v1 = v1 * sc * (float)sc_d.y;
+        asm volatile("" : "+v"(v0), "+v"(v1));   // y rounded as stored (not fused into the combiner's sum)
         if (!comb) {                             // y of this pick for the row's combiner
             st_tag(yb + (size_t)k * H, tag, v0);
             st_tag(yb + (size_t)k * H + 1, tag, v1);
             return;
         }
-    }
-    // combiner: the other picks' y (lower workgroup ids) loaded by all waves, two picks per wave and round, summed by
-    // wave 0 in k order after its own pick's; the last combiner also polls every other workgroup's started word in
-    // the first round
-    const int nfin = A.M * nbn, me = m * nbn + nb;
-    const bool fin = me == nfin - 1;
-    const int nstart = A.n_gu + A.npairs * nbn - 1;       // every workgroup before this one
-    float o0 = 0.f, o1 = 0.f;
-    for (int k0 = 0; k0 < A.topk - 1 || (fin && k0 == 0); k0 += kCombRound) {
-        uint64_t yw[2][2];
+        // combiner: wave 0 loads the other picks' y (lower workgroup ids) itself, up to kCombPicks per round, and sums
+        // them in k order before its own pick's
+        float o0 = 0.f, o1 = 0.f;
+        for (int k0 = 0; k0 < A.topk - 1; k0 += kCombPicks) {
+            uint64_t yw[kCombPicks][2];
+            int it = 0;
+            for (;;) {
+                bool ok = true;
+#pragma unroll
+                for (int j = 0; j < kCombPicks; ++j) {
+                    const bool in = k0 + j < A.topk - 1;
+                    yw[j][0] = in ? ld_tag(yb + (size_t)(k0 + j) * H) : 0;
+                    yw[j][1] = in ? ld_tag(yb + (size_t)(k0 + j) * H + 1) : 0;
+                    ok = ok && (!in || (tag_is(yw[j][0], tag) && tag_is(yw[j][1], tag)));
+                }
+                if (__all(ok) || spin_out(it)) break;
+            }
+#pragma unroll
+            for (int j = 0; j < kCombPicks; ++j)
+                if (k0 + j < A.topk - 1) {
+                    o0 += tag_val(yw[j][0]);
+                    o1 += tag_val(yw[j][1]);
+                }
+        }
+        o0 += v0;
+        o1 += v1;
+        const size_t oo = (size_t)m * A.out_stride + c;
+        st_act(A.out, A.x_dt, oo, o0);
+        st_act(A.out, A.x_dt, oo + 1, o1);
+    } else {
+        // the last combiner's other waves: every other workgroup has raised its started word (its inputs consumed)
+        const int nstart = A.n_gu + A.npairs * nbn - 1;       // every workgroup before this one
         int it = 0;
         for (;;) {
             bool ok = true;
-#pragma unroll
-            for (int i = 0; i < 2; ++i) {
-                const int j = k0 + wv + kWaves * i;
-                const bool in = j < A.topk - 1;
-                yw[i][0] = in ? ld_tag(yb + (size_t)j * H) : 0;
-                yw[i][1] = in ? ld_tag(yb + (size_t)j * H + 1) : 0;
-                ok = ok && (!in || (tag_is(yw[i][0], tag) && tag_is(yw[i][1], tag)));
-            }
-            if (fin && k0 == 0)
-                for (int i = tid; i < nstart; i += kThreads) ok = ok && tag_is(ld_tag(A.xstart + i), tag);
-            if (__syncthreads_and(ok) || spin_out(it)) break;
+            for (int i = tid - 64; i < nstart; i += kThreads - 64) ok = ok && tag_is(ld_tag(A.xstart + i), tag);
+            if (__all(ok) || spin_out(it)) break;
         }
-#pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const int j = wv + kWaves * i;
-            if (k0 + j < A.topk - 1) {
-                S.u.dn.yc[j][2 * l] = tag_val(yw[i][0]);
-                S.u.dn.yc[j][2 * l + 1] = tag_val(yw[i][1]);
-            }
-        }
-        __syncthreads();
-        if (wv == 0)
-            for (int j = 0; j < kCombRound && k0 + j < A.topk - 1; ++j) {
-                o0 += S.u.dn.yc[j][2 * l];
-                o1 += S.u.dn.yc[j][2 * l + 1];
-            }
-        __syncthreads();
     }
-    if (wv != 0) return;
-    o0 += v0;
-    o1 += v1;
-    const size_t oo = (size_t)m * A.out_stride + c;
-    st_act(A.out, A.x_dt, oo, o0);
-    st_act(A.out, A.x_dt, oo + 1, o1);
     if (!fin) return;
+    __syncthreads();
+    if (wv != 0) return;
     // the last (row, block) of the layer: every other workgroup has consumed its inputs; advance the epoch and commit
     // the cache fills
     if (l == 0) {
