@@ -706,8 +706,19 @@ __device__ __forceinline__ void down_wg(const DecodeArgs& A, int blk, LayerShare
     }
 }
 
-template <int K>
-__global__ void __launch_bounds__(kThreads) moe_layer_kernel(DecodeArgs A) {
+// LEAN: the plain resident call (no cache: no ensure, victims, write-through, commit or precomputed pair pointers),
+// compiled without those paths so that the kernel's code is a fraction of the full one
+template <int K, bool LEAN>
+__global__ void __launch_bounds__(kThreads) moe_layer_kernel(DecodeArgs A0) {
+    DecodeArgs A = A0;
+    if constexpr (LEAN) {
+        A.fused = 0;
+        A.fill = nullptr;
+        A.pair_ptr = nullptr;
+        A.commit_ptrs = nullptr;
+        A.n_vict_wg = 0;
+        A.vict_inline = 0;
+    }
     __shared__ __align__(16) uint8_t lds[sizeof(LayerShared) > sizeof(EnsureShared) ? sizeof(LayerShared)
                                                                                      : sizeof(EnsureShared)];
     LayerShared& S = *reinterpret_cast<LayerShared*>(lds);
@@ -757,9 +768,17 @@ hipError_t launch_moe_layer(int K, const DecodeArgs& a, hipStream_t s) {
     const int n_gu = a.n_gu;
     const int n_dn = a.npairs * (a.g.H / 128);
     dim3 grid((unsigned)(a.fused + a.n_vict_wg + n_gu + n_dn));
-    if (K == 2) hipLaunchKernelGGL(moe_layer_kernel<2>, grid, dim3(kThreads), 0, s, a);
-    else if (K == 3) hipLaunchKernelGGL(moe_layer_kernel<3>, grid, dim3(kThreads), 0, s, a);
-    else if (K == 4) hipLaunchKernelGGL(moe_layer_kernel<4>, grid, dim3(kThreads), 0, s, a);
+    const bool lean = !a.fused && !a.fill && !a.pair_ptr && !a.commit_ptrs && !a.n_vict_wg && !a.vict_inline;
+    if (K == 2) {
+        if (lean) hipLaunchKernelGGL((moe_layer_kernel<2, true>), grid, dim3(kThreads), 0, s, a);
+        else hipLaunchKernelGGL((moe_layer_kernel<2, false>), grid, dim3(kThreads), 0, s, a);
+    } else if (K == 3) {
+        if (lean) hipLaunchKernelGGL((moe_layer_kernel<3, true>), grid, dim3(kThreads), 0, s, a);
+        else hipLaunchKernelGGL((moe_layer_kernel<3, false>), grid, dim3(kThreads), 0, s, a);
+    } else if (K == 4) {
+        if (lean) hipLaunchKernelGGL((moe_layer_kernel<4, true>), grid, dim3(kThreads), 0, s, a);
+        else hipLaunchKernelGGL((moe_layer_kernel<4, false>), grid, dim3(kThreads), 0, s, a);
+    }
     else return hipErrorInvalidValue;
     return hipGetLastError();
 }
