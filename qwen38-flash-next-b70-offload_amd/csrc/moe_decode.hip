@@ -16,7 +16,7 @@
 // Every value handed from one workgroup to another is a tagged word (tag = call epoch + 1 in the high half, the fp32
 // value in the low half) written with one 64-bit agent-scope store into a library-owned zeroed buffer: a consumer polls
 // the data itself, so no producer waits for its stores and no counter is shared (same-address atomics serialize at
-// the coherence point). A consumer needing many words (the gate/up sums) first polls one word per producer.
+// the coherence point). A consumer polls the data words themselves (the gate/up sums: 4 ksn words per lane and round).
 // Gate/up WGs have lower ids, so on every XCD they are dispatched before any down WG and never wait: the down WGs'
 // wait always ends (it is also bounded, with an error flag, so a broken assumption cannot hang the GPU).
 //
@@ -46,7 +46,7 @@ __device__ __align__(16) int g_status[4];
 __device__ int* g_status_host;
 
 constexpr int kSpinMax = 1 << 22;
-constexpr uint64_t kDownLoadDelay = 120;         // 1.2 us in s_memrealtime ticks
+constexpr uint64_t kDownLoadDelay = 200;         // 2 us in s_memrealtime ticks
 
 // tagged exchange words: (tag << 32) | fp32 bits, one single-copy-atomic 64-bit agent-scope access
 __device__ __forceinline__ void st_tag(uint64_t* p, unsigned tag, float v) {
@@ -512,15 +512,6 @@ __device__ __forceinline__ void down_wg(const DecodeArgs& A, int blk, LayerShare
         const uint64_t* pg = A.xpart + (size_t)a * ksn * 2 * I;
         for (int b = wv; b < I / 128; b += kWaves) {
             const int cI = b * 128 + 2 * l;
-            {   // one word per producing workgroup first: lane s < 4 ksn watches (slice s >> 2, proj, group)
-                const int sk = l >> 2, sp = (l >> 1) & 1, sg = l & 1;
-                const uint64_t* q = pg + (size_t)sk * 2 * I + sp * I + (2 * b + sg) * 64;
-                int it = 0;
-                for (;;) {
-                    const bool ok = l >= 4 * ksn || tag_is(ld_tag(q), tag);
-                    if (__all(ok) || spin_out(it)) break;
-                }
-            }
             float g0 = 0.f, g1 = 0.f, u0 = 0.f, u1 = 0.f;
             for (int k0 = 0; k0 < ksn; k0 += 2) {        // the K-slices in order, two at a time
                 uint64_t v[2][4];
@@ -706,18 +697,25 @@ __device__ __forceinline__ void down_wg(const DecodeArgs& A, int blk, LayerShare
     }
 }
 
-// LEAN: the plain resident call (no cache: no ensure, victims, write-through, commit or precomputed pair pointers),
-// compiled without those paths so that the kernel's code is a fraction of the full one
-template <int K, bool LEAN>
+// MODE 1: the plain resident call (no cache: no ensure, victims, write-through, commit or precomputed pair pointers),
+// compiled without those paths (21.6 KB of code against 54.6 KB for K = 3, no SGPR spills); MODE 2: the tier's cached
+// call (ensure inside the launch, victims copied inline by the writers of each miss, no victim workgroups); MODE 0:
+// every other combination. Each instantiation carries only its own paths, so the hot code of a call stays small.
+template <int K, int MODE>
 __global__ void __launch_bounds__(kThreads) moe_layer_kernel(DecodeArgs A0) {
     DecodeArgs A = A0;
-    if constexpr (LEAN) {
+    if constexpr (MODE == 1) {       // lean
         A.fused = 0;
         A.fill = nullptr;
         A.pair_ptr = nullptr;
         A.commit_ptrs = nullptr;
         A.n_vict_wg = 0;
         A.vict_inline = 0;
+    } else if constexpr (MODE == 2) {   // fused ensure, victims copied inline
+        A.fused = 1;
+        A.pair_ptr = nullptr;
+        A.n_vict_wg = 0;
+        A.vict_inline = 1;
     }
     __shared__ __align__(16) uint8_t lds[sizeof(LayerShared) > sizeof(EnsureShared) ? sizeof(LayerShared)
                                                                                      : sizeof(EnsureShared)];
@@ -769,15 +767,19 @@ hipError_t launch_moe_layer(int K, const DecodeArgs& a, hipStream_t s) {
     const int n_dn = a.npairs * (a.g.H / 128);
     dim3 grid((unsigned)(a.fused + a.n_vict_wg + n_gu + n_dn));
     const bool lean = !a.fused && !a.fill && !a.pair_ptr && !a.commit_ptrs && !a.n_vict_wg && !a.vict_inline;
+    const int mode = lean ? 1 : (a.fused && !a.pair_ptr && !a.n_vict_wg && a.vict_inline ? 2 : 0);
     if (K == 2) {
-        if (lean) hipLaunchKernelGGL((moe_layer_kernel<2, true>), grid, dim3(kThreads), 0, s, a);
-        else hipLaunchKernelGGL((moe_layer_kernel<2, false>), grid, dim3(kThreads), 0, s, a);
+        if (mode == 1) hipLaunchKernelGGL((moe_layer_kernel<2, 1>), grid, dim3(kThreads), 0, s, a);
+        else if (mode == 2) hipLaunchKernelGGL((moe_layer_kernel<2, 2>), grid, dim3(kThreads), 0, s, a);
+        else hipLaunchKernelGGL((moe_layer_kernel<2, 0>), grid, dim3(kThreads), 0, s, a);
     } else if (K == 3) {
-        if (lean) hipLaunchKernelGGL((moe_layer_kernel<3, true>), grid, dim3(kThreads), 0, s, a);
-        else hipLaunchKernelGGL((moe_layer_kernel<3, false>), grid, dim3(kThreads), 0, s, a);
+        if (mode == 1) hipLaunchKernelGGL((moe_layer_kernel<3, 1>), grid, dim3(kThreads), 0, s, a);
+        else if (mode == 2) hipLaunchKernelGGL((moe_layer_kernel<3, 2>), grid, dim3(kThreads), 0, s, a);
+        else hipLaunchKernelGGL((moe_layer_kernel<3, 0>), grid, dim3(kThreads), 0, s, a);
     } else if (K == 4) {
-        if (lean) hipLaunchKernelGGL((moe_layer_kernel<4, true>), grid, dim3(kThreads), 0, s, a);
-        else hipLaunchKernelGGL((moe_layer_kernel<4, false>), grid, dim3(kThreads), 0, s, a);
+        if (mode == 1) hipLaunchKernelGGL((moe_layer_kernel<4, 1>), grid, dim3(kThreads), 0, s, a);
+        else if (mode == 2) hipLaunchKernelGGL((moe_layer_kernel<4, 2>), grid, dim3(kThreads), 0, s, a);
+        else hipLaunchKernelGGL((moe_layer_kernel<4, 0>), grid, dim3(kThreads), 0, s, a);
     }
     else return hipErrorInvalidValue;
     return hipGetLastError();
