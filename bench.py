@@ -366,6 +366,175 @@ def run_linear(args, dev):
     print(json.dumps(out), flush=True)
 
 
+C4_H, C4_I, C4_E, C4_TOPK, C4_L, C4_KS, C4_DISTINCT, C4_SEED = 4096, 1536, 128, 8, 48, (2, 3, 4), 8, 20261205
+C4_SETTLE = 30               # untimed steps first: the 30 % pool fills within a few steps of uniform routing
+C4_ROOF_CALLS = 20           # resident roofline: R x 16 calls per bitrate in one graph
+
+
+def run_config4(args, dev):
+    """Config-4 decode leg: 48 MoE layers of 128 experts (H 4096, I 1536, SwiGLU), top-8 uniform-random routing, the
+    bitrate of layer l is K = 2, 3, 4 cycling, an HBM slot pool of 30 % of all expert bytes (slots of the largest
+    blob), bs = --bs. No RAM-tier budget: every expert has a pinned host record, as the workload states.
+    (1) Cached decode: each step replays one HIP graph of the 48 forward_cached calls (device LRU cache inside the
+    layer kernel; misses read zero-copy from the host records over PCIe and written through into their new slot).
+    Reports tok/s, and the HBM bytes of the experts served from slots (U_hit x blob(K_l) per call, counted from the
+    device decision log) per second of step time as a fraction of the HBM peak; miss bytes are PCIe traffic.
+    (2) Resident roofline per bitrate: C4_ROOF_CALLS x 16 moe_forward calls of that bitrate, every pick in its own HBM
+    slot (a fresh slot per pick, cycling through the pool), captured in one graph and timed with HIP events.
+    Host records of the layers that share a bitrate alias one pinned arena holding that bitrate's 8 distinct
+    synthetic experts (record e = expert e % 8); the cache's decisions and the bytes it moves do not depend on the
+    record contents."""
+    import ctypes
+
+    import numpy as np
+    import torch
+    from exl3xpu import moe_offload, nvtier, synth
+    H, I, E, topk, L, bs = C4_H, C4_I, C4_E, C4_TOPK, C4_L, args.bs
+    t0 = time.perf_counter()
+    X = moe_offload.ops()
+    Ks = [C4_KS[li % len(C4_KS)] for li in range(L)]
+    blob = {k: int(X.blob_bytes(H, I, k)) for k in C4_KS}
+    srcs = {k: nvtier.SyntheticExpertSource(H, I, k, C4_SEED + k, n_distinct=C4_DISTINCT) for k in C4_KS}
+
+    class AliasedStore(moe_offload.ExpertStore):
+        arenas: dict = {}
+
+        def _new_records(self, li, blobs):
+            k = Ks[li]
+            if k not in self.arenas:
+                a = self.X.host_alloc(E * self.blob)
+                view = a.view(E, self.blob)
+                for e in range(E):
+                    view[e, :blob[k]].copy_(torch.from_numpy(srcs[k].buf[e % C4_DISTINCT]))
+                self.arenas[k] = view
+            v = self.arenas[k]
+            return moe_offload._HostRecords(v.data_ptr(), self.blob, v.data_ptr(), v.data_ptr() + E * self.blob, v)
+
+    total = sum(E * blob[k] for k in Ks)
+    S = int(0.3 * total / max(blob.values()))
+    store = AliasedStore(H, I, max(C4_KS), E, S, device=dev, max_layers=L)
+    store.mixed_bitrates()
+    keys = [f"model.layers.{li}.mlp" for li in range(L)]
+    for li, key in enumerate(keys):
+        store.add_layer(key)
+        store.K_of[key] = Ks[li]
+    log(f"config 4 setup {time.perf_counter() - t0:.1f} s: {S} slots x {store.blob} B ({S * store.blob / 2**30:.1f} GiB), "
+        f"expert bytes {total / 2**30:.1f} GiB")
+    steps = args.steps
+    ids_np, w_np = synth.uniform_trace(C4_SEED, C4_SETTLE + steps, L, E, topk, M=bs)
+    ids_all = torch.from_numpy(ids_np).to(dev)
+    w_all = torch.from_numpy(w_np).to(dev)
+    xs = torch.randn(L, bs, H, generator=torch.Generator().manual_seed(C4_SEED)).to(torch.bfloat16).to(dev)
+    ids_s = torch.empty(L, bs, topk, dtype=torch.int32, device=dev)
+    w_s = torch.empty(L, bs, topk, dtype=torch.float32, device=dev)
+    step_t = torch.zeros(1, dtype=torch.int64, device=dev)
+    P = bs * topk
+    rl = 3 + 4 * P
+    logbuf = torch.zeros(1 + (C4_SETTLE + steps + 2) * L * rl, dtype=torch.int32, device=dev)
+    X.moe_set_decision_log(logbuf)
+
+    def layers():
+        torch.index_select(ids_all, 0, step_t, out=ids_s.view(1, L, bs, topk))
+        torch.index_select(w_all, 0, step_t, out=w_s.view(1, L, bs, topk))
+        step_t.add_(1)
+        return [store.forward_cached(keys[li], xs[li], ids_s[li], w_s[li]) for li in range(L)]
+
+    layers()                                    # the first step eagerly (library set-up), then the graph
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, capture_error_mode="thread_local"):
+        layers()
+    for _ in range(C4_SETTLE - 1):
+        graph.replay()
+    torch.cuda.synchronize()
+    n0 = int(logbuf[0].item())
+    t1 = time.perf_counter()
+    for _ in range(steps):
+        graph.replay()
+    torch.cuda.synchronize()
+    el = time.perf_counter() - t1
+    X.moe_set_decision_log(torch.zeros(0, dtype=torch.int32, device=dev))
+    recs = logbuf[1:1 + int(logbuf[0].item()) * rl].view(-1, rl).cpu().numpy()[n0:]
+    assert recs.shape[0] == steps * L, f"decision log holds {recs.shape[0]} records, expected {steps * L}"
+    layer_of = np.tile(np.arange(L), steps)
+    distinct = np.array([len(set(r[2:2 + P].tolist())) for r in recs])
+    miss = recs[:, 2 + P]
+    kb = np.array([blob[Ks[li]] for li in layer_of], dtype=np.float64)
+    hit_bytes = float(((distinct - miss) * kb).sum())
+    miss_bytes = float((miss * kb).sum())
+    status = (ctypes.c_int32 * 4)()
+    from exl3xpu import capi
+    capi.check(capi.lib().exl3_device_status(status, torch.cuda.current_stream().cuda_stream), "device status")
+    tok_s = steps * bs / el
+    hit_gbs = hit_bytes / el / 1e9
+    log(f"config 4 cached decode bs={bs}: {steps} steps in {el:.3f} s = {tok_s:.2f} tok/s; per step {distinct.sum() / steps:.0f} "
+        f"distinct picks, {miss.sum() / steps:.0f} misses ({miss_bytes / steps / 1e9:.2f} GB over PCIe), "
+        f"hit bytes {hit_bytes / steps / 1e9:.2f} GB -> {hit_gbs:.1f} GB/s")
+    # resident roofline per bitrate: every pick its own slot, cycling through the pool
+    roof = {}
+    slots = store.slots.view(-1)
+    for k in C4_KS:
+        nb = blob[k]
+        src = torch.from_numpy(srcs[k].buf).to(dev)
+        for s_ in range(S):
+            slots[s_ * store.blob:s_ * store.blob + nb].copy_(src[s_ % C4_DISTINCT])
+        R = C4_ROOF_CALLS * 16
+        rid, rw = synth.uniform_trace(C4_SEED + 100 + k, R, 1, E, topk, M=bs)
+        tbl = torch.zeros(R, E, dtype=torch.int64)
+        ub = np.zeros(R)
+        s_ = 0
+        for r in range(R):
+            u = sorted(set(rid[r, 0].reshape(-1).tolist()))
+            for e in u:
+                tbl[r, e] = store.slot_base + (s_ % S) * store.blob
+                s_ += 1
+            ub[r] = len(u) * nb
+        tbl = tbl.to(dev)
+        rid_d = torch.from_numpy(rid[:, 0]).to(dev)
+        rw_d = torch.from_numpy(rw[:, 0]).to(dev)
+        xr = xs[0]
+        for r in range(2):
+            X.moe_forward(xr, rid_d[r], rw_d[r], tbl[r], I, k, E)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, capture_error_mode="thread_local"):
+            for r in range(R):
+                X.moe_forward(xr, rid_d[r], rw_d[r], tbl[r], I, k, E)
+        g.replay()
+        torch.cuda.synchronize()
+        st = torch.cuda.current_stream()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(st)
+        g.replay()
+        e1.record(st)
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / R
+        gbs = float(ub.mean()) / (us * 1e-6) / 1e9
+        roof[f"K{k}"] = {"us_per_call": round(us, 2), "bytes_per_call": float(ub.mean()), "GBps": round(gbs, 1),
+                         "frac": round(gbs / HBM_PEAK, 4)}
+        log(f"config 4 resident K={k} bs={bs}: {us:.2f} us per call, {ub.mean() / 1e6:.1f} MB -> {gbs:.0f} GB/s")
+    out = {
+        "metric": "config 4: MoE decode tok/s (48L x 128E top-8, H 4096 / I 1536, EXL3 K 2/3/4 cycling, 30 % HBM pool, "
+                  "uniform routing); HBM bytes of hit experts per second",
+        "value": round(tok_s, 3), "unit": "tok/s", "n_gpus": 1, "steps": steps, "warmup": C4_SETTLE,
+        "ms_per_step": round(el / steps * 1e3, 3), "higher_is_better": True, "dtype": "bf16",
+        "data": "synthetic: seeded EXL3 experts (8 distinct per bitrate), seeded uniform routing trace",
+        "config": {"workload": f"config 4 decode bs={bs}", "layers": L, "experts": E, "topk": topk, "hidden": H,
+                   "intermediate": I, "K_cycle": list(C4_KS), "batch": bs, "hbm_slots": S,
+                   "slot_bytes": store.blob, "pool_fraction": 0.3},
+        "per_step": {"distinct_picks": float(distinct.sum() / steps), "misses": float(miss.sum() / steps),
+                     "hit_bytes": hit_bytes / steps, "pcie_miss_bytes": miss_bytes / steps},
+        "hit_hbm": {"GBps": round(hit_gbs, 1), "frac": round(hit_gbs / HBM_PEAK, 4),
+                    "note": "U_hit x blob(K_l) summed over the timed calls / step time (the steps are PCIe-bound: "
+                            "about 70 % of the picks miss the 30 % pool under uniform routing)"},
+        "resident_roofline": roof,
+        "device_status": int(status[0]),
+    }
+    if status[0]:
+        out["valid"] = False
+    print(json.dumps(out), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -386,6 +555,9 @@ def main():
     ap.add_argument("--prefill-tiered", action="store_true",
                     help="the prefill leg through the tier (8,000 HBM slots, zero-copy RAM-tier reads)")
     ap.add_argument("--prefill-staged", action="store_true", help="(disabled) the staged prefill variant")
+    ap.add_argument("--config4", action="store_true",
+                    help="config 4: mixed-bitrate decode (H 4096, I 1536, 128 experts, top-8, 30 %% pool, uniform "
+                         "routing) and its resident roofline per bitrate")
     ap.add_argument("--roofline-only", action="store_true",
                     help="counter runs: only the HBM-resident layer calls, after 3 device copies of 256 MiB (the "
                          "known-size calibration kernel for FETCH_SIZE / WRITE_SIZE)")
@@ -409,6 +581,10 @@ def main():
         return run_linear(args, dev)
     if args.prefill_tiered:
         return run_prefill_tiered(args, dev)
+    if args.config4:
+        if "--steps" not in sys.argv:
+            args.steps = 60
+        return run_config4(args, dev)
     t0 = time.perf_counter()
     # config 1 (--bookkeeping): the same cache and tier on 128 x 128 experts, so that a layer call is the fused ensure
     # plus a 64 KB GEMV; the 4,000-step trace from an empty cache, no warm-up

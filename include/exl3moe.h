@@ -68,10 +68,11 @@ int exl3_set_splits(int64_t gu_p, int64_t dn_p);
 int exl3_set_mr(int64_t mr);
 /* moe_set_debug (a8:728): accepted for API compatibility; kernel skipping for timing probes is not provided */
 int exl3_set_debug(int64_t v);
-/* Decision log of the device cache (no reference counterpart; test hook): int32 buffer [1 + cap * (3 + 4P)],
- * buf[0] = records written; one record per ensure call of 3 + 4P int32: [T, ring count, P post-mask ids, misses nm,
- * P filled experts (-1 pad), P (write-back key or -1, slot) pairs (-2 pad)]. NULL = off. */
-int exl3_set_decision_log(int32_t* buf, int64_t cap_records);
+/* Decision log of the device cache (no reference counterpart; test hook): int32 buffer [1 + cap_words],
+ * buf[0] = ensure calls counted; one record per ensure call of 3 + 4P int32 (P picks of the call; one P per log):
+ * [T, ring count, P post-mask ids, misses nm, P filled experts (-1 pad), P (write-back key or -1, slot) pairs (-2
+ * pad)], record i at buf + 1 + i (3 + 4P), written only if it ends within the cap_words words. NULL = off. */
+int exl3_set_decision_log(int32_t* buf, int64_t cap_words);
 
 /* ---- routed-expert MoE --------------------------------------------------------------------------------------------- */
 

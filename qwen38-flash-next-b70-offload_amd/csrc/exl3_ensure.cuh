@@ -159,7 +159,7 @@ __device__ void ensure_wg(const EnsureArgs& A, EnsureShared& Z, int* done) {
             }
             if (A.log) {
                 const int idx = A.log[0];
-                if (idx < A.log_cap) {
+                if ((int64_t)(idx + 1) * (3 + 4 * P) <= A.log_cap) {   // the record fits the buffer
                     int32_t* r = A.log + 1 + (int64_t)idx * (3 + 4 * P);
                     if (lane == 0) {
                         r[0] = T;
@@ -332,7 +332,7 @@ __device__ void ensure_wg(const EnsureArgs& A, EnsureShared& Z, int* done) {
     }
     if (A.log && wv == 0) {                      // decision record, same layout as the oracle's
         const int idx = A.log[0];
-        if (idx < A.log_cap) {
+        if ((int64_t)(idx + 1) * (3 + 4 * P) <= A.log_cap) {   // the record fits the buffer
             int32_t* r = A.log + 1 + (int64_t)idx * (3 + 4 * P);
             if (lane == 0) {
                 r[0] = T;

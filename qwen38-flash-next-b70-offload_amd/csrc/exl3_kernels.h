@@ -31,7 +31,8 @@ struct EnsureArgs {
     int64_t* fill_all; int32_t* fill_list; int max_fill;
     const uint8_t* ram_res; int32_t* ring; int ring_cap; const int32_t* safe;   // tier (null ram_res: off)
     int32_t* vict;                                 // victim list [1 + 2E] or null
-    int32_t* log; int64_t log_cap;                 // decision log (debug) or null: [count, records...]
+    int32_t* log; int64_t log_cap;                 // decision log (debug) or null: [count, records...]; log_cap:
+                                                   // int32 words after the count (a record is written if it fits)
     int64_t* pair_ptr;                             // out: blob pointer of every post-mask pick [P] (or null)
     int32_t* pair_own;                             // out (ensure inside the layer kernel): 1 if pick i is the first
                                                    // pick of its post-mask expert [P] (or null)

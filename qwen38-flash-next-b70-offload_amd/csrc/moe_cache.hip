@@ -192,7 +192,7 @@ __global__ void __launch_bounds__(kEnsureThreads) ensure_kernel(EnsureArgs A) {
             }
             if (A.log) {
                 const int idx = A.log[0];
-                if (idx < A.log_cap) {
+                if ((int64_t)(idx + 1) * (3 + 4 * P) <= A.log_cap) {   // the record fits the buffer
                     int32_t* r = A.log + 1 + (int64_t)idx * (3 + 4 * P);
                     if (lane == 0) {
                         r[0] = T;
@@ -398,7 +398,7 @@ __global__ void __launch_bounds__(kEnsureThreads) ensure_kernel(EnsureArgs A) {
         for (int i = tid; i < P; i += kEnsureThreads) A.pair_ptr[i] = A.ptrs_all[A.layer * E + pid[i]];
     if (A.log && wv == 0) {                                   // decision record, same layout as the oracle's
         const int idx = A.log[0];
-        if (idx < A.log_cap) {
+        if ((int64_t)(idx + 1) * (3 + 4 * P) <= A.log_cap) {   // the record fits the buffer
             int32_t* r = A.log + 1 + (int64_t)idx * (3 + 4 * P);
             if (lane == 0) {
                 r[0] = T;

@@ -192,9 +192,10 @@ int exl3_set_debug(int64_t v) {
     return EXL3_OK;
 }
 
-int exl3_set_decision_log(int32_t* buf, int64_t cap_records) {
+int exl3_set_decision_log(int32_t* buf, int64_t cap_words) {
+    if (buf && cap_words < 0) return fail(EXL3_EINVAL, "set_decision_log: cap_words=%lld", (long long)cap_words);
     g_cfg.log = buf;
-    g_cfg.log_cap = buf ? cap_records : 0;
+    g_cfg.log_cap = buf ? cap_words : 0;
     return EXL3_OK;
 }
 

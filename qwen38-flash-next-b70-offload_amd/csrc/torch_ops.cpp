@@ -214,7 +214,7 @@ void moe_svm_prefetch(at::Tensor ptrs, int64_t nbytes, at::Tensor like) {
 void moe_set_decision_log(at::Tensor buf) {
     if (!buf.numel()) return check(exl3_set_decision_log(nullptr, 0), "moe_set_decision_log");
     TORCH_CHECK(buf.scalar_type() == at::kInt && buf.is_cuda() && buf.is_contiguous(), "decision log: device int32");
-    check(exl3_set_decision_log(buf.data_ptr<int>(), 1 << 30), "moe_set_decision_log");
+    check(exl3_set_decision_log(buf.data_ptr<int>(), buf.numel() - 1), "moe_set_decision_log");
 }
 at::Tensor dequant(at::Tensor trellis, int64_t k_tiles, int64_t n_tiles, int64_t K) {
     TORCH_CHECK(trellis.is_cuda() && trellis.is_contiguous(), "dequant: contiguous device words");

@@ -550,3 +550,38 @@ def test_cache_midsize_rows(M):
     wb = recs[:, :, 3 + 2 * P:3 + 4 * P:2]
     assert (wb >= 0).any()                                                 # and victims were written back
     tier.close()
+
+
+@pytest.mark.parametrize("fused", [1, 0])
+def test_decision_log_stops_at_its_buffer(fused):
+    """A decision log shorter than the run: every call is counted, the records that fit are written, and nothing is
+    written past the buffer (a guard region after it keeps its fill value)."""
+    from exl3xpu import moe_offload, nvtier
+    H, I, K, E, S, P = 128, 128, 3, 16, 4, 4
+    print(f"case decision log bound fused={fused}", flush=True)
+    store = moe_offload.ExpertStore(H, I, K, E, S, max_layers=1)
+    src = nvtier.SyntheticExpertSource(H, I, K, 77, n_distinct=E)
+    store.add_layer("layer0", torch.from_numpy(src.buf))
+    X = store.X
+    rl = cache.rec_len(P)
+    fit, calls = 3, 7
+    buf = torch.full((1 + fit * rl + 64,), -7, dtype=torch.int32, device="cuda")
+    buf[0] = 0
+    X.moe_set_fused_ensure(fused)
+    X.moe_set_decision_log(buf[:1 + fit * rl])
+    rng = np.random.default_rng(5)
+    x = torch.randn(1, H, generator=torch.Generator().manual_seed(1)).to(torch.bfloat16).cuda()
+    try:
+        for _ in range(calls):
+            ids = torch.from_numpy(rng.choice(E, P, replace=False).astype(np.int32)).view(1, P).cuda()
+            w = torch.full((1, P), 1.0 / P, dtype=torch.float32, device="cuda")
+            store.forward_cached("layer0", x, ids, w)
+        torch.cuda.synchronize()
+    finally:
+        X.moe_set_decision_log(torch.zeros(0, dtype=torch.int32, device="cuda"))
+        X.moe_set_fused_ensure(1)
+    b = buf.cpu().numpy()
+    assert b[0] == calls
+    recs = b[1:1 + fit * rl].reshape(fit, rl)
+    assert (recs[:, 2:2 + P] >= 0).all() and (recs[:, 2:2 + P] < E).all()   # the picks of every record that fits
+    assert (b[1 + fit * rl:] == -7).all(), "the log wrote past its buffer"
