@@ -50,6 +50,19 @@ int64_t exl3_blob_bytes(int H, int I, int K);
 int exl3_set_tier(uint8_t* ram_res, int32_t* miss_ring, int64_t ring_numel, const int32_t* safe);
 /* moe_set_victims (a8:757): device int32 [1 + 2E] victim list, NULL = no victim write-back */
 int exl3_set_victims(int32_t* vict);
+/* Write-back target of each victim of a cached call (replaces the fixed-address write-back of
+ * plugin/exl3xpu/nvtier.py:22-53, where every key owns a page of a sparse memfd): device int64 [E], written by the
+ * ensure beside the victim list and read by the copies; NULL = the fixed record host_base[layer] + e * host_stride. */
+int exl3_set_victim_addrs(int64_t* vict_addr);
+/* The RAM tier's record pool (replaces the sparse memfd and the hole punches of plugin/exl3xpu/nvtier.py:19-53 and
+ * 109-126 that hold RAM to the budget): the host record of every key is host_addr[key] (device int64 [L*E]) instead of
+ * a fixed address, and a victim whose RAM copy is not valid is written back into the next free record of the step's
+ * queue wbq (device int64 [wbq_cap], installed by exl3_tier_exchange_pool). wbq_state (device int32 [2 + wbq_cap]):
+ * [0] = records taken, [1 + i] = the key written into wbq[i], [1 + wbq_cap] = write-backs dropped because the queue
+ * was used up (the victim then leaves HBM without a copy and stays masked until a fill brings it back). Needs the
+ * victim list and exl3_set_victim_addrs; the fixed-record paths (exl3_moe_prefetch, exl3_moe_prefetch_plan, the
+ * copy-engine worker) return EXL3_EUNSUPPORTED while it is set. host_addr == NULL turns it off. */
+int exl3_set_record_pool(int64_t* host_addr, const int64_t* wbq, int32_t* wbq_state, int64_t wbq_cap);
 /* moe_set_host_stride (a8:765): stride of a key's RAM-tier address, 0 = the slot stride */
 int exl3_set_host_stride(int64_t stride);
 /* Bytes between HBM slots, 0 = the blob size of the call (no reference counterpart: the reference assumes one expert
@@ -184,6 +197,19 @@ int exl3_scatter_flags(uint8_t* flags, int64_t n_flags, const int32_t* packed, i
 int exl3_tier_exchange(uint8_t* flags, int64_t n_flags, const int32_t* packed, int64_t n_diff, const int32_t* ring,
                        int64_t ring_cap, int64_t ring_from, int32_t* ring_mirror, const void* const* src,
                        void* const* dst, const int64_t* nbytes, int n_copies, void* stream);
+
+/* exl3_tier_exchange with the record pool (replaces the evict/punch bookkeeping of plugin/exl3xpu/nvtier.py:282-386):
+ * first upd (pinned int64 [2 n_upd], (key, record address) pairs, keys outside [0, n_flags) skipped) sets
+ * host_addr[key] and, for a key not in an HBM slot (slot_of[key] < 0), ptrs_all[key]; then, when wbq is not NULL, one
+ * workgroup copies wbq_state [2 + wbq_cap] into wbq_mirror (pinned), installs next (pinned int64 [wbq_cap]) as the
+ * queue of the following decode step and clears the taken and dropped counts; then the diff, ring and copies as
+ * exl3_tier_exchange. upd and next are read in place: the caller keeps them unchanged until the launch has run. */
+int exl3_tier_exchange_pool(uint8_t* flags, int64_t n_flags, const int32_t* packed, int64_t n_diff,
+                            const int32_t* ring, int64_t ring_cap, int64_t ring_from, int32_t* ring_mirror,
+                            const void* const* src, void* const* dst, const int64_t* nbytes, int n_copies,
+                            const int64_t* upd, int64_t n_upd, int64_t* host_addr, int64_t* ptrs_all,
+                            const int32_t* slot_of, const int64_t* next, int64_t* wbq, int32_t* wbq_state,
+                            int32_t* wbq_mirror, int64_t wbq_cap, void* stream);
 
 /* Device health flags (no reference counterpart): flags4[0] = bounded waits of the fused decode kernel that timed
  * out since load (0 in a healthy run; a timeout means an output was computed from an incomplete intermediate, so

@@ -303,18 +303,59 @@ __device__ void ensure_wg(const EnsureArgs& A, EnsureShared& Z, int* done) {
                 }
             }
             __syncthreads();
-            for (int mi = tid; mi < nm; mi += NT) {
-                const int s = Z.vslot[mi], e = Z.miss[mi];
-                const int old = A.slot_key[s];
-                const int wb = (old >= 0 && A.ram_res && A.ram_res[old]) ? -1 : old;
+            // one miss per thread (nm <= E <= NT): its slot's old owner is the victim; an owner whose RAM copy is not
+            // valid is written back (wb = its key) into a record: its fixed record, or with the record pool the
+            // next free record the host queued for this step (none left: the write-back is dropped and counted)
+            const int mi = tid;
+            int s = 0, e = 0, old = -1, wb = -1;
+            if (mi < nm) {
+                s = Z.vslot[mi];
+                e = Z.miss[mi];
+                old = A.slot_key[s];
+                wb = (old >= 0 && A.ram_res && A.ram_res[old]) ? -1 : old;
+            }
+            int64_t waddr = 0;
+            if (A.host_addr && A.vict) {         // write-backs on: each takes a record of the step's queue
+                int tot;
+                const int rank = wg_excl_scan<NW>(wb >= 0 ? 1 : 0, Z.sw, tot);
+                const int used0 = A.wbq_state[0];
+                if (wb >= 0) {
+                    const int q = used0 + rank;
+                    if (q < A.wbq_cap) {
+                        waddr = A.wbq[q];
+                        A.wbq_state[1 + q] = wb;
+                    } else {
+                        wb = -1;
+                    }
+                }
+                __syncthreads();                 // every thread has read the count before it moves
+                if (tid == 0) {
+                    const int taken = min(tot, max(0, A.wbq_cap - used0));
+                    A.wbq_state[0] = used0 + taken;
+                    A.wbq_state[1 + A.wbq_cap] += tot - taken;
+                }
+            } else if (wb >= 0) {
+                waddr = A.host_base[wb / E] + (int64_t)(wb % E) * A.hstride;
+            }
+            if (mi < nm) {
                 Z.vwb[mi] = wb;
                 if (A.vict) {
                     st_agent_i32(A.vict + 1 + 2 * mi, wb);
                     st_agent_i32(A.vict + 2 + 2 * mi, s);
+                    if (A.vict_addr) st_agent_i64(A.vict_addr + mi, waddr);
                 }
                 if (old >= 0) {
                     A.slot_of[old] = -1;
-                    A.ptrs_all[old] = A.host_base[old / E] + (int64_t)(old % E) * A.hstride;
+                    // the victim's blob is read from its RAM record from now on: the write-back target, else the
+                    // record it already has (a dropped write-back leaves the key masked until a fill brings it back)
+                    int64_t hp = waddr;
+                    if (A.host_addr) {
+                        if (waddr) A.host_addr[old] = waddr;
+                        else hp = A.host_addr[old];
+                    } else if (wb < 0) {
+                        hp = A.host_base[old / E] + (int64_t)(old % E) * A.hstride;
+                    }
+                    A.ptrs_all[old] = hp;
                 }
                 const int key = kb + e;
                 A.slot_key[s] = key;

@@ -21,6 +21,7 @@ constexpr int kVictimChunkBytes = 64 * 1024;   // bytes of a victim slot copied 
 struct VictimArgs {
     const int32_t* vict; const int64_t* host_base; int64_t slot_base; int64_t blob; int64_t hstride; int E;
     uint8_t* ram_res; int chunk_bytes;
+    const int64_t* vaddr;                          // write-back target of victim i [E] (written by the ensure)
 };
 
 struct EnsureArgs {
@@ -31,6 +32,13 @@ struct EnsureArgs {
     int64_t* fill_all; int32_t* fill_list; int max_fill;
     const uint8_t* ram_res; int32_t* ring; int ring_cap; const int32_t* safe;   // tier (null ram_res: off)
     int32_t* vict;                                 // victim list [1 + 2E] or null
+    int64_t* vict_addr;                            // with vict: the write-back target of victim i [E] (0: none)
+    // record pool of the RAM tier (host_addr null: fixed records at host_base[layer] + e * hstride)
+    int64_t* host_addr;                            // host record address of every key [L * E] (stale when not in RAM)
+    const int64_t* wbq;                            // free records for this step's write-backs [wbq_cap]
+    int32_t* wbq_state;                            // [0] records taken, [1 + i] key written back into wbq[i],
+                                                   // [1 + wbq_cap] write-backs dropped (no record left)
+    int wbq_cap;
     int32_t* log; int64_t log_cap;                 // decision log (debug) or null: [count, records...]; log_cap:
                                                    // int32 words after the count (a record is written if it fits)
     int64_t* pair_ptr;                             // out: blob pointer of every post-mask pick [P] (or null)
@@ -146,8 +154,15 @@ hipError_t launch_table_update(int64_t* ptrs_all, int32_t* slot_of, int32_t* slo
 struct TierCopy { const uint8_t* src; uint8_t* dst; int64_t n; };   // n bytes, device -> pinned host
 struct TierCopies { TierCopy c[4]; int n; };
 struct TierRing { const int32_t* ring; int64_t cap, from; int32_t* mirror; };  // ring null: no mirroring
+// record pool of the RAM tier: the step's address updates (key, address) applied to host_addr and ptrs_all, then the
+// write-back queue: state [2 + cap] copied to the pinned mirror, the next step's records installed, the state cleared
+struct TierPool {
+    const int64_t* upd; int64_t n_upd; int64_t* host_addr; int64_t* ptrs_all;   // upd: pinned [2 n_upd]
+    const int32_t* slot_of;                        // ptrs_all of a key in an HBM slot keeps the slot
+    const int64_t* next; int64_t* wbq; int32_t* state; int32_t* mirror; int cap;  // next: pinned [cap]; wbq null: off
+};
 hipError_t launch_tier_exchange(uint8_t* flags, int64_t n_flags, const int32_t* packed, int64_t n_diff,
-                                const TierRing& rg, const TierCopies& cp, hipStream_t s);
+                                const TierRing& rg, const TierCopies& cp, const TierPool& pl, hipStream_t s);
 // prefill.hip
 hipError_t launch_align(const int32_t* ids, const float* w, int npairs, int topk, int E, int pad, int* chunk_scratch,
                         const AlignOut& o, hipStream_t s);

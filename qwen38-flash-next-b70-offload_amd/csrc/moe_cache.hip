@@ -345,18 +345,58 @@ __global__ void __launch_bounds__(kEnsureThreads) ensure_kernel(EnsureArgs A) {
                 else if (u == tau && ieq < take_eq) vslot[tot_lt + beq + ieq++] = s;
             }
             __syncthreads();
-            for (int mi = tid; mi < nm; mi += kEnsureThreads) {
-                const int s = vslot[mi], e = miss[mi];
-                const int old = A.slot_key[s];
-                const int wb = (old >= 0 && A.ram_res && A.ram_res[old]) ? -1 : old;
+            // one miss per thread (nm <= E <= kEnsureThreads); victims as in ensure_wg: the old owner of the slot is
+            // written back into its fixed record or, with the record pool, into the next free record of the step
+            const int mi = tid;
+            int s = 0, e = 0, old = -1, wb = -1;
+            if (mi < nm) {
+                s = vslot[mi];
+                e = miss[mi];
+                old = A.slot_key[s];
+                wb = (old >= 0 && A.ram_res && A.ram_res[old]) ? -1 : old;
+            }
+            int64_t waddr = 0;
+            if (A.host_addr && A.vict) {         // write-backs on: each takes a record of the step's queue
+                int tot;
+                const int rank = block_excl_scan(wb >= 0 ? 1 : 0, sw, tot);
+                const int used0 = A.wbq_state[0];
+                if (wb >= 0) {
+                    const int q = used0 + rank;
+                    if (q < A.wbq_cap) {
+                        waddr = A.wbq[q];
+                        A.wbq_state[1 + q] = wb;
+                    } else {
+                        wb = -1;
+                    }
+                }
+                __syncthreads();
+                if (tid == 0) {
+                    const int taken = min(tot, max(0, A.wbq_cap - used0));
+                    A.wbq_state[0] = used0 + taken;
+                    A.wbq_state[1 + A.wbq_cap] += tot - taken;
+                }
+            } else if (wb >= 0) {
+                waddr = A.host_base[wb / E] + (int64_t)(wb % E) * A.hstride;
+            }
+            if (mi < nm) {
                 vwb[mi] = wb;
                 if (A.vict) {
                     A.vict[1 + 2 * mi] = wb;
                     A.vict[2 + 2 * mi] = s;
+                    if (A.vict_addr) A.vict_addr[mi] = waddr;
                 }
                 if (old >= 0) {
                     A.slot_of[old] = -1;
-                    A.ptrs_all[old] = A.host_base[old / E] + (int64_t)(old % E) * A.hstride;
+                    // the victim's blob is read from its RAM record from now on: the write-back target, else the
+                    // record it already has (a dropped write-back leaves the key masked until a fill brings it back)
+                    int64_t hp = waddr;
+                    if (A.host_addr) {
+                        if (waddr) A.host_addr[old] = waddr;
+                        else hp = A.host_addr[old];
+                    } else if (wb < 0) {
+                        hp = A.host_base[old / E] + (int64_t)(old % E) * A.hstride;
+                    }
+                    A.ptrs_all[old] = hp;
                 }
                 const int key = A.layer * E + e;
                 A.slot_key[s] = key;
@@ -489,16 +529,17 @@ __device__ __forceinline__ void copy_chunk(const uint8_t* src, uint8_t* dst, int
         *(uint4*)(dst + o) = *(const uint4*)(src + o);
 }
 
-__global__ void __launch_bounds__(256) cached_victim_kernel(const int32_t* vict, const int64_t* host_base,
-                                                            int64_t hstride, int E, int64_t slot_base, int64_t sstride,
-                                                            uint8_t* ram_res, int chunks) {
+__global__ void __launch_bounds__(256) cached_victim_kernel(const int32_t* vict, const int64_t* vaddr,
+                                                            const int64_t* host_base, int64_t hstride, int E,
+                                                            int64_t slot_base, int64_t sstride, uint8_t* ram_res,
+                                                            int chunks) {
     const int mi = blockIdx.x / chunks, ch = blockIdx.x % chunks;
     if (mi >= vict[0]) return;
     const int old = vict[1 + 2 * mi], s = vict[2 + 2 * mi];
     if (old < 0) return;                                       // no write-back (empty slot, or a valid RAM copy)
     if (ram_res && ch == 0 && threadIdx.x == 0) ram_res[old] = 1;
     copy_chunk((const uint8_t*)(slot_base + (int64_t)s * sstride),
-               (uint8_t*)(host_base[old / E] + (int64_t)(old % E) * hstride), sstride, ch);
+               (uint8_t*)(vaddr ? vaddr[mi] : host_base[old / E] + (int64_t)(old % E) * hstride), sstride, ch);
 }
 
 __global__ void __launch_bounds__(256) cached_fill_kernel(const int32_t* fill_list, const int64_t* ptrs_all,
@@ -525,7 +566,7 @@ hipError_t launch_cached_fills(const EnsureArgs& a, int64_t blob, int max_n, uin
     if (a.vict) {
         const int vchunks = (int)((a.blob + kPrefetchChunk - 1) / kPrefetchChunk);     // whole slots (a.blob: stride)
         hipLaunchKernelGGL(cached_victim_kernel, dim3((unsigned)(max_n * vchunks)), dim3(256), 0, s, a.vict,
-                           a.host_base, a.hstride, a.E, a.slot_base, a.blob, ram_res, vchunks);
+                           a.vict_addr, a.host_base, a.hstride, a.E, a.slot_base, a.blob, ram_res, vchunks);
     }
     const int chunks = (int)((blob + kPrefetchChunk - 1) / kPrefetchChunk);
     hipLaunchKernelGGL(cached_fill_kernel, dim3((unsigned)(max_n * chunks)), dim3(256), 0, s, a.fill_list, a.ptrs_all,
@@ -594,9 +635,28 @@ __device__ __forceinline__ void copy_part(const TierCopy& c, int64_t t, int64_t 
 }
 
 __global__ void __launch_bounds__(256) tier_exchange_kernel(uint8_t* flags, int64_t n_flags, const int32_t* packed,
-                                                            int64_t n_diff, TierRing rg, TierCopies cp) {
+                                                            int64_t n_diff, TierRing rg, TierCopies cp, TierPool pl) {
     const int64_t nt = (int64_t)gridDim.x * blockDim.x;
     const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    // record pool: the records of keys that become RAM-resident with this diff (their flag rises in the same launch,
+    // so the next decode step sees both); a key in an HBM slot keeps the slot in its table entry; keys outside
+    // [0, n_flags) are ignored
+    for (int64_t i = t; i < pl.n_upd; i += nt) {
+        const int64_t key = pl.upd[2 * i], addr = pl.upd[2 * i + 1];
+        if (key >= 0 && key < n_flags) {
+            pl.host_addr[key] = addr;
+            if (pl.slot_of[key] < 0) pl.ptrs_all[key] = addr;
+        }
+    }
+    if (pl.wbq && blockIdx.x == 0) {             // the write-back queue, in order, by one workgroup
+        for (int i = threadIdx.x; i < 2 + pl.cap; i += blockDim.x) pl.mirror[i] = pl.state[i];
+        __syncthreads();
+        for (int i = threadIdx.x; i < pl.cap; i += blockDim.x) pl.wbq[i] = pl.next[i];
+        if (threadIdx.x == 0) {
+            pl.state[0] = 0;
+            pl.state[1 + pl.cap] = 0;
+        }
+    }
     for (int64_t i = t; i < n_diff; i += nt) {
         const int32_t p = packed[i];
         const int64_t key = p >> 1;
@@ -615,12 +675,13 @@ __global__ void __launch_bounds__(256) tier_exchange_kernel(uint8_t* flags, int6
 }
 
 hipError_t launch_tier_exchange(uint8_t* flags, int64_t n_flags, const int32_t* packed, int64_t n_diff,
-                                const TierRing& rg, const TierCopies& cp, hipStream_t s) {
+                                const TierRing& rg, const TierCopies& cp, const TierPool& pl, hipStream_t s) {
     int64_t work = std::max<int64_t>(n_diff, rg.ring ? 256 : 0);
+    work = std::max(work, std::max<int64_t>(pl.n_upd, pl.wbq ? 256 : 0));
     for (int k = 0; k < cp.n; ++k) work = std::max(work, cp.c[k].n >> 4);
     if (work <= 0) return hipSuccess;
     const unsigned blocks = (unsigned)std::min<int64_t>(128, (work + 255) / 256);
-    hipLaunchKernelGGL(tier_exchange_kernel, dim3(blocks), dim3(256), 0, s, flags, n_flags, packed, n_diff, rg, cp);
+    hipLaunchKernelGGL(tier_exchange_kernel, dim3(blocks), dim3(256), 0, s, flags, n_flags, packed, n_diff, rg, cp, pl);
     return hipGetLastError();
 }
 

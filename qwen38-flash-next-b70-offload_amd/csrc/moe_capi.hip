@@ -37,6 +37,11 @@ struct Config {
     int32_t* pend = nullptr;                      // copy-engine prefetch: pending plans committed by every ensure
     const int32_t* done_seq = nullptr;
     int n_layers = 0;
+    int64_t* vict_addr = nullptr;                 // write-back target of each victim of a call [E]
+    int64_t* host_addr = nullptr;                 // record pool of the RAM tier: host record of every key [L * E]
+    const int64_t* wbq = nullptr;                 // the step's free records for write-backs [wbq_cap]
+    int32_t* wbq_state = nullptr;                 // [0] taken, [1 + i] key written into wbq[i], [1 + cap] dropped
+    int wbq_cap = 0;
 };
 Config g_cfg;
 
@@ -146,6 +151,29 @@ int exl3_set_tier(uint8_t* ram_res, int32_t* miss_ring, int64_t ring_numel, cons
 
 int exl3_set_victims(int32_t* vict) {
     g_cfg.vict = vict;
+    return EXL3_OK;
+}
+
+int exl3_set_victim_addrs(int64_t* vict_addr) {
+    g_cfg.vict_addr = vict_addr;
+    return EXL3_OK;
+}
+
+int exl3_set_record_pool(int64_t* host_addr, const int64_t* wbq, int32_t* wbq_state, int64_t wbq_cap) {
+    if (!host_addr) {
+        g_cfg.host_addr = nullptr;
+        g_cfg.wbq = nullptr;
+        g_cfg.wbq_state = nullptr;
+        g_cfg.wbq_cap = 0;
+        return EXL3_OK;
+    }
+    if (!wbq || !wbq_state || wbq_cap <= 0 || wbq_cap > (1 << 20))
+        return fail(EXL3_EINVAL, "set_record_pool: queue [cap] and state [2 + cap] required (cap=%lld)",
+                    (long long)wbq_cap);
+    g_cfg.host_addr = host_addr;
+    g_cfg.wbq = wbq;
+    g_cfg.wbq_state = wbq_state;
+    g_cfg.wbq_cap = (int)wbq_cap;
     return EXL3_OK;
 }
 
@@ -361,6 +389,8 @@ int exl3_moe_prefetch(const int32_t* ids, int n_ids, int64_t* ptrs_all, int laye
                       int32_t* slot_key, int32_t* slot_last, int32_t* tick, int n_slots, const int64_t* host_base,
                       int64_t slot_base, int32_t* pf_list, int32_t* pf_slot, int max_fill, int n_experts, int64_t blob,
                       void* stream) {
+    if (g_cfg.host_addr)                          // its copies address fixed host records
+        return fail(EXL3_EUNSUPPORTED, "moe_prefetch: not with the RAM tier's record pool");
     const int E = n_experts;
     if (n_ids < 0 || layer < 0 || max_fill < 0 || blob <= 0)
         return fail(EXL3_EINVAL, "moe_prefetch: n_ids=%d layer=%d max_fill=%d blob=%lld", n_ids, layer, max_fill,
@@ -415,6 +445,8 @@ int exl3_moe_prefetch_plan(const int32_t* ids, int n_ids, int64_t* ptrs_all, int
                            const int64_t* host_base, int64_t slot_base, int32_t* pf_list, int32_t* pf_slot,
                            int32_t* plans, int32_t* plan_seq, int32_t* pend, const int32_t* done_seq, int n_layers,
                            int max_fill, int n_experts, int64_t blob, void* stream) {
+    if (g_cfg.host_addr)                          // its copies address fixed host records
+        return fail(EXL3_EUNSUPPORTED, "moe_prefetch_plan: not with the RAM tier's record pool");
     const int E = n_experts;
     if (n_ids < 0 || layer < 0 || max_fill < 0 || blob <= 0 || n_layers <= layer)
         return fail(EXL3_EINVAL, "moe_prefetch_plan: n_ids=%d layer=%d n_layers=%d max_fill=%d", n_ids, layer,
@@ -460,6 +492,8 @@ int exl3_moe_prefetch_plan(const int32_t* ids, int n_ids, int64_t* ptrs_all, int
 
 int exl3_prefetch_worker_start(int32_t* plans, const int64_t* host_base_host, int64_t slot_base, int64_t blob,
                                int32_t* done_seq, int32_t* seq_host, int n_layers, int n_experts, void* stream) {
+    if (g_cfg.host_addr)                          // its copies address fixed host records
+        return fail(EXL3_EUNSUPPORTED, "prefetch_worker_start: not with the RAM tier's record pool");
     std::lock_guard<std::mutex> lk(g_pfw_mu);
     if (g_pfw) return fail(EXL3_EINVAL, "prefetch worker already running");
     if (!plans || !host_base_host || !done_seq || !seq_host || n_layers <= 0 || n_experts <= 0 || blob <= 0)
@@ -559,6 +593,14 @@ static int cached_impl(const void* x, int x_dtype, int64_t x_stride, int M, int 
     ea.ring_cap = g_cfg.ring_cap;
     ea.safe = g_cfg.safe;
     ea.vict = g_cfg.vict;
+    ea.vict_addr = g_cfg.vict ? g_cfg.vict_addr : nullptr;
+    ea.host_addr = g_cfg.host_addr;
+    ea.wbq = g_cfg.wbq;
+    ea.wbq_state = g_cfg.wbq_state;
+    ea.wbq_cap = g_cfg.wbq_cap;
+    if (ea.host_addr && (!ea.vict || !ea.vict_addr))
+        return fail(EXL3_EINVAL, "moe_forward_cached: the record pool needs the victim list and its addresses "
+                                 "(exl3_set_victims, exl3_set_victim_addrs)");
     ea.log = g_cfg.log;
     ea.log_cap = g_cfg.log_cap;
     if (exceeds_decode(M, topk)) {
@@ -610,6 +652,7 @@ static int cached_impl(const void* x, int x_dtype, int64_t x_stride, int M, int 
         va.E = E;
         va.ram_res = g_cfg.ram_res;
         va.chunk_bytes = kVictimChunkBytes;
+        va.vaddr = ea.vict_addr;
         mv = std::min(std::min(ea.max_fill, E), P);
     }
     int64_t* pl = ptrs_all + (int64_t)layer * E;
@@ -736,9 +779,10 @@ int exl3_scatter_flags(uint8_t* flags, int64_t n_flags, const int32_t* packed, i
     return e == hipSuccess ? EXL3_OK : hip_fail(e, "scatter_flags");
 }
 
-int exl3_tier_exchange(uint8_t* flags, int64_t n_flags, const int32_t* packed, int64_t n_diff, const int32_t* ring,
-                       int64_t ring_cap, int64_t ring_from, int32_t* ring_mirror, const void* const* src,
-                       void* const* dst, const int64_t* nbytes, int n_copies, void* stream) {
+static int tier_exchange_impl(uint8_t* flags, int64_t n_flags, const int32_t* packed, int64_t n_diff,
+                              const int32_t* ring, int64_t ring_cap, int64_t ring_from, int32_t* ring_mirror,
+                              const void* const* src, void* const* dst, const int64_t* nbytes, int n_copies,
+                              const TierPool& pl, void* stream) {
     if (n_diff < 0 || n_flags < 0 || n_diff > (int64_t)1 << 31 || n_copies < 0 || n_copies > 4)
         return fail(EXL3_EINVAL, "tier_exchange: n_diff=%lld n_copies=%d", (long long)n_diff, n_copies);
     if (n_diff && (!flags || !packed)) return fail(EXL3_EINVAL, "tier_exchange: null flags / diff");
@@ -757,8 +801,40 @@ int exl3_tier_exchange(uint8_t* flags, int64_t n_flags, const int32_t* packed, i
             return fail(EXL3_EINVAL, "tier_exchange: copy %d not 16-byte aligned", k);
         cp.c[cp.n++] = TierCopy{(const uint8_t*)src[k], (uint8_t*)dst[k], nbytes[k]};
     }
-    hipError_t e = launch_tier_exchange(flags, n_flags, packed, n_diff, rg, cp, (hipStream_t)stream);
+    hipError_t e = launch_tier_exchange(flags, n_flags, packed, n_diff, rg, cp, pl, (hipStream_t)stream);
     return e == hipSuccess ? EXL3_OK : hip_fail(e, "tier_exchange");
+}
+
+int exl3_tier_exchange(uint8_t* flags, int64_t n_flags, const int32_t* packed, int64_t n_diff, const int32_t* ring,
+                       int64_t ring_cap, int64_t ring_from, int32_t* ring_mirror, const void* const* src,
+                       void* const* dst, const int64_t* nbytes, int n_copies, void* stream) {
+    return tier_exchange_impl(flags, n_flags, packed, n_diff, ring, ring_cap, ring_from, ring_mirror, src, dst, nbytes,
+                              n_copies, TierPool{}, stream);
+}
+
+int exl3_tier_exchange_pool(uint8_t* flags, int64_t n_flags, const int32_t* packed, int64_t n_diff,
+                            const int32_t* ring, int64_t ring_cap, int64_t ring_from, int32_t* ring_mirror,
+                            const void* const* src, void* const* dst, const int64_t* nbytes, int n_copies,
+                            const int64_t* upd, int64_t n_upd, int64_t* host_addr, int64_t* ptrs_all,
+                            const int32_t* slot_of, const int64_t* next, int64_t* wbq, int32_t* wbq_state,
+                            int32_t* wbq_mirror, int64_t wbq_cap, void* stream) {
+    if (n_upd < 0 || (n_upd && (!upd || !host_addr || !ptrs_all || !slot_of)))
+        return fail(EXL3_EINVAL, "tier_exchange_pool: %lld address updates with null tables", (long long)n_upd);
+    if (wbq && (!next || !wbq_state || !wbq_mirror || wbq_cap <= 0 || wbq_cap > (1 << 20)))
+        return fail(EXL3_EINVAL, "tier_exchange_pool: queue cap=%lld with null arrays", (long long)wbq_cap);
+    TierPool pl{};
+    pl.upd = upd;
+    pl.n_upd = n_upd;
+    pl.host_addr = host_addr;
+    pl.ptrs_all = ptrs_all;
+    pl.slot_of = slot_of;
+    pl.next = next;
+    pl.wbq = wbq;
+    pl.state = wbq_state;
+    pl.mirror = wbq_mirror;
+    pl.cap = wbq ? (int)wbq_cap : 0;
+    return tier_exchange_impl(flags, n_flags, packed, n_diff, ring, ring_cap, ring_from, ring_mirror, src, dst, nbytes,
+                              n_copies, pl, stream);
 }
 
 int exl3_device_status(int32_t* flags4, void* stream) {

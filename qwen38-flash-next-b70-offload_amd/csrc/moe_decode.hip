@@ -200,6 +200,7 @@ struct LayerShared {
     float red[kWaves][128];  // per-wave column sums
     int64_t fdst;            // write-through target of the pair (0: none)
     int fwb;                 // victims copied inline: write-back owner of that slot's old bytes (-1: none)
+    int64_t fwa;             // its write-back target (the owner's RAM record)
     int last;
 };
 
@@ -240,7 +241,8 @@ __device__ __forceinline__ void victim_wg(const DecodeArgs& A, int blk) {
         if (old >= 0) {
             if (V.ram_res && c == 0 && threadIdx.x == 0) V.ram_res[old] = 1;
             src = (const uint4*)(V.slot_base + (int64_t)s * V.blob);
-            dst = (uint4*)(V.host_base[old / V.E] + (int64_t)(old % V.E) * V.hstride);
+            dst = (uint4*)(V.vaddr ? (A.fused ? ld_agent_i64(V.vaddr + i) : V.vaddr[i])
+                                   : V.host_base[old / V.E] + (int64_t)(old % V.E) * V.hstride);
             q0 = (int64_t)c * (kVictChunk >> 4);
             q1 = min(V.blob >> 4, q0 + (kVictChunk >> 4));
         }
@@ -270,17 +272,21 @@ __device__ __forceinline__ const uint8_t* pair_base(const DecodeArgs& A, int a, 
 // Victims copied inline (slots at the blob size: a victim and the expert that replaces it share one layout): the one
 // writer of each miss (the first pick of its expert) copies the victim's old bytes at exactly the positions it is
 // about to overwrite to the victim's RAM copy (the reference's VictimCopyKernel a8:1168-1189, split over the
-// writers); the last workgroup flags the victims RAM-resident. Returns the write-back owner of the slot at f, or -1.
-__device__ __forceinline__ int inline_victim(const DecodeArgs& A, int64_t f) {
+// writers); the last workgroup flags the victims RAM-resident. Returns the write-back owner of the slot at f, or -1,
+// and in wa its write-back target: the record the ensure chose, or the owner's fixed record.
+__device__ __forceinline__ int inline_victim(const DecodeArgs& A, int64_t f, int64_t& wa) {
     const int32_t* vl = A.va.vict;               // fields read once: the loop below has only loads
     const int s = (int)((f - A.va.slot_base) / A.va.blob);
     const int nv = ld_agent_i32(vl);
     for (int i = 0; i < nv; ++i)
-        if (ld_agent_i32(vl + 2 + 2 * i) == s) return ld_agent_i32(vl + 1 + 2 * i);
+        if (ld_agent_i32(vl + 2 + 2 * i) == s) {
+            const int wb = ld_agent_i32(vl + 1 + 2 * i);
+            if (wb >= 0)
+                wa = A.va.vaddr ? ld_agent_i64(A.va.vaddr + i)
+                                : A.va.host_base[wb / A.va.E] + (int64_t)(wb % A.va.E) * A.va.hstride;
+            return wb;
+        }
     return -1;
-}
-__device__ __forceinline__ uint8_t* victim_host(const DecodeArgs& A, int wb) {
-    return (uint8_t*)(A.va.host_base[wb / A.va.E] + (int64_t)(wb % A.va.E) * A.va.hstride);
 }
 
 // the same with the ensure running inside the launch: the pair applies the tier mask itself (expert in neither HBM
@@ -363,12 +369,14 @@ __device__ __forceinline__ void gateup_wg(const DecodeArgs& A, int blk, LayerSha
             }
             if (f && A.n_vict_wg) wait_count(&g_cnt_all[1], A.n_vict_wg);   // after the victims' old bytes were read
             S.fdst = f;
-            S.fwb = f && A.vict_inline ? inline_victim(A, f) : -1;
+            int64_t wa = 0;
+            S.fwb = f && A.vict_inline ? inline_victim(A, f, wa) : -1;
+            S.fwa = wa;
         }
         __syncthreads();
         dst = (uint8_t*)S.fdst;
     }
-    uint8_t* hv = dst && S.fwb >= 0 ? victim_host(A, S.fwb) : nullptr;     // the victim's RAM copy
+    uint8_t* hv = dst && S.fwb >= 0 ? (uint8_t*)S.fwa : nullptr;            // the victim's RAM copy
     if (dst && r == 0) {                         // the vectors (suh, svh) after the trellis words
         const uint32_t* sv = (const uint32_t*)(base + A.g.off_suh_g);
         uint32_t* dv = (uint32_t*)(dst + A.g.off_suh_g);
@@ -501,7 +509,9 @@ __device__ __forceinline__ void down_wg(const DecodeArgs& A, int blk, LayerShare
         }
         if (f && A.n_vict_wg) wait_count(&g_cnt_all[1], A.n_vict_wg);      // and for the victims' old bytes
         S.fdst = f;
-        S.fwb = f && A.vict_inline ? inline_victim(A, f) : -1;
+        int64_t wa = 0;
+        S.fwb = f && A.vict_inline ? inline_victim(A, f, wa) : -1;
+        S.fwa = wa;
     }
     const int ksn = gu_kslices(H);
     half2_t* xs = S.u.dn.xd;                     // the pair's down input, [I/2] half2
@@ -563,7 +573,7 @@ __device__ __forceinline__ void down_wg(const DecodeArgs& A, int blk, LayerShare
     if (tid == 0) st_tag(A.xstart + A.n_gu + blk, tag, 0.f);     // ids, pointers, w and fill target consumed
     uint32_t* trd = S.fdst ? (uint32_t*)((uint8_t*)S.fdst + A.g.gu_bytes) : nullptr;
     if (trd && S.fwb >= 0) {                     // the victim's old down words at this wave's positions, first
-        uint32_t* tro = (uint32_t*)(victim_host(A, S.fwb) + A.g.gu_bytes);
+        uint32_t* tro = (uint32_t*)((uint8_t*)S.fwa + A.g.gu_bytes);
         for (int c = 0; c < nch; ++c) g0.copy_old(trd, tro, tiles_n, (wv + kWaves * c) * 4, ct0);
     }
     float acc[GV::NCP][2], tacc[GV::NCP][2];

@@ -22,6 +22,8 @@ SIGNATURES = {
     "exl3_blob_bytes": (c_i64, [c_i32, c_i32, c_i32]),
     "exl3_set_tier": (c_i32, [c_p, c_p, c_i64, c_p]),
     "exl3_set_victims": (c_i32, [c_p]),
+    "exl3_set_victim_addrs": (c_i32, [c_p]),
+    "exl3_set_record_pool": (c_i32, [c_p, c_p, c_p, c_i64]),
     "exl3_set_host_stride": (c_i32, [c_i64]),
     "exl3_set_slot_stride": (c_i32, [c_i64]),
     "exl3_set_fused_ensure": (c_i32, [c_i64]),
@@ -55,6 +57,8 @@ SIGNATURES = {
     "exl3_set_status_mirror": (c_i32, [c_p]),
     "exl3_scatter_flags": (c_i32, [c_p, c_i64, c_p, c_i64, c_p]),
     "exl3_tier_exchange": (c_i32, [c_p, c_i64, c_p, c_i64, c_p, c_i64, c_i64, c_p, c_p, c_p, c_p, c_i32, c_p]),
+    "exl3_tier_exchange_pool": (c_i32, [c_p, c_i64, c_p, c_i64, c_p, c_i64, c_i64, c_p, c_p, c_p, c_p, c_i32,
+                                        c_p, c_i64, c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_i64, c_p]),
     "exl3_admit_decide": (c_i32, [c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_i64, c_p, c_p, c_p, c_p, c_p, c_p, c_p]),
     "exl3_host_alloc": (c_p, [c_i64]),
     "exl3_host_free": (c_i32, [c_p]),

@@ -39,15 +39,73 @@ def _env_int(name: str, default: int) -> int:
     return int(os.environ.get(name, str(default)))
 
 
+class RecordPool:
+    """Pinned, device-mapped host records of one stride, allocated `chunk` records at a time when none is free and
+    reused through a free list, so that the RAM tier pins the records it holds (its budget plus a bounded headroom)
+    rather than one record per expert (the reference keeps a sparse memfd of every expert and punches the pages of
+    evicted ones, nvtier.py:19-53, 109-126). Records are 4 KiB aligned when the stride is (direct I/O)."""
+
+    def __init__(self, X, stride: int, chunk: int = 32):
+        self.X, self.stride, self.chunk = X, int(stride), max(1, int(chunk))
+        self.arenas = []
+        self.free = []                                  # addresses; the last one is taken first
+        self.in_use = 0
+        self.high = 0
+
+    def _grow(self) -> None:
+        a = self.X.host_alloc(self.chunk * self.stride)
+        self.arenas.append(a)
+        base = a.data_ptr()
+        self.free.extend(base + (self.chunk - 1 - i) * self.stride for i in range(self.chunk))
+
+    def take(self, n: int) -> np.ndarray:
+        n = int(n)
+        while len(self.free) < n:
+            self._grow()
+        out = np.array(self.free[len(self.free) - n:][::-1], dtype=np.int64)
+        del self.free[len(self.free) - n:]
+        self.in_use += n
+        self.high = max(self.high, self.in_use)
+        return out
+
+    def give(self, addrs) -> None:
+        a = [int(v) for v in np.asarray(addrs, dtype=np.int64).reshape(-1) if v]
+        self.free.extend(a)
+        self.in_use -= len(a)
+
+    @property
+    def records(self) -> int:
+        return len(self.arenas) * self.chunk
+
+    @property
+    def pinned_bytes(self) -> int:
+        return self.records * self.stride
+
+    def view(self, addr: int, nbytes: int) -> torch.Tensor:
+        """CPU uint8 view of nbytes at a record address (tests and tools)."""
+        for a in self.arenas:
+            lo = a.data_ptr()
+            if lo <= addr < lo + a.numel():
+                off = addr - lo
+                return a[off:off + nbytes]
+        raise KeyError(f"RecordPool: {addr:#x} is not a record")
+
+
 class TierStore(ExpertStore):
     """ExpertStore whose host records sit at fixed-stride addresses of one pinned arena: key li * E + e at
     base + key * stride (the reference maps a sparse 2 MiB-stride memfd, nvtier.py:22-53). The stride defaults to the
     blob rounded up to 4 KiB, the record size of the expert file. Ks: the bitrate of each layer in add_layer order
-    when layers differ; slots and records then take the largest blob."""
+    when layers differ; slots and records then take the largest blob.
+
+    pool=True: no arena; the RAM tier (NvTierAsync) takes a record from a RecordPool for each key it holds and the
+    device tables follow it (host_addr_dev: record of every key, set by the tier; victims are written back into free
+    records the tier queues per step). Until a key has a record its table entry points at one zeroed null record.
+    The fixed-record paths (make_resident, evict, stage_layer, forward_prefill_staged, the prefetch ops) raise."""
 
     _own_host_arrays = False
 
-    def __init__(self, H, I, K, E, n_slots, n_layers, stride=None, device=None, Ks=None):  # noqa: E741
+    def __init__(self, H, I, K, E, n_slots, n_layers, stride=None, device=None, Ks=None,  # noqa: E741
+                 pool: bool = False, pool_chunk: int = 32):
         self.Ks = [int(k) for k in Ks] if Ks is not None else None
         if self.Ks is not None and len(self.Ks) != n_layers:
             raise ValueError(f"TierStore: {len(self.Ks)} bitrates for {n_layers} layers")
@@ -58,19 +116,79 @@ class TierStore(ExpertStore):
         if self.stride < self.blob or self.stride % 16:
             raise ValueError(f"TierStore: stride {self.stride} must hold a blob ({self.blob} B), 16-byte multiple")
         self.L = n_layers
-        self.size = n_layers * E * self.stride
-        self.arena = self.X.host_alloc(self.size)
-        self.base = self.arena.data_ptr()
+        if pool:
+            self.pool = RecordPool(self.X, self.stride, pool_chunk)
+            self.null_record = self.X.host_alloc(self.stride)
+            self.null_record.zero_()
+            self.base = self.null_record.data_ptr()
+            self.size = 0
+            n = n_layers * E
+            self.rec_of = np.zeros(n, dtype=np.int64)          # host record of every key (0: none)
+            self.host_addr_dev = torch.full((n,), s64(self.base), dtype=torch.int64, device=self.dev)
+        else:
+            self.pool = None
+            self.size = n_layers * E * self.stride
+            self.arena = self.X.host_alloc(self.size)
+            self.base = self.arena.data_ptr()
 
     def _host_stride(self) -> int:
         return self.stride
 
     def _new_records(self, li: int, blobs) -> _HostRecords:
+        if self.pool is not None:
+            if blobs is not None:
+                raise ValueError("TierStore(pool=True): records are filled by the tier from its source")
+            return _HostRecords(self.base, 0, self.base, self.base + self.stride, None)
         span = self.E * self.stride
         view = self.arena[li * span:(li + 1) * span].view(self.E, self.stride)[:, :self.blob]
         if blobs is not None:
             view.copy_(blobs)
         return _HostRecords(self.base + li * span, self.stride, self.base, self.base + self.size, view)
+
+    def _fixed_records(self, what: str) -> None:
+        if self.pool is not None:
+            raise RuntimeError(f"TierStore.{what}: needs fixed host records (this store uses the record pool)")
+
+    def make_resident(self, key, experts, stream=None) -> int:
+        self._fixed_records("make_resident")
+        return super().make_resident(key, experts, stream)
+
+    def evict(self, key, experts) -> None:
+        self._fixed_records("evict")
+        return super().evict(key, experts)
+
+    def stage_layer(self, key, buf: int, stream):
+        self._fixed_records("stage_layer")
+        return super().stage_layer(key, buf, stream)
+
+    def forward_prefill_staged(self, key, x, topk_ids, topk_w):
+        self._fixed_records("forward_prefill_staged")
+        return super().forward_prefill_staged(key, x, topk_ids, topk_w)
+
+    def prefetch(self, key, ids, max_fill: int = 16) -> None:
+        self._fixed_records("prefetch")
+        return super().prefetch(key, ids, max_fill)
+
+    def start_copy_prefetch(self) -> None:
+        self._fixed_records("start_copy_prefetch")
+        return super().start_copy_prefetch()
+
+    def reset_cache(self) -> None:
+        super().reset_cache()
+        if self.pool is not None:                       # tables back to each key's record (or the null record)
+            n = self.L * self.E
+            self.ptrs_all[:n].copy_(self.host_addr_dev)
+
+    def publish_records(self, keys) -> None:
+        """Device side of new records (synchronous callers): host_addr_dev[key] = rec_of[key], and the table entry of
+        each key not in an HBM slot, on the current stream."""
+        keys = np.asarray(keys, dtype=np.int64).reshape(-1)
+        if keys.size == 0:
+            return
+        k = torch.from_numpy(keys).to(self.dev)
+        a = torch.from_numpy(self.rec_of[keys].copy()).to(self.dev)
+        self.host_addr_dev[k] = a
+        self.ptrs_all[k] = torch.where(self.slot_of_dev[k] < 0, a, self.ptrs_all[k])
 
     def add_layer(self, key, blobs=None):
         if len(self.layer_index) >= self.L:
@@ -82,7 +200,12 @@ class TierStore(ExpertStore):
         return None
 
     def addr(self, key: int) -> int:
-        """Host record address of key = layer row * E + e."""
+        """Host record address of key = layer row * E + e (with the record pool: the record it holds)."""
+        if self.pool is not None:
+            a = int(self.rec_of[int(key)])
+            if not a:
+                raise KeyError(f"TierStore: key {key} holds no record")
+            return a
         return self.base + int(key) * self.stride
 
 
@@ -251,9 +374,17 @@ class NvTier:
     rule), or budget_records when given. ckpt_layer[li] is the checkpoint layer of store row li (record = that
     layer * E + e)."""
 
+    _pool_ok = False                               # the record pool's queue protocol lives in NvTierAsync.step
+
     def __init__(self, store: TierStore, source, meta=None, ram_budget_bytes=2 << 30, ring_cap=1 << 16, safe=0,
                  dev=None, ckpt_layer=None, budget_records: int | None = None, latency: int = 8):
         self.st, self.E = store, store.E
+        self.pool = store.pool
+        if self.pool is not None:
+            if not self._pool_ok:
+                raise ValueError(f"{type(self).__name__}: a TierStore with the record pool needs NvTierAsync")
+            if _env_int("EXL3_NVTIER_NO_VICTIM", 0) == 1:
+                raise ValueError("NvTier: the record pool needs victim write-back (EXL3_NVTIER_NO_VICTIM=1 is set)")
         self._own_src = isinstance(source, (str, os.PathLike))   # a file opened here is closed by close()
         self.src = ExpertFile(source, meta) if self._own_src else source
         self.ckpt = np.asarray(ckpt_layer if ckpt_layer is not None else range(store.L), dtype=np.int64)
@@ -301,10 +432,15 @@ class NvTier:
         self.fill_many([key])
 
     def fill_many(self, keys) -> None:
-        """Read the records of `keys` into the arena (reader threads) and mark them RAM-resident (host books)."""
+        """Read the records of `keys` into the arena (reader threads) and mark them RAM-resident (host books). With
+        the record pool, keys without a record take one first and the device tables follow (current stream)."""
         keys = [int(k) for k in keys]
         if not keys:
             return
+        if self.pool is not None:
+            need = [k for k in keys if not self.st.rec_of[k]]
+            if need:
+                self.st.rec_of[need] = self.pool.take(len(need))
         t = time.perf_counter()
         if len(keys) < 4:
             for k in keys:
@@ -314,9 +450,18 @@ class NvTier:
         self.res[keys] = 1
         self.stats["nvme_reads"] += len(keys)
         self.stats["nvme_ms"] += (time.perf_counter() - t) * 1e3
+        if self.pool is not None:
+            self.st.publish_records(keys)
 
     def ram_bytes(self) -> int:
         return int(self.res.sum()) * self.st.stride
+
+    def pinned_bytes(self) -> int:
+        """Pinned host memory holding expert records: the record pool's chunks, or the whole fixed arena."""
+        return self.pool.pinned_bytes if self.pool is not None else self.st.size
+
+    def _flags_changed(self, keys, val: int) -> None:
+        """Host-side hook after a synchronous path set device flags of `keys` to val (the device is idle)."""
 
     def warm(self, keys_ckpt, max_bytes):
         """Fill the RAM tier with the hottest experts of a routing prior (checkpoint keys layer * E + e, hottest
@@ -334,10 +479,14 @@ class NvTier:
         keys = keys[np.sort(first)]                     # distinct, in prior order
         room = max(0, int(max_bytes // self.st.stride) - int(self.res.sum()))
         todo = keys[:room]
+        if self.pool is not None and todo.size:
+            torch.cuda.synchronize(self.dev)
         self.fill_many(todo)
         if hasattr(self, "age"):
             self.age[todo] = 0
-        self.res_dev.copy_(torch.from_numpy(self.res))
+        if todo.size:
+            self.res_dev.index_fill_(0, torch.from_numpy(todo.astype(np.int64)).to(self.dev), 1)
+            self._flags_changed(todo, 1)
         return int(todo.size), time.perf_counter() - t0
 
     # ---- prefill
@@ -353,15 +502,25 @@ class NvTier:
         ids_np = ids.reshape(-1).to("cpu", torch.int64).numpy() if torch.is_tensor(ids) else np.asarray(ids).reshape(-1)
         keys = np.unique(ids_np) + li * self.E
         miss = keys[self.res[keys] == 0]
+        pool = self.pool is not None
+        ready = set()
+        if pool and miss.size:
+            # the record pool: the device is idle from here on (records released below are read by nothing), and
+            # fills in flight for these keys are finished here instead of at their step
+            torch.cuda.synchronize(self.dev)
+            ready = self._take_inflight(miss)
         inflight = getattr(self, "inflight", np.zeros(n, dtype=bool))
         over = int(self.res.sum()) + int(inflight.sum()) + miss.size - self.budget
         if miss.size and over > 0:
             torch.cuda.synchronize(self.dev)
-            back = (self.res_dev.cpu().numpy() == 1) & (self.res == 0)       # victims written back since the last step
-            self.res[back] = 1
             age = getattr(self, "age", np.zeros(n, dtype=np.int64))
-            if hasattr(self, "age"):
-                age[back] = self.tick
+            if not pool:
+                # victims written back since the last step (with the record pool the step adopts them, when it
+                # learns their records)
+                back = (self.res_dev.cpu().numpy() == 1) & (self.res == 0)
+                self.res[back] = 1
+                if hasattr(self, "age"):
+                    age[back] = self.tick
             ok = (self.res == 1) & ~inflight
             ok[list(self.pinned)] = False
             ok[keys] = False
@@ -372,8 +531,16 @@ class NvTier:
                 self.res[ev] = 0
                 self.transient[ev] = False
                 self.res_dev.index_fill_(0, torch.from_numpy(ev).to(self.dev), 0)
+                if pool:
+                    r = self.st.rec_of[ev]
+                    self.pool.give(r[r != 0])
+                    self.st.rec_of[ev] = 0
+                    self._flags_changed(ev, 0)
             self.stats["prefill_evicts"] = self.stats.get("prefill_evicts", 0) + int(ev.size)
-        self.fill_many(miss)
+        self.fill_many([k for k in miss.tolist() if k not in ready])
+        if ready:
+            self.res[sorted(ready)] = 1
+            self.st.publish_records(sorted(ready))
         if miss.size:
             if hasattr(self, "inflight"):
                 self.inflight[miss] = False
@@ -381,6 +548,7 @@ class NvTier:
                 self.age[miss] = self.tick
             self.transient[miss] = True
             self.res_dev.index_fill_(0, torch.from_numpy(miss.astype(np.int64)).to(self.dev), 1)
+            self._flags_changed(miss, 1)
         self.stats["prefill_fills"] = self.stats.get("prefill_fills", 0) + int(miss.size)
         return int(miss.size)
 
@@ -491,11 +659,15 @@ class _TierStreamer:
 class NvTierFast(NvTier):
     """Vectorised bookkeeping with background fills (the reference's NvTierFast, nvtier.py:175-278): per-key age,
     in-flight and pinned masks; the fills admitted at host step n are read by worker tasks and become resident at
-    host step n + latency (a deterministic completion time in place of wall-clock NVMe reads)."""
+    host step n + latency (a deterministic completion time in place of wall-clock NVMe reads), or, with
+    completion="wallclock" (EXL3_NVTIER_COMPLETION=wallclock), at the first host step after their reads finished
+    (the reference's behaviour, nvtier.py:190-215; the admissions then depend on the disk's timing). With the record
+    pool the admitted keys take their records, and their reads start, at the next host step, once the records of the
+    keys evicted with them are free again."""
 
     FILL_CHUNKS = 4
 
-    def __init__(self, *a, **k):
+    def __init__(self, *a, completion: str | None = None, **k):
         super().__init__(*a, **k)
         n = self.L * self.E
         self.age = np.zeros(n, dtype=np.int64)
@@ -503,7 +675,12 @@ class NvTierFast(NvTier):
         self.pin_mask = np.zeros(n, dtype=bool)
         self.pin_mask[sorted(self.pinned)] = True
         self.inflight = np.zeros(n, dtype=bool)
+        self.completion = completion or os.environ.get("EXL3_NVTIER_COMPLETION", "steps")
+        if self.completion not in ("steps", "wallclock"):
+            raise ValueError(f"NvTierFast: completion {self.completion!r} is 'steps' or 'wallclock'")
         self._due = {}                              # host step -> [(keys, future)]
+        self._fut_of = {}                           # key -> (keys, future) of its started fill
+        self._to_start = []                         # record pool: [(keys, due step)] admitted, not started
         self._hstep = 0
 
     def _read_keys(self, keys) -> None:
@@ -515,16 +692,73 @@ class NvTierFast(NvTier):
         keys = [int(k) for k in keys]
         if not keys:
             return
-        due = self._due.setdefault(hs + self.latency, [])
-        for part in np.array_split(np.asarray(keys), min(self.FILL_CHUNKS, len(keys))):
-            due.append((part.tolist(), self._pool().submit(self._read_keys, part.tolist())))
         self.stats["nvme_reads"] += len(keys)
+        if self.pool is not None:
+            self._to_start.append((keys, hs + self.latency))
+            return
+        self._submit(keys, hs + self.latency)
+
+    def _submit(self, keys, due: int) -> None:
+        lst = self._due.setdefault(due, [])
+        for part in np.array_split(np.asarray(keys, dtype=np.int64), min(self.FILL_CHUNKS, len(keys))):
+            kl = part.tolist()
+            fut = self._pool().submit(self._read_keys, list(kl))
+            lst.append((kl, fut))
+            for key in kl:
+                self._fut_of[key] = (kl, fut)
+
+    def _start_fills(self) -> None:
+        """Record pool: the admissions of the previous host step take their records and start their reads."""
+        for keys, due in self._to_start:
+            keys = [k for k in keys if self.inflight[k]]        # a prefill may have filled some meanwhile
+            if keys:
+                self.st.rec_of[keys] = self.pool.take(len(keys))
+                self._submit(keys, due)
+        self._to_start = []
+
+    def _take_inflight(self, keys) -> set:
+        """Finish the fills in flight of `keys` now (synchronous paths): admissions not started are dropped from the
+        start list, started reads are waited for and leave their step; returns the keys whose record is filled."""
+        ks = {int(k) for k in keys if self.inflight[int(k)]}
+        if not ks:
+            return set()
+        rest = []
+        for kl, due in self._to_start:
+            kl = [k for k in kl if k not in ks]
+            if kl:
+                rest.append((kl, due))
+        self._to_start = rest
+        ready = set()
+        for key in ks:
+            ent = self._fut_of.pop(key, None)
+            if ent is not None:
+                ent[1].result()
+                ent[0].remove(key)
+                ready.add(key)
+        self.inflight[sorted(ks)] = False
+        return ready
 
     def _completed(self, hs: int) -> list:
         done = []
-        for keys, fut in self._due.pop(hs, []):
-            fut.result()
-            done.extend(keys)
+        if self.completion == "wallclock":
+            for d in sorted(self._due):
+                keep = []
+                for keys, fut in self._due[d]:
+                    if fut.done():
+                        fut.result()
+                        done.extend(keys)
+                    else:
+                        keep.append((keys, fut))
+                if keep:
+                    self._due[d] = keep
+                else:
+                    del self._due[d]
+        else:
+            for keys, fut in self._due.pop(hs, []):
+                fut.result()
+                done.extend(keys)
+        for key in done:
+            self._fut_of.pop(key, None)
         return done
 
 
@@ -609,9 +843,20 @@ class NvTierAsync(NvTierFast):
     read in place from a pinned double buffer, mirrors the miss-ring entries appended since the last snapshot into a
     pinned ring mirror, and copies the RAM flags, the slot table and the device status words into pinned double
     buffers; no host allocation, no extra synchronisation. A non-zero status (a bounded wait of a decode kernel timed
-    out, so an output was computed from incomplete data) raises RuntimeError at the next step."""
+    out, so an output was computed from incomplete data) raises RuntimeError at the next step.
 
-    def __init__(self, *a, **k):
+    With a TierStore(pool=True) the tier pins a RecordPool instead of a record per expert (exl3_tier_exchange_pool):
+    every key it holds owns one record; a victim written back takes the next record of the step's write-back queue
+    (wb_queue records, EXL3_NVTIER_WB_QUEUE, default 48; the exchange installs the next queue and mirrors what the
+    last one gave to which key); the records of evicted keys return to the pool after the exchange that clears their
+    flags has run; admitted fills take records at the next step. The pool then holds at most budget + 3 * wb_queue
+    records (two queues outstanding and one step of adopted write-backs), rounded up to its chunk. A write-back that
+    finds the queue used up is dropped (stats["wb_dropped"]): the victim leaves HBM without a copy and stays masked
+    until a fill brings it back."""
+
+    _pool_ok = True
+
+    def __init__(self, *a, wb_queue: int | None = None, **k):
         super().__init__(*a, **k)
         from . import capi
         self._capi = capi
@@ -652,6 +897,83 @@ class NvTierAsync(NvTierFast):
         self.res = self.policy.res
         self.log_decisions = False
         self.decisions = []                # (admitted keys, evicted keys) per step when log_decisions
+        if self.pool is not None:
+            self._pool_init(int(wb_queue) if wb_queue else _env_int("EXL3_NVTIER_WB_QUEUE", 48))
+
+    # ---- record pool
+    def _pool_init(self, cap: int) -> None:
+        if cap <= 0:
+            raise ValueError(f"NvTierAsync: write-back queue of {cap} records")
+        X, d, n = self.st.X, self.dev, self._n
+        self.wb_cap = cap
+        self._vict_addr = torch.zeros(self.E, dtype=torch.int64, device=d)
+        self._wbq = torch.zeros(cap, dtype=torch.int64, device=d)
+        self._wbq_state = torch.zeros(2 + cap, dtype=torch.int32, device=d)
+        self._h_next = [X.host_alloc(8 * cap).view(torch.int64) for _ in range(2)]
+        self._h_wbm = [X.host_alloc(4 * (2 + cap)).view(torch.int32) for _ in range(2)]
+        for t in self._h_wbm:
+            t.zero_()
+        self._np_next = [t.numpy() for t in self._h_next]
+        self._np_wbm = [t.numpy() for t in self._h_wbm]
+        self._h_upd = [X.host_alloc(16 * n).view(torch.int64) for _ in range(2)]
+        self._np_upd = [t.numpy() for t in self._h_upd]
+        self._pending = [[], []]           # records of keys evicted by the step that used buffer b
+        self._q_recs = [np.zeros(0, np.int64), np.zeros(0, np.int64)]    # the queue installed by exchange b
+        q0 = self.pool.take(cap)           # the queue of the first decode step, as if installed by exchange 1
+        self._wbq.copy_(torch.from_numpy(q0))
+        self._q_recs[1] = q0
+        for key in ("wb_taken", "wb_dropped", "pool_rebind"):
+            self.stats[key] = 0
+        L = self._capi.lib()
+        torch.cuda.synchronize(d)
+        self._capi.check(L.exl3_set_victim_addrs(self._vict_addr.data_ptr()), "set_victim_addrs")
+        self._capi.check(L.exl3_set_record_pool(self.st.host_addr_dev.data_ptr(), self._wbq.data_ptr(),
+                                                self._wbq_state.data_ptr(), cap), "set_record_pool")
+
+    def _pool_collect(self, j: int, k: int) -> None:
+        """After the exchange of buffer j has run: free the records of the keys its step evicted, and settle the
+        queue that exchange found in use (installed by exchange k): taken records belong to the keys written back
+        into them, the rest return to the pool."""
+        st, pool, cap = self.st, self.pool, self.wb_cap
+        pool.give(self._pending[j])
+        self._pending[j] = []
+        m = self._np_wbm[j]
+        taken = int(m[0])
+        q = self._q_recs[k]
+        if taken > q.size:
+            raise RuntimeError(f"exl3xpu tier: the device took {taken} write-back records of a queue of {q.size}")
+        if taken:
+            keys = m[1:1 + taken].astype(np.int64)
+            old = st.rec_of[keys]
+            if (old != 0).any():           # a key written back while the books still gave it a record
+                self._pending[k].extend(old[old != 0].tolist())
+                self.stats["pool_rebind"] += int((old != 0).sum())
+            st.rec_of[keys] = q[:taken]
+        pool.give(q[taken:])
+        self._q_recs[k] = np.zeros(0, np.int64)
+        self.stats["wb_taken"] += taken
+        self.stats["wb_dropped"] += int(m[1 + cap])
+
+    def _flags_changed(self, keys, val: int) -> None:
+        """A synchronous path changed device flags while the device is idle: make the snapshot the next step will
+        read show them (the previous upload overlaid first), so that the step does not mistake them for write-backs
+        or reverse them."""
+        keys = np.asarray(keys, dtype=np.int64).reshape(-1)
+        for b in range(2):
+            if self._have[b]:
+                if self._last_diff is not None:
+                    dk, dv = self._last_diff
+                    self._np_res[b][dk] = dv
+                self._np_res[b][keys] = val
+        self._last_diff = None
+
+    def close(self) -> None:
+        if self.pool is not None:
+            torch.cuda.synchronize(self.dev)
+            L = self._capi.lib()
+            self._capi.check(L.exl3_set_record_pool(None, None, None, 0), "set_record_pool")
+            self._capi.check(L.exl3_set_victim_addrs(None), "set_victim_addrs")
+        super().close()
 
     @property
     def inflight_keys(self):
@@ -669,6 +991,8 @@ class NvTierAsync(NvTierFast):
         k, j = self._k, self._k ^ 1
         self._k = j
         n_diff = 0
+        n_upd = 0
+        pool = self.pool is not None
         seen0 = pol.ring_seen
         if self._have[j]:
             tw = time.perf_counter()
@@ -678,14 +1002,30 @@ class NvTierAsync(NvTierFast):
             if bad:
                 raise RuntimeError(f"exl3xpu: {bad} bounded waits of the decode kernels timed out on the device "
                                    "(outputs computed from incomplete data); the device state is not trustworthy")
+            if pool:
+                self._pool_collect(j, k)
+                self._start_fills()
             view = self._view
             np.copyto(view, self._np_res[j])
             if self._last_diff is not None:         # the flags uploaded with that snapshot
                 dk, dv = self._last_diff
                 view[dk] = dv
-            adm, ev_keys, diff, vals = pol.decide(view, self._np_ring, self._np_slot[j], self._completed(hs))
+            done = self._completed(hs)
+            adm, ev_keys, diff, vals = pol.decide(view, self._np_ring, self._np_slot[j], done)
             self._ring_from = int(self._np_ring[0]) & 0xFFFFFFFF
             self._queue_fills(adm, hs)
+            if pool:
+                st = self.st
+                r = st.rec_of[ev_keys]
+                self._pending[k].extend(r[r != 0].tolist())
+                st.rec_of[ev_keys] = 0
+                dn = np.asarray(done, dtype=np.int64)
+                dn = dn[pol.res[dn] == 1]
+                if dn.size:                         # completed fills: their records go up with their flags
+                    u = self._np_upd[k]
+                    u[0:2 * dn.size:2] = dn
+                    u[1:2 * dn.size:2] = st.rec_of[dn]
+                    n_upd = int(dn.size)
             if len(diff):
                 # buffer k was last read by the exchange of step n-2, which ran before the snapshot just waited for
                 self._np_diff[k][:len(diff)] = (diff << 1) | vals
@@ -704,10 +1044,23 @@ class NvTierAsync(NvTierFast):
         # this step's diff and the snapshot of the device state after decode step n, in one launch
         srcs, dsts, nbs = self._xargs[k]
         L = self._capi.lib()
-        self._capi.check(L.exl3_tier_exchange(self.res_dev.data_ptr(), self._n, self._h_diff[k].data_ptr(), n_diff,
-                                              self.ring.data_ptr(), self.ring.numel() - 1, self._ring_from,
-                                              self._h_ring.data_ptr(), srcs, dsts, nbs, 3, cur.cuda_stream),
-                         "nvtier exchange")
+        if pool:
+            q = self.pool.take(self.wb_cap)         # the write-back queue of decode step n + 1
+            self._np_next[k][:] = q
+            self._q_recs[k] = q
+            st = self.st
+            self._capi.check(L.exl3_tier_exchange_pool(
+                self.res_dev.data_ptr(), self._n, self._h_diff[k].data_ptr(), n_diff, self.ring.data_ptr(),
+                self.ring.numel() - 1, self._ring_from, self._h_ring.data_ptr(), srcs, dsts, nbs, 3,
+                self._h_upd[k].data_ptr(), n_upd, st.host_addr_dev.data_ptr(), st.ptrs_all.data_ptr(),
+                st.slot_of_dev.data_ptr(), self._h_next[k].data_ptr(), self._wbq.data_ptr(),
+                self._wbq_state.data_ptr(), self._h_wbm[k].data_ptr(), self.wb_cap, cur.cuda_stream),
+                "nvtier exchange")
+        else:
+            self._capi.check(L.exl3_tier_exchange(self.res_dev.data_ptr(), self._n, self._h_diff[k].data_ptr(),
+                                                  n_diff, self.ring.data_ptr(), self.ring.numel() - 1,
+                                                  self._ring_from, self._h_ring.data_ptr(), srcs, dsts, nbs, 3,
+                                                  cur.cuda_stream), "nvtier exchange")
         self._snap_ev[k].record(cur)
         self._have[k] = True
         self.stats["steps"] += 1

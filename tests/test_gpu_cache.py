@@ -13,13 +13,14 @@ pytestmark = pytest.mark.gpu
 GOLD = os.path.join(os.path.dirname(__file__), "golden")
 
 
-def _setup(L, E, S, H, I, K, budget, qmax, age, latency, ring_cap, seed):
+def _setup(L, E, S, H, I, K, budget, qmax, age, latency, ring_cap, seed, pool=False, wb_queue=None):
     from exl3xpu import nvtier
-    store = nvtier.TierStore(H, I, K, E, S, n_layers=L)
+    store = nvtier.TierStore(H, I, K, E, S, n_layers=L, pool=pool)
     for li in range(L):
         store.add_layer(f"model.layers.{li}.mlp")
     src = nvtier.SyntheticExpertSource(H, I, K, seed, n_distinct=16)
-    tier = nvtier.NvTierAsync(store, src, ring_cap=ring_cap, budget_records=budget, latency=latency)
+    tier = nvtier.NvTierAsync(store, src, ring_cap=ring_cap, budget_records=budget, latency=latency,
+                              wb_queue=wb_queue)
     tier.policy.admit_age, tier.policy.admit_qmax = age, qmax
     tier.log_decisions = True
     # reference table: every expert's true blob in HBM (independent of the cache)
@@ -60,15 +61,17 @@ def _run(store, tier, ids, w, H, check_out_every=0, ref_ptr=None, M=1):
     return lg[1:].reshape(steps, L, rl), bad
 
 
-@pytest.mark.parametrize("fused", [1, 0])
-def test_cache_golden_small(fused):
-    """fused 1: the ensure runs inside the layer kernel; 0: as its own launch before it."""
+@pytest.mark.parametrize("fused,pool", [(1, False), (0, False), (1, True), (0, True)])
+def test_cache_golden_small(fused, pool):
+    """fused 1: the ensure runs inside the layer kernel; 0: as its own launch before it. pool: the RAM tier keeps
+    its records in a RecordPool (write-back queue of 8 records) instead of one fixed record per expert."""
+    from pool_checks import check_pool, write_backs
     g = np.load(os.path.join(GOLD, "cache_small.npz"))
     L, E, S, P = int(g["L"]), int(g["E"]), int(g["S"]), int(g["P"])
-    print(f"case cache golden L={L} E={E} S={S} fused={fused}", flush=True)
+    print(f"case cache golden L={L} E={E} S={S} fused={fused} pool={pool}", flush=True)
     H = I = 128
     store, tier, blobs, ref_ptr = _setup(L, E, S, H, I, 3, int(g["budget"]), int(g["qmax"]), int(g["age"]),
-                                         int(g["latency"]), int(g["ring_cap"]), 3)
+                                         int(g["latency"]), int(g["ring_cap"]), 3, pool=pool, wb_queue=8)
     store.X.moe_set_fused_ensure(fused)
     try:
         recs, bad = _run(store, tier, g["ids"], g["w"], H, check_out_every=1, ref_ptr=ref_ptr)
@@ -83,42 +86,53 @@ def test_cache_golden_small(fused):
         assert ev.tolist() == flat[pos + na:pos + na + ne].tolist(), n
         pos += na + ne
     assert bad == 0
+    if pool:
+        wb = write_backs(g["recs"], P)
+        check_pool(store, tier, tier.src, int(g["budget"]), int(wb[:-1].sum()))
     tier.close()
 
 
-def test_cache_config1_trace_bitexact():
+@pytest.mark.parametrize("pool", [False, True])
+def test_cache_config1_trace_bitexact(pool):
     """48 layers x 512 experts, 8,000 slots, RAM budget 1,075 records, 4,000-step Zipf(1.1) trace of 10 picks per
     layer, 8-step fill latency, AGE 4, QMAX 256: every device and host decision equals the oracle's. Experts are tiny
-    (H = I = 128): the decisions do not depend on the expert shape."""
+    (H = I = 128): the decisions do not depend on the expert shape. pool: the RAM tier in a RecordPool (write-back
+    queue of 48 records; the trace writes back up to 14 victims per step once HBM is full)."""
+    from pool_checks import check_pool, write_backs
     L, E, S, P, steps = 48, 512, 8000, 10, int(os.environ.get("EXL3_TEST_C1_STEPS", "4000"))
-    print(f"case cache config1 steps={steps}", flush=True)
+    print(f"case cache config1 steps={steps} pool={pool}", flush=True)
     ids, w = synth.zipf_trace(20261202, steps, L, E, P)
     ids, w = ids[:, :, 0], w[:, :, 0]
     co = cache.CacheOracle(L, E, S, budget=1075, age=4, qmax=256, latency=8)
     orecs, olog = co.run(ids, w)
-    store, tier, blobs, ref_ptr = _setup(L, E, S, 128, 128, 3, 1075, 256, 4, 8, 1 << 16, 7)
+    store, tier, blobs, ref_ptr = _setup(L, E, S, 128, 128, 3, 1075, 256, 4, 8, 1 << 16, 7, pool=pool)
     recs, bad = _run(store, tier, ids, w, 128, check_out_every=97, ref_ptr=ref_ptr)
     mism = np.nonzero((recs != orecs).any(axis=-1))
     assert mism[0].size == 0, f"first mismatch at step/layer {mism[0][0]}/{mism[1][0]}"
     for n, ((a1, e1), (a2, e2)) in enumerate(zip(tier.decisions, olog)):
         assert a1.tolist() == a2.tolist() and e1.tolist() == e2.tolist(), n
     assert bad == 0
+    if pool:
+        check_pool(store, tier, tier.src, 1075, int(write_backs(orecs, P)[:-1].sum()))
     tier.close()
 
 
-@pytest.mark.parametrize("fused", [1, 0])
-def test_cache_multirow_tier(fused):
+@pytest.mark.parametrize("fused,pool", [(1, False), (0, False), (1, True), (0, True)])
+def test_cache_multirow_tier(fused, pool):
     """4 rows x top-10 per call (40 picks, duplicates across rows: the ensure inside the layer kernel when fused),
     6 layers x 128 experts, 150 slots, RAM tier of 160 records (AGE 4, QMAX 64, 3-step fill latency), Zipf(1.1)
-    routing: every device record and host decision equals the oracle's and every output equals the plain forward."""
+    routing: every device record and host decision equals the oracle's and every output equals the plain forward.
+    pool: the RAM tier in a RecordPool with a write-back queue of 48 records (the trace writes back up to 40 victims
+    per step)."""
+    from pool_checks import check_pool, write_backs
     L, E, S, M, TK, steps = 6, 128, 150, 4, 10, 80
-    print(f"case cache multirow tier M={M} top-{TK} fused={fused}", flush=True)
+    print(f"case cache multirow tier M={M} top-{TK} fused={fused} pool={pool}", flush=True)
     ids, w = synth.zipf_trace(20261203, steps, L, E, TK, M=M)
     ids = np.ascontiguousarray(ids.reshape(steps, L, M * TK))
     w = np.ascontiguousarray(w.reshape(steps, L, M * TK))
     co = cache.CacheOracle(L, E, S, ring_cap=1 << 12, budget=160, age=4, qmax=64, latency=3)
     orecs, olog = co.run(ids, w)
-    store, tier, blobs, ref_ptr = _setup(L, E, S, 128, 128, 3, 160, 64, 4, 3, 1 << 12, 11)
+    store, tier, blobs, ref_ptr = _setup(L, E, S, 128, 128, 3, 160, 64, 4, 3, 1 << 12, 11, pool=pool, wb_queue=48)
     store.X.moe_set_fused_ensure(fused)
     try:
         recs, bad = _run(store, tier, ids, w, 128, check_out_every=1, ref_ptr=ref_ptr, M=M)
@@ -130,6 +144,10 @@ def test_cache_multirow_tier(fused):
         assert a1.tolist() == a2.tolist() and e1.tolist() == e2.tolist(), n
     assert bad == 0
     assert recs[:, :, 1].sum() > 0 and recs[:, :, 2 + M * TK].sum() > 0   # masked picks and fills happened
+    if pool:
+        wb = write_backs(orecs, M * TK)
+        assert wb.sum() > 0
+        check_pool(store, tier, tier.src, 160, int(wb[:-1].sum()))
     tier.close()
 
 

@@ -41,14 +41,22 @@ def c2_store():
     del store
 
 
-@pytest.mark.parametrize("bs,budget,steps", [(1, 1075, 300), (2, 1075, 200), (4, 1075, 150),
-                                             (1, 3763, 300), (2, 3763, 200), (4, 3763, 150)])
-def test_config2_tier_stack(c2_store, bs, budget, steps):
+@pytest.mark.parametrize("bs,budget,steps,pool", [(1, 1075, 300, False), (2, 1075, 200, False),
+                                                  (4, 1075, 150, False), (1, 3763, 300, False),
+                                                  (2, 3763, 200, False), (4, 3763, 150, False),
+                                                  (1, 1075, 300, True), (4, 1075, 150, True)])
+def test_config2_tier_stack(c2_store, bs, budget, steps, pool):
+    """pool: the RAM tier pins a RecordPool (budget + 3 x 48 queue records at most, in 32-record chunks) instead of
+    the 24,576-record arena; decisions and outputs must not change."""
     from exl3xpu import nvtier
     store, src, ref_ptr, _ = c2_store
     g = C2
     L, E, S, P = g["L"], g["E"], g["S"], bs * g["topk"]
-    print(f"case config2 bs={bs} budget={budget} steps={steps}", flush=True)
+    print(f"case config2 bs={bs} budget={budget} steps={steps} pool={pool}", flush=True)
+    if pool:
+        store = nvtier.TierStore(g["H"], g["I"], g["K"], g["E"], g["S"], n_layers=g["L"], pool=True)
+        for li in range(g["L"]):
+            store.add_layer(f"model.layers.{li}.mlp")
     store.reset_cache()
     ids, w = synth.zipf_trace(20261210 + bs, steps, L, E, g["topk"], M=bs)
     ids = np.ascontiguousarray(ids.reshape(steps, L, P))
@@ -96,6 +104,13 @@ def test_config2_tier_stack(c2_store, bs, budget, steps):
     fills = int((recs[:, :, 2 + P] > 0).sum())
     print(f"config2 bs={bs} budget={budget}: ring count {masked}, calls with fills {fills}", flush=True)
     assert masked > 0 and fills > 0
+    if pool:
+        from pool_checks import check_pool, write_backs
+        check_pool(store, tier, src, budget, int(write_backs(orecs, P)[:-1].sum()))
+        full = L * E * store.stride
+        print(f"config2 pool: {tier.pinned_bytes() / 2**30:.2f} GiB pinned ({tier.pool.records} records, high-water "
+              f"{tier.pool.high}) instead of {full / 2**30:.2f} GiB", flush=True)
+        assert tier.pinned_bytes() <= (budget + 3 * tier.wb_cap + tier.pool.chunk) * store.stride
 
 
 def _c4_case(L, E, K_cycle, nd, seed):

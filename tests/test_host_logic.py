@@ -232,3 +232,36 @@ def test_status_watch_raises_when_the_mirror_moves():
         with pytest.raises(RuntimeError, match="1 bounded waits"):
             call()
     st.check_device_status()
+
+
+def test_record_pool_reuses_records_and_grows_by_chunks():
+    """RecordPool bookkeeping on plain CPU memory (host_alloc stubbed): records come lowest address first from each
+    chunk, given-back records are reused before the pool grows, the high-water mark and the pinned bytes follow,
+    and view() finds a record's bytes."""
+    class Stub:
+        def __init__(self):
+            self.allocs = []
+
+        def host_alloc(self, n):
+            t = torch.zeros(n, dtype=torch.uint8)
+            self.allocs.append(t)
+            return t
+
+    X = Stub()
+    pool = nvtier.RecordPool(X, 4096, chunk=4)
+    a = pool.take(3)
+    base = X.allocs[0].data_ptr()
+    assert a.tolist() == [base, base + 4096, base + 8192]
+    assert pool.records == 4 and pool.in_use == 3 and pool.high == 3
+    b = pool.take(2)                                   # one left in the first chunk, then a second chunk
+    assert len(X.allocs) == 2 and pool.records == 8 and pool.pinned_bytes == 8 * 4096
+    assert len(set(a.tolist()) | set(b.tolist())) == 5
+    pool.give(a[:2])
+    pool.give(np.zeros(2, dtype=np.int64))             # zeros (no record) are ignored
+    assert pool.in_use == 3 and pool.high == 5
+    c = pool.take(2)
+    assert sorted(c.tolist()) == sorted(a[:2].tolist()) and pool.records == 8
+    pool.view(int(c[0]), 16)[:] = 7
+    assert int(X.allocs[0][int(c[0]) - base]) == 7
+    with pytest.raises(KeyError):
+        pool.view(12345, 16)
