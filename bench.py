@@ -544,6 +544,9 @@ def main():
                     "the HBM cache and the RAM tier start empty and reach their steady state after about 1,000 steps "
                     "of the Zipf trace")
     ap.add_argument("--bs", type=int, default=1)
+    ap.add_argument("--fixed-arena", action="store_true",
+                    help="the RAM tier in one pinned record per expert (30 GB at 48 x 512 experts) instead of the "
+                         "record pool (the budget plus the write-back queues)")
     ap.add_argument("--roofline-steps", type=int, default=20)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--budget-records", type=int, default=BUDGET)
@@ -591,13 +594,14 @@ def main():
     Hm, Im = (128, 128) if args.bookkeeping else (H, I)
     if args.bookkeeping:             # the trace's first two steps run eagerly (library set-up), the other 3,998 timed
         args.steps, args.warmup, args.settle = 3998, 0, 2
-    store = nvtier.TierStore(Hm, Im, K, E, SLOTS, n_layers=L, device=dev)
+    store = nvtier.TierStore(Hm, Im, K, E, SLOTS, n_layers=L, device=dev, pool=not args.fixed_arena)
     keys = [f"model.layers.{li}.mlp" for li in range(L)]
     for k in keys:
         store.add_layer(k)
     src = nvtier.SyntheticExpertSource(Hm, Im, K, SEED, n_distinct=64)
     tier = nvtier.NvTierAsync(store, src, budget_records=args.budget_records, latency=8)
-    log(f"setup {time.perf_counter() - t0:.1f} s: slots {SLOTS} x {store.blob} B, pinned arena {store.size / 2**30:.1f} GiB")
+    log(f"setup {time.perf_counter() - t0:.1f} s: slots {SLOTS} x {store.blob} B, RAM tier "
+        f"{'fixed arena' if args.fixed_arena else 'record pool'} {tier.pinned_bytes() / 2**30:.2f} GiB pinned")
     steps, warm, bs, settle = args.steps, args.warmup, args.bs, max(0, args.settle)
     if args.roofline_only:
         steps, warm, settle = 0, 0, 0
@@ -669,7 +673,15 @@ def main():
     status = (ctypes.c_int32 * 4)()
     capi.check(capi.lib().exl3_device_status(status, torch.cuda.current_stream().cuda_stream), "device status")
     tok_s = steps * bs / el if steps else 0.0
-    d = {k: tier.stats.get(k, 0) - st0.get(k, 0) for k in ("masked", "evicts", "nvme_reads", "admit_dropped", "wait_ms")}
+    d = {k: tier.stats.get(k, 0) - st0.get(k, 0) for k in ("masked", "evicts", "nvme_reads", "admit_dropped", "wait_ms",
+                                                          "wb_taken", "wb_dropped")}
+    ram_tier = {"mode": "fixed arena" if args.fixed_arena else "record pool",
+                "pinned_gib": round(tier.pinned_bytes() / 2**30, 3), "record_bytes": store.stride,
+                "budget_records": args.budget_records}
+    if tier.pool is not None:
+        ram_tier.update(records=tier.pool.records, high_water=tier.pool.high, wb_queue=tier.wb_cap,
+                        write_backs_per_step=round(d["wb_taken"] / max(steps, 1), 3),
+                        write_backs_dropped=int(tier.stats["wb_dropped"]))
     host_ms = {k: round(v / max(steps, 1) * 1e3, 4) for k, v in host_s.items()}
     host_ms["tier_wait"] = round(d.pop("wait_ms") / max(steps, 1), 4)     # of tier_step: waiting for the GPU
     sd = max(steps, 1)
@@ -693,7 +705,7 @@ def main():
                                    "latency; one forward_cached call per layer (HIP graph) + the host tier step",
                        "layers": L, "experts": E, "topk": TOPK, "hbm_slots": SLOTS,
                        "ram_budget_records": args.budget_records},
-            "device_status": int(status[0]),
+            "device_status": int(status[0]), "ram_tier": ram_tier,
         }
         log(f"bookkeeping: {gpu_ms * 1e3 / L:.2f} us per layer call (median step {gpu_ms:.3f} ms on the GPU), host tier "
             f"step {host_ms['tier_step'] - host_ms['tier_wait']:.3f} ms of work; {dec_s:.0f} decisions/s")
@@ -751,8 +763,8 @@ def main():
         "ms_per_step": round(el / sd * 1e3, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "bf16", "data": "synthetic: seeded EXL3 3bpw experts (64 distinct blobs), seeded Zipf(1.1) routing trace",
         "config": {"workload": "decode bs=%d through 48 MoE layers x 512 experts (H 2048, I 512), top-10, EXL3 K=3; "
-                               "8,000 HBM slots + pinned RAM tier (%d records), admission AGE 4 / QMAX 256, "
-                               "8-step fill latency" % (bs, args.budget_records),
+                               "8,000 HBM slots + pinned RAM tier (%d records, %s), admission AGE 4 / QMAX 256, "
+                               "8-step fill latency" % (bs, args.budget_records, ram_tier["mode"]),
                    "layers": L, "experts": E, "topk": TOPK, "hidden": H, "intermediate": I, "K": K, "batch": bs,
                    "hbm_slots": SLOTS, "ram_budget_records": args.budget_records},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK, "unit": "GB/s",
@@ -768,6 +780,7 @@ def main():
         "per_step": {"masked": d["masked"] / sd, "fills": d["nvme_reads"] / sd, "evicts": d["evicts"] / sd,
                      "admit_dropped": d["admit_dropped"] / sd},
         "untimed_steps": {"settle": settle, "warmup": warm},
+        "ram_tier": ram_tier,
         "device_status": int(status[0]),
     }
     if status[0]:

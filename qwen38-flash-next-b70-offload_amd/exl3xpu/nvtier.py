@@ -660,10 +660,11 @@ class NvTierFast(NvTier):
     """Vectorised bookkeeping with background fills (the reference's NvTierFast, nvtier.py:175-278): per-key age,
     in-flight and pinned masks; the fills admitted at host step n are read by worker tasks and become resident at
     host step n + latency (a deterministic completion time in place of wall-clock NVMe reads), or, with
-    completion="wallclock" (EXL3_NVTIER_COMPLETION=wallclock), at the first host step after their reads finished
-    (the reference's behaviour, nvtier.py:190-215; the admissions then depend on the disk's timing). With the record
-    pool the admitted keys take their records, and their reads start, at the next host step, once the records of the
-    keys evicted with them are free again."""
+    completion="wallclock" (EXL3_NVTIER_COMPLETION=wallclock), at the first host step after their own read finished:
+    each key is read on FIFO queue key % N of N single-reader queues (N = EXL3_NVTIER_DECODE_FILL_QUEUES, default 8;
+    the reference's decode-fill queues, nvtier.py:643-693), so the admissions then depend on the disk's timing. With
+    the record pool the admitted keys take their records, and their reads start, at the next host step, once the
+    records of the keys evicted with them are free again."""
 
     FILL_CHUNKS = 4
 
@@ -680,6 +681,7 @@ class NvTierFast(NvTier):
             raise ValueError(f"NvTierFast: completion {self.completion!r} is 'steps' or 'wallclock'")
         self._due = {}                              # host step -> [(keys, future)]
         self._fut_of = {}                           # key -> (keys, future) of its started fill
+        self._fifos = None                          # wall-clock mode: the decode-fill queues
         self._to_start = []                         # record pool: [(keys, due step)] admitted, not started
         self._hstep = 0
 
@@ -700,12 +702,29 @@ class NvTierFast(NvTier):
 
     def _submit(self, keys, due: int) -> None:
         lst = self._due.setdefault(due, [])
+        if self.completion == "wallclock":
+            if self._fifos is None:
+                self._fifos = [ThreadPoolExecutor(1) for _ in range(max(1, _env_int("EXL3_NVTIER_DECODE_FILL_QUEUES",
+                                                                                   8)))]
+            for key in keys:
+                kl = [int(key)]
+                fut = self._fifos[int(key) % len(self._fifos)].submit(self._read, int(key))
+                lst.append((kl, fut))
+                self._fut_of[int(key)] = (kl, fut)
+            return
         for part in np.array_split(np.asarray(keys, dtype=np.int64), min(self.FILL_CHUNKS, len(keys))):
             kl = part.tolist()
             fut = self._pool().submit(self._read_keys, list(kl))
             lst.append((kl, fut))
             for key in kl:
                 self._fut_of[key] = (kl, fut)
+
+    def close(self) -> None:
+        if self._fifos is not None:
+            for q in self._fifos:
+                q.shutdown(wait=True)
+            self._fifos = None
+        super().close()
 
     def _start_fills(self) -> None:
         """Record pool: the admissions of the previous host step take their records and start their reads."""

@@ -540,6 +540,41 @@ def test_tier_fills_from_expert_file(tmp_path):
     assert tier.src.reads > 0 and recs[:, :, 2 + M * TK].sum() > 0
 
 
+def test_tier_pool_wallclock_from_expert_file(tmp_path):
+    """The record pool with fills from a packed expert file that complete by wall clock (each read on decode-fill
+    queue key % 8, resident at the first host step after it finished): the same trace as test_cache_multirow_tier.
+    The admissions now follow the disk's timing, so there is no oracle record to compare; instead every output
+    equals the plain forward on the true blobs with the post-mask picks, fills and write-backs happened, no
+    write-back was dropped, the pool stayed within budget + 3 x queue records and every resident key's record holds
+    its own blob."""
+    from pool_checks import check_pool
+    from exl3xpu import nvtier
+    L, E, S, M, TK, steps, H, I, K = 6, 128, 150, 4, 10, 60, 128, 128, 3
+    ids, w = synth.zipf_trace(20261203, steps, L, E, TK, M=M)
+    ids = np.ascontiguousarray(ids.reshape(steps, L, M * TK))
+    w = np.ascontiguousarray(w.reshape(steps, L, M * TK))
+    src = nvtier.SyntheticExpertSource(H, I, K, 11, n_distinct=16)
+    path = str(tmp_path / "experts.bin")
+    nvtier.write_expert_file(path, src, L, E, H, I, K)
+    store = nvtier.TierStore(H, I, K, E, S, n_layers=L, pool=True)
+    for li in range(L):
+        store.add_layer(f"model.layers.{li}.mlp")
+    tier = nvtier.NvTierAsync(store, path, ring_cap=1 << 12, budget_records=160, latency=3, completion="wallclock",
+                              wb_queue=48)
+    tier.policy.admit_age, tier.policy.admit_qmax = 4, 64
+    print(f"case tier pool wall-clock fills from expert file (direct I/O {tier.src.direct})", flush=True)
+    blobs = torch.from_numpy(src.buf).cuda()
+    ref_ptr = torch.tensor([blobs[r % src.n].data_ptr() for r in range(L * E)], dtype=torch.int64, device="cuda")
+    try:
+        recs, bad = _run(store, tier, ids, w, H, check_out_every=1, ref_ptr=ref_ptr, M=M)
+        assert bad == 0
+        assert tier.src.reads > 0 and recs[:, :, 2 + M * TK].sum() > 0
+        assert tier.stats["wb_taken"] > 0
+        check_pool(store, tier, src, 160)
+    finally:
+        tier.close()
+
+
 @pytest.mark.parametrize("M", [150, 255])
 def test_cache_midsize_rows(M):
     """Cached calls between the decode kernel's limit (1,024 picks) and prefill_min_m (256): M = 150 and 255 rows x

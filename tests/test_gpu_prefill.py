@@ -327,15 +327,17 @@ def test_prefill_zero_copy_config0_shapes():
     assert torch.equal(out, ref)
 
 
-def _plugin_sequence(H, I, K, E, S, L, topk, dsteps, budget, n_distinct, prompts, seed):
+def _plugin_sequence(H, I, K, E, S, L, topk, dsteps, budget, n_distinct, prompts, seed, pool=False, tail=(),
+                     dsteps2=0):
     """The tier plugin's call sequence (plugin/sglang_plugin.tier.py:531-561 `apply`, 944-956 the host step after every
     model step) over this API, tier mode: the prompts of `prompts` ((tokens, staged?) pairs; staged prompts of at
     least 256 tokens go through stage_forward, the others through ensure_for_prefill and the zero-copy forward), then
-    decode steps through forward_cached (tier mask, RAM hits written through), NvTierAsync.step after every model
-    step. Every prompt output equals the all-resident output bit for bit; every decode output equals the uncached
-    forward on the true blobs with the post-mask picks."""
+    decode steps through forward_cached (tier mask, RAM hits written through), then the prompts of `tail` and dsteps2
+    more decode steps, NvTierAsync.step after every model step. Every prompt output equals the all-resident output
+    bit for bit; every decode output equals the uncached forward on the true blobs with the post-mask picks. pool:
+    the RAM tier in a RecordPool (its invariants checked at the end)."""
     from exl3xpu import nvtier
-    store = nvtier.TierStore(H, I, K, E, S, n_layers=L)
+    store = nvtier.TierStore(H, I, K, E, S, n_layers=L, pool=pool)
     keys = [f"model.layers.{li}.mlp" for li in range(L)]
     for k in keys:
         store.add_layer(k)
@@ -358,6 +360,8 @@ def _plugin_sequence(H, I, K, E, S, L, topk, dsteps, budget, n_distinct, prompts
     try:
         steps = [(M, st, seed * 10 + 90 + n) for n, (M, st) in enumerate(prompts)]
         steps += [(1, False, seed * 10 + 100 + n) for n in range(dsteps)]
+        steps += [(M, st, seed * 10 + 70 + n) for n, (M, st) in enumerate(tail)]
+        steps += [(1, False, seed * 10 + 300 + n) for n in range(dsteps2)]
         for M, stage, sd in steps:
             for li in range(L):
                 ids, w = synth.softmax_topk(sd * 7 + li, M, E, topk)
@@ -372,10 +376,14 @@ def _plugin_sequence(H, I, K, E, S, L, topk, dsteps, budget, n_distinct, prompts
                     bad.append((M, sd, li))
             tier.step()                            # the host step hook after every model step
         torch.cuda.synchronize()
+        if pool:
+            from pool_checks import check_pool
+            check_pool(store, tier, src, budget)
     finally:
         tier.close()
     assert not bad, f"outputs differ at (M, seed, layer) {bad[:4]}"
     assert masked > 0                              # the decode steps exercised the tier mask
+    return tier
 
 
 def test_plugin_caller_sequence():
@@ -384,6 +392,19 @@ def test_plugin_caller_sequence():
     steps."""
     print("case plugin caller sequence", flush=True)
     _plugin_sequence(256, 128, 3, 32, 24, 3, 4, 40, 40, 3 * 32, [(300, True), (24, False)], 23)
+
+
+def test_plugin_caller_sequence_record_pool():
+    """The plugin's sequence with the RAM tier in a RecordPool (H 256, I 128, 32 experts, top-4, 3 layers, 24 HBM
+    slots, a 40-record budget, write-back queue 48): a staged 300-token prompt, a 24-token prompt, 40 decode steps,
+    then a 24-token and a staged 300-token prompt while fills are in flight and write-backs unsettled (the prefill
+    path finishes those fills and patches the snapshot the next host step reads), then 30 more decode steps. Outputs
+    as in the other sequences; at the end the pool's invariants hold (no dropped write-back, within budget +
+    3 x queue records, every resident key's record holds its blob)."""
+    print("case plugin caller sequence record pool", flush=True)
+    tier = _plugin_sequence(256, 128, 3, 32, 24, 3, 4, 40, 40, 3 * 32, [(300, True), (24, False)], 31, pool=True,
+                            tail=[(24, False), (300, True)], dsteps2=30)
+    assert tier.stats["wb_taken"] > 0 and tier.stats.get("prefill_evicts", 0) > 0
 
 
 def test_plugin_caller_sequence_config0_shapes():
