@@ -241,13 +241,14 @@ int exl3_dequant(const uint32_t* trellis, int k_tiles, int n_tiles, int K, uint1
 
 /* exl3_supported (exl3_ops.sycl:759-767): 1 when (K, cb) is implemented, else 0 */
 int exl3_linear_supported(int K, int cb);
-/* workspace bytes of exl3_linear_small: n/128 int32 arrival counters (rounded up to 256 bytes) first, then the fp32
- * partial sums over K-slices of 512 rows [ceil(k/512)][M][n] */
+/* workspace bytes of exl3_linear_small: the tagged partial sums over K-slices of 512 rows [ceil(k/512)][M][n], 64-bit
+ * words ((1 << 32) | fp32 bits), rounded up to 256 bytes */
 size_t exl3_linear_workspace(int M, int k, int n);
 /* the small-M path (exl3_gemm_small, exl3_ops.sycl:560-600): M <= 8 rows, x and out dtype EXL3_DT_* with row
  * strides; one launch on `stream` (input Hadamards, dequant-GEMV, and the output Hadamard by the last workgroup of
- * each 128-column block). The workspace's counter bytes must be zero before the first call (e.g. memset once at
- * allocation); every call leaves them zero. Calls that share a workspace must not run concurrently. */
+ * each 128-column block, which polls the other workgroups' tagged partials and clears them). The workspace must be
+ * zero before the first call (e.g. memset once at allocation); every call leaves it zero. Calls that share a
+ * workspace must not run concurrently. */
 int exl3_linear_small(const void* x, int x_dtype, int64_t x_stride, int M, int k, int n, const void* trellis, int K,
                       int cb, const void* suh, int S, const void* svh, const int32_t* shard_of_nb, void* out,
                       int out_dtype, int64_t out_stride, void* workspace, size_t workspace_bytes, void* stream);

@@ -114,9 +114,11 @@ struct LinearArgs {
     const _Float16* svh;                           // [n]
     const int32_t* shard_of_nb;                    // [n/128]
     _Float16* xh;                                  // [S][M][k] (the large-M path's input Hadamards)
-    float* part;                                   // [P][M][n] partial sums over the K-slices
-    int* cnt;                                      // [n/128] arrival counters: zero on entry, left zero
+    uint64_t* part;                                // [P][M][n] tagged partial sums over the K-slices: zero on
+                                                   // entry, left zero
     int P;                                         // K-slices (4 blocks of 128 rows each)
+    int* status;                                   // device status words (a timed-out poll adds 1 to [0])
+    int* const* status_host;                       // the device word holding their host mirror's address (or null)
 };
 hipError_t launch_linear_had_in(const LinearArgs& a, hipStream_t s);
 // the fused small-M linear (M <= kLinMaxRows): input Hadamards, dequant-GEMV and output Hadamard in one launch
@@ -128,16 +130,16 @@ hipError_t launch_linear_had_out(const void* parts, int y_half, int P, int M, in
 hipError_t launch_linear_reconstruct(int K, const uint32_t* tr, int k, int n, int n0, int n1, _Float16* w,
                                      hipStream_t s);
 static inline int linear_kslices(int k) { return (k / 128 + 3) / 4; }
-// small-M workspace: the arrival counters [n/128] int32, then the partial sums [P][M][n] fp32
-static inline size_t linear_counter_bytes(int n) { return align256((size_t)(n / 128) * 4); }
+// small-M workspace: the tagged partial sums [P][M][n] (64-bit words)
 static inline size_t linear_workspace_bytes(int M, int k, int n) {
-    return linear_counter_bytes(n) + align256((size_t)linear_kslices(k) * M * n * 4);
+    return align256((size_t)linear_kslices(k) * M * n * 8);
 }
 
 // decode.hip
 hipError_t launch_moe_layer(int K, const DecodeArgs& a, hipStream_t s);
 int read_status(int* out, hipStream_t s);
 hipError_t status_address(void** p);
+hipError_t status_host_slot(void** p);           // device address of the word holding the host mirror's address
 hipError_t set_status_mirror(int* host_word);
 hipError_t launch_dequant(int K, const uint32_t* tr, _Float16* out, int k_tiles, int n_tiles, hipStream_t s);
 // cache.hip

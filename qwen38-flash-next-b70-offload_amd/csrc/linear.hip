@@ -3,13 +3,17 @@
 // natural word order (reference: experimental/n111-victim-ring/csrc/exl3_ops.sycl:651-757; HadInKernel /
 // HadOutKernel, exl3_esimd.h:286-343; ReconstructKernel, exl3_esimd.h:869-936).
 //
-// Small M (<= kLinMaxRows), one launch: a workgroup of 4 waves takes 4 consecutive 128-row blocks of one 64-column
-// group; each wave computes the input Hadamards of its own block for every row in registers, then runs the 8 x 4-tile
-// dequant-GEMV (the MoE gate/up wave GEMV on natural-order words), every codebook value decoded once and multiplied
-// into all M rows on the raw codebook integers (sum w x = c1 sum h x + c2 sum x). The 4 waves are summed in LDS into
-// one fp32 partial per K-slice; the last of the 2P workgroups of a 128-column block to arrive (an atomic counter that
-// it resets) sums the P partials in slice order and applies the output Hadamard x svh. Large M: the input-Hadamard
-// kernel, fp16 W slices (lin_reconstruct_kernel) for a library GEMM, then the output kernel on its fp16 product.
+// Small M (<= kLinMaxRows), one launch: a workgroup of 4 waves takes 4 consecutive 128-row blocks (one K-slice) of
+// one 64-column group; each wave computes the input Hadamards of its own block for every row in registers, then runs
+// the 8 x 4-tile dequant-GEMV (the MoE gate/up wave GEMV on natural-order words), every codebook value decoded once
+// and multiplied into all M rows on the raw codebook integers (sum w x = c1 sum h x + c2 sum x). The 4 waves are
+// summed in LDS into one fp32 partial per K-slice. The 2P workgroups of a 128-column block hand their partials to the
+// block's last workgroup in dispatch order as tagged 64-bit words ((1 << 32) | fp32 bits, agent scope); it polls them
+// (all loads of a round in flight together; bounded, a timeout counted in the device status words), sums the P slices
+// in order, applies the output Hadamard x svh and clears the words it read, so the exchange area is zero between
+// calls and needs no counter or epoch. k <= 512 (one slice): one workgroup of 8 waves per 128-column block, no hand-off.
+// Large M: the input-Hadamard kernel, fp16 W slices (lin_reconstruct_kernel) for a library GEMM, then the output
+// kernel on its fp16 product.
 #include <hip/hip_runtime.h>
 
 #include "exl3_common.cuh"
@@ -107,24 +111,29 @@ __global__ void __launch_bounds__(256) lin_had_in_kernel(LinearArgs A) {
         half2_t{(half_t)(v0 * kRsqrt128), (half_t)(v1 * kRsqrt128)};
 }
 
-// s0, s1 = sum over i < n, in index order, of the float pair at p + i * stride (8-byte aligned); agent-scope loads,
-// 16 pairs per round trip
-__device__ __forceinline__ void sum2_agent(const float* p, int n, size_t stride, float& s0, float& s1) {
-    s0 = s1 = 0.f;
-    for (int i = 0; i < n; i += 16) {
-        uint64_t v[16];
-#pragma unroll
-        for (int j = 0; j < 16; ++j)
-            v[j] = i + j < n ? __hip_atomic_load((const uint64_t*)(p + (size_t)(i + j) * stride), __ATOMIC_RELAXED,
-                                                 __HIP_MEMORY_SCOPE_AGENT)
-                             : 0u;
-#pragma unroll
-        for (int j = 0; j < 16; ++j)
-            if (i + j < n) {
-                s0 += __uint_as_float((uint32_t)v[j]);
-                s1 += __uint_as_float((uint32_t)(v[j] >> 32));
-            }
+// tagged hand-off words of the small-M path: (1 << 32) | fp32 bits; zero (cleared) between calls
+__device__ __forceinline__ void lin_st_tag(uint64_t* p, float v) {
+    __hip_atomic_store(p, (1ull << 32) | __float_as_uint(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint64_t lin_ld(const uint64_t* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void lin_clear(uint64_t* p) {
+    __hip_atomic_store(p, (uint64_t)0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+constexpr int kLinSpinMax = 1 << 22;
+// bounded poll bookkeeping: true once the budget is spent (counted in the device status words and their host mirror)
+__device__ __forceinline__ bool lin_spin_out(const LinearArgs& A, int& it) {
+    if (++it > kLinSpinMax) {
+        if (lane_id() == 0 && A.status) {
+            atomicAdd(A.status, 1);
+            int* h = *A.status_host;
+            if (h) __hip_atomic_fetch_add(h, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        }
+        return true;
     }
+    __builtin_amdgcn_s_sleep(1);
+    return false;
 }
 
 // One wave's share: the weights of 128-row block kb x 64-column group cg (loads issued first), the input Hadamards of
@@ -203,13 +212,15 @@ __device__ __forceinline__ void lin_wave(const LinearArgs& A, int kb, int cg, in
 template <int K, int MR>
 __global__ void __launch_bounds__(64 * kLinWaves) lin_small_kernel(LinearArgs A, void* out, int out_dt,
                                                                   int64_t out_stride) {
+    constexpr int RPW = (MR + kLinWaves - 1) / kLinWaves;   // output rows per wave of the owner
     __shared__ half2_t xq[kLinWaves][MR][64];
     __shared__ float ssw[kLinWaves][MR];
     __shared__ float red[kLinWaves][MR][64];
-    __shared__ int last;
+    __shared__ float own[MR][64];
     const int P = A.P;
     const int cg = blockIdx.x / P, ks = blockIdx.x % P, nb = cg >> 1;
     const int wv = threadIdx.x >> 6, l = lane_id();
+    const bool owner = (cg & 1) && ks == P - 1;   // the block's last workgroup in dispatch order
     lin_wave<K, MR>(A, ks * kLinWaves + wv, cg, nb, xq[wv], ssw[wv], red[wv]);
     __syncthreads();
     for (int i = threadIdx.x; i < MR * 64; i += 64 * kLinWaves) {
@@ -221,26 +232,78 @@ __global__ void __launch_bounds__(64 * kLinWaves) lin_small_kernel(LinearArgs A,
             t += red[w][m][c];
             xs += ssw[w][m];
         }
-        st_agent(A.part + ((size_t)ks * A.M + m) * A.n + cg * 64 + c, kC1 * t + kC2 * xs);
+        const float v = kC1 * t + kC2 * xs;
+        if (owner) own[m][c] = v;
+        else lin_st_tag(A.part + ((size_t)ks * A.M + m) * A.n + cg * 64 + c, v);
     }
-    wait_stores();
+    if (!owner) return;
     __syncthreads();
-    if (threadIdx.x == 0) {
-        last = counter_add(A.cnt + nb, 1) == 2 * P - 1;
-        if (last) counter_reset(A.cnt + nb);     // every arrival of this block is in: ready for the next call
-    }
-    __syncthreads();
-    if (!last) return;
-    // the block's output rows: the P partials in slice order, then the output Hadamard x svh (one wave per row)
+    // the block's output rows m = wv + r * 4: lane l sums columns 2l, 2l + 1 of block nb over the P slices in order;
+    // lanes 32.. take slice P - 1 from this workgroup's own partial. Up to 8 slices of all the wave's rows are polled
+    // together (every load issued before any tag is checked).
+    if (wv >= A.M) return;                       // no output row for this wave
     const half2_t sv = *(const half2_t*)(A.svh + nb * 128 + 2 * l);
-    for (int m = wv; m < A.M; m += kLinWaves) {
-        const float* q = A.part + (size_t)m * A.n + nb * 128 + 2 * l;
-        float v0, v1;
-        sum2_agent(q, P, (size_t)A.M * A.n, v0, v1);
-        wave_fwht128(v0, v1);
+    const bool hi = l >= 32;
+    const size_t sstride = (size_t)A.M * A.n;
+    float v0[RPW], v1[RPW];
+#pragma unroll
+    for (int r = 0; r < RPW; ++r) v0[r] = v1[r] = 0.f;
+    for (int s0 = 0; s0 < P; s0 += 8) {
+        const int ns = min(8, P - s0);
+        uint64_t w[RPW][8][2];
+        int it = 0;
+        for (;;) {
+#pragma unroll
+            for (int r = 0; r < RPW; ++r) {
+                const int m = min(wv + r * kLinWaves, A.M - 1);
+                const uint64_t* q = A.part + (size_t)m * A.n + nb * 128 + 2 * l;
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const size_t o = (size_t)min(s0 + j, P - 1) * sstride;
+                    w[r][j][0] = lin_ld(q + o);
+                    w[r][j][1] = lin_ld(q + o + 1);
+                }
+            }
+            bool ok = true;
+#pragma unroll
+            for (int r = 0; r < RPW; ++r)
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const bool need = wv + r * kLinWaves < A.M && j < ns && !(hi && s0 + j == P - 1);
+                    ok &= !need | (((uint32_t)(w[r][j][0] >> 32) == 1u) & ((uint32_t)(w[r][j][1] >> 32) == 1u));
+                }
+            if (__all(ok) || lin_spin_out(A, it)) break;
+        }
+#pragma unroll
+        for (int r = 0; r < RPW; ++r) {
+            const int m = wv + r * kLinWaves;
+            if (m >= A.M) continue;
+            uint64_t* q = A.part + (size_t)m * A.n + nb * 128 + 2 * l;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const int sl = s0 + j;
+                if (j >= ns) continue;
+                if (hi && sl == P - 1) {
+                    v0[r] += own[m][2 * l - 64];
+                    v1[r] += own[m][2 * l - 63];
+                } else {
+                    v0[r] += __uint_as_float((uint32_t)w[r][j][0]);
+                    v1[r] += __uint_as_float((uint32_t)w[r][j][1]);
+                    lin_clear(q + sl * sstride);
+                    lin_clear(q + sl * sstride + 1);
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < RPW; ++r) {
+        const int m = wv + r * kLinWaves;
+        if (m >= A.M) continue;
+        float a0 = v0[r], a1 = v1[r];
+        wave_fwht128(a0, a1);
         const size_t o = (size_t)m * out_stride + nb * 128 + 2 * l;
-        st_act(out, out_dt, o, v0 * kRsqrt128 * (float)sv.x);
-        st_act(out, out_dt, o + 1, v1 * kRsqrt128 * (float)sv.y);
+        st_act(out, out_dt, o, a0 * kRsqrt128 * (float)sv.x);
+        st_act(out, out_dt, o + 1, a1 * kRsqrt128 * (float)sv.y);
     }
 }
 
@@ -334,26 +397,22 @@ hipError_t launch_linear_had_in(const LinearArgs& a, hipStream_t s) {
     return hipGetLastError();
 }
 
+template <int K, int MR>
+static void small_launch(const LinearArgs& a, void* out, int out_dt, int64_t out_stride, hipStream_t s) {
+    if (a.P == 1)
+        hipLaunchKernelGGL((lin_small1_kernel<K, MR>), dim3((unsigned)(a.n / 128)), dim3(64 * kLin1Waves), 0, s, a, out,
+                           out_dt, out_stride);
+    else
+        hipLaunchKernelGGL((lin_small_kernel<K, MR>), dim3((unsigned)((a.n / 64) * a.P)), dim3(64 * kLinWaves), 0, s,
+                           a, out, out_dt, out_stride);
+}
+
 template <int K>
 static hipError_t small_rows(const LinearArgs& a, void* out, int out_dt, int64_t out_stride, hipStream_t s) {
-    if (a.P == 1) {
-        const dim3 grid1((unsigned)(a.n / 128)), block1(64 * kLin1Waves);
-        if (a.M <= 1) hipLaunchKernelGGL((lin_small1_kernel<K, 1>), grid1, block1, 0, s, a, out, out_dt, out_stride);
-        else if (a.M <= 2)
-            hipLaunchKernelGGL((lin_small1_kernel<K, 2>), grid1, block1, 0, s, a, out, out_dt, out_stride);
-        else if (a.M <= 4)
-            hipLaunchKernelGGL((lin_small1_kernel<K, 4>), grid1, block1, 0, s, a, out, out_dt, out_stride);
-        else if (a.M <= kLinMaxRows)
-            hipLaunchKernelGGL((lin_small1_kernel<K, kLinMaxRows>), grid1, block1, 0, s, a, out, out_dt, out_stride);
-        else return hipErrorInvalidValue;
-        return hipGetLastError();
-    }
-    const dim3 grid((unsigned)((a.n / 64) * a.P)), block(64 * kLinWaves);
-    if (a.M <= 1) hipLaunchKernelGGL((lin_small_kernel<K, 1>), grid, block, 0, s, a, out, out_dt, out_stride);
-    else if (a.M <= 2) hipLaunchKernelGGL((lin_small_kernel<K, 2>), grid, block, 0, s, a, out, out_dt, out_stride);
-    else if (a.M <= 4) hipLaunchKernelGGL((lin_small_kernel<K, 4>), grid, block, 0, s, a, out, out_dt, out_stride);
-    else if (a.M <= kLinMaxRows)
-        hipLaunchKernelGGL((lin_small_kernel<K, kLinMaxRows>), grid, block, 0, s, a, out, out_dt, out_stride);
+    if (a.M <= 1) small_launch<K, 1>(a, out, out_dt, out_stride, s);
+    else if (a.M <= 2) small_launch<K, 2>(a, out, out_dt, out_stride, s);
+    else if (a.M <= 4) small_launch<K, 4>(a, out, out_dt, out_stride, s);
+    else if (a.M <= kLinMaxRows) small_launch<K, kLinMaxRows>(a, out, out_dt, out_stride, s);
     else return hipErrorInvalidValue;
     return hipGetLastError();
 }

@@ -874,6 +874,28 @@ size_t exl3_linear_workspace(int M, int k, int n) {
     return linear_workspace_bytes(M, k, n);
 }
 
+// this device's status words and the word holding their host mirror's address, looked up once per device
+static std::mutex g_lin_status_mu;
+static void* g_lin_status[kMaxDevices][2];
+static hipError_t linear_status(int** st, int* const** sh) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> lk(g_lin_status_mu);
+    if (!g_lin_status[dev][0]) {
+        void* a = nullptr;
+        void* b = nullptr;
+        if ((e = status_address(&a)) != hipSuccess) return e;
+        if ((e = status_host_slot(&b)) != hipSuccess) return e;
+        g_lin_status[dev][1] = b;
+        g_lin_status[dev][0] = a;
+    }
+    *st = (int*)g_lin_status[dev][0];
+    *sh = (int* const*)g_lin_status[dev][1];
+    return hipSuccess;
+}
+
 static int linear_dims(const char* what, int M, int k, int n, int S) {
     if (M < 0 || k <= 0 || n <= 0 || S <= 0 || k % 128 || n % 128)
         return fail(EXL3_EINVAL, "%s: M=%d k=%d n=%d S=%d (k, n multiples of 128)", what, M, k, n, S);
@@ -906,10 +928,11 @@ int exl3_linear_small(const void* x, int x_dtype, int64_t x_stride, int M, int k
     a.suh = (const _Float16*)suh;
     a.svh = (const _Float16*)svh;
     a.shard_of_nb = shard_of_nb;
-    a.cnt = (int*)workspace;
-    a.part = (float*)((uint8_t*)workspace + linear_counter_bytes(n));
+    a.part = (uint64_t*)workspace;
     a.P = linear_kslices(k);
-    const hipError_t e = launch_linear_small(K, a, out, out_dtype, out_stride, (hipStream_t)stream);
+    hipError_t e = linear_status(&a.status, &a.status_host);
+    if (e != hipSuccess) return hip_fail(e, "linear_small: status words");
+    e = launch_linear_small(K, a, out, out_dtype, out_stride, (hipStream_t)stream);
     return e == hipSuccess ? EXL3_OK : hip_fail(e, "linear_small launch");
 }
 

@@ -801,6 +801,7 @@ int read_status(int* out, hipStream_t s) {
 
 // device address of the status words on the current device (each device holds its own copy)
 hipError_t status_address(void** p) { return hipGetSymbolAddress(p, HIP_SYMBOL(g_status)); }
+hipError_t status_host_slot(void** p) { return hipGetSymbolAddress(p, HIP_SYMBOL(g_status_host)); }
 
 // the host mirror of the timeout count on the current device (a synchronous copy of the pointer into the symbol)
 hipError_t set_status_mirror(int* host_word) {

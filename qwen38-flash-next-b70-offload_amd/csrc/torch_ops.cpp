@@ -241,7 +241,7 @@ void linear_checks(const at::Tensor& trellis, const at::Tensor& suh, const at::T
                 "exl3xpu_C.linear: shard_of_nb int32 [n / 128]");
 }
 
-// The small-M workspace. Its arrival counters must be zero when a call starts; every call leaves them zero.
+// The small-M workspace. Its tagged partials must be zero when a call starts; every call leaves them zero.
 // Eager calls on one (device, stream) share one buffer, zeroed when it is allocated, and run in stream order. A call
 // made while its stream is being captured into a HIP graph gets a buffer of that capture alone (keyed by the capture
 // id), allocated and zeroed inside the capture: the zero fill (a fill kernel, not a memset node) is then a node of
