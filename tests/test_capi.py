@@ -53,9 +53,10 @@ def test_linear_entry_points_validate_without_a_gpu():
     L = capi.lib()
     assert [L.exl3_linear_supported(k, 2) for k in range(1, 8)] == [0, 1, 1, 1, 1, 1, 0]
     assert L.exl3_linear_supported(3, 1) == 0
-    # int32 counters [n / 128] + fp32 parts [ceil(k / 512), M, n], each 256-byte aligned
-    assert L.exl3_linear_workspace(1, 2048, 4096) == 256 + 4 * 4096 * 4
-    assert L.exl3_linear_workspace(8, 2560, 12288) == 512 + 5 * 8 * 12288 * 4
+    # tagged 64-bit parts [ceil(k / 512), M, n], 256-byte aligned
+    assert L.exl3_linear_workspace(1, 2048, 4096) == 4 * 4096 * 8
+    assert L.exl3_linear_workspace(8, 2560, 12288) == 5 * 8 * 12288 * 8
+    assert L.exl3_linear_workspace(1, 128, 128) == 1024
     assert L.exl3_linear_small(None, 0, 0, 1, 100, 256, None, 3, 2, None, 1, None, None, None, 0, 0, None, 0,
                                None) == 1                       # k not a multiple of 128
     assert L.exl3_linear_small(None, 0, 0, 9, 128, 256, None, 3, 2, None, 1, None, None, None, 0, 0, None, 0,
