@@ -312,6 +312,30 @@ __device__ __forceinline__ float ld_act(const void* x, int dt, size_t i) {
     if (dt == 2) return ((const float*)x)[i];
     return (float)((const half_t*)x)[i];
 }
+// activations i and i + 1 as raw bits (the low 32 for the 16-bit types, all 64 for fp32) from two 32-bit loads that
+// are always issued, at any alignment and without a branch: the aligned word holding element i and, when the pair
+// reaches into it, the next one (else the same word again, so nothing past the pair is read). act2_cvt converts them
+// once they are needed, so that loads issued after these need not wait for them.
+__device__ __forceinline__ uint64_t ld_act2_raw(const void* x, int dt, size_t i) {
+    const uintptr_t a = (uintptr_t)x + i * (dt == 2 ? 4 : 2);
+    const uint32_t* w = (const uint32_t*)(a & ~(uintptr_t)3);
+    const unsigned sh = (unsigned)(a & 3) * 8;
+    const uint32_t* wn = (dt == 2 || sh) ? w + 1 : w;
+    const uint32_t w0 = *w, w1 = *wn;
+    return ((((uint64_t)w1) << 32) | w0) >> sh;
+}
+__device__ __forceinline__ void act2_cvt(uint64_t r, int dt, float& a, float& b) {
+    if (dt == 2) {
+        a = __uint_as_float((uint32_t)r);
+        b = __uint_as_float((uint32_t)(r >> 32));
+    } else if (dt == 1) {
+        a = bf16_to_f32((bf16_bits)(r & 0xffffu));
+        b = bf16_to_f32((bf16_bits)((r >> 16) & 0xffffu));
+    } else {
+        a = (float)__builtin_bit_cast(half_t, (uint16_t)(r & 0xffffu));
+        b = (float)__builtin_bit_cast(half_t, (uint16_t)((r >> 16) & 0xffffu));
+    }
+}
 __device__ __forceinline__ void st_act(void* y, int dt, size_t i, float v) {
     if (dt == 1) ((bf16_bits*)y)[i] = f32_to_bf16(v);
     else if (dt == 2) ((float*)y)[i] = v;

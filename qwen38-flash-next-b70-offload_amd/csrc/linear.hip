@@ -145,23 +145,33 @@ __device__ __forceinline__ void lin_wave(const LinearArgs& A, int kb, int cg, in
     using GQ = typename LinGemvSel<K, kLinMfma<K, MR>>::type;
     const int kbn = A.k / 128, l = lane_id();
     const bool in_k = kb < kbn;                  // waves past the end of k add nothing
-    // the loads that depend on nothing go first: the weights, the activations and the block's shard index
+    // the loads that depend on nothing go first: the activations (raw bits), every shard's suh row of the block (up
+    // to 4 shards, beside the shard index, so that no load waits for another), then the weights; the Hadamard waits
+    // only for the first two
+    uint64_t xr[MR];
+#pragma unroll
+    for (int m = 0; m < MR; ++m) {
+        xr[m] = 0;
+        if (in_k && m < A.M) {
+            const size_t xo = (size_t)m * A.x_stride + kb * 128 + 2 * l;
+            xr[m] = ld_act2_raw(A.x, A.x_dt, xo);
+        }
+    }
+    const int g = A.shard_of_nb[nb];
+    const size_t so = (size_t)min(kb, kbn - 1) * 128 + 2 * l;
+    uint32_t sus[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) sus[j] = *(const uint32_t*)(A.suh + (size_t)min(j, A.S - 1) * A.k + so);
     GQ gv;
     if (in_k) gv.load_nat(A.tr, A.n / 16, kb * 8, cg * 4);
     float xv[MR][2];
 #pragma unroll
-    for (int m = 0; m < MR; ++m) {
-        xv[m][0] = xv[m][1] = 0.f;
-        if (in_k && m < A.M) {
-            const size_t xo = (size_t)m * A.x_stride + kb * 128 + 2 * l;
-            xv[m][0] = ld_act(A.x, A.x_dt, xo);
-            xv[m][1] = ld_act(A.x, A.x_dt, xo + 1);
-        }
-    }
-    const int g = A.shard_of_nb[nb];
+    for (int m = 0; m < MR; ++m) act2_cvt(xr[m], A.x_dt, xv[m][0], xv[m][1]);
     const bool live = in_k && (unsigned)g < (unsigned)A.S;   // a shard index outside [0, S) leaves its columns zero
-    half2_t su = half2_t{(half_t)0.f, (half_t)0.f};
-    if (live) su = *(const half2_t*)(A.suh + (size_t)g * A.k + kb * 128 + 2 * l);
+    uint32_t suw = 0;
+    if (live) suw = A.S > 4 ? *(const uint32_t*)(A.suh + (size_t)g * A.k + so)
+                            : g == 0 ? sus[0] : g == 1 ? sus[1] : g == 2 ? sus[2] : sus[3];
+    const half2_t su = __builtin_bit_cast(half2_t, suw);
 #pragma unroll
     for (int m = 0; m < MR; ++m) {               // xh = fp16(H(fp16(x su)) / sqrt 128) of this block, and its sum
         float v0 = 0.f, v1 = 0.f;

@@ -335,20 +335,23 @@ __device__ __forceinline__ void gateup_wg(const DecodeArgs& A, int blk, LayerSha
     const int hb = ks * 8 + wv;
     const bool live = hb < nhb;
     const int tiles_n = 2 * I / 16, ct0 = pj * (I / 16) + cg * 4, rt0 = hb * 8;
-    // x and suh of this wave's block first, so that its input Hadamard need not wait for the weight words
-    float xa0 = 0.f, xa1 = 0.f;
-    half_t sa0 = 0, sa1 = 0;
+    // x and suh of this wave's block first, as raw bits (no conversion, so no load waits for another), so that its
+    // input Hadamard need not wait for the weight words
+    uint64_t xr = 0;
+    uint32_t sr = 0;
     if (live) {
         const half_t* suh = (const half_t*)(base + (pj ? A.g.off_suh_u : A.g.off_suh_g));
         const int k0 = hb * 128 + 2 * l;
         const size_t xo = (size_t)m * A.x_stride + k0;
-        xa0 = ld_act(A.x, A.x_dt, xo);
-        xa1 = ld_act(A.x, A.x_dt, xo + 1);
-        sa0 = suh[k0];
-        sa1 = suh[k0 + 1];
+        xr = ld_act2_raw(A.x, A.x_dt, xo);
+        sr = *(const uint32_t*)(suh + k0);       // the blob's vectors are 4-byte aligned, k0 even
     }
     GQ g;
     if (live) g.load((const uint32_t*)base, tiles_n, rt0, ct0);
+    float xa0, xa1;
+    act2_cvt(xr, A.x_dt, xa0, xa1);
+    const half2_t sa = __builtin_bit_cast(half2_t, sr);
+    const half_t sa0 = sa.x, sa1 = sa.y;
     const unsigned tag = wv == 0 ? call_tag() : 0u;
     float ssum = 0.f;
     if (live) {                                  // input Hadamard of x * suh over this wave's block
