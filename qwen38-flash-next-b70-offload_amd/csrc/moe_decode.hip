@@ -529,19 +529,20 @@ __device__ __forceinline__ void down_wg(const DecodeArgs& A, int blk, LayerShare
             for (int k0 = 0; k0 < ksn; k0 += 2) {        // the K-slices in order, two at a time
                 uint64_t v[2][4];
                 int it = 0;
-                for (;;) {
-                    bool ok = true;
+                for (;;) {                   // all eight loads in flight (no branch), then the tag checks
 #pragma unroll
                     for (int k = 0; k < 2; ++k) {
-                        const uint64_t* q = pg + (size_t)(k0 + k) * 2 * I + cI;
-                        const bool in = k0 + k < ksn;
-                        v[k][0] = in ? ld_tag(q) : 0;
-                        v[k][1] = in ? ld_tag(q + 1) : 0;
-                        v[k][2] = in ? ld_tag(q + I) : 0;
-                        v[k][3] = in ? ld_tag(q + I + 1) : 0;
-#pragma unroll
-                        for (int i = 0; i < 4; ++i) ok = ok && (!in || tag_is(v[k][i], tag));
+                        const uint64_t* q = pg + (size_t)min(k0 + k, ksn - 1) * 2 * I + cI;
+                        v[k][0] = ld_tag(q);
+                        v[k][1] = ld_tag(q + 1);
+                        v[k][2] = ld_tag(q + I);
+                        v[k][3] = ld_tag(q + I + 1);
                     }
+                    bool ok = true;
+#pragma unroll
+                    for (int k = 0; k < 2; ++k)
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) ok &= (k0 + k >= ksn) | tag_is(v[k][i], tag);
                     if (__all(ok) || spin_out(it)) break;
                 }
 #pragma unroll
@@ -583,12 +584,17 @@ __device__ __forceinline__ void down_wg(const DecodeArgs& A, int blk, LayerShare
     float xsum = 0.f;
 #pragma unroll
     for (int cp = 0; cp < GV::NCP; ++cp) acc[cp][0] = acc[cp][1] = 0.f;
+    // chunk c is in g0 and chunk c + 1 in g1: compute g0, move g1 into g0 (it has to have arrived by now anyway),
+    // then load chunk c + 2 into g1, so that every load overlaps one chunk's compute (with the buffer picked at run
+    // time instead, the compiler made each prefetch wait for its own loads)
     for (int c = 0; c < nch; ++c) {
         const int r0 = (wv + kWaves * c) * 4;
-        GV& gc = (c & 1) ? g1 : g0;
-        if (trd) gc.write_through(trd, tiles_n, r0, ct0);
-        gc.compute(0, xs + r0 * 8, tacc);
-        if (c + 2 < nch) gc.load(tr, tiles_n, r0 + 8 * kWaves, ct0);
+        if (trd) g0.write_through(trd, tiles_n, r0, ct0);
+        g0.compute(0, xs + r0 * 8, tacc);
+        if (c + 1 < nch) {
+            g0 = g1;
+            if (c + 2 < nch) g1.load(tr, tiles_n, r0 + 8 * kWaves, ct0);
+        }
 #pragma unroll
         for (int cp = 0; cp < GV::NCP; ++cp) {
             acc[cp][0] += tacc[cp][0];
@@ -640,15 +646,17 @@ __device__ __forceinline__ void down_wg(const DecodeArgs& A, int blk, LayerShare
         for (int k0 = 0; k0 < A.topk - 1; k0 += kCombPicks) {
             uint64_t yw[kCombPicks][2];
             int it = 0;
-            for (;;) {
-                bool ok = true;
+            for (;;) {                       // all loads in flight (no branch), then the tag checks
 #pragma unroll
                 for (int j = 0; j < kCombPicks; ++j) {
-                    const bool in = k0 + j < A.topk - 1;
-                    yw[j][0] = in ? ld_tag(yb + (size_t)(k0 + j) * H) : 0;
-                    yw[j][1] = in ? ld_tag(yb + (size_t)(k0 + j) * H + 1) : 0;
-                    ok = ok && (!in || (tag_is(yw[j][0], tag) && tag_is(yw[j][1], tag)));
+                    const uint64_t* q = yb + (size_t)min(k0 + j, A.topk - 2) * H;
+                    yw[j][0] = ld_tag(q);
+                    yw[j][1] = ld_tag(q + 1);
                 }
+                bool ok = true;
+#pragma unroll
+                for (int j = 0; j < kCombPicks; ++j)
+                    ok &= (k0 + j >= A.topk - 1) | (tag_is(yw[j][0], tag) & tag_is(yw[j][1], tag));
                 if (__all(ok) || spin_out(it)) break;
             }
 #pragma unroll
