@@ -158,11 +158,28 @@ def test_prefill_large_expert_shapes(K):
 
 def test_prefill_full_chunk_vs_decode():
     """8,192 tokens x 512 experts (H 2048, I 512, K=3), top-10: the prefill output against the decode kernel run on
-    64-row slices of the same inputs (fp32 activations and outputs: the only difference is the prefill's fp16 y)."""
+    64-row slices of the same inputs (fp32 activations and outputs: the only difference is the prefill's fp16 y), and
+    32 seeded rows of it against the oracle's prefill rounding points (expert_pair, variant "prefill")."""
     H, I, K, E, M, topk = 2048, 512, 3, 512, 8192, 10
     print("case prefill full chunk vs decode", flush=True)
     x, ids, w, blobs, table, keep = _case(H, I, K, E, M, topk, 7300, n_distinct=64)
     pf = _run(x, ids, w, table, I, K, E, fp32=True)
+    rows_o = np.sort(np.random.default_rng(7301).choice(M, size=32, replace=False))
+    ews = {}
+    ref = np.zeros((rows_o.size, H), dtype=np.float32)
+    for i, m in enumerate(rows_o):
+        xf = exl3.bf16_to_f32(x[m])
+        acc = np.zeros(H, dtype=np.float32)
+        for k in range(topk):
+            e = int(ids[m, k])
+            if e % 64 not in ews:
+                ews[e % 64] = exl3.ExpertWeights(blobs[e], H, I, K)
+            acc = (acc + exl3.expert_pair(xf, ews[e % 64], float(w[m, k]), "prefill")).astype(np.float32)
+        ref[i] = acc
+    ro = rel_l2(pf[rows_o], ref)
+    worst = (np.linalg.norm(pf[rows_o] - ref, axis=1) / np.linalg.norm(ref, axis=1)).max()
+    print(f"full chunk: rel-L2 prefill vs oracle on {rows_o.size} rows {ro:.2e}, worst row {worst:.2e}", flush=True)
+    assert ro <= TOL and worst <= 2 * TOL
     xs = torch.from_numpy(exl3.bf16_to_f32(x)).cuda()
     it, wt = torch.from_numpy(ids).cuda(), torch.from_numpy(w).cuda()
     dec = []
