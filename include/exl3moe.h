@@ -239,12 +239,12 @@ int exl3_dequant(const uint32_t* trellis, int k_tiles, int n_tiles, int K, uint1
  * [k/16][n/16][16K] read as little-endian uint32 words, natural order); suh fp16 [S][k], svh fp16 [n]; k, n multiples
  * of 128. Codebook cb = 2 (mul1) with K = 2..6 is implemented, as the reference builds by default. */
 
-/* exl3_supported (exl3_ops.sycl:759-767): 1 when (K, cb) is implemented, else 0 */
+/* exl3_supported (exl3_ops.sycl:767-773): 1 when (K, cb) is implemented, else 0 */
 int exl3_linear_supported(int K, int cb);
 /* workspace bytes of exl3_linear_small: the tagged partial sums over K-slices of 512 rows [ceil(k/512)][M][n], 64-bit
  * words ((1 << 32) | fp32 bits), rounded up to 256 bytes */
 size_t exl3_linear_workspace(int M, int k, int n);
-/* the small-M path (exl3_gemm_small, exl3_ops.sycl:560-600): M <= 8 rows, x and out dtype EXL3_DT_* with row
+/* the small-M path (exl3_gemm_small, exl3_ops.sycl:258-321): M <= 8 rows, x and out dtype EXL3_DT_* with row
  * strides; one launch on `stream` (input Hadamards, dequant-GEMV, and the output Hadamard by the last workgroup of
  * each 128-column block, which polls the other workgroups' tagged partials and clears them). The workspace must be
  * zero before the first call (e.g. memset once at allocation); every call leaves it zero. Calls that share a
