@@ -267,8 +267,8 @@ LINEAR_PREFILL_M = 1024
 
 def run_linear(args, dev):
     """Dense-linear leg: torch.ops.exl3xpu_C.linear over the dense projections of 48 decoder layers (per layer the fused
-    groups 2048 -> 12,288 of 4 shards, 4096 -> 2048, 2048 -> 1024 of 2 shards and 512 -> 2048; EXL3 K=3, seeded random
-    trellis, bs=1 bf16 activations): 192 calls per token captured in one HIP graph and timed with HIP events around its
+    groups 2048 -> 12,288 of 4 shards, 4096 -> 2048, 2048 -> 1024 of 2 shards and 512 -> 2048; EXL3 K=3 mul1 unless
+    --linear-k / --linear-cb say otherwise, seeded random trellis, bs=1 bf16 activations): 192 calls per token captured in one HIP graph and timed with HIP events around its
     replays. value = tokens per second of those calls; roofline = trellis bytes per token / time per token against the
     8 TB/s HBM peak (each call's three kernels included). The same groups at 1,024 rows (the reconstruct + fp16 GEMM
     path) give the prefill figure. cpu_baseline: oracle/cpu_path.CpuLinear (decode through the codebook table on every
@@ -279,13 +279,14 @@ def run_linear(args, dev):
 
     g = torch.Generator(device=dev).manual_seed(SEED + 7)
     sign = lambda n, scale: (torch.where(torch.rand(n, device=dev, generator=g) < 0.5, -1.0, 1.0) * scale).half()
+    Kl, cb = args.linear_k, args.linear_cb
     layers = []
     for _ in range(L):
         grp = []
         for k, widths in LINEAR_GROUPS:
-            shards = [(torch.randint(-32768, 32768, (k // 16, w // 16, 16 * K), dtype=torch.int16, device=dev,
+            shards = [(torch.randint(-32768, 32768, (k // 16, w // 16, 16 * Kl), dtype=torch.int16, device=dev,
                                      generator=g), sign(k, 1.0), sign(w, 0.02)) for w in widths]
-            grp.append(FusedGroup(shards, dev))
+            grp.append(FusedGroup(shards, dev, cb=cb))
         layers.append(grp)
     tr_bytes = sum(fg.trellis.numel() * 2 for fg in layers[0]) * L
     bs = args.bs
@@ -336,12 +337,14 @@ def run_linear(args, dev):
     torch.cuda.synchronize()
     t_pf = ev0.elapsed_time(ev1) / L * 1e-3
     out = {
-        "metric": "dense EXL3 linear decode tok/s bs=1 (48 layers of fused projections, EXL3 3bpw); % of HBM peak",
+        "metric": "dense EXL3 linear decode tok/s bs=1 (48 layers of fused projections, EXL3 %dbpw%s); "
+                  "%% of HBM peak" % (Kl, "" if cb == 2 else ", codebook " + ("3inst", "mcg")[cb]),
         "value": round(1.0 / t_tok, 1), "unit": "tok/s", "n_gpus": 1, "steps": steps, "warmup": warm,
         "ms_per_step": round(t_tok * 1e3, 4), "higher_is_better": True, "dtype": "bf16 in/out, fp32 accumulate",
         "data": "synthetic", "vs_baseline": None,
         "config": {"workload": "dense projections of one decode token through 48 layers: per layer 2048->12288 (4 "
-                               "shards), 4096->2048, 2048->1024 (2 shards), 512->2048; EXL3 K=3; bs=%d" % bs,
+                               "shards), 4096->2048, 2048->1024 (2 shards), 512->2048; EXL3 K=%d, codebook %s; "
+                               "bs=%d" % (Kl, ("3inst", "mcg", "mul1")[cb], bs),
                    "calls_per_token": L * len(LINEAR_GROUPS), "trellis_bytes_per_token": tr_bytes},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK, 4), "traffic": None},
@@ -355,7 +358,7 @@ def run_linear(args, dev):
         from oracle import cpu_path
         n = len(os.sched_getaffinity(0))
         torch.set_num_threads(n)
-        cl = cpu_path.CpuLinear(K)
+        cl = cpu_path.CpuLinear(Kl, cb)
         cpu_groups = [(fg.trellis.cpu(), fg.suh.cpu(), fg.svh.cpu(), fg.bounds) for fg in layers[0]]
         xc = [x.float().cpu() for x in xin]
         t_cpu = _median_s(lambda: [cl(x, *gr) for gr, x in zip(cpu_groups, xc)], CPU_WARM, CPU_REPS)
@@ -553,6 +556,9 @@ def main():
     ap.add_argument("--eager", action="store_true", help="launch the 48 layer calls eagerly instead of a HIP graph")
     ap.add_argument("--prefill", action="store_true", help="the prefill leg (8,192-token chunk, staged) instead of decode")
     ap.add_argument("--linear", action="store_true", help="the dense EXL3 linear leg instead of MoE decode")
+    ap.add_argument("--linear-k", type=int, default=K, help="bits per weight of the linear leg's trellis")
+    ap.add_argument("--linear-cb", type=int, default=2, choices=(0, 1, 2),
+                    help="codebook of the linear leg: 2 mul1, 1 mcg, 0 3inst (the last two at K = 4 or 6)")
     ap.add_argument("--bookkeeping", action="store_true",
                     help="config 1: the cache and tier decisions on 128 x 128 experts over the 4,000-step trace")
     ap.add_argument("--prefill-tiered", action="store_true",

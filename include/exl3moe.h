@@ -235,9 +235,10 @@ int exl3_dequant(const uint32_t* trellis, int k_tiles, int n_tiles, int K, uint1
 /* ---- the dense EXL3 linear (exl3xpu_C.linear, experimental/n111-victim-ring/csrc/exl3_ops.sycl:651-757; the
  * plugin's Exl3XpuLinearMethod.apply, plugin/sglang_plugin.tier.py:380-388) -------------------------------------
  * out[M, n] = svh * H(sum_k xh[g][m][k] W[k][n]) / sqrt 128 with xh[g] = fp16(H(fp16(x * suh[g])) / sqrt 128), g the
- * shard of output block n / 128 (shard_of_nb int32 [n/128]), W the mul1 codebook of the checkpoint trellis (int16
+ * shard of output block n / 128 (shard_of_nb int32 [n/128]), W the codebook values of the checkpoint trellis (int16
  * [k/16][n/16][16K] read as little-endian uint32 words, natural order); suh fp16 [S][k], svh fp16 [n]; k, n multiples
- * of 128. Codebook cb = 2 (mul1) with K = 2..6 is implemented, as the reference builds by default. */
+ * of 128. Codebooks: cb = 2 (mul1) with K = 2..6, and cb = 0 (3inst) and 1 (mcg) with K = 4 and 6 (the reference's
+ * set when built with EXL3_ALL_CODEBOOKS, exl3_esimd.h:69-79). */
 
 /* exl3_supported (exl3_ops.sycl:767-773): 1 when (K, cb) is implemented, else 0 */
 int exl3_linear_supported(int K, int cb);

@@ -93,8 +93,9 @@ class CpuLinear(CpuExperts):
     trellis (natural word order) decoded through the codebook table on every call, then the input Hadamards per shard,
     fp32 matmuls of each shard's columns, and the output Hadamard x svh."""
 
-    def __init__(self, K):
+    def __init__(self, K, cb: int = 2):
         super().__init__(128, 128, K)
+        self.cb = torch.from_numpy(exl3.codebook_table(cb).astype(np.float32))
 
     def __call__(self, x: torch.Tensor, trellis: torch.Tensor, suh: torch.Tensor, svh: torch.Tensor, bounds):
         """x fp32 [M, k]; trellis int16 [k/16, n/16, 16K]; suh fp16 [S, k]; svh fp16 [n]; bounds [0, ..., n]."""

@@ -3,7 +3,8 @@
 TEST INFRASTRUCTURE ONLY (see oracle/__init__.py): the checker, never the product.
 
 Reference files restated here (paths relative to the reference repository root):
-  kernels/moe-a8/exl3_esimd.h            Geo (4-35), decode_cb_h mul1 (40-68), tile_states (120-149),
+  kernels/moe-a8/exl3_esimd.h            Geo (4-35), decode_cb_h mul1 (40-68) and 3inst / mcg (69-79),
+                                         tile_states (120-149),
                                          fwht128 + kRsqrt128 (210-223), ReconstructKernel (869-936)
   kernels/moe-a8/exl3_moe.a8.sycl        blob layout (1-22, 42-54), GateUpKernel (121-260), DownKernel (264-368),
                                          CombineKernel (371-395), GateUpDpasKernel/DownDpasKernel (422-635),
@@ -13,6 +14,11 @@ Reference files restated here (paths relative to the reference repository root):
 Parity pinning (what fixes each function independently of this file; tests/test_oracle_exl3.py):
   codebook_mul1   exhaustive closed form checked against pure-Python integer arithmetic + struct 'e' (IEEE half)
                   rounding, hand-computed known answers, range and h-range invariants, committed table hash.
+  codebook_lcg    (3inst, mcg) exhaustive check against pure-Python integer arithmetic + struct 'e' (IEEE half)
+                  decoding of both halves and an exact-rational sum rounded half-to-even; hand-computed known answers;
+                  the exponent-range invariant of the mask/xor step; a zero mean over the 65,536 states (a wrong
+                  mask gives 0.70). The generator constants themselves rest on the reference's source text only: the
+                  reference holds no vectors for these codebooks (parity of the constants unpinned).
   tile_states     bit-by-bit brute force on random tiles; trellis invariants (low K bits of state t are symbol t,
                   consecutive states overlap by 16-K bits); tail-biting wrap.
   tile_pos        bijection onto the 16x16 tile.
@@ -76,15 +82,34 @@ def codebook_mul1(states: np.ndarray) -> np.ndarray:
     return (h * C1 + C2).astype(np.float16)
 
 
-_CB_TABLE = None
+# codebooks 3inst (id 0) and mcg (id 1): x = state * a + b mod 2^32 (exl3_esimd.h:72-73), then
+# m = (x & 0x8FFF8FFF) ^ 0x3B603B60 and w = RNE_fp16(half(m & 0xFFFF) + half(m >> 16)) (exl3_esimd.h:74-78)
+LCG = {0: (89226354, 64248484), 1: (0xCBAC1FED, 0)}
+LCG_MASK, LCG_XOR = 0x8FFF8FFF, 0x3B603B60
 
 
-def codebook_table() -> np.ndarray:
-    """All 65,536 codebook values, fp16."""
-    global _CB_TABLE
-    if _CB_TABLE is None:
-        _CB_TABLE = codebook_mul1(np.arange(65536, dtype=np.uint32))
-    return _CB_TABLE
+def codebook_lcg(states: np.ndarray, cb: int) -> np.ndarray:
+    """16-bit trellis state -> fp16 weight for codebook 0 (3inst) or 1 (mcg). numpy's float16 add converts both
+    halves to float32, adds (exact: both are normal halves within a factor 16 of each other) and rounds once to
+    float16 (RNE), which is the IEEE half addition."""
+    a, b = LCG[cb]
+    x = (np.asarray(states, dtype=np.uint64) * np.uint64(a) + np.uint64(b)) & np.uint64(0xFFFFFFFF)
+    m = ((x & np.uint64(LCG_MASK)) ^ np.uint64(LCG_XOR)).astype(np.uint32)
+    lo = (m & 0xFFFF).astype(np.uint16).view(np.float16)
+    hi = (m >> 16).astype(np.uint16).view(np.float16)
+    return lo + hi
+
+
+_CB_TABLES: dict = {}
+
+
+def codebook_table(cb: int = 2) -> np.ndarray:
+    """All 65,536 values of codebook cb (2 = mul1, 1 = mcg, 0 = 3inst), fp16."""
+    t = _CB_TABLES.get(cb)
+    if t is None:
+        st = np.arange(65536, dtype=np.uint32)
+        t = _CB_TABLES[cb] = codebook_mul1(st) if cb == 2 else codebook_lcg(st, cb)
+    return t
 
 
 # ------------------------------------------------------------------------------------------------
@@ -120,11 +145,11 @@ def tile_states(words: np.ndarray, K: int) -> np.ndarray:
     return out
 
 
-def decode_tiles(words: np.ndarray, K: int) -> np.ndarray:
-    """words uint32 [..., 8K] -> fp16 tiles [..., 16, 16] (W_inner, row = k, col = n). ReconstructKernel
-    (exl3_esimd.h:869-936) restated: bit-exact dequantization."""
+def decode_tiles(words: np.ndarray, K: int, cb: int = 2) -> np.ndarray:
+    """words uint32 [..., 8K] -> fp16 tiles [..., 16, 16] (W_inner, row = k, col = n) of codebook cb.
+    ReconstructKernel (exl3_esimd.h:869-936) restated: bit-exact dequantization."""
     st = tile_states(words, K)
-    vals = codebook_table()[st]
+    vals = codebook_table(cb)[st]
     row, col = tile_pos(np.arange(256))
     tiles = np.empty(st.shape[:-1] + (16, 16), dtype=np.float16)
     tiles[..., row, col] = vals

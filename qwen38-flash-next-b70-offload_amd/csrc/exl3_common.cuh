@@ -68,6 +68,32 @@ __device__ __forceinline__ half2_t cb_w2(uint32_t s0, uint32_t s1) {
                                      half2_t{(half_t)kC2, (half_t)kC2});
 }
 
+// codebooks 3inst (CB 0) and mcg (CB 1) (exl3_esimd.h:69-79): x = s * a + b mod 2^32, m = (x & 0x8FFF8FFF) ^
+// 0x3B603B60, w = RNE_fp16(half(m & 0xFFFF) + half(m >> 16)). The mask and xor leave both halves normal with
+// magnitude in [1/8, 2), so no subnormal arises in the sum.
+template <int CB>
+__device__ __forceinline__ uint32_t cb_lcg_m(uint32_t s) {
+    static_assert(CB == 0 || CB == 1, "3inst or mcg");
+    const uint32_t x = CB == 0 ? s * 89226354u + 64248484u : s * 0xCBAC1FEDu;
+    return (x & 0x8FFF8FFFu) ^ 0x3B603B60u;
+}
+// the values of states s0 and s1 (s0 in the low half): v_perm_b32 gathers the two low halves and the two high halves
+// of m into one register each, then one v_pk_add_f16 adds them (RNE)
+template <int CB>
+__device__ __forceinline__ half2_t cb_w2_lcg(uint32_t s0, uint32_t s1) {
+    const uint32_t m0 = cb_lcg_m<CB>(s0), m1 = cb_lcg_m<CB>(s1);
+    const uint32_t lo = __builtin_amdgcn_perm(m1, m0, 0x05040100u);
+    const uint32_t hi = __builtin_amdgcn_perm(m1, m0, 0x07060302u);
+    return __builtin_bit_cast(half2_t, lo) + __builtin_bit_cast(half2_t, hi);
+}
+// the pair a dot product takes for codebook CB: mul1 (CB 2) the raw h (its affine is applied to the dot product by
+// the caller), 3inst / mcg the weights themselves
+template <int CB>
+__device__ __forceinline__ half2_t cb_dot_pair(uint32_t s0, uint32_t s1) {
+    if constexpr (CB == 2) return cb_h2(s0, s1);
+    else return cb_w2_lcg<CB>(s0, s1);
+}
+
 // ---- trellis state extraction -----------------------------------------------------------------------------------------
 // Period-relative stream bits: [-32, 0) = previous period's last word, [32j, 32j+32) = word j of the period.
 // Every 16-bit window lies either inside one word or inside a funnel F_m = stream bits [32m-16, 32m+16) around a word

@@ -18,27 +18,31 @@ __device__ __forceinline__ void accum_period(const Period<K>& P, const half2_t (
 }
 
 // the same for MR activation rows at once: each pair of codebook values is decoded once and multiplied into every row
-template <int K, int NQ, int MR, int u>
+// (codebook CB: mul1 as raw h, 3inst / mcg as the weights, see cb_dot_pair)
+template <int K, int NQ, int MR, int u, int CB = 2>
 __device__ __forceinline__ void accum_period_mr(const Period<K>& P, const half2_t (&xv)[MR][2][NQ],
                                                 float (&acc)[MR][2]) {
     if constexpr (u < Geo<K>::V) {
-        const half2_t h = cb_h2(P.template state<u>(), P.template state<u + 1>());
+        const half2_t h = cb_dot_pair<CB>(P.template state<u>(), P.template state<u + 1>());
 #pragma unroll
         for (int m = 0; m < MR; ++m)
             acc[m][(u >> 2) & 1] = __builtin_amdgcn_fdot2(h, xv[m][(u >> 1) & 1][u >> 3], acc[m][(u >> 2) & 1], false);
-        accum_period_mr<K, NQ, MR, u + 2>(P, xv, acc);
+        accum_period_mr<K, NQ, MR, u + 2, CB>(P, xv, acc);
     }
 }
 
 // bit-exact store of one period's values (row/col of value u depend on the period for K != 3), decoded in pairs as
-// the prefill decoder does, so that the exhaustive dequant checks cover both halves of cb_w2
-template <int K, int u>
+// the prefill decoder does, so that the exhaustive dequant checks cover both halves of cb_w2 (cb_w2_lcg for the
+// 3inst / mcg codebooks, CB 0 / 1)
+template <int K, int u, int CB = 2>
 __device__ __forceinline__ void dequant_store(const Period<K>& P, int p, _Float16* o, size_t n_out) {
     if constexpr (u < Geo<K>::V) {
-        const half2_t w = cb_w2(P.template state<u>(), P.template state<u + 1>());
+        half2_t w;
+        if constexpr (CB == 2) w = cb_w2(P.template state<u>(), P.template state<u + 1>());
+        else w = cb_w2_lcg<CB>(P.template state<u>(), P.template state<u + 1>());
         o[(size_t)val_row<K>(p, u) * n_out + val_col<K>(p, u)] = w.x;
         o[(size_t)val_row<K>(p, u + 1) * n_out + val_col<K>(p, u + 1)] = w.y;
-        dequant_store<K, u + 2>(P, p, o, n_out);
+        dequant_store<K, u + 2, CB>(P, p, o, n_out);
     }
 }
 
@@ -127,8 +131,8 @@ struct Gemv4 {
         }
     }
 
-    // compute() for MR activation rows: xq = [MR][64] half2, row m's 128-row block at xq + 64 m
-    template <int MR>
+    // compute() for MR activation rows: xq = [MR][64] half2, row m's 128-row block at xq + 64 m; codebook CB
+    template <int MR, int CB = 2>
     __device__ __forceinline__ void compute_mr(const half2_t* xq, float (&acc)[MR][NCQ][2]) const {
         const int l = lane_id();
         const int p = l % G, j = l / G;
@@ -151,7 +155,7 @@ struct Gemv4 {
                 t[m][0] = acc[m][ps % NCQ][0];
                 t[m][1] = acc[m][ps % NCQ][1];
             }
-            accum_period_mr<K, NQ, MR, 0>(P, xv, t);
+            accum_period_mr<K, NQ, MR, 0, CB>(P, xv, t);
 #pragma unroll
             for (int m = 0; m < MR; ++m) {
                 acc[m][ps % NCQ][0] = t[m][0];

@@ -121,13 +121,15 @@ struct LinearArgs {
     int* const* status_host;                       // the device word holding their host mirror's address (or null)
 };
 hipError_t launch_linear_had_in(const LinearArgs& a, hipStream_t s);
-// the fused small-M linear (M <= kLinMaxRows): input Hadamards, dequant-GEMV and output Hadamard in one launch
-hipError_t launch_linear_small(int K, const LinearArgs& a, void* out, int out_dt, int64_t out_stride, hipStream_t s);
+// the fused small-M linear (M <= kLinMaxRows): input Hadamards, dequant-GEMV and output Hadamard in one launch;
+// codebook cb: 2 mul1 (K = 2..6), 1 mcg or 0 3inst (K = 4, 6)
+hipError_t launch_linear_small(int K, int cb, const LinearArgs& a, void* out, int out_dt, int64_t out_stride,
+                               hipStream_t s);
 // out = svh * H(sum of P parts) / sqrt 128; parts fp32 (y_half 0) or one fp16 matrix (y_half 1, P 1)
 hipError_t launch_linear_had_out(const void* parts, int y_half, int P, int M, int n, const _Float16* svh, void* out,
                                  int out_dt, int64_t out_stride, hipStream_t s);
 // W[k][n1 - n0] fp16 (the codebook's weights) of tile-columns [n0/16, n1/16) of a natural-order trellis
-hipError_t launch_linear_reconstruct(int K, const uint32_t* tr, int k, int n, int n0, int n1, _Float16* w,
+hipError_t launch_linear_reconstruct(int K, int cb, const uint32_t* tr, int k, int n, int n0, int n1, _Float16* w,
                                      hipStream_t s);
 static inline int linear_kslices(int k) { return (k / 128 + 3) / 4; }
 // small-M workspace: the tagged partial sums [P][M][n] (64-bit words)

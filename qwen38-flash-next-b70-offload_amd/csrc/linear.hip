@@ -1,12 +1,14 @@
 // The dense EXL3 linear on gfx950: out[M, n] = svh * H(sum_k xh[g(n)][m][k] W[k][n]) / sqrt 128, with
-// xh[g] = fp16(H(fp16(x * suh[g])) / sqrt 128) per shard g and W the mul1 codebook of a trellis in the checkpoint's
+// xh[g] = fp16(H(fp16(x * suh[g])) / sqrt 128) per shard g and W the codebook values of a trellis in the checkpoint's
 // natural word order (reference: experimental/n111-victim-ring/csrc/exl3_ops.sycl:651-757; HadInKernel /
-// HadOutKernel, exl3_esimd.h:286-343; ReconstructKernel, exl3_esimd.h:869-936).
+// HadOutKernel, exl3_esimd.h:286-343; ReconstructKernel, exl3_esimd.h:869-936). Codebooks: mul1 at K = 2..6, and
+// 3inst / mcg at K = 4 and 6 (the reference's EXL3_ALL_CODEBOOKS set, exl3_ops.sycl:767-773).
 //
 // Small M (<= kLinMaxRows), one launch: a workgroup of 4 waves takes 4 consecutive 128-row blocks (one K-slice) of
 // one 64-column group; each wave computes the input Hadamards of its own block for every row in registers, then runs
 // the 8 x 4-tile dequant-GEMV (the MoE gate/up wave GEMV on natural-order words), every codebook value decoded once
-// and multiplied into all M rows on the raw codebook integers (sum w x = c1 sum h x + c2 sum x). The 4 waves are
+// and multiplied into all M rows (mul1: on the raw codebook integers, sum w x = c1 sum h x + c2 sum x; 3inst / mcg:
+// on the fp16 weights themselves). The 4 waves are
 // summed in LDS into one fp32 partial per K-slice. The 2P workgroups of a 128-column block hand their partials to the
 // block's last workgroup in dispatch order as tagged 64-bit words ((1 << 32) | fp32 bits, agent scope); it polls them
 // (all loads of a round in flight together; bounded, a timeout counted in the device status words), sums the P slices
@@ -92,7 +94,7 @@ struct GemvMfma {
 // MFMA from 4 rows on (at 1 and 2 rows the VALU multiply-adds cost less than the MFMA path's operand handling:
 // 7.7 / 8.8 us against 8.2 / 8.9 us per call at bs 1 / 2 on the 48-layer dense workload; 10.2 / 13.5 against
 // 10.8 / 15.8 at bs 4 / 8)
-template <int K, int MR> constexpr bool kLinMfma = Geo<K>::V == 32 && Geo<K>::G == 8 && MR >= 4;
+template <int K, int MR, int CB = 2> constexpr bool kLinMfma = CB == 2 && Geo<K>::V == 32 && Geo<K>::G == 8 && MR >= 4;
 template <int K, bool M> struct LinGemvSel { using type = Gemv4<K>; };
 template <int K> struct LinGemvSel<K, true> { using type = GemvMfma<K>; };
 
@@ -139,10 +141,10 @@ __device__ __forceinline__ bool lin_spin_out(const LinearArgs& A, int& it) {
 // One wave's share: the weights of 128-row block kb x 64-column group cg (loads issued first), the input Hadamards of
 // that block for every row into xqw [MR][64] (their sums into sswv [MR]), the dequant-GEMV, and the wave's 64 column
 // sums per row into redw [MR][64]
-template <int K, int MR>
+template <int K, int MR, int CB>
 __device__ __forceinline__ void lin_wave(const LinearArgs& A, int kb, int cg, int nb, half2_t (*xqw)[64], float* sswv,
                                          float (*redw)[64]) {
-    using GQ = typename LinGemvSel<K, kLinMfma<K, MR>>::type;
+    using GQ = typename LinGemvSel<K, kLinMfma<K, MR, CB>>::type;
     const int kbn = A.k / 128, l = lane_id();
     const bool in_k = kb < kbn;                  // waves past the end of k add nothing
     // the loads that depend on nothing go first: the activations (raw bits), every shard's suh row of the block (up
@@ -185,7 +187,7 @@ __device__ __forceinline__ void lin_wave(const LinearArgs& A, int kb, int cg, in
         const float s = wave_sum((float)v.x + (float)v.y);
         if (l == 0) sswv[m] = s;
     }
-    if constexpr (kLinMfma<K, MR>) {
+    if constexpr (kLinMfma<K, MR, CB>) {
         float4_t acc[2][2];
 #pragma unroll
         for (int c = 0; c < 2; ++c)
@@ -205,7 +207,7 @@ __device__ __forceinline__ void lin_wave(const LinearArgs& A, int kb, int cg, in
         for (int m = 0; m < MR; ++m)
 #pragma unroll
             for (int q = 0; q < GQ::NCQ; ++q) acc[m][q][0] = acc[m][q][1] = 0.f;
-        if (live) gv.template compute_mr<MR>(&xqw[0][0], acc);     // the wave's own LDS rows: no barrier
+        if (live) gv.template compute_mr<MR, CB>(&xqw[0][0], acc);     // the wave's own LDS rows: no barrier
 #pragma unroll
         for (int m = 0; m < MR; ++m)
 #pragma unroll
@@ -219,7 +221,14 @@ __device__ __forceinline__ void lin_wave(const LinearArgs& A, int kb, int cg, in
     }
 }
 
-template <int K, int MR>
+// a K-slice's column sum from its 4 blocks' raw sums t and activation sums xs: mul1 applies the codebook affine here
+template <int CB>
+__device__ __forceinline__ float lin_colsum(float t, float xs) {
+    if constexpr (CB == 2) return kC1 * t + kC2 * xs;
+    else return t;
+}
+
+template <int K, int MR, int CB>
 __global__ void __launch_bounds__(64 * kLinWaves) lin_small_kernel(LinearArgs A, void* out, int out_dt,
                                                                   int64_t out_stride) {
     constexpr int RPW = (MR + kLinWaves - 1) / kLinWaves;   // output rows per wave of the owner
@@ -231,7 +240,7 @@ __global__ void __launch_bounds__(64 * kLinWaves) lin_small_kernel(LinearArgs A,
     const int cg = blockIdx.x / P, ks = blockIdx.x % P, nb = cg >> 1;
     const int wv = threadIdx.x >> 6, l = lane_id();
     const bool owner = (cg & 1) && ks == P - 1;   // the block's last workgroup in dispatch order
-    lin_wave<K, MR>(A, ks * kLinWaves + wv, cg, nb, xq[wv], ssw[wv], red[wv]);
+    lin_wave<K, MR, CB>(A, ks * kLinWaves + wv, cg, nb, xq[wv], ssw[wv], red[wv]);
     __syncthreads();
     for (int i = threadIdx.x; i < MR * 64; i += 64 * kLinWaves) {
         const int m = i >> 6, c = i & 63;
@@ -242,7 +251,7 @@ __global__ void __launch_bounds__(64 * kLinWaves) lin_small_kernel(LinearArgs A,
             t += red[w][m][c];
             xs += ssw[w][m];
         }
-        const float v = kC1 * t + kC2 * xs;
+        const float v = lin_colsum<CB>(t, xs);
         if (owner) own[m][c] = v;
         else lin_st_tag(A.part + ((size_t)ks * A.M + m) * A.n + cg * 64 + c, v);
     }
@@ -338,8 +347,9 @@ __global__ void __launch_bounds__(256) lin_had_out_kernel(const TPart* part, int
     st_act(out, out_dt, o + 1, v1 * kRsqrt128 * (float)sv.y);
 }
 
-// one wave per (tile-row, strip of NTW tiles) of tile-columns [t0, t1): W[k][16 (t1 - t0)] fp16, bit-exact
-template <int K>
+// one wave per (tile-row, strip of NTW tiles) of tile-columns [t0, t1): W[k][16 (t1 - t0)] fp16 of codebook CB,
+// bit-exact
+template <int K, int CB>
 __global__ void __launch_bounds__(256) lin_reconstruct_kernel(const uint32_t* __restrict__ tr, int k_tiles,
                                                               int n_tiles, int t0, int t1, half_t* __restrict__ w) {
     using GM = Geo<K>;
@@ -359,14 +369,14 @@ __global__ void __launch_bounds__(256) lin_reconstruct_kernel(const uint32_t* __
     Period<K> P;
     P.set(wd, prev);
     const size_t ld = (size_t)nt * 16;
-    dequant_store<K, 0>(P, p, w + (size_t)r * 16 * ld + (size_t)tl * 16, ld);
+    dequant_store<K, 0, CB>(P, p, w + (size_t)r * 16 * ld + (size_t)tl * 16, ld);
 }
 
 // k <= 512 (one K-slice): a workgroup of 8 waves takes both 64-column groups of a 128-column block (waves 0-3 the
 // first, 4-7 the second, one 128-row block each), sums the slice in LDS and applies the output Hadamard itself: no
 // partials in global memory and no arrival counter. Same sums in the same order as lin_small_kernel with P = 1.
 constexpr int kLin1Waves = 8;
-template <int K, int MR>
+template <int K, int MR, int CB>
 __global__ void __launch_bounds__(64 * kLin1Waves) lin_small1_kernel(LinearArgs A, void* out, int out_dt,
                                                                     int64_t out_stride) {
     __shared__ half2_t xq[kLin1Waves][MR][64];
@@ -375,7 +385,7 @@ __global__ void __launch_bounds__(64 * kLin1Waves) lin_small1_kernel(LinearArgs 
     __shared__ float yb[MR][128];
     const int nb = blockIdx.x;
     const int wv = threadIdx.x >> 6, l = lane_id();
-    lin_wave<K, MR>(A, wv & 3, 2 * nb + (wv >> 2), nb, xq[wv], ssw[wv], red[wv]);
+    lin_wave<K, MR, CB>(A, wv & 3, 2 * nb + (wv >> 2), nb, xq[wv], ssw[wv], red[wv]);
     __syncthreads();
     for (int i = threadIdx.x; i < MR * 128; i += 64 * kLin1Waves) {
         const int m = i >> 7, c = i & 127, w0 = (c >> 6) * 4;
@@ -386,7 +396,7 @@ __global__ void __launch_bounds__(64 * kLin1Waves) lin_small1_kernel(LinearArgs 
             t += red[w0 + w][m][c & 63];
             xs += ssw[w][m];
         }
-        yb[m][c] = 0.f + (kC1 * t + kC2 * xs);
+        yb[m][c] = 0.f + lin_colsum<CB>(t, xs);
     }
     __syncthreads();
     const half2_t sv = *(const half2_t*)(A.svh + nb * 128 + 2 * l);
@@ -407,33 +417,39 @@ hipError_t launch_linear_had_in(const LinearArgs& a, hipStream_t s) {
     return hipGetLastError();
 }
 
-template <int K, int MR>
+template <int K, int MR, int CB>
 static void small_launch(const LinearArgs& a, void* out, int out_dt, int64_t out_stride, hipStream_t s) {
     if (a.P == 1)
-        hipLaunchKernelGGL((lin_small1_kernel<K, MR>), dim3((unsigned)(a.n / 128)), dim3(64 * kLin1Waves), 0, s, a, out,
-                           out_dt, out_stride);
+        hipLaunchKernelGGL((lin_small1_kernel<K, MR, CB>), dim3((unsigned)(a.n / 128)), dim3(64 * kLin1Waves), 0, s, a,
+                           out, out_dt, out_stride);
     else
-        hipLaunchKernelGGL((lin_small_kernel<K, MR>), dim3((unsigned)((a.n / 64) * a.P)), dim3(64 * kLinWaves), 0, s,
-                           a, out, out_dt, out_stride);
+        hipLaunchKernelGGL((lin_small_kernel<K, MR, CB>), dim3((unsigned)((a.n / 64) * a.P)), dim3(64 * kLinWaves), 0,
+                           s, a, out, out_dt, out_stride);
 }
 
-template <int K>
+template <int K, int CB>
 static hipError_t small_rows(const LinearArgs& a, void* out, int out_dt, int64_t out_stride, hipStream_t s) {
-    if (a.M <= 1) small_launch<K, 1>(a, out, out_dt, out_stride, s);
-    else if (a.M <= 2) small_launch<K, 2>(a, out, out_dt, out_stride, s);
-    else if (a.M <= 4) small_launch<K, 4>(a, out, out_dt, out_stride, s);
-    else if (a.M <= kLinMaxRows) small_launch<K, kLinMaxRows>(a, out, out_dt, out_stride, s);
+    if (a.M <= 1) small_launch<K, 1, CB>(a, out, out_dt, out_stride, s);
+    else if (a.M <= 2) small_launch<K, 2, CB>(a, out, out_dt, out_stride, s);
+    else if (a.M <= 4) small_launch<K, 4, CB>(a, out, out_dt, out_stride, s);
+    else if (a.M <= kLinMaxRows) small_launch<K, kLinMaxRows, CB>(a, out, out_dt, out_stride, s);
     else return hipErrorInvalidValue;
     return hipGetLastError();
 }
 
-hipError_t launch_linear_small(int K, const LinearArgs& a, void* out, int out_dt, int64_t out_stride, hipStream_t s) {
-    switch (K) {
-        case 2: return small_rows<2>(a, out, out_dt, out_stride, s);
-        case 3: return small_rows<3>(a, out, out_dt, out_stride, s);
-        case 4: return small_rows<4>(a, out, out_dt, out_stride, s);
-        case 5: return small_rows<5>(a, out, out_dt, out_stride, s);
-        case 6: return small_rows<6>(a, out, out_dt, out_stride, s);
+// (K, codebook) pairs built: mul1 (2) at K = 2..6, 3inst (0) and mcg (1) at K = 4 and 6
+hipError_t launch_linear_small(int K, int cb, const LinearArgs& a, void* out, int out_dt, int64_t out_stride,
+                               hipStream_t s) {
+    switch (cb * 8 + K) {
+        case 16 + 2: return small_rows<2, 2>(a, out, out_dt, out_stride, s);
+        case 16 + 3: return small_rows<3, 2>(a, out, out_dt, out_stride, s);
+        case 16 + 4: return small_rows<4, 2>(a, out, out_dt, out_stride, s);
+        case 16 + 5: return small_rows<5, 2>(a, out, out_dt, out_stride, s);
+        case 16 + 6: return small_rows<6, 2>(a, out, out_dt, out_stride, s);
+        case 8 + 4: return small_rows<4, 1>(a, out, out_dt, out_stride, s);
+        case 8 + 6: return small_rows<6, 1>(a, out, out_dt, out_stride, s);
+        case 4: return small_rows<4, 0>(a, out, out_dt, out_stride, s);
+        case 6: return small_rows<6, 0>(a, out, out_dt, out_stride, s);
         default: return hipErrorInvalidValue;
     }
 }
@@ -451,19 +467,23 @@ hipError_t launch_linear_had_out(const void* parts, int y_half, int P, int M, in
     return hipGetLastError();
 }
 
-hipError_t launch_linear_reconstruct(int K, const uint32_t* tr, int k, int n, int n0, int n1, _Float16* w,
+hipError_t launch_linear_reconstruct(int K, int cb, const uint32_t* tr, int k, int n, int n0, int n1, _Float16* w,
                                      hipStream_t s) {
     const int k_tiles = k / 16, n_tiles = n / 16, t0 = n0 / 16, t1 = n1 / 16;
     auto launch = [&](auto kern, int ntw) {
         const int waves = k_tiles * ((t1 - t0 + ntw - 1) / ntw);
         hipLaunchKernelGGL(kern, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, s, tr, k_tiles, n_tiles, t0, t1, w);
     };
-    switch (K) {
-        case 2: launch(lin_reconstruct_kernel<2>, Geo<2>::NTW); break;
-        case 3: launch(lin_reconstruct_kernel<3>, Geo<3>::NTW); break;
-        case 4: launch(lin_reconstruct_kernel<4>, Geo<4>::NTW); break;
-        case 5: launch(lin_reconstruct_kernel<5>, Geo<5>::NTW); break;
-        case 6: launch(lin_reconstruct_kernel<6>, Geo<6>::NTW); break;
+    switch (cb * 8 + K) {
+        case 16 + 2: launch(lin_reconstruct_kernel<2, 2>, Geo<2>::NTW); break;
+        case 16 + 3: launch(lin_reconstruct_kernel<3, 2>, Geo<3>::NTW); break;
+        case 16 + 4: launch(lin_reconstruct_kernel<4, 2>, Geo<4>::NTW); break;
+        case 16 + 5: launch(lin_reconstruct_kernel<5, 2>, Geo<5>::NTW); break;
+        case 16 + 6: launch(lin_reconstruct_kernel<6, 2>, Geo<6>::NTW); break;
+        case 8 + 4: launch(lin_reconstruct_kernel<4, 1>, Geo<4>::NTW); break;
+        case 8 + 6: launch(lin_reconstruct_kernel<6, 1>, Geo<6>::NTW); break;
+        case 4: launch(lin_reconstruct_kernel<4, 0>, Geo<4>::NTW); break;
+        case 6: launch(lin_reconstruct_kernel<6, 0>, Geo<6>::NTW); break;
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();

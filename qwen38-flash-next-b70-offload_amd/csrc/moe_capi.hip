@@ -867,7 +867,12 @@ int exl3_dequant(const uint32_t* trellis, int k_tiles, int n_tiles, int K, uint1
 
 // ---- the dense EXL3 linear ---------------------------------------------------------------------------------------
 
-int exl3_linear_supported(int K, int cb) { return cb == 2 && K >= 2 && K <= 6 ? 1 : 0; }
+// mul1 at K = 2..6; 3inst and mcg at K = 4 and 6 (the reference's set with EXL3_ALL_CODEBOOKS, exl3_ops.sycl:767-773)
+int exl3_linear_supported(int K, int cb) {
+    if (cb == 2) return K >= 2 && K <= 6 ? 1 : 0;
+    if (cb == 0 || cb == 1) return K == 4 || K == 6 ? 1 : 0;
+    return 0;
+}
 
 size_t exl3_linear_workspace(int M, int k, int n) {
     if (M < 0 || k <= 0 || n <= 0) return 0;
@@ -932,7 +937,7 @@ int exl3_linear_small(const void* x, int x_dtype, int64_t x_stride, int M, int k
     a.P = linear_kslices(k);
     hipError_t e = linear_status(&a.status, &a.status_host);
     if (e != hipSuccess) return hip_fail(e, "linear_small: status words");
-    e = launch_linear_small(K, a, out, out_dtype, out_stride, (hipStream_t)stream);
+    e = launch_linear_small(K, cb, a, out, out_dtype, out_stride, (hipStream_t)stream);
     return e == hipSuccess ? EXL3_OK : hip_fail(e, "linear_small launch");
 }
 
@@ -971,7 +976,7 @@ int exl3_reconstruct(const void* trellis, int k, int n, int n0, int n1, int K, i
     if (k <= 0 || n <= 0 || k % 16 || n % 16 || n0 < 0 || n1 > n || n0 >= n1 || n0 % 16 || n1 % 16)
         return fail(EXL3_EINVAL, "reconstruct: k=%d n=%d columns [%d, %d)", k, n, n0, n1);
     if (!trellis || !w) return fail(EXL3_EINVAL, "reconstruct: null pointer");
-    const hipError_t e = launch_linear_reconstruct(K, (const uint32_t*)trellis, k, n, n0, n1, (_Float16*)w,
+    const hipError_t e = launch_linear_reconstruct(K, cb, (const uint32_t*)trellis, k, n, n0, n1, (_Float16*)w,
                                                    (hipStream_t)stream);
     return e == hipSuccess ? EXL3_OK : hip_fail(e, "reconstruct launch");
 }

@@ -53,6 +53,7 @@ def test_linear_entry_points_validate_without_a_gpu():
     L = capi.lib()
     assert [L.exl3_linear_supported(k, 2) for k in range(1, 8)] == [0, 1, 1, 1, 1, 1, 0]
     assert L.exl3_linear_supported(3, 1) == 0
+    assert [L.exl3_linear_supported(k, cb) for cb in (0, 1) for k in (2, 3, 4, 5, 6)] == [0, 0, 1, 0, 1] * 2
     # tagged 64-bit parts [ceil(k / 512), M, n], 256-byte aligned
     assert L.exl3_linear_workspace(1, 2048, 4096) == 4 * 4096 * 8
     assert L.exl3_linear_workspace(8, 2560, 12288) == 5 * 8 * 12288 * 8

@@ -25,7 +25,7 @@ def _group(ck):
     b = ck["bounds"]
     shards = [(tr[:, b[g] // 16:b[g + 1] // 16].contiguous(), torch.from_numpy(ck["suh"][g]),
                torch.from_numpy(ck["svh"][b[g]:b[g + 1]])) for g in range(len(b) - 1)]
-    return FusedGroup(shards, "cuda")
+    return FusedGroup(shards, "cuda", cb=ck["cb"])
 
 
 def _x(seed, M, k, dtype):
@@ -231,3 +231,55 @@ def test_linear_small_two_graphs_on_one_capture_stream():
         yc = g(xs[2])
         torch.cuda.synchronize()
         assert torch.equal(yc, want_c), rep
+
+
+@pytest.mark.parametrize("K", [4, 6])
+@pytest.mark.parametrize("cb", [0, 1])
+def test_codebooks_3inst_mcg_vs_oracle(K, cb):
+    """The 3inst (0) and mcg (1) codebooks at K = 4 and 6: reconstructed weights bit-exact, the fused path at 1, 3 and
+    8 rows over one K-slice (k = 512) and over four (k = 2048, the tagged hand-off), and the large-M path, against the
+    oracle."""
+    from exl3xpu.linear import C
+    print(f"case codebook cb={cb} K={K}", flush=True)
+    ck = olin.checkpoint(500 + 10 * cb + K, 512, [256, 128, 128], K, cb)
+    ref = olin.weight(ck["trellis"], K, cb).view(np.uint16)
+    tr = torch.from_numpy(ck["trellis"]).cuda()
+    w = torch.empty((512, 512), dtype=torch.float16, device="cuda")
+    C().exl3_reconstruct(tr, w, 0, K, cb)
+    torch.cuda.synchronize()
+    assert np.array_equal(w.cpu().numpy().view(np.uint16), ref)
+    g = _group(ck)
+    for M in (1, 3, 8):
+        xf, x = _x(M + K + cb, M, 512, torch.bfloat16)
+        y = g(x)
+        torch.cuda.synchronize()
+        r = _rel(y.float().cpu().numpy(), _round(olin.linear(xf, ck, "small"), torch.bfloat16))
+        assert r < TOL, (M, r)
+    xf, x = _x(40 + K, 21, 512, torch.float16)
+    y = g(x, slice_n=256)
+    torch.cuda.synchronize()
+    r = _rel(y.float().cpu().numpy(), _round(olin.linear(xf, ck, "large"), torch.float16))
+    assert r < TOL, ("large", r)
+    ck4 = olin.checkpoint(600 + 10 * cb + K, 2048, [512, 256], K, cb)
+    g4 = _group(ck4)
+    xf, x = _x(70 + K, 2, 2048, torch.bfloat16)
+    y = g4(x)
+    torch.cuda.synchronize()
+    r = _rel(y.float().cpu().numpy(), _round(olin.linear(xf, ck4, "small"), torch.bfloat16))
+    assert r < TOL, ("k-slices", r)
+
+
+@pytest.mark.parametrize("cb", [0, 1])
+def test_reconstruct_codebooks_nearly_all_states(cb):
+    """3inst / mcg through the GPU decoder over 4,096 random K=4 tiles (1M values; with this seed every one of the
+    65,536 states occurs): every value equals the oracle's, bit for bit."""
+    from exl3xpu.linear import C
+    K = 4
+    rng = np.random.default_rng(90 + cb)
+    tr = rng.integers(0, 1 << 16, size=(64, 64, 16 * K), dtype=np.uint16).view(np.int16)
+    ref = olin.weight(tr, K, cb).view(np.uint16)
+    w = torch.empty((1024, 1024), dtype=torch.float16, device="cuda")
+    C().exl3_reconstruct(torch.from_numpy(tr).cuda(), w, 0, K, cb)
+    torch.cuda.synchronize()
+    assert np.array_equal(w.cpu().numpy().view(np.uint16), ref)
+    assert len(np.unique(exl3.tile_states(exl3.trellis_words(tr), K))) == 65536

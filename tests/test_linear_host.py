@@ -24,6 +24,14 @@ def test_fused_group_packs_like_the_oracle_checkpoint():
     assert g.shard_of_nb.tolist() == [0, 0, 1, 2, 2, 2]
 
 
+def test_fused_group_codebook_id():
+    from exl3xpu.linear import FusedGroup
+    sh = _shards(olin.checkpoint(6, 256, [128], 4))
+    assert FusedGroup(sh, "cpu", cb=1).cb == 1 and FusedGroup(sh, "cpu", cb=0).cb == 0
+    with pytest.raises(ValueError):
+        FusedGroup(sh, "cpu", cb=3)
+
+
 def test_fused_group_rejects_mixed_or_unaligned_shards():
     from exl3xpu.linear import FusedGroup
     a = _shards(olin.checkpoint(4, 256, [128], 3))[0]
@@ -55,7 +63,9 @@ def test_linear_meta_shape_and_support():
                  [0, 512, 768], 3, 2, 8, 4096)
     assert tuple(y.shape) == (2, 3, 768) and y.dtype == torch.bfloat16
     assert [c.exl3_supported(k, 2) for k in range(1, 8)] == [False, True, True, True, True, True, False]
-    assert not c.exl3_supported(3, 1)
+    for cb in (0, 1):       # 3inst / mcg: K = 4 and 6, as the reference's EXL3_ALL_CODEBOOKS build
+        assert [c.exl3_supported(k, cb) for k in range(1, 8)] == [False, False, False, True, False, True, False]
+    assert not c.exl3_supported(4, 3)
 
 
 @pytest.mark.parametrize("K", [2, 4, 6])

@@ -45,6 +45,42 @@ def test_codebook_known_answers_and_range():
     assert [int(v) for v in exl3.codebook_table().view(np.uint16)[h["probe_states"]]] == h["probe_bits"]
 
 
+@pytest.mark.parametrize("cb", [0, 1])
+def test_codebook_lcg_exhaustive_vs_python_ints(cb):
+    """3inst / mcg, every state: pure-Python integer arithmetic, both halves decoded by the struct module and summed
+    exactly (Python floats hold the sum of two halves exactly), then one IEEE half rounding (struct 'e' packs
+    half-to-even): independent of numpy's float16 arithmetic."""
+    tab = exl3.codebook_table(cb).view(np.uint16)
+    a, b = ((89226354, 64248484), (0xCBAC1FED, 0))[cb]
+    for s in range(65536):
+        x = (s * a + b) & 0xFFFFFFFF
+        m = (x & 0x8FFF8FFF) ^ 0x3B603B60
+        lo = struct.unpack("<e", struct.pack("<H", m & 0xFFFF))[0]
+        hi = struct.unpack("<e", struct.pack("<H", m >> 16))[0]
+        assert tab[s] == _half_bits(lo + hi), (cb, s)
+
+
+def test_codebook_lcg_known_answers_and_invariants():
+    """Hand-computed values, the exponent range the mask / xor step forces on both halves (fields 12..15, so every
+    half is normal with magnitude in [1/8, 2) and every weight in (-4, 4)), and a zero mean over all states."""
+    t3, tm = exl3.codebook_table(0), exl3.codebook_table(1)
+    # 3inst, state 0: x = 64248484 = 0x03D45AA4 -> m = 0x38B431C4: 0.587890625 + 0.18017578125 = 0.76806640625
+    assert t3.view(np.uint16)[0] == 0x3A25 and float(t3[0]) == 0.76806640625
+    # mcg, state 0: m = 0x3B603B60: 0.921875 + 0.921875 = 1.84375; state 1: x = 0xCBAC1FED -> m = 0xB0CC348D:
+    # -0.14990234375 + 0.284423828125 = 0.134521484375
+    assert tm.view(np.uint16)[0] == 0x3F60 and tm.view(np.uint16)[1] == 0x304E
+    st = np.arange(65536, dtype=np.uint64)
+    for cb, tab in ((0, t3), (1, tm)):
+        a, b = exl3.LCG[cb]
+        m = (((st * np.uint64(a) + np.uint64(b)) & np.uint64(0xFFFFFFFF)) & np.uint64(0x8FFF8FFF)) ^ np.uint64(0x3B603B60)
+        for half in (m & np.uint64(0xFFFF), m >> np.uint64(16)):
+            e = (half >> np.uint64(10)) & np.uint64(0x1F)
+            assert e.min() == 12 and e.max() == 15
+        w = tab.astype(np.float64)
+        assert np.isfinite(w).all() and np.abs(w).max() < 4.0
+        assert abs(w.mean()) < 0.01 and 1.2 < w.std() < 1.3
+
+
 def _brute_states(words, K):
     """Bit-by-bit: bit b of the tile stream is bit 31 - b%32 of word b//32 (MSB first); state t = the 16 bits
     ending (exclusive) at (t+1)K, circular."""

@@ -9,7 +9,7 @@ from oracle import exl3, linear, synth
 
 
 def _dense(xf, ck):
-    W = linear.weight(ck["trellis"], ck["K"]).astype(np.float64)
+    W = linear.weight(ck["trellis"], ck["K"], ck["cb"]).astype(np.float64)
     k, n = W.shape
     Hb = np.kron(np.eye(k // 128), hadamard(128)).astype(np.float64)
     Hn = np.kron(np.eye(n // 128), hadamard(128)).astype(np.float64)
@@ -25,9 +25,9 @@ def _rel(a, b):
     return float(np.linalg.norm(np.asarray(a, np.float64) - b) / np.linalg.norm(b))
 
 
-@pytest.mark.parametrize("K", [2, 3, 4, 5, 6])
-def test_linear_vs_dense_float64(K):
-    ck = linear.checkpoint(30 + K, 256, [128, 256, 128], K)        # three shards (q, k, v style)
+@pytest.mark.parametrize("K,cb", [(2, 2), (3, 2), (4, 2), (5, 2), (6, 2), (4, 0), (4, 1), (6, 0), (6, 1)])
+def test_linear_vs_dense_float64(K, cb):
+    ck = linear.checkpoint(30 + K, 256, [128, 256, 128], K, cb)    # three shards (q, k, v style)
     xf = exl3.bf16_to_f32(synth.activations(40 + K, 3, 256))
     ref = _dense(xf, ck)
     for variant, tol in (("small", 2e-3), ("large", 3e-3)):
