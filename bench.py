@@ -113,6 +113,7 @@ def cpu_baseline():
 PREFILL_TOKENS = 8192
 PREFILL_WARMUP_CALLS = 30     # untimed prefill layer calls before the 48 timed ones
 MFMA_PEAK_F16 = 2500.0   # TFLOP/s, MI355X dense fp16
+MFMA_PEAK_I8 = 5000.0    # TOP/s, MI355X dense int8
 
 
 def run_prefill(args, dev):
@@ -319,7 +320,10 @@ def run_linear(args, dev):
     t_tok = ev0.elapsed_time(ev1) / steps * 1e-3
     gbs = tr_bytes / t_tok / 1e9
 
-    # the large-M path: one layer's groups at 1,024 rows, eager
+    # the large-M path: one layer's groups at 1,024 rows, eager (the W8A8 route with --linear-int8, K = 4 / 6)
+    from exl3xpu.linear import C as linear_ops
+    q8 = bool(args.linear_int8 and cb == 2 and Kl in (4, 6))
+    linear_ops().exl3_set_int8(1 if q8 else 0)
     Mp = LINEAR_PREFILL_M
     xp = [torch.randn(Mp, k, device=dev, generator=g).to(torch.bfloat16) for k, _ in LINEAR_GROUPS]
     flops = sum(2.0 * Mp * fg.k * fg.n for fg in layers[0])
@@ -336,6 +340,8 @@ def run_linear(args, dev):
     ev1.record()
     torch.cuda.synchronize()
     t_pf = ev0.elapsed_time(ev1) / L * 1e-3
+    linear_ops().exl3_set_int8(0)
+    mm_peak = MFMA_PEAK_I8 if q8 else MFMA_PEAK_F16
     out = {
         "metric": "dense EXL3 linear decode tok/s bs=1 (48 layers of fused projections, EXL3 %dbpw%s); "
                   "%% of HBM peak" % (Kl, "" if cb == 2 else ", codebook " + ("3inst", "mcg")[cb]),
@@ -349,7 +355,8 @@ def run_linear(args, dev):
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK, 4), "traffic": None},
         "prefill_1024_rows": {"ms_per_layer": round(t_pf * 1e3, 4), "tflops": round(flops / t_pf / 1e12, 1),
-                              "frac_fp16_mfma": round(flops / t_pf / 1e12 / MFMA_PEAK_F16, 4)},
+                              "route": "w8a8 int8 GEMM" if q8 else "fp16 GEMM",
+                              ("frac_int8_mfma" if q8 else "frac_fp16_mfma"): round(flops / t_pf / 1e12 / mm_peak, 4)},
     }
     log(f"dense linear: {t_tok * 1e6:.1f} us per token ({t_tok * 1e6 / (L * len(LINEAR_GROUPS)):.2f} us per call), "
         f"{gbs:.0f} GB/s of trellis ({gbs / HBM_PEAK * 100:.1f} % of HBM peak); 1,024 rows: {t_pf * 1e3:.3f} ms per "
@@ -557,6 +564,8 @@ def main():
     ap.add_argument("--prefill", action="store_true", help="the prefill leg (8,192-token chunk, staged) instead of decode")
     ap.add_argument("--linear", action="store_true", help="the dense EXL3 linear leg instead of MoE decode")
     ap.add_argument("--linear-k", type=int, default=K, help="bits per weight of the linear leg's trellis")
+    ap.add_argument("--linear-int8", action="store_true",
+                    help="the linear leg's 1,024-row figure through the W8A8 route (mul1, K = 4 or 6)")
     ap.add_argument("--linear-cb", type=int, default=2, choices=(0, 1, 2),
                     help="codebook of the linear leg: 2 mul1, 1 mcg, 0 3inst (the last two at K = 4 or 6)")
     ap.add_argument("--bookkeeping", action="store_true",

@@ -263,6 +263,22 @@ int exl3_had_out(const void* y, int M, int n, const void* svh, void* out, int ou
  * columns [n0, n1) (multiples of 16) of a natural-order trellis of k x n, bit-exact */
 int exl3_reconstruct(const void* trellis, int k, int n, int n0, int n1, int K, int cb, void* w, void* stream);
 
+/* ---- the W8A8 route of the large-M linear (exl3_ops.sycl:520-537, 668-740: opt-in through exl3_set_int8, mul1 at
+ * K = 4 and 6, more than 16 rows): int8 activations with one scale per (shard, row), int8 weights at the static
+ * scale 127 / 3.453125, an int8 GEMM with int32 sums (the caller's library GEMM), then the output Hadamard. ---- */
+/* HadInQ8Kernel (exl3_esimd.h:341-421): xq int8 [S][ms][k] = rne(xh * inv) and sx fp32 [S][ms] = sc, with xh the
+ * fp16 input Hadamard of exl3_had_in, amax its largest magnitude over the row, sc = amax / 127 (1 for a zero row) and
+ * inv = 1 / sc; ms >= M is the row stride of xq and sx */
+int exl3_had_in_q8(const void* x, int x_dtype, int64_t x_stride, int M, int k, const void* suh, int S, void* xq,
+                   void* sx, int64_t ms, void* stream);
+/* launch_reconstruct_q8 (exl3_ops.sycl:528-537): w int8 [k][n1 - n0] = rne(W * 127 / 3.453125) of the mul1 weights
+ * of columns [n0, n1), K = 2..6 */
+int exl3_reconstruct_q8(const void* trellis, int k, int n, int n0, int n1, int K, void* w, void* stream);
+/* HadOutQ8Kernel (exl3_esimd.h:423-440): out[M, n] = svh * H(y * (sx[m] * sw)) / sqrt 128 for y int32 [M][n] (one
+ * shard group's columns, n a multiple of 128), sx fp32 [M], sw the weight scale (3.453125 / 127) */
+int exl3_had_out_q8(const int32_t* y, int M, int n, const float* sx, float sw, const void* svh, void* out,
+                    int out_dtype, int64_t out_stride, void* stream);
+
 /* ---- RAM-tier admission (host) ---------------------------------------------------------------------------------- */
 
 /* Books of the admission step besides the per-key arrays; the counters accumulate over calls. */

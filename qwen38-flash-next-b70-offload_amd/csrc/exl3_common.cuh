@@ -332,6 +332,14 @@ __device__ __forceinline__ bf16_bits f32_to_bf16(float f) {
     u += 0x7FFFu + ((u >> 16) & 1u);      // round to nearest even (finite inputs)
     return (bf16_bits)(u >> 16);
 }
+// fp16 of an fp32 value rounded as a step of its own. Written as (half_t)(a * b), the product and the conversion fold
+// into one v_fma_mixlo_f16, which rounds the exact product once to fp16; the reference rounds the product to fp32 and
+// then to fp16, and the two disagree where the fp32 product lands on an fp16 tie. The empty asm keeps the fp32 value.
+__device__ __forceinline__ half_t to_half(float v) {
+    asm volatile("" : "+v"(v));
+    return (half_t)v;
+}
+
 // activation dtypes: 0 fp16, 1 bf16, 2 fp32
 __device__ __forceinline__ float ld_act(const void* x, int dt, size_t i) {
     if (dt == 1) return bf16_to_f32(((const bf16_bits*)x)[i]);
@@ -365,7 +373,7 @@ __device__ __forceinline__ void act2_cvt(uint64_t r, int dt, float& a, float& b)
 __device__ __forceinline__ void st_act(void* y, int dt, size_t i, float v) {
     if (dt == 1) ((bf16_bits*)y)[i] = f32_to_bf16(v);
     else if (dt == 2) ((float*)y)[i] = v;
-    else ((half_t*)y)[i] = (half_t)v;
+    else ((half_t*)y)[i] = to_half(v);
 }
 
 // ---- cross-workgroup exchange ------------------------------------------------------------------------------------------

@@ -131,6 +131,13 @@ hipError_t launch_linear_had_out(const void* parts, int y_half, int P, int M, in
 // W[k][n1 - n0] fp16 (the codebook's weights) of tile-columns [n0/16, n1/16) of a natural-order trellis
 hipError_t launch_linear_reconstruct(int K, int cb, const uint32_t* tr, int k, int n, int n0, int n1, _Float16* w,
                                      hipStream_t s);
+// the W8A8 route: xq int8 [S][ms][k] and sx fp32 [S][ms] (row stride ms >= M); int8 mul1 weights of columns
+// [n0, n1); out[:, group] = svh * H(y * sx * sw) / sqrt 128 for y int32 [M][ng] of one shard group
+hipError_t launch_linear_had_in_q8(const LinearArgs& a, int8_t* xq, float* sx, int64_t ms, hipStream_t s);
+hipError_t launch_linear_reconstruct_q8(int K, const uint32_t* tr, int k, int n, int n0, int n1, int8_t* w,
+                                        hipStream_t s);
+hipError_t launch_linear_had_out_q8(const int32_t* y, const float* sx, float sw, int M, int ng, const _Float16* svh,
+                                    void* out, int out_dt, int64_t out_stride, hipStream_t s);
 static inline int linear_kslices(int k) { return (k / 128 + 3) / 4; }
 // small-M workspace: the tagged partial sums [P][M][n] (64-bit words)
 static inline size_t linear_workspace_bytes(int M, int k, int n) {

@@ -18,6 +18,8 @@
 // kernel on its fp16 product.
 #include <hip/hip_runtime.h>
 
+#include <type_traits>
+
 #include "exl3_common.cuh"
 #include "exl3_gemv.cuh"
 #include "exl3_kernels.h"
@@ -106,11 +108,11 @@ __global__ void __launch_bounds__(256) lin_had_in_kernel(LinearArgs A) {
     const int kb = wave % kbn, m = (wave / kbn) % A.M, g = wave / (kbn * A.M);
     const size_t xo = (size_t)m * A.x_stride + kb * 128 + 2 * l;
     const half_t* su = A.suh + (size_t)g * A.k + kb * 128 + 2 * l;
-    float v0 = (float)(half_t)(ld_act(A.x, A.x_dt, xo) * (float)su[0]);
-    float v1 = (float)(half_t)(ld_act(A.x, A.x_dt, xo + 1) * (float)su[1]);
+    float v0 = (float)to_half(ld_act(A.x, A.x_dt, xo) * (float)su[0]);
+    float v1 = (float)to_half(ld_act(A.x, A.x_dt, xo + 1) * (float)su[1]);
     wave_fwht128(v0, v1);
     *(half2_t*)(A.xh + ((size_t)g * A.M + m) * A.k + kb * 128 + 2 * l) =
-        half2_t{(half_t)(v0 * kRsqrt128), (half_t)(v1 * kRsqrt128)};
+        half2_t{to_half(v0 * kRsqrt128), to_half(v1 * kRsqrt128)};
 }
 
 // tagged hand-off words of the small-M path: (1 << 32) | fp32 bits; zero (cleared) between calls
@@ -178,11 +180,11 @@ __device__ __forceinline__ void lin_wave(const LinearArgs& A, int kb, int cg, in
     for (int m = 0; m < MR; ++m) {               // xh = fp16(H(fp16(x su)) / sqrt 128) of this block, and its sum
         float v0 = 0.f, v1 = 0.f;
         if (live && m < A.M) {
-            v0 = (float)(half_t)(xv[m][0] * (float)su.x);
-            v1 = (float)(half_t)(xv[m][1] * (float)su.y);
+            v0 = (float)to_half(xv[m][0] * (float)su.x);
+            v1 = (float)to_half(xv[m][1] * (float)su.y);
         }
         wave_fwht128(v0, v1);
-        const half2_t v = half2_t{(half_t)(v0 * kRsqrt128), (half_t)(v1 * kRsqrt128)};
+        const half2_t v = half2_t{to_half(v0 * kRsqrt128), to_half(v1 * kRsqrt128)};
         xqw[m][l] = v;
         const float s = wave_sum((float)v.x + (float)v.y);
         if (l == 0) sswv[m] = s;
@@ -347,11 +349,120 @@ __global__ void __launch_bounds__(256) lin_had_out_kernel(const TPart* part, int
     st_act(out, out_dt, o + 1, v1 * kRsqrt128 * (float)sv.y);
 }
 
-// one wave per (tile-row, strip of NTW tiles) of tile-columns [t0, t1): W[k][16 (t1 - t0)] fp16 of codebook CB,
-// bit-exact
-template <int K, int CB>
+// ---- the W8A8 route of the large-M linear (exl3_ops.sycl:520-537, 668-740; opt-in): every mul1 codebook value lies
+// in [-3.453125, 3.453125], so one static int8 scale serves all weights; the activations get one scale per (shard,
+// row), the GEMM runs on int8 with int32 sums ------------------------------------------------------------------------
+
+constexpr float kQ8WMax = 3.453125f;             // the largest |mul1 codebook value| (exl3_ops.sycl:526)
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, lane_xor(v, m));
+    return v;
+}
+
+// xq[g][m][:] = int8(rne(xh * inv)) and sx[g][m] = sc, with xh the fp16 path's input Hadamard of row m for shard g,
+// amax its largest magnitude, sc = amax / 127 (1 for an all-zero row) and inv = 1 / sc (HadInQ8Kernel and
+// HadInQ8WgKernel, exl3_esimd.h:341-421). One workgroup of 8 waves per (g, m), wave w taking blocks w, w + 8, ...:
+// with NB > 0 each wave keeps its (at most NB) blocks in registers between the row maximum and the quantization;
+// NB = 0 (rows of more than 16,384) recomputes each block for the second pass.
+constexpr int kQ8Waves = 8;
+template <int NB>
+__global__ void __launch_bounds__(64 * kQ8Waves) lin_had_in_q8_kernel(LinearArgs A, int8_t* __restrict__ xq,
+                                                                      float* __restrict__ sx, int64_t ms) {
+    __shared__ float wmax[kQ8Waves];
+    const int m = blockIdx.x % A.M, g = blockIdx.x / A.M;
+    const int wv = threadIdx.x >> 6, l = lane_id(), kbn = A.k / 128;
+    const half_t* su = A.suh + (size_t)g * A.k + 2 * l;
+    auto block = [&](int kb, float& v0, float& v1) {    // the fp16 path's xh of block kb (whole wave)
+        const size_t xo = (size_t)m * A.x_stride + kb * 128 + 2 * l;
+        v0 = (float)to_half(ld_act(A.x, A.x_dt, xo) * (float)su[kb * 128]);
+        v1 = (float)to_half(ld_act(A.x, A.x_dt, xo + 1) * (float)su[kb * 128 + 1]);
+        wave_fwht128(v0, v1);
+        v0 = (float)to_half(v0 * kRsqrt128);
+        v1 = (float)to_half(v1 * kRsqrt128);
+    };
+    constexpr int NR = NB > 0 ? NB : 1;
+    float v[NR][2];
+    float mx = 0.f;
+    if constexpr (NB > 0) {
+#pragma unroll
+        for (int j = 0; j < NB; ++j) {           // kb depends on the wave only: whole waves stay together
+            const int kb = wv + kQ8Waves * j;
+            v[j][0] = v[j][1] = 0.f;
+            if (kb < kbn) block(kb, v[j][0], v[j][1]);
+            mx = fmaxf(mx, fmaxf(fabsf(v[j][0]), fabsf(v[j][1])));
+        }
+    } else {
+        for (int kb = wv; kb < kbn; kb += kQ8Waves) {
+            block(kb, v[0][0], v[0][1]);
+            mx = fmaxf(mx, fmaxf(fabsf(v[0][0]), fabsf(v[0][1])));
+        }
+    }
+    mx = wave_max(mx);
+    if (l == 0) wmax[wv] = mx;
+    __syncthreads();
+    float amax = wmax[0];
+#pragma unroll
+    for (int w = 1; w < kQ8Waves; ++w) amax = fmaxf(amax, wmax[w]);
+    const float sc = amax > 0.f ? amax / 127.f : 1.f;
+    const float inv = 1.f / sc;
+    if (threadIdx.x == 0) sx[(size_t)g * ms + m] = sc;
+    int8_t* q = xq + ((size_t)g * ms + m) * A.k + 2 * l;
+    auto store = [&](int kb, float v0, float v1) {
+        const int q0 = (int)__builtin_rintf(v0 * inv), q1 = (int)__builtin_rintf(v1 * inv);
+        *(uint16_t*)(q + kb * 128) = (uint16_t)((q0 & 0xFF) | ((q1 & 0xFF) << 8));
+    };
+    if constexpr (NB > 0) {
+#pragma unroll
+        for (int j = 0; j < NB; ++j) {
+            const int kb = wv + kQ8Waves * j;
+            if (kb < kbn) store(kb, v[j][0], v[j][1]);
+        }
+    } else {
+        for (int kb = wv; kb < kbn; kb += kQ8Waves) {
+            block(kb, v[0][0], v[0][1]);
+            store(kb, v[0][0], v[0][1]);
+        }
+    }
+}
+
+// int8 store of one period's mul1 values: w = int8(rne(W * 127 / 3.453125)) (ReconstructKernel with an int8 output,
+// exl3_esimd.h:869-936 and exl3_ops.sycl:528-537)
+template <int K, int u>
+__device__ __forceinline__ void dequant_store_q8(const Period<K>& P, int p, int8_t* o, size_t n_out, float inv) {
+    if constexpr (u < Geo<K>::V) {
+        const half2_t w = cb_w2(P.template state<u>(), P.template state<u + 1>());
+        o[(size_t)val_row<K>(p, u) * n_out + val_col<K>(p, u)] = (int8_t)(int)__builtin_rintf((float)w.x * inv);
+        o[(size_t)val_row<K>(p, u + 1) * n_out + val_col<K>(p, u + 1)] = (int8_t)(int)__builtin_rintf((float)w.y * inv);
+        dequant_store_q8<K, u + 2>(P, p, o, n_out, inv);
+    }
+}
+
+// out[m, c] = svh[c] * H(y[m, :] * (sx[m] * sw)) / sqrt 128 over the ng columns of one shard group, y int32 [M][ng]
+// (HadOutQ8Kernel, exl3_esimd.h:423-440): one wave per (row, 128-column block)
+__global__ void __launch_bounds__(256) lin_had_out_q8_kernel(const int32_t* __restrict__ y, const float* __restrict__ sx,
+                                                             float sw, int M, int ng, const half_t* __restrict__ svh,
+                                                             void* out, int out_dt, int64_t out_stride) {
+    const int wave = blockIdx.x * 4 + (threadIdx.x >> 6), l = lane_id();
+    const int nbn = ng / 128;
+    if (wave >= M * nbn) return;                 // whole waves
+    const int nb = wave % nbn, m = wave / nbn;
+    const int32_t* yr = y + (size_t)m * ng + nb * 128 + 2 * l;
+    const float s = sx[m] * sw;
+    float v0 = (float)yr[0] * s, v1 = (float)yr[1] * s;
+    wave_fwht128(v0, v1);
+    const half2_t sv = *(const half2_t*)(svh + nb * 128 + 2 * l);
+    const size_t o = (size_t)m * out_stride + nb * 128 + 2 * l;
+    st_act(out, out_dt, o, v0 * kRsqrt128 * (float)sv.x);
+    st_act(out, out_dt, o + 1, v1 * kRsqrt128 * (float)sv.y);
+}
+
+// one wave per (tile-row, strip of NTW tiles) of tile-columns [t0, t1): W[k][16 (t1 - t0)] of codebook CB, fp16
+// bit-exact (TW = half_t) or, for mul1, int8 at the static scale 127 / 3.453125 (TW = int8_t)
+template <int K, int CB, typename TW>
 __global__ void __launch_bounds__(256) lin_reconstruct_kernel(const uint32_t* __restrict__ tr, int k_tiles,
-                                                              int n_tiles, int t0, int t1, half_t* __restrict__ w) {
+                                                              int n_tiles, int t0, int t1, TW* __restrict__ w) {
     using GM = Geo<K>;
     constexpr int G = GM::G, D = GM::D, NTW = GM::NTW;
     const int nt = t1 - t0, strips = (nt + NTW - 1) / NTW;
@@ -369,7 +480,10 @@ __global__ void __launch_bounds__(256) lin_reconstruct_kernel(const uint32_t* __
     Period<K> P;
     P.set(wd, prev);
     const size_t ld = (size_t)nt * 16;
-    dequant_store<K, 0, CB>(P, p, w + (size_t)r * 16 * ld + (size_t)tl * 16, ld);
+    if constexpr (std::is_same_v<TW, int8_t>)
+        dequant_store_q8<K, 0>(P, p, w + (size_t)r * 16 * ld + (size_t)tl * 16, ld, 127.f / kQ8WMax);
+    else
+        dequant_store<K, 0, CB>(P, p, w + (size_t)r * 16 * ld + (size_t)tl * 16, ld);
 }
 
 // k <= 512 (one K-slice): a workgroup of 8 waves takes both 64-column groups of a 128-column block (waves 0-3 the
@@ -475,17 +589,57 @@ hipError_t launch_linear_reconstruct(int K, int cb, const uint32_t* tr, int k, i
         hipLaunchKernelGGL(kern, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, s, tr, k_tiles, n_tiles, t0, t1, w);
     };
     switch (cb * 8 + K) {
-        case 16 + 2: launch(lin_reconstruct_kernel<2, 2>, Geo<2>::NTW); break;
-        case 16 + 3: launch(lin_reconstruct_kernel<3, 2>, Geo<3>::NTW); break;
-        case 16 + 4: launch(lin_reconstruct_kernel<4, 2>, Geo<4>::NTW); break;
-        case 16 + 5: launch(lin_reconstruct_kernel<5, 2>, Geo<5>::NTW); break;
-        case 16 + 6: launch(lin_reconstruct_kernel<6, 2>, Geo<6>::NTW); break;
-        case 8 + 4: launch(lin_reconstruct_kernel<4, 1>, Geo<4>::NTW); break;
-        case 8 + 6: launch(lin_reconstruct_kernel<6, 1>, Geo<6>::NTW); break;
-        case 4: launch(lin_reconstruct_kernel<4, 0>, Geo<4>::NTW); break;
-        case 6: launch(lin_reconstruct_kernel<6, 0>, Geo<6>::NTW); break;
+        case 16 + 2: launch(lin_reconstruct_kernel<2, 2, half_t>, Geo<2>::NTW); break;
+        case 16 + 3: launch(lin_reconstruct_kernel<3, 2, half_t>, Geo<3>::NTW); break;
+        case 16 + 4: launch(lin_reconstruct_kernel<4, 2, half_t>, Geo<4>::NTW); break;
+        case 16 + 5: launch(lin_reconstruct_kernel<5, 2, half_t>, Geo<5>::NTW); break;
+        case 16 + 6: launch(lin_reconstruct_kernel<6, 2, half_t>, Geo<6>::NTW); break;
+        case 8 + 4: launch(lin_reconstruct_kernel<4, 1, half_t>, Geo<4>::NTW); break;
+        case 8 + 6: launch(lin_reconstruct_kernel<6, 1, half_t>, Geo<6>::NTW); break;
+        case 4: launch(lin_reconstruct_kernel<4, 0, half_t>, Geo<4>::NTW); break;
+        case 6: launch(lin_reconstruct_kernel<6, 0, half_t>, Geo<6>::NTW); break;
         default: return hipErrorInvalidValue;
     }
+    return hipGetLastError();
+}
+
+hipError_t launch_linear_had_in_q8(const LinearArgs& a, int8_t* xq, float* sx, int64_t ms, hipStream_t s) {
+    const int per_wave = (a.k / 128 + kQ8Waves - 1) / kQ8Waves;
+    auto launch = [&](auto kern) {
+        hipLaunchKernelGGL(kern, dim3((unsigned)(a.S * a.M)), dim3(64 * kQ8Waves), 0, s, a, xq, sx, ms);
+    };
+    if (per_wave <= 1) launch(lin_had_in_q8_kernel<1>);
+    else if (per_wave <= 2) launch(lin_had_in_q8_kernel<2>);
+    else if (per_wave <= 4) launch(lin_had_in_q8_kernel<4>);
+    else if (per_wave <= 8) launch(lin_had_in_q8_kernel<8>);
+    else if (per_wave <= 16) launch(lin_had_in_q8_kernel<16>);
+    else launch(lin_had_in_q8_kernel<0>);
+    return hipGetLastError();
+}
+
+hipError_t launch_linear_reconstruct_q8(int K, const uint32_t* tr, int k, int n, int n0, int n1, int8_t* w,
+                                        hipStream_t s) {
+    const int k_tiles = k / 16, n_tiles = n / 16, t0 = n0 / 16, t1 = n1 / 16;
+    auto launch = [&](auto kern, int ntw) {
+        const int waves = k_tiles * ((t1 - t0 + ntw - 1) / ntw);
+        hipLaunchKernelGGL(kern, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, s, tr, k_tiles, n_tiles, t0, t1, w);
+    };
+    switch (K) {
+        case 2: launch(lin_reconstruct_kernel<2, 2, int8_t>, Geo<2>::NTW); break;
+        case 3: launch(lin_reconstruct_kernel<3, 2, int8_t>, Geo<3>::NTW); break;
+        case 4: launch(lin_reconstruct_kernel<4, 2, int8_t>, Geo<4>::NTW); break;
+        case 5: launch(lin_reconstruct_kernel<5, 2, int8_t>, Geo<5>::NTW); break;
+        case 6: launch(lin_reconstruct_kernel<6, 2, int8_t>, Geo<6>::NTW); break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_linear_had_out_q8(const int32_t* y, const float* sx, float sw, int M, int ng, const _Float16* svh,
+                                    void* out, int out_dt, int64_t out_stride, hipStream_t s) {
+    const int waves = M * (ng / 128);
+    hipLaunchKernelGGL(lin_had_out_q8_kernel, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, s, y, sx, sw, M, ng,
+                       svh, out, out_dt, out_stride);
     return hipGetLastError();
 }
 

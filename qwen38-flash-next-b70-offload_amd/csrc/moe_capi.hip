@@ -981,6 +981,46 @@ int exl3_reconstruct(const void* trellis, int k, int n, int n0, int n1, int K, i
     return e == hipSuccess ? EXL3_OK : hip_fail(e, "reconstruct launch");
 }
 
+int exl3_had_in_q8(const void* x, int x_dtype, int64_t x_stride, int M, int k, const void* suh, int S, void* xq,
+                   void* sx, int64_t ms, void* stream) {
+    if (int r = linear_dims("had_in_q8", M, k, 128, S)) return r;
+    if (x_dtype < EXL3_DT_F16 || x_dtype > EXL3_DT_F32) return fail(EXL3_EINVAL, "had_in_q8: x dtype");
+    if (ms < M) return fail(EXL3_EINVAL, "had_in_q8: row stride %lld < M=%d", (long long)ms, M);
+    if (M == 0) return EXL3_OK;
+    if (!x || !suh || !xq || !sx || x_stride < k) return fail(EXL3_EINVAL, "had_in_q8: bad arguments");
+    LinearArgs a{};
+    a.x = x;
+    a.x_dt = x_dtype;
+    a.x_stride = x_stride;
+    a.M = M;
+    a.k = k;
+    a.S = S;
+    a.suh = (const _Float16*)suh;
+    const hipError_t e = launch_linear_had_in_q8(a, (int8_t*)xq, (float*)sx, ms, (hipStream_t)stream);
+    return e == hipSuccess ? EXL3_OK : hip_fail(e, "had_in_q8 launch");
+}
+
+int exl3_reconstruct_q8(const void* trellis, int k, int n, int n0, int n1, int K, void* w, void* stream) {
+    if (K < 2 || K > 6) return fail(EXL3_EUNSUPPORTED, "reconstruct_q8: K=%d (mul1, K = 2..6)", K);
+    if (k <= 0 || n <= 0 || k % 16 || n % 16 || n0 < 0 || n1 > n || n0 >= n1 || n0 % 16 || n1 % 16)
+        return fail(EXL3_EINVAL, "reconstruct_q8: k=%d n=%d columns [%d, %d)", k, n, n0, n1);
+    if (!trellis || !w) return fail(EXL3_EINVAL, "reconstruct_q8: null pointer");
+    const hipError_t e = launch_linear_reconstruct_q8(K, (const uint32_t*)trellis, k, n, n0, n1, (int8_t*)w,
+                                                      (hipStream_t)stream);
+    return e == hipSuccess ? EXL3_OK : hip_fail(e, "reconstruct_q8 launch");
+}
+
+int exl3_had_out_q8(const int32_t* y, int M, int n, const float* sx, float sw, const void* svh, void* out,
+                    int out_dtype, int64_t out_stride, void* stream) {
+    if (int r = linear_dims("had_out_q8", M, 128, n, 1)) return r;
+    if (out_dtype < EXL3_DT_F16 || out_dtype > EXL3_DT_F32) return fail(EXL3_EINVAL, "had_out_q8: out dtype");
+    if (M == 0) return EXL3_OK;
+    if (!y || !sx || !svh || !out || out_stride < n) return fail(EXL3_EINVAL, "had_out_q8: bad arguments");
+    const hipError_t e = launch_linear_had_out_q8(y, sx, sw, M, n, (const _Float16*)svh, out, out_dtype, out_stride,
+                                                  (hipStream_t)stream);
+    return e == hipSuccess ? EXL3_OK : hip_fail(e, "had_out_q8 launch");
+}
+
 void* exl3_host_alloc(int64_t nbytes) {
     void* p = nullptr;
     if (nbytes <= 0) {

@@ -355,10 +355,10 @@ __device__ __forceinline__ void gateup_wg(const DecodeArgs& A, int blk, LayerSha
     const unsigned tag = wv == 0 ? call_tag() : 0u;
     float ssum = 0.f;
     if (live) {                                  // input Hadamard of x * suh over this wave's block
-        float v0 = (float)(half_t)(xa0 * (float)sa0);
-        float v1 = (float)(half_t)(xa1 * (float)sa1);
+        float v0 = (float)to_half(xa0 * (float)sa0);
+        float v1 = (float)to_half(xa1 * (float)sa1);
         wave_fwht128(v0, v1);
-        const half_t h0 = (half_t)(v0 * kRsqrt128), h1 = (half_t)(v1 * kRsqrt128);
+        const half_t h0 = to_half(v0 * kRsqrt128), h1 = to_half(v1 * kRsqrt128);
         S.u.gu.xq[wv][l] = half2_t{h0, h1};
         ssum = wave_sum((float)h0 + (float)h1);
     }
@@ -561,16 +561,16 @@ __device__ __forceinline__ void down_wg(const DecodeArgs& A, int blk, LayerShare
             }
             wave_fwht128(g0, g1);
             wave_fwht128(u0, u1);
-            g0 = (float)(half_t)(g0 * kRsqrt128 * (float)e_g.x);
-            g1 = (float)(half_t)(g1 * kRsqrt128 * (float)e_g.y);
-            u0 = (float)(half_t)(u0 * kRsqrt128 * (float)e_u.x);
-            u1 = (float)(half_t)(u1 * kRsqrt128 * (float)e_u.y);
-            float a0 = (float)(half_t)silu_mul(g0, u0);
-            float a1 = (float)(half_t)silu_mul(g1, u1);
-            a0 = (float)(half_t)(a0 * (float)e_d.x);
-            a1 = (float)(half_t)(a1 * (float)e_d.y);
+            g0 = (float)to_half(g0 * kRsqrt128 * (float)e_g.x);
+            g1 = (float)to_half(g1 * kRsqrt128 * (float)e_g.y);
+            u0 = (float)to_half(u0 * kRsqrt128 * (float)e_u.x);
+            u1 = (float)to_half(u1 * kRsqrt128 * (float)e_u.y);
+            float a0 = (float)to_half(silu_mul(g0, u0));
+            float a1 = (float)to_half(silu_mul(g1, u1));
+            a0 = (float)to_half(a0 * (float)e_d.x);
+            a1 = (float)to_half(a1 * (float)e_d.y);
             wave_fwht128(a0, a1);
-            xs[b * 64 + l] = half2_t{(half_t)(a0 * kRsqrt128), (half_t)(a1 * kRsqrt128)};
+            xs[b * 64 + l] = half2_t{to_half(a0 * kRsqrt128), to_half(a1 * kRsqrt128)};
         }
     }
     __syncthreads();

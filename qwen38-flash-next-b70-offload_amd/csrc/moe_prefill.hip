@@ -293,7 +293,7 @@ __device__ __forceinline__ void xh_blocks(const PrefillArgs& A, half_t (*tbuf)[3
             ld_act8<DT>(A.x, xrow + k, xv);
             const half8_t sv = *(const half8_t*)(suh + k);
 #pragma unroll
-            for (int j = 0; j < 8; ++j) bx[ks][j] = (half_t)(xv[j] * (float)sv[j]);
+            for (int j = 0; j < 8; ++j) bx[ks][j] = to_half(xv[j] * (float)sv[j]);
         }
 #pragma unroll
         for (int nb = 0; nb < 4; ++nb) {
@@ -307,8 +307,8 @@ __device__ __forceinline__ void xh_blocks(const PrefillArgs& A, half_t (*tbuf)[3
             for (int q = 0; q < 4; ++q) {                        // rows n = 32 nb + 8 q + 4 (l / 32) + 0..3
                 const int n = nb * 32 + q * 8 + (l >> 5) * 4;
                 typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
-                const half4_t hv = half4_t{(half_t)(acc[4 * q] * kRsqrt128), (half_t)(acc[4 * q + 1] * kRsqrt128),
-                                           (half_t)(acc[4 * q + 2] * kRsqrt128), (half_t)(acc[4 * q + 3] * kRsqrt128)};
+                const half4_t hv = half4_t{to_half(acc[4 * q] * kRsqrt128), to_half(acc[4 * q + 1] * kRsqrt128),
+                                           to_half(acc[4 * q + 2] * kRsqrt128), to_half(acc[4 * q + 3] * kRsqrt128)};
                 *(half4_t*)(tb + (l & 31) * kXhRow + n) = hv;
             }
         }
@@ -662,15 +662,15 @@ __global__ void __launch_bounds__(kPfThreads) prefill_gateup_kernel(PrefillArgs 
                 const float rs = row_sign() * kRsqrt128;
 #pragma unroll
                 for (int j = 0; j < 8; ++j) {
-                    const float gj = (float)(half_t)(g[j] * rs * (float)hg[j]);
-                    const float uj = (float)(half_t)(u[j] * rs * (float)hu[j]);
-                    const float aj = (float)(half_t)silu_mul(gj, uj);
-                    av[j] = (float)(half_t)(aj * (float)hd[j]);
+                    const float gj = (float)to_half(g[j] * rs * (float)hg[j]);
+                    const float uj = (float)to_half(u[j] * rs * (float)hu[j]);
+                    const float aj = (float)to_half(silu_mul(gj, uj));
+                    av[j] = (float)to_half(aj * (float)hd[j]);
                 }
                 row_fwht128_signed(av);
                 half8_t o;
 #pragma unroll
-                for (int j = 0; j < 8; ++j) o[j] = (half_t)(av[j] * rs);
+                for (int j = 0; j < 8; ++j) o[j] = to_half(av[j] * rs);
                 if (row < rows) *(half8_t*)(A.abuf + (size_t)(s0 + r0 + row) * I + cb8) = o;
             }
             __syncthreads();
@@ -725,7 +725,7 @@ __global__ void __launch_bounds__(kPfThreads) prefill_down_kernel(PrefillArgs A)
                 const float sc = row_sign() * kRsqrt128 * pw[i];
                 half8_t o;
 #pragma unroll
-                for (int j = 0; j < 8; ++j) o[j] = (half_t)(v[j] * sc * (float)hs[j]);
+                for (int j = 0; j < 8; ++j) o[j] = to_half(v[j] * sc * (float)hs[j]);
                 if (row < rows) *(half8_t*)(A.y + (size_t)(s0 + r0 + row) * H + cb8) = o;
             }
             __syncthreads();

@@ -7,6 +7,7 @@
 #include <torch/library.h>
 
 #include <algorithm>
+#include <atomic>
 #include <map>
 #include <mutex>
 #include <tuple>
@@ -313,6 +314,39 @@ void reconstruct(at::Tensor trellis, at::Tensor w, int64_t n0, int64_t K, int64_
           "exl3xpu_C.exl3_reconstruct");
 }
 
+// the W8A8 route's switch (exl3_set_int8, exl3_ops.sycl:524): off unless the caller turns it on
+std::atomic<bool> g_int8{false};
+void set_int8(int64_t on) { g_int8.store(on != 0); }
+
+// the W8A8 route (exl3_ops.sycl:668-740, the path without oneDNN): int8 xh with one scale per (shard, row), then per
+// shard group the int8 weights at the static scale, the library's int8 GEMM (int32 sums) and the output Hadamard of
+// y * sx * sw into the group's columns of out
+void linear_q8(const at::Tensor& x2, const at::Tensor& trellis, const at::Tensor& suh, const at::Tensor& svh,
+               at::IntArrayRef group_bounds, int64_t K, at::Tensor& out) {
+    const int64_t M = x2.size(0), k = x2.size(1), n = svh.size(0), S = suh.size(0);
+    void* st = cur_stream(x2);
+    auto xq = at::empty({S, M, k}, x2.options().dtype(at::kChar));
+    auto sx = at::empty({S, M}, x2.options().dtype(at::kFloat));
+    check(exl3_had_in_q8(x2.data_ptr(), dtype_code(x2), x2.stride(0), (int)M, (int)k, suh.data_ptr(), (int)S,
+                         xq.data_ptr(), sx.data_ptr(), M, st),
+          "exl3xpu_C.linear (int8 had_in)");
+    const float sw = 3.453125f / 127.0f;
+    for (int64_t g = 0; g < S; ++g) {
+        const int64_t g0 = group_bounds[g], g1 = group_bounds[g + 1], ng = g1 - g0;
+        TORCH_CHECK(g0 <= g1 && g1 <= n && g0 % 128 == 0 && ng % 128 == 0,
+                    "exl3xpu_C.linear: int8 route needs shard groups of whole 128-column blocks");
+        if (ng == 0) continue;
+        auto w = at::empty({k, ng}, x2.options().dtype(at::kChar));
+        check(exl3_reconstruct_q8(trellis.data_ptr(), (int)k, (int)n, (int)g0, (int)g1, (int)K, w.data_ptr(), st),
+              "exl3xpu_C.linear (int8 weights)");
+        auto y = at::_int_mm(xq[g], w);                               // [M, ng] int32
+        auto og = out.narrow(1, g0, ng);
+        check(exl3_had_out_q8(y.data_ptr<int32_t>(), (int)M, (int)ng, sx.data_ptr<float>() + g * M, sw,
+                              svh.narrow(0, g0, ng).data_ptr(), og.data_ptr(), dtype_code(out), out.stride(0), st),
+              "exl3xpu_C.linear (int8 had_out)");
+    }
+}
+
 // exl3_linear (exl3_ops.sycl:651-757): M <= small_m_max (at most 8 rows here) -> the fused path; otherwise the input
 // Hadamards, per shard group the reconstructed fp16 weights in slices of slice_n columns times xh[g] (a library
 // GEMM, fp16 output), then the output Hadamard
@@ -334,6 +368,10 @@ at::Tensor linear(at::Tensor x, at::Tensor trellis, at::Tensor suh, at::Tensor s
     const int64_t S = suh.size(0);
     TORCH_CHECK((int64_t)group_bounds.size() == S + 1 && group_bounds[0] == 0 && group_bounds[S] == n,
                 "exl3xpu_C.linear: group_bounds [0, ..., n] with one group per suh row");
+    if (g_int8.load() && cb == 2 && (K == 4 || K == 6) && M > 16) {     // exl3_ops.sycl:668
+        linear_q8(x2, trellis, suh, svh, group_bounds, K, out);
+        return out.view(shape);
+    }
     auto xh = at::empty({S, M, k}, x.options().dtype(at::kHalf));
     had_in_rm(x2, suh, xh);
     auto y = at::empty({M, n}, x.options().dtype(at::kHalf));
@@ -375,6 +413,7 @@ TORCH_LIBRARY(exl3xpu_C, m) {
           "int K, int cb) -> ()");
     m.impl("exl3_gemm_small", c10::DispatchKey::CUDA, &gemm_small);
     m.def("exl3_supported(int K, int cb) -> bool", &linear_supported);
+    m.def("exl3_set_int8(int on) -> ()", &set_int8);
     m.def("exl3_had_in_rm(Tensor x, Tensor suh, Tensor(a!) xh) -> ()");
     m.impl("exl3_had_in_rm", c10::DispatchKey::CUDA, &had_in_rm);
     m.def("exl3_had_out_h(Tensor y, Tensor svh, Tensor(a!) out) -> ()");

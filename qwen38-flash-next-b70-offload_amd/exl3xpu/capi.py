@@ -73,6 +73,9 @@ SIGNATURES = {
     "exl3_had_in": (c_i32, [c_p, c_i32, c_i64, c_i32, c_i32, c_p, c_i32, c_p, c_p]),
     "exl3_had_out": (c_i32, [c_p, c_i32, c_i32, c_p, c_p, c_i32, c_i64, c_p]),
     "exl3_reconstruct": (c_i32, [c_p, c_i32, c_i32, c_i32, c_i32, c_i32, c_i32, c_p, c_p]),
+    "exl3_had_in_q8": (c_i32, [c_p, c_i32, c_i64, c_i32, c_i32, c_p, c_i32, c_p, c_p, c_i64, c_p]),
+    "exl3_reconstruct_q8": (c_i32, [c_p, c_i32, c_i32, c_i32, c_i32, c_i32, c_p, c_p]),
+    "exl3_had_out_q8": (c_i32, [c_p, c_i32, c_i32, c_p, ctypes.c_float, c_p, c_p, c_i32, c_i64, c_p]),
 }
 
 

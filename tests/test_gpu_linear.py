@@ -283,3 +283,69 @@ def test_reconstruct_codebooks_nearly_all_states(cb):
     torch.cuda.synchronize()
     assert np.array_equal(w.cpu().numpy().view(np.uint16), ref)
     assert len(np.unique(exl3.tile_states(exl3.trellis_words(tr), K))) == 65536
+
+
+@pytest.mark.parametrize("K", [4, 6])
+def test_linear_int8_route_vs_oracle(K):
+    """exl3_set_int8(1): above 16 rows, mul1 at K = 4 / 6 takes the W8A8 route. Its integer parts (xq, the row scales
+    sx, the int8 weights) equal the oracle's bit for bit through the C-ABI; its output matches the oracle's W8A8
+    restatement (rel-L2 2e-3: only the float steps after the exact integer GEMM differ) and the fp16 route within the
+    int8 quantization error. At 16 rows, at K = 3 and with the switch off the fp16 route runs, bit-identical."""
+    from exl3xpu import capi
+    from exl3xpu.linear import C
+    print(f"case int8 route K={K}", flush=True)
+    L = capi.lib()
+    ck = olin.checkpoint(700 + K, 512, [256, 128, 128], K)
+    g = _group(ck)
+    M, S = 40, 3
+    xf, x = _x(80 + K, M, 512, torch.bfloat16)
+    xq = torch.empty((S, M, 512), dtype=torch.int8, device="cuda")
+    sx = torch.empty((S, M), dtype=torch.float32, device="cuda")
+    wq = torch.empty((512, 384), dtype=torch.int8, device="cuda")
+    capi.check(L.exl3_had_in_q8(x.data_ptr(), 1, x.stride(0), M, 512, g.suh.data_ptr(), S, xq.data_ptr(),
+                                sx.data_ptr(), M, capi.stream_handle()), "had_in_q8")
+    capi.check(L.exl3_reconstruct_q8(g.trellis.data_ptr(), 512, 512, 128, 512, K, wq.data_ptr(),
+                                     capi.stream_handle()), "reconstruct_q8")
+    torch.cuda.synchronize()
+    rq, rs = olin.q8_act(xf, ck["suh"])
+    assert np.array_equal(xq.cpu().numpy(), rq)
+    assert np.array_equal(sx.cpu().numpy().view(np.uint32), rs.view(np.uint32))
+    assert np.array_equal(wq.cpu().numpy(), olin.q8_weight(ck["trellis"], K)[:, 128:])
+    y16, y16_16 = g(x), g(x[:16])
+    C().exl3_set_int8(1)
+    try:
+        y8, y8_16 = g(x), g(x[:16])
+        ck3 = olin.checkpoint(710, 512, [256], 3)
+        g3 = _group(ck3)
+        y3_on = g3(x)
+        torch.cuda.synchronize()
+    finally:
+        C().exl3_set_int8(0)
+    y3_off = g3(x)
+    torch.cuda.synchronize()
+    r = _rel(y8.float().cpu().numpy(), _round(olin.linear_q8(xf, ck), torch.bfloat16))
+    assert r < TOL, r
+    r16 = _rel(y8.float().cpu().numpy(), y16.float().cpu().numpy())
+    assert 1e-3 < r16 < 3e-2, r16
+    assert torch.equal(y8_16, y16_16) and torch.equal(y3_on, y3_off)
+
+
+@pytest.mark.parametrize("k", [1024, 4096, 16512])
+def test_had_in_q8_row_lengths_bitexact(k):
+    """The int8 input Hadamard over rows of 8, 32 and 129 blocks (blocks held in registers, 1 and 4 per wave, and
+    the recomputing kernel for rows longer than 16,384): xq and the row scales equal the oracle's bit for bit."""
+    from exl3xpu import capi
+    print(f"case had_in_q8 k={k}", flush=True)
+    L = capi.lib()
+    ck = olin.checkpoint(720, k, [128, 128], 4)
+    g = _group(ck)
+    M, S = 17, 2
+    xf, x = _x(81, M, k, torch.float16)
+    xq = torch.empty((S, M + 3, k), dtype=torch.int8, device="cuda")
+    sx = torch.empty((S, M + 3), dtype=torch.float32, device="cuda")
+    capi.check(L.exl3_had_in_q8(x.data_ptr(), 0, x.stride(0), M, k, g.suh.data_ptr(), S, xq.data_ptr(),
+                                sx.data_ptr(), M + 3, capi.stream_handle()), "had_in_q8")
+    torch.cuda.synchronize()
+    rq, rs = olin.q8_act(xf, ck["suh"])
+    assert np.array_equal(xq[:, :M].cpu().numpy(), rq)
+    assert np.array_equal(sx[:, :M].cpu().numpy().view(np.uint32), rs.view(np.uint32))

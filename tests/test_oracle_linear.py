@@ -55,3 +55,41 @@ def test_weight_natural_order_matches_tile_decode():
     for r, c in ((0, 0), (3, 7), (7, 15)):
         t = exl3.decode_tiles(words[r, c], 3)
         assert np.array_equal(W[16 * r:16 * r + 16, 16 * c:16 * c + 16], t)
+
+
+@pytest.mark.parametrize("K", [4, 6])
+def test_linear_q8_vs_dense_float64(K):
+    """The W8A8 route against the float64 reconstruction: within the int8 quantization error (a wrong or missing
+    scale is off by orders of magnitude), and its integer GEMM equals float64 products of the int8 operands."""
+    ck = linear.checkpoint(60 + K, 512, [256, 128, 128], K)
+    xf = exl3.bf16_to_f32(synth.activations(70 + K, 24, 512))
+    ref = _dense(xf, ck)
+    r8 = _rel(linear.linear_q8(xf, ck), ref)
+    r16 = _rel(linear.linear(xf, ck, "large"), ref)
+    assert r8 < 2e-2 and r16 < 3e-3, (r8, r16)
+    xq, sx = linear.q8_act(xf, ck["suh"])
+    wq = linear.q8_weight(ck["trellis"], K)
+    y = xq[1].astype(np.int64) @ wq[:, 256:384].astype(np.int64)
+    assert np.array_equal(y, np.rint(xq[1].astype(np.float64) @ wq[:, 256:384].astype(np.float64)).astype(np.int64))
+
+
+def test_q8_scale_invariants():
+    """Each row's largest |xq| is 127 and |xh - xq sc| <= sc / 2 (round to nearest); an all-zero row gets scale 1 and
+    zeros; the codebook's largest magnitude (its minimum, -3.453125 at h = 1024) maps to -127 and every weight stays
+    within [-127, 127]."""
+    ck = linear.checkpoint(80, 256, [128, 128], 4)
+    xf = exl3.bf16_to_f32(synth.activations(81, 20, 256))
+    xf[3] = 0.0
+    xq, sx = linear.q8_act(xf, ck["suh"])
+    xh = linear.had_in(xf, ck["suh"]).astype(np.float64)
+    live = np.ones(20, bool)
+    live[3] = False
+    assert (np.abs(xq[:, live].astype(np.int64)).max(axis=2) == 127).all()
+    assert (sx[:, 3] == 1.0).all() and not xq[:, 3].any()
+    err = np.abs(xh - xq.astype(np.float64) * sx[:, :, None].astype(np.float64))
+    assert (err <= sx[:, :, None].astype(np.float64) * (0.5 + 1e-6)).all()
+    cbv = exl3.codebook_table(2).astype(np.float32)
+    q = np.rint(cbv * linear.Q8_WINV)
+    assert cbv.min() == -3.453125 and np.abs(cbv).max() == 3.453125 and q.min() == -127 and q.max() <= 127
+    wq = linear.q8_weight(ck["trellis"], 4)
+    assert np.abs(wq.astype(np.int64)).max() <= 127
