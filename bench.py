@@ -554,6 +554,8 @@ def main():
                     "the HBM cache and the RAM tier start empty and reach their steady state after about 1,000 steps "
                     "of the Zipf trace")
     ap.add_argument("--bs", type=int, default=1)
+    ap.add_argument("--victim-ring", type=int, default=0,
+                    help="write victims back through a ring of this many HBM slots drained by the host (0: off)")
     ap.add_argument("--fixed-arena", action="store_true",
                     help="the RAM tier in one pinned record per expert (30 GB at 48 x 512 experts) instead of the "
                          "record pool (the budget plus the write-back queues)")
@@ -614,7 +616,8 @@ def main():
     for k in keys:
         store.add_layer(k)
     src = nvtier.SyntheticExpertSource(Hm, Im, K, SEED, n_distinct=64)
-    tier = nvtier.NvTierAsync(store, src, budget_records=args.budget_records, latency=8)
+    tier = nvtier.NvTierAsync(store, src, budget_records=args.budget_records, latency=8,
+                              victim_ring=args.victim_ring or None)
     log(f"setup {time.perf_counter() - t0:.1f} s: slots {SLOTS} x {store.blob} B, RAM tier "
         f"{'fixed arena' if args.fixed_arena else 'record pool'} {tier.pinned_bytes() / 2**30:.2f} GiB pinned")
     steps, warm, bs, settle = args.steps, args.warmup, args.bs, max(0, args.settle)
@@ -689,7 +692,7 @@ def main():
     capi.check(capi.lib().exl3_device_status(status, torch.cuda.current_stream().cuda_stream), "device status")
     tok_s = steps * bs / el if steps else 0.0
     d = {k: tier.stats.get(k, 0) - st0.get(k, 0) for k in ("masked", "evicts", "nvme_reads", "admit_dropped", "wait_ms",
-                                                          "wb_taken", "wb_dropped")}
+                                                          "wb_taken", "wb_dropped", "vr_claims", "vr_drops")}
     ram_tier = {"mode": "fixed arena" if args.fixed_arena else "record pool",
                 "pinned_gib": round(tier.pinned_bytes() / 2**30, 3), "record_bytes": store.stride,
                 "budget_records": args.budget_records}
@@ -697,6 +700,9 @@ def main():
         ram_tier.update(records=tier.pool.records, high_water=tier.pool.high, wb_queue=tier.wb_cap,
                         write_backs_per_step=round(d["wb_taken"] / max(steps, 1), 3),
                         write_backs_dropped=int(tier.stats["wb_dropped"]))
+    if tier.vr_K:                        # write-backs through the victim ring instead of the pool's queue
+        ram_tier.update(victim_ring=tier.vr_K, write_backs_per_step=round(d["vr_claims"] / max(steps, 1), 3),
+                        write_backs_dropped=int(tier.stats["vr_drops"]))
     host_ms = {k: round(v / max(steps, 1) * 1e3, 4) for k, v in host_s.items()}
     host_ms["tier_wait"] = round(d.pop("wait_ms") / max(steps, 1), 4)     # of tier_step: waiting for the GPU
     sd = max(steps, 1)

@@ -63,6 +63,16 @@ int exl3_set_victim_addrs(int64_t* vict_addr);
  * victim list and exl3_set_victim_addrs; the fixed-record paths (exl3_moe_prefetch, exl3_moe_prefetch_plan, the
  * copy-engine worker) return EXL3_EUNSUPPORTED while it is set. host_addr == NULL turns it off. */
 int exl3_set_record_pool(int64_t* host_addr, const int64_t* wbq, int32_t* wbq_state, int64_t wbq_cap);
+/* moe_set_victim_ring (experimental/n111-victim-ring/a9.patch:17-30): victims are written back into a ring of K slots
+ * in device memory (buf, at least K x the slot stride bytes) instead of into their RAM records, and the host drains
+ * the ring. meta (device int32 [4 + 2K]): [0] next search position, [1] claims made, [2] write-backs dropped because
+ * no ring slot was free, [3] K, then key[K] (-1 = free, else the key whose bytes the slot holds) and seq[K] (the claim
+ * number of that key); the ensure claims free slots in circular order from [0], in victim order (a9.patch:46-65).
+ * sel (device int32 [E]): the ring slot of victim i of the last call (-1 = none). The device never flags a ring
+ * victim RAM-resident and never frees a slot: the host does both once the slot's copy to RAM has completed. Needs the
+ * victim list and exl3_set_victim_addrs; works with fixed records and with the record pool; the prefetch paths
+ * return EXL3_EUNSUPPORTED while it is set. meta == NULL turns it off. K <= 256. */
+int exl3_set_victim_ring(int32_t* meta, int32_t* sel, void* buf, int64_t buf_bytes, int64_t K);
 /* moe_set_host_stride (a8:765): stride of a key's RAM-tier address, 0 = the slot stride */
 int exl3_set_host_stride(int64_t stride);
 /* Bytes between HBM slots, 0 = the blob size of the call (no reference counterpart: the reference assumes one expert

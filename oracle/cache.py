@@ -59,6 +59,11 @@ def lib():
         L.co_host_step.argtypes = [P, P, P, P, P]
         L.co_run.restype = I64
         L.co_run.argtypes = [P, P, P, I32, I32, I32, P, P, I64]
+        L.co_set_ring.argtypes = [P, I32]
+        for name in ("co_vr_key", "co_vr_seq"):
+            getattr(L, name).restype = P
+            getattr(L, name).argtypes = [P]
+        L.co_vr_stats.argtypes = [P, P]
         _lib = L
     return _lib
 
@@ -75,11 +80,15 @@ class CacheOracle:
     """Device cache + host tier state machine. L layers x E experts, S slots, ring capacity R.
     tier=False: plain device LRU (no mask, no RAM tier, no write-back flags)."""
 
-    def __init__(self, L, E, S, ring_cap=1 << 16, tier=True, budget=1075, age=4, qmax=256, latency=8, safe=0):
+    def __init__(self, L, E, S, ring_cap=1 << 16, tier=True, budget=1075, age=4, qmax=256, latency=8, safe=0,
+                 victim_ring: int = 0):
         self.L, self.E, self.S, self.R, self.tier = L, E, S, ring_cap, tier
         self.qmax = qmax
         self._c = lib().co_new(L, E, S, ring_cap, int(tier), budget, age, qmax, max(1, latency), safe)
         n = L * E
+        self.vr_K = int(victim_ring)
+        if self.vr_K:
+            lib().co_set_ring(self._c, self.vr_K)
 
         def arr(name, cnt, dt):
             p = getattr(lib(), name)(self._c)
@@ -94,6 +103,15 @@ class CacheOracle:
         self.res = arr("co_res", n, np.uint8)
         self.inflight = arr("co_inflight", n, np.uint8)
         self.age = arr("co_age", n, np.int64)
+        if self.vr_K:
+            self.vr_key = arr("co_vr_key", self.vr_K, np.int32)
+            self.vr_seq = arr("co_vr_seq", self.vr_K, np.int32)
+
+    def ring_stats(self) -> dict:
+        """Victim ring: next search position, claims made, write-backs dropped, protocol error flag."""
+        o = np.zeros(4, dtype=np.int64)
+        lib().co_vr_stats(self._c, _ptr(o))
+        return dict(pos=int(o[0]), claims=int(o[1]), drops=int(o[2]), error=int(o[3]))
 
     def __del__(self):
         if getattr(self, "_c", None):

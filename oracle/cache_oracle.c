@@ -22,6 +22,13 @@
  *                                              worker), the protocol the tests follow.
  *   plugin/exl3xpu/nvtier.py:57-87, 179-188    tier init (pinned safe expert per layer, tick = 1)
  *   plugin/exl3xpu/nvtier.py:282-386, 708-806  NvTierAsync one-step-lagged snapshot + _async_step_admit
+ *   experimental/n111-victim-ring/a9.patch:46-65, nvtier.py:655-884
+ *                                              victim ring (co_set_ring): the ensure claims ring slots for written-back
+ *                                              victims serially in victim order (free slot = key < 0, searched
+ *                                              circularly from the next search position; none free: dropped), never
+ *                                              flags them RAM-resident; the host step takes the new claims of the
+ *                                              lagged snapshot into flight and lands them one host step later (RAM-
+ *                                              resident like a completed fill, the slot freed before the next call)
  *
  * Canonical choices where the reference is not deterministic (documented contract):
  *   - misses in ascending expert id; victims = ascending-slot({u < tau}) ++ first `want` of ascending-slot({u == tau});
@@ -57,6 +64,12 @@ typedef struct {
     int64_t stats_masked, stats_evicts, stats_admit_dropped, stats_ring_overflow;
     /* pending copy-engine prefetch plans per layer: count, tick, (expert, slot) x 16 */
     int32_t *pend_n, *pend_T, *pend_e, *pend_s;
+    /* victim ring (vr_K = 0: off): device meta, its snapshots, the host's handled claim numbers, the claims taken
+     * into flight by the last host step (they land at the next one) and the slots to free */
+    int vr_K, vr_p, vr_claims, vr_drops, vr_error;
+    int32_t *vr_key, *vr_seq, *snap_vr[2];
+    int64_t *vr_seen;
+    int32_t *vr_fly_r, *vr_fly_k, vr_n_fly, *vr_free, vr_n_free;
 } co_t;
 
 static void *xcalloc(size_t n, size_t s) { void *p = calloc(n ? n : 1, s); return p; }
@@ -106,7 +119,30 @@ void co_free(co_t *c) {
     free(c->done); free(c->n_done);
     free(c->u_tmp); free(c->i_tmp); free(c->l_tmp); free(c->l_tmp2); free(c->cnt_tmp); free(c->view); free(c->resn);
     free(c->pend_n); free(c->pend_T); free(c->pend_e); free(c->pend_s);
+    if (c->vr_K) {
+        free(c->vr_key); free(c->vr_seq); free(c->snap_vr[0]); free(c->snap_vr[1]); free(c->vr_seen);
+        free(c->vr_fly_r); free(c->vr_fly_k); free(c->vr_free);
+    }
     free(c);
+}
+
+/* turn the victim ring on with K slots (before the first call) */
+void co_set_ring(co_t *c, int K) {
+    c->vr_K = K; c->vr_p = 0; c->vr_claims = 0; c->vr_drops = 0; c->vr_error = 0;
+    c->vr_key = (int32_t *)xcalloc(K, 4); c->vr_seq = (int32_t *)xcalloc(K, 4);
+    for (int r = 0; r < K; ++r) c->vr_key[r] = -1;
+    for (int b = 0; b < 2; ++b) {
+        c->snap_vr[b] = (int32_t *)xcalloc(2 * (size_t)K, 4);
+        for (int r = 0; r < K; ++r) c->snap_vr[b][r] = -1;
+    }
+    c->vr_seen = (int64_t *)xcalloc(K, 8);
+    c->vr_fly_r = (int32_t *)xcalloc(K, 4); c->vr_fly_k = (int32_t *)xcalloc(K, 4); c->vr_n_fly = 0;
+    c->vr_free = (int32_t *)xcalloc(2 * (size_t)K, 4); c->vr_n_free = 0;
+}
+int32_t *co_vr_key(co_t *c) { return c->vr_key; }
+int32_t *co_vr_seq(co_t *c) { return c->vr_seq; }
+void co_vr_stats(co_t *c, int64_t *out) {
+    out[0] = c->vr_p; out[1] = c->vr_claims; out[2] = c->vr_drops; out[3] = c->vr_error;
 }
 
 /* state accessors (ctypes maps them onto numpy arrays) */
@@ -218,8 +254,23 @@ static int ensure_impl(co_t *c, int layer, int32_t *ids, float *w, int P, int ma
             int key = layer * E + e;
             c->slot_key[s] = key; c->slot_of[key] = s; c->slot_last[s] = plan ? 0x7FFFFFFF : T;
             if (plan) { c->pend_e[layer * 16 + mi] = e; c->pend_s[layer * 16 + mi] = s; }
+            if (tier && wb >= 0 && c->vr_K) {                  /* ring claim, a9.patch:50-63 */
+                int r = -1;
+                for (int j = 0; j < c->vr_K; ++j) {
+                    int q = c->vr_p + j;
+                    if (q >= c->vr_K) q -= c->vr_K;
+                    if (c->vr_key[q] < 0) { r = q; break; }
+                }
+                if (r >= 0) {
+                    c->vr_key[r] = wb; c->vr_seq[r] = ++c->vr_claims;
+                    c->vr_p = r + 1 == c->vr_K ? 0 : r + 1;
+                } else {
+                    c->vr_drops += 1;
+                    wb = -1;                                    /* dropped: no write-back */
+                }
+            }
             if (rec) { rec[3 + P + mi] = e; rec[3 + 2 * P + 2 * mi] = wb; rec[3 + 2 * P + 2 * mi + 1] = s; }
-            if (tier && wb >= 0) c->ram_res[wb] = 1;            /* VictimCopyKernel a8:1180 */
+            if (tier && wb >= 0 && !c->vr_K) c->ram_res[wb] = 1;   /* VictimCopyKernel a8:1180 */
         }
         free(V);
     }
@@ -273,6 +324,10 @@ int64_t co_host_step(co_t *c, int32_t *admit_out, int32_t *n_admit, int32_t *evi
     memcpy(c->snap_res[k], c->ram_res, n);
     memcpy(c->snap_ring[k], c->ring, 4 * (size_t)(1 + c->R));
     for (int i = 0; i < n; ++i) c->snap_vram[k][i] = c->slot_of[i] >= 0;
+    if (c->vr_K) {
+        memcpy(c->snap_vr[k], c->vr_key, 4 * (size_t)c->vr_K);
+        memcpy(c->snap_vr[k] + c->vr_K, c->vr_seq, 4 * (size_t)c->vr_K);
+    }
     c->have_snap[k] = 1;
     int j = k ^ 1;
     int64_t hstep = c->hstep++;
@@ -291,6 +346,27 @@ int64_t co_host_step(co_t *c, int32_t *admit_out, int32_t *n_admit, int32_t *evi
         res[kk] = 1; c->age[kk] = c->htick; c->inflight[kk] = 0;
     }
     c->n_done[slot_now] = 0;
+    if (c->vr_K) {
+        /* ring drains taken into flight by the last host step land now (n111 nvtier.py:787-794) */
+        for (int i = 0; i < c->vr_n_fly; ++i) {
+            int kk = c->vr_fly_k[i];
+            res[kk] = 1; c->age[kk] = c->htick; c->inflight[kk] = 0;
+            c->vr_free[c->vr_n_free++] = c->vr_fly_r[i];
+        }
+        c->vr_n_fly = 0;
+        /* new claims of the snapshot (n111 nvtier.py:798-806): in flight, or, when the key is RAM-resident already,
+         * nothing to copy and the slot is freed */
+        const int32_t *sk = c->snap_vr[j], *ss = c->snap_vr[j] + c->vr_K;
+        for (int r = 0; r < c->vr_K; ++r) {
+            if (sk[r] < 0 || ss[r] == c->vr_seen[r]) continue;
+            c->vr_seen[r] = ss[r];
+            int kk = sk[r];
+            if (c->res[kk]) { c->vr_free[c->vr_n_free++] = r; continue; }
+            if (c->inflight[kk]) c->vr_error = 1;
+            c->inflight[kk] = 1;
+            c->vr_fly_r[c->vr_n_fly] = r; c->vr_fly_k[c->vr_n_fly++] = kk;
+        }
+    }
     /* new misses with multiplicity (nvtier.py:765-775) */
     /* the device count wraps modulo 2^32 (the reference's Python int does not; it never reaches 2^31 in its runs) */
     uint32_t cnt = (uint32_t)ring[0];
@@ -366,6 +442,8 @@ int64_t co_host_step(co_t *c, int32_t *admit_out, int32_t *n_admit, int32_t *evi
     for (int i = 0; i < n; ++i)
         if (res[i] != view[i]) { c->last_dk[c->n_last] = i; c->last_dv[c->n_last] = res[i]; c->n_last++; c->ram_res[i] = res[i]; }
     memcpy(c->res, res, n);
+    for (int i = 0; i < c->vr_n_free; ++i) c->vr_key[c->vr_free[i]] = -1;   /* before the next call */
+    c->vr_n_free = 0;
     return newm > 0 ? newm : 0;
 }
 

@@ -376,6 +376,47 @@ __device__ __forceinline__ void st_act(void* y, int dt, size_t i, float v) {
     else ((half_t*)y)[i] = to_half(v);
 }
 
+// ---- victim ring claim (experimental/n111-victim-ring/a9.patch:46-65) ------------------------------------------------
+// The call's write-backs, in victim order, take the free slots (key < 0) of the ring in circular order from the next
+// search position meta[0], each with the next claim number (meta[1] + 1, ...); once no free slot is left the rest are
+// dropped and counted (meta[2]); the search position moves past the last slot claimed. This is the order in which the
+// reference's serial loop claims, computed with two workgroup scans instead of one slot at a time. scan(v, total)
+// is the workgroup's exclusive scan (it contains barriers, so every thread calls this uniformly); rank_slot holds K
+// ints of LDS. Returns this thread's ring slot, or -1 (no write-back, or dropped).
+template <int NT, typename Scan>
+__device__ __forceinline__ int ring_claim(int32_t* meta, int K, int key, int* rank_slot, Scan scan) {
+    const int tid = threadIdx.x;
+    int nwb;
+    const int wbrank = scan(key >= 0 ? 1 : 0, nwb);
+    const int p = meta[0], seq0 = meta[1];
+    int nfree = 0;
+    for (int c0 = 0; c0 < K; c0 += NT) {         // the ring in circular order from p, NT slots at a time
+        const int t = c0 + tid;
+        int j = p + t;
+        j = j >= K ? j - K : j;
+        const bool fr = t < K && meta[4 + j] < 0;
+        int nf;
+        const int r = nfree + scan(fr ? 1 : 0, nf);
+        if (fr && r < nwb) rank_slot[r] = j;
+        nfree += nf;
+    }
+    __syncthreads();
+    const int nclaim = min(nwb, nfree);
+    int slot = -1;
+    if (key >= 0 && wbrank < nclaim) {
+        slot = rank_slot[wbrank];
+        meta[4 + slot] = key;
+        meta[4 + K + slot] = seq0 + 1 + wbrank;
+    }
+    if (tid == 0) {                              // every thread read meta[0] and meta[1] before the first barrier
+        const int last = nclaim > 0 ? rank_slot[nclaim - 1] : -1;
+        if (nclaim > 0) meta[0] = last + 1 == K ? 0 : last + 1;
+        meta[1] = seq0 + nclaim;
+        meta[2] += nwb - nclaim;
+    }
+    return slot;
+}
+
 // ---- cross-workgroup exchange ------------------------------------------------------------------------------------------
 // Each XCD has a private L2, and an agent-scope fence (__threadfence) writes back and invalidates the whole L2
 // (buffer_wbl2 / buffer_inv). Data exchanged between workgroups of one kernel therefore uses agent-scope atomic stores

@@ -15,6 +15,7 @@ constexpr int kMaxI = 4096;         // intermediate size of the decode kernels (
 constexpr int kEnsRegSlots = 32;    // slot_last values held in registers per thread: S <= 512 * 32
 constexpr int kEnsMaxP = 64;        // picks (one per lane of wave 0)
 constexpr int kEnsMaxE = 512;       // experts (one per thread)
+constexpr int kVictimRingMax = 256; // victim ring slots (the claim's rank table lives in the ensure's 256-int LDS scratch)
 
 constexpr int kVictimChunkBytes = 64 * 1024;   // bytes of a victim slot copied by one workgroup
 
@@ -39,6 +40,11 @@ struct EnsureArgs {
     int32_t* wbq_state;                            // [0] records taken, [1 + i] key written back into wbq[i],
                                                    // [1 + wbq_cap] write-backs dropped (no record left)
     int wbq_cap;
+    // victim ring (vr_meta null: off; needs vict and vict_addr): write-backs go to ring slots in device memory and the
+    // host drains them to RAM later. vr_meta int32 [4 + 2 vr_K]: [0] next search position, [1] claims made, [2]
+    // write-backs dropped (ring full), [3] vr_K, then key[vr_K] (-1: free, else the key awaiting its drain) and
+    // seq[vr_K] (the claim number of that key); vr_sel [E]: the ring slot of victim i (-1: none); slots of blob bytes
+    int32_t* vr_meta; int32_t* vr_sel; int64_t vr_base; int vr_K;
     int32_t* log; int64_t log_cap;                 // decision log (debug) or null: [count, records...]; log_cap:
                                                    // int32 words after the count (a record is written if it fits)
     int64_t* pair_ptr;                             // out: blob pointer of every post-mask pick [P] (or null)

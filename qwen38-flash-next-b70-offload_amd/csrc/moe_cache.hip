@@ -356,7 +356,14 @@ __global__ void __launch_bounds__(kEnsureThreads) ensure_kernel(EnsureArgs A) {
                 wb = (old >= 0 && A.ram_res && A.ram_res[old]) ? -1 : old;
             }
             int64_t waddr = 0;
-            if (A.host_addr && A.vict) {         // write-backs on: each takes a record of the step's queue
+            const bool ring = A.vr_meta && A.vict;
+            if (ring) {                          // victim ring: a free ring slot or dropped
+                const int r = ring_claim<kEnsureThreads>(A.vr_meta, A.vr_K, wb, hist,
+                                                         [&](int v, int& t) { return block_excl_scan(v, sw, t); });
+                if (mi < nm) A.vr_sel[mi] = r;
+                if (r >= 0) waddr = A.vr_base + (int64_t)r * A.blob;
+                else wb = -1;
+            } else if (A.host_addr && A.vict) {  // write-backs on: each takes a record of the step's queue
                 int tot;
                 const int rank = block_excl_scan(wb >= 0 ? 1 : 0, sw, tot);
                 const int used0 = A.wbq_state[0];
@@ -388,12 +395,13 @@ __global__ void __launch_bounds__(kEnsureThreads) ensure_kernel(EnsureArgs A) {
                 if (old >= 0) {
                     A.slot_of[old] = -1;
                     // the victim's blob is read from its RAM record from now on: the write-back target, else the
-                    // record it already has (a dropped write-back leaves the key masked until a fill brings it back)
+                    // record it already has (a dropped write-back leaves the key masked until a fill brings it back).
+                    // A ring slot is no record: the key stays masked until the host has drained it into one.
                     int64_t hp = waddr;
                     if (A.host_addr) {
-                        if (waddr) A.host_addr[old] = waddr;
+                        if (waddr && !ring) A.host_addr[old] = waddr;
                         else hp = A.host_addr[old];
-                    } else if (wb < 0) {
+                    } else if (wb < 0 || ring) {
                         hp = A.host_base[old / E] + (int64_t)(old % E) * A.hstride;
                     }
                     A.ptrs_all[old] = hp;

@@ -42,6 +42,11 @@ struct Config {
     const int64_t* wbq = nullptr;                 // the step's free records for write-backs [wbq_cap]
     int32_t* wbq_state = nullptr;                 // [0] taken, [1 + i] key written into wbq[i], [1 + cap] dropped
     int wbq_cap = 0;
+    int32_t* vr_meta = nullptr;                   // victim ring: [4 + 2K] search position, claims, drops, K, keys, seqs
+    int32_t* vr_sel = nullptr;                    // ring slot of each victim of a call [E]
+    uint8_t* vr_buf = nullptr;                    // K ring slots in device memory
+    int64_t vr_bytes = 0;
+    int vr_K = 0;
 };
 Config g_cfg;
 
@@ -156,6 +161,26 @@ int exl3_set_victims(int32_t* vict) {
 
 int exl3_set_victim_addrs(int64_t* vict_addr) {
     g_cfg.vict_addr = vict_addr;
+    return EXL3_OK;
+}
+
+int exl3_set_victim_ring(int32_t* meta, int32_t* sel, void* buf, int64_t buf_bytes, int64_t K) {
+    if (!meta) {
+        g_cfg.vr_meta = nullptr;
+        g_cfg.vr_sel = nullptr;
+        g_cfg.vr_buf = nullptr;
+        g_cfg.vr_bytes = 0;
+        g_cfg.vr_K = 0;
+        return EXL3_OK;
+    }
+    if (!sel || !buf || K <= 0 || K > kVictimRingMax || buf_bytes <= 0)
+        return fail(EXL3_EINVAL, "set_victim_ring: K=%lld (1..%d) with meta, sel and a buffer", (long long)K,
+                    kVictimRingMax);
+    g_cfg.vr_meta = meta;
+    g_cfg.vr_sel = sel;
+    g_cfg.vr_buf = (uint8_t*)buf;
+    g_cfg.vr_bytes = buf_bytes;
+    g_cfg.vr_K = (int)K;
     return EXL3_OK;
 }
 
@@ -391,6 +416,8 @@ int exl3_moe_prefetch(const int32_t* ids, int n_ids, int64_t* ptrs_all, int laye
                       void* stream) {
     if (g_cfg.host_addr)                          // its copies address fixed host records
         return fail(EXL3_EUNSUPPORTED, "moe_prefetch: not with the RAM tier's record pool");
+    if (g_cfg.vr_meta)                            // its victims would bypass the ring
+        return fail(EXL3_EUNSUPPORTED, "moe_prefetch: not with the victim ring");
     const int E = n_experts;
     if (n_ids < 0 || layer < 0 || max_fill < 0 || blob <= 0)
         return fail(EXL3_EINVAL, "moe_prefetch: n_ids=%d layer=%d max_fill=%d blob=%lld", n_ids, layer, max_fill,
@@ -447,6 +474,8 @@ int exl3_moe_prefetch_plan(const int32_t* ids, int n_ids, int64_t* ptrs_all, int
                            int max_fill, int n_experts, int64_t blob, void* stream) {
     if (g_cfg.host_addr)                          // its copies address fixed host records
         return fail(EXL3_EUNSUPPORTED, "moe_prefetch_plan: not with the RAM tier's record pool");
+    if (g_cfg.vr_meta)                            // its victims would bypass the ring
+        return fail(EXL3_EUNSUPPORTED, "moe_prefetch_plan: not with the victim ring");
     const int E = n_experts;
     if (n_ids < 0 || layer < 0 || max_fill < 0 || blob <= 0 || n_layers <= layer)
         return fail(EXL3_EINVAL, "moe_prefetch_plan: n_ids=%d layer=%d n_layers=%d max_fill=%d", n_ids, layer,
@@ -494,6 +523,8 @@ int exl3_prefetch_worker_start(int32_t* plans, const int64_t* host_base_host, in
                                int32_t* done_seq, int32_t* seq_host, int n_layers, int n_experts, void* stream) {
     if (g_cfg.host_addr)                          // its copies address fixed host records
         return fail(EXL3_EUNSUPPORTED, "prefetch_worker_start: not with the RAM tier's record pool");
+    if (g_cfg.vr_meta)                            // its victims would bypass the ring
+        return fail(EXL3_EUNSUPPORTED, "prefetch_worker_start: not with the victim ring");
     std::lock_guard<std::mutex> lk(g_pfw_mu);
     if (g_pfw) return fail(EXL3_EINVAL, "prefetch worker already running");
     if (!plans || !host_base_host || !done_seq || !seq_host || n_layers <= 0 || n_experts <= 0 || blob <= 0)
@@ -601,6 +632,20 @@ static int cached_impl(const void* x, int x_dtype, int64_t x_stride, int M, int 
     if (ea.host_addr && (!ea.vict || !ea.vict_addr))
         return fail(EXL3_EINVAL, "moe_forward_cached: the record pool needs the victim list and its addresses "
                                  "(exl3_set_victims, exl3_set_victim_addrs)");
+    if (g_cfg.vr_meta && ea.vict) {              // victim ring: write-backs into ring slots of the slot stride
+        if (!ea.vict_addr)
+            return fail(EXL3_EINVAL, "moe_forward_cached: the victim ring needs the victim addresses "
+                                     "(exl3_set_victim_addrs)");
+        if ((int64_t)g_cfg.vr_K * ea.blob > g_cfg.vr_bytes)
+            return fail(EXL3_EINVAL, "moe_forward_cached: victim ring of %lld bytes < %d slots of %lld",
+                        (long long)g_cfg.vr_bytes, g_cfg.vr_K, (long long)ea.blob);
+        ea.vr_meta = g_cfg.vr_meta;
+        ea.vr_sel = g_cfg.vr_sel;
+        ea.vr_base = (int64_t)g_cfg.vr_buf;
+        ea.vr_K = g_cfg.vr_K;
+    }
+    // with the ring the host flags a victim RAM-resident once its drain has landed, never the device
+    uint8_t* vict_res = ea.vr_meta ? nullptr : g_cfg.ram_res;
     ea.log = g_cfg.log;
     ea.log_cap = g_cfg.log_cap;
     if (exceeds_decode(M, topk)) {
@@ -616,7 +661,7 @@ static int cached_impl(const void* x, int x_dtype, int64_t x_stride, int M, int 
         hipError_t e = launch_ensure(ea, st);
         if (e == hipErrorInvalidValue) return fail(EXL3_EUNSUPPORTED, "moe_forward_cached: ensure state does not fit in LDS");
         if (e != hipSuccess) return hip_fail(e, "ensure launch");
-        e = launch_cached_fills(ea, g.blob, std::min(std::min(ea.max_fill, E), P), g_cfg.ram_res, st);
+        e = launch_cached_fills(ea, g.blob, std::min(std::min(ea.max_fill, E), P), vict_res, st);
         if (e != hipSuccess) return hip_fail(e, "cached fills launch");
         return forward_impl(x, x_dtype, x_stride, M, H, topk_ids, topk_w, topk, ptrs_all + (int64_t)layer * E, I, K, E,
                             out, out_stride, workspace, workspace_bytes, st, nullptr, nullptr, nullptr, nullptr, nullptr);
@@ -650,7 +695,7 @@ static int cached_impl(const void* x, int x_dtype, int64_t x_stride, int M, int 
         va.blob = ea.blob;                        // a victim may be an expert of another bitrate: copy the slot
         va.hstride = ea.hstride;
         va.E = E;
-        va.ram_res = g_cfg.ram_res;
+        va.ram_res = vict_res;
         va.chunk_bytes = kVictimChunkBytes;
         va.vaddr = ea.vict_addr;
         mv = std::min(std::min(ea.max_fill, E), P);

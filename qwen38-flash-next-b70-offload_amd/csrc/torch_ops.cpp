@@ -191,6 +191,20 @@ void moe_set_mr(int64_t mr) { check(exl3_set_mr(mr), "moe_set_mr"); }
 void moe_set_debug(int64_t v) { check(exl3_set_debug(v), "moe_set_debug"); }
 void moe_set_pair_max_m(int64_t v) { check(exl3_set_pair_max_m(v), "moe_set_pair_max_m"); }
 void moe_set_prefill_min_m(int64_t v) { check(exl3_set_prefill_min_m(v), "moe_set_prefill_min_m"); }
+// moe_set_victim_ring (experimental/n111-victim-ring/a9.patch:17-30): meta int32 [4 + 2K], sel int32 [E], buf the
+// K ring slots; an empty meta turns the ring off
+void moe_set_victim_ring(at::Tensor meta, at::Tensor sel, at::Tensor buf) {
+    if (!meta.numel()) return check(exl3_set_victim_ring(nullptr, nullptr, nullptr, 0, 0), "moe_set_victim_ring");
+    TORCH_CHECK(meta.scalar_type() == at::kInt && sel.scalar_type() == at::kInt && meta.is_contiguous() &&
+                    sel.is_contiguous() && meta.is_cuda() && sel.is_cuda() && buf.is_cuda(),
+                "moe_set_victim_ring: device int32 meta and sel");
+    const int64_t K = (meta.numel() - 4) / 2;
+    TORCH_CHECK(K > 0 && meta.numel() == 4 + 2 * K && buf.numel() > 0, "victim ring: meta [4 + 2K], buf [K * blob]");
+    check(exl3_set_victim_ring(meta.data_ptr<int>(), sel.data_ptr<int>(), buf.data_ptr(),
+                               (int64_t)buf.numel() * (int64_t)buf.element_size(), K),
+          "moe_set_victim_ring");
+}
+
 void moe_set_victims(at::Tensor v) {
     if (!v.numel()) return check(exl3_set_victims(nullptr), "moe_set_victims");
     TORCH_CHECK(v.scalar_type() == at::kInt && v.is_cuda(), "moe_set_victims: device int32 tensor");
@@ -455,6 +469,7 @@ TORCH_LIBRARY(exl3xpu_moe, m) {
     m.def("moe_set_pair_max_m(int v) -> ()", &moe_set_pair_max_m);
     m.def("moe_set_prefill_min_m(int v) -> ()", &moe_set_prefill_min_m);
     m.def("moe_set_victims(Tensor v) -> ()", &moe_set_victims);
+    m.def("moe_set_victim_ring(Tensor meta, Tensor sel, Tensor buf) -> ()", &moe_set_victim_ring);
     m.def("moe_set_tier(Tensor ram_res, Tensor miss, Tensor safe) -> ()", &moe_set_tier);
     m.def("moe_set_host_stride(int s) -> ()", &moe_set_host_stride);
     m.def("moe_set_slot_stride(int s) -> ()", &moe_set_slot_stride);

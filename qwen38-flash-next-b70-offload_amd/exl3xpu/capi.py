@@ -24,6 +24,7 @@ SIGNATURES = {
     "exl3_set_victims": (c_i32, [c_p]),
     "exl3_set_victim_addrs": (c_i32, [c_p]),
     "exl3_set_record_pool": (c_i32, [c_p, c_p, c_p, c_i64]),
+    "exl3_set_victim_ring": (c_i32, [c_p, c_p, c_p, c_i64, c_i64]),
     "exl3_set_host_stride": (c_i32, [c_i64]),
     "exl3_set_slot_stride": (c_i32, [c_i64]),
     "exl3_set_fused_ensure": (c_i32, [c_i64]),

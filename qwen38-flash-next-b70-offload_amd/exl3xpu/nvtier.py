@@ -871,11 +871,22 @@ class NvTierAsync(NvTierFast):
     flags has run; admitted fills take records at the next step. The pool then holds at most budget + 3 * wb_queue
     records (two queues outstanding and one step of adopted write-backs), rounded up to its chunk. A write-back that
     finds the queue used up is dropped (stats["wb_dropped"]): the victim leaves HBM without a copy and stays masked
-    until a fill brings it back."""
+    until a fill brings it back.
+
+    victim_ring=K (or EXL3_NVTIER_VICTIM_RING=1 with EXL3_NVTIER_VRING_K, default 128; the reference's
+    NvTierAsyncRing, experimental/n111-victim-ring/nvtier.py:655-884): victims go to a ring of K slots in HBM
+    (exl3_set_victim_ring) instead of to host memory, and the host drains them. From each snapshot the step takes the
+    ring's new claims (a slot whose claim number it has not handled), marks their keys in flight (so that the policy
+    neither admits them nor forgets them in the budget, and a miss on them waits for the data that is about to land),
+    gives each a record (its fixed record, or one from the pool) and copies the slot there on a side stream once the
+    decode step that wrote it has finished. A drain lands at the next host step (completion "steps"; at the first
+    step after its copy finished with "wallclock"): the key becomes RAM-resident like a completed fill and its slot
+    is freed (key = -1 written on the compute stream before the next decode step). The device never flags a ring
+    victim resident and only claims free slots; a full ring drops the write-back (stats["vr_drops"])."""
 
     _pool_ok = True
 
-    def __init__(self, *a, wb_queue: int | None = None, **k):
+    def __init__(self, *a, wb_queue: int | None = None, victim_ring: int | None = None, **k):
         super().__init__(*a, **k)
         from . import capi
         self._capi = capi
@@ -918,6 +929,146 @@ class NvTierAsync(NvTierFast):
         self.decisions = []                # (admitted keys, evicted keys) per step when log_decisions
         if self.pool is not None:
             self._pool_init(int(wb_queue) if wb_queue else _env_int("EXL3_NVTIER_WB_QUEUE", 48))
+        self.vr_K = 0
+        if victim_ring is None and _env_int("EXL3_NVTIER_VICTIM_RING", 0) == 1:
+            victim_ring = _env_int("EXL3_NVTIER_VRING_K", 128)
+        if victim_ring:
+            self._ring_init(int(victim_ring))
+
+    # ---- victim ring
+    def _ring_init(self, K: int) -> None:
+        if not 1 <= K <= 256:
+            raise ValueError(f"NvTierAsync: victim ring of {K} slots (1..256)")
+        if _env_int("EXL3_NVTIER_NO_VICTIM", 0) == 1:
+            raise ValueError("NvTierAsync: the victim ring needs victim write-back (EXL3_NVTIER_NO_VICTIM=1 is set)")
+        X, d, st = self.st.X, self.dev, self.st
+        self.vr_K = K
+        meta = torch.full((4 + 2 * K,), -1, dtype=torch.int32)
+        meta[:4] = torch.tensor([0, 0, 0, K], dtype=torch.int32)
+        meta[4 + K:] = 0
+        self.vr_meta = meta.to(d)
+        self.vr_sel = torch.full((self.E,), -1, dtype=torch.int32, device=d)
+        self.vr_stride = int(st.slot_stride)
+        self.vr_buf = torch.empty(K * self.vr_stride, dtype=torch.uint8, device=d)
+        self._h_vr = [X.host_alloc(4 * (4 + 2 * K)).view(torch.int32) for _ in range(2)]
+        for t in self._h_vr:
+            t.fill_(-1)
+        self._np_vr = [t.numpy() for t in self._h_vr]
+        self._h_vfree = [X.host_alloc(8 * K).view(torch.int64) for _ in range(2)]
+        self._vr_seen = np.zeros(K, dtype=np.int64)      # claim number handled per slot (claims count from 1)
+        self._vr_fly = []                                # [(event, due host step, [(slot, key), ...])]
+        self._vr_cs = torch.cuda.Stream(d)
+        self._vr_claims = self._vr_drops = 0
+        for key in ("vr_claims", "vr_drops", "vr_issued", "vr_landed"):
+            self.stats[key] = 0
+        if not hasattr(self, "_vict_addr"):
+            self._vict_addr = torch.zeros(self.E, dtype=torch.int64, device=d)
+        L = self._capi.lib()
+        for b in range(2):                               # the ring's meta joins the snapshot copies
+            srcs, dsts, nbs = self._xargs[b]
+            self._xargs[b] = ((ctypes.c_void_p * 4)(*list(srcs), self.vr_meta.data_ptr()),
+                              (ctypes.c_void_p * 4)(*list(dsts), self._h_vr[b].data_ptr()),
+                              (ctypes.c_int64 * 4)(*list(nbs), 4 * (4 + 2 * K)))
+        torch.cuda.synchronize(d)
+        self._capi.check(L.exl3_set_victim_addrs(self._vict_addr.data_ptr()), "set_victim_addrs")
+        self._capi.check(L.exl3_set_victim_ring(self.vr_meta.data_ptr(), self.vr_sel.data_ptr(),
+                                                self.vr_buf.data_ptr(), self.vr_buf.numel(), K), "set_victim_ring")
+
+    def _ring_landed(self, hs: int, wait_all: bool = False) -> tuple:
+        """Drains that have landed: (keys, ring slots); with wait_all every drain in flight."""
+        keys, slots, keep = [], [], []
+        for ev, due, items in self._vr_fly:
+            if wait_all or (due <= hs if self.completion == "steps" else ev.query()):
+                ev.synchronize()
+                for r, key in items:
+                    slots.append(r)
+                    keys.append(key)
+            else:
+                keep.append((ev, due, items))
+        self._vr_fly = keep
+        self.stats["vr_landed"] += len(keys)
+        return keys, slots
+
+    def _ring_claims(self, m: np.ndarray, k: int, hs: int, after) -> list:
+        """New claims in the ring meta m (a snapshot, or the live meta with the device idle): their keys go in flight
+        with a record each, and copies slot -> record start on the side stream after the event `after` (the end of
+        the decode step that wrote the slots). A claim whose key a synchronous path has made RAM-resident meanwhile
+        needs no copy: its slot is returned, to be freed."""
+        K = self.vr_K
+        if int(m[3]) != K:                               # the snapshot holds the meta only after the first exchange
+            return []
+        self.stats["vr_claims"] += int(m[1]) - self._vr_claims
+        self.stats["vr_drops"] += int(m[2]) - self._vr_drops
+        self._vr_claims, self._vr_drops = int(m[1]), int(m[2])
+        vk, vs = m[4:4 + K], m[4 + K:4 + 2 * K].astype(np.int64)
+        new = np.nonzero((vk >= 0) & (vs != self._vr_seen))[0]
+        if not new.size:
+            return []
+        self._vr_seen[new] = vs[new]
+        st, pol = self.st, self.policy
+        keys = vk[new].astype(np.int64)
+        have = pol.res[keys] == 1
+        if pol.inflight[keys[~have]].any():
+            raise RuntimeError("exl3xpu tier: a victim ring claim for a key whose fill is in flight")
+        skip = new[have].tolist()
+        new, keys = new[~have], keys[~have]
+        if not new.size:
+            return skip
+        if self.pool is not None:
+            old = st.rec_of[keys]
+            if (old != 0).any():
+                self._pending[k].extend(old[old != 0].tolist())
+            st.rec_of[keys] = self.pool.take(keys.size)
+        pol.inflight[keys] = True
+        cs = self._vr_cs
+        if after is not None:
+            cs.wait_event(after)
+        L, h = self._capi.lib(), ctypes.c_void_p(cs.cuda_stream)
+        base = self.vr_buf.data_ptr()
+        for r, key in zip(new.tolist(), keys.tolist()):
+            self._capi.check(L.exl3_memcpy_async(st.addr(key), base + r * self.vr_stride, self.vr_stride, h),
+                             "victim ring drain")
+        ev = torch.cuda.Event()
+        ev.record(cs)
+        self._vr_fly.append((ev, hs + 1, list(zip(new.tolist(), keys.tolist()))))
+        self.stats["vr_issued"] += int(new.size)
+        return skip
+
+    def _ring_free(self, slots, k: int) -> None:
+        """Free ring slots on the compute stream (their copies have completed), before the next decode step."""
+        if not slots:
+            return
+        buf = self._h_vfree[k]
+        buf[:len(slots)] = torch.tensor(slots, dtype=torch.int64) + 4
+        idx = buf[:len(slots)].to(self.dev, non_blocking=True)
+        self.vr_meta.index_fill_(0, idx, -1)
+
+    def ring_settle(self) -> None:
+        """Drain the whole ring now (synchronous paths; the device goes idle): the claims of the device's current
+        meta are copied too, every drain lands, the keys become RAM-resident on the host and the device, their
+        records are published and their slots freed."""
+        if not self.vr_K:
+            return
+        torch.cuda.synchronize(self.dev)
+        skip = self._ring_claims(self.vr_meta.cpu().numpy(), self._k, self._hstep, None)
+        keys, slots = self._ring_landed(self._hstep, wait_all=True)
+        slots = slots + skip
+        if keys:
+            pol = self.policy
+            ka = np.asarray(keys, dtype=np.int64)
+            pol.res[ka] = 1
+            pol.age[ka] = pol.tick
+            pol.inflight[ka] = False
+            if self.pool is not None:
+                self.st.publish_records(keys)
+            self.res_dev.index_fill_(0, torch.from_numpy(ka).to(self.dev), 1)
+            self._flags_changed(ka, 1)
+        self._ring_free(slots, self._k)
+        torch.cuda.synchronize(self.dev)
+
+    def ensure_for_prefill(self, li: int, ids) -> int:
+        self.ring_settle()
+        return super().ensure_for_prefill(li, ids)
 
     # ---- record pool
     def _pool_init(self, cap: int) -> None:
@@ -987,6 +1138,12 @@ class NvTierAsync(NvTierFast):
         self._last_diff = None
 
     def close(self) -> None:
+        if self.vr_K:
+            torch.cuda.synchronize(self.dev)
+            self._capi.check(self._capi.lib().exl3_set_victim_ring(None, None, None, 0, 0), "set_victim_ring")
+            if self.pool is None:
+                self._capi.check(self._capi.lib().exl3_set_victim_addrs(None), "set_victim_addrs")
+            self.vr_K = 0
         if self.pool is not None:
             torch.cuda.synchronize(self.dev)
             L = self._capi.lib()
@@ -1024,13 +1181,18 @@ class NvTierAsync(NvTierFast):
             if pool:
                 self._pool_collect(j, k)
                 self._start_fills()
+            vr_keys, vr_slots = self._ring_landed(hs) if self.vr_K else ([], [])
+            if self.vr_K:
+                vr_slots += self._ring_claims(self._np_vr[j], k, hs, self._snap_ev[j])
             view = self._view
             np.copyto(view, self._np_res[j])
             if self._last_diff is not None:         # the flags uploaded with that snapshot
                 dk, dv = self._last_diff
                 view[dk] = dv
-            done = self._completed(hs)
+            done = self._completed(hs) + vr_keys
             adm, ev_keys, diff, vals = pol.decide(view, self._np_ring, self._np_slot[j], done)
+            if self.vr_K:
+                self._ring_free(vr_slots, k)
             self._ring_from = int(self._np_ring[0]) & 0xFFFFFFFF
             self._queue_fills(adm, hs)
             if pool:
@@ -1070,7 +1232,7 @@ class NvTierAsync(NvTierFast):
             st = self.st
             self._capi.check(L.exl3_tier_exchange_pool(
                 self.res_dev.data_ptr(), self._n, self._h_diff[k].data_ptr(), n_diff, self.ring.data_ptr(),
-                self.ring.numel() - 1, self._ring_from, self._h_ring.data_ptr(), srcs, dsts, nbs, 3,
+                self.ring.numel() - 1, self._ring_from, self._h_ring.data_ptr(), srcs, dsts, nbs, len(nbs),
                 self._h_upd[k].data_ptr(), n_upd, st.host_addr_dev.data_ptr(), st.ptrs_all.data_ptr(),
                 st.slot_of_dev.data_ptr(), self._h_next[k].data_ptr(), self._wbq.data_ptr(),
                 self._wbq_state.data_ptr(), self._h_wbm[k].data_ptr(), self.wb_cap, cur.cuda_stream),
@@ -1078,8 +1240,8 @@ class NvTierAsync(NvTierFast):
         else:
             self._capi.check(L.exl3_tier_exchange(self.res_dev.data_ptr(), self._n, self._h_diff[k].data_ptr(),
                                                   n_diff, self.ring.data_ptr(), self.ring.numel() - 1,
-                                                  self._ring_from, self._h_ring.data_ptr(), srcs, dsts, nbs, 3,
-                                                  cur.cuda_stream), "nvtier exchange")
+                                                  self._ring_from, self._h_ring.data_ptr(), srcs, dsts, nbs,
+                                                  len(nbs), cur.cuda_stream), "nvtier exchange")
         self._snap_ev[k].record(cur)
         self._have[k] = True
         self.stats["steps"] += 1

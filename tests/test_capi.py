@@ -47,6 +47,13 @@ def test_setters():
     assert L.exl3_set_host_stride(0) == 0
     assert L.exl3_set_tier(None, None, 0, None) == 0
     assert L.exl3_set_pair_max_m(4) == 0 and L.exl3_set_prefill_min_m(256) == 0
+    # the victim ring: K in 1..256 with meta, sel and a buffer (pointers are only stored, never touched here)
+    fake = 0x1000
+    assert L.exl3_set_victim_ring(fake, fake, fake, 1 << 20, 257) == 1
+    assert L.exl3_set_victim_ring(fake, None, fake, 1 << 20, 8) == 1
+    assert L.exl3_set_victim_ring(fake, fake, fake, 0, 8) == 1
+    assert L.exl3_set_victim_ring(fake, fake, fake, 1 << 20, 8) == 0
+    assert L.exl3_set_victim_ring(None, None, None, 0, 0) == 0
 
 
 def test_linear_entry_points_validate_without_a_gpu():

@@ -13,14 +13,15 @@ pytestmark = pytest.mark.gpu
 GOLD = os.path.join(os.path.dirname(__file__), "golden")
 
 
-def _setup(L, E, S, H, I, K, budget, qmax, age, latency, ring_cap, seed, pool=False, wb_queue=None):
+def _setup(L, E, S, H, I, K, budget, qmax, age, latency, ring_cap, seed, pool=False, wb_queue=None,
+           victim_ring=None):
     from exl3xpu import nvtier
     store = nvtier.TierStore(H, I, K, E, S, n_layers=L, pool=pool)
     for li in range(L):
         store.add_layer(f"model.layers.{li}.mlp")
     src = nvtier.SyntheticExpertSource(H, I, K, seed, n_distinct=16)
     tier = nvtier.NvTierAsync(store, src, ring_cap=ring_cap, budget_records=budget, latency=latency,
-                              wb_queue=wb_queue)
+                              wb_queue=wb_queue, victim_ring=victim_ring)
     tier.policy.admit_age, tier.policy.admit_qmax = age, qmax
     tier.log_decisions = True
     # reference table: every expert's true blob in HBM (independent of the cache)
@@ -638,3 +639,52 @@ def test_decision_log_stops_at_its_buffer(fused):
     recs = b[1:1 + fit * rl].reshape(fit, rl)
     assert (recs[:, 2:2 + P] >= 0).all() and (recs[:, 2:2 + P] < E).all()   # the picks of every record that fits
     assert (b[1 + fit * rl:] == -7).all(), "the log wrote past its buffer"
+
+
+@pytest.mark.parametrize("fused,pool,K", [(1, False, 96), (0, False, 96), (1, True, 96), (1, False, 4),
+                                          (0, True, 4)])
+def test_tier_victim_ring(fused, pool, K):
+    """The victim ring (experimental/n111-victim-ring): victims go to K ring slots in HBM and the host drains them.
+    Every device record (with ring-full drops as write-backs of -1) and every host decision equals the oracle's ring
+    mode, the ring's meta equals the oracle's after the run, and every cached output equals the plain forward on the
+    true blobs (the reference's own test of this path, n111_test.py). After the ring is drained, every RAM-resident
+    key's record holds its true blob. K = 4 overflows on this trace (drops), K = 96 does not."""
+    from exl3xpu import nvtier
+    L, E, S, M, TK, steps = 4, 96, 90, 2, 8, 60
+    print(f"case victim ring K={K} fused={fused} pool={pool}", flush=True)
+    ids, w = synth.zipf_trace(20261204, steps, L, E, TK, M=M)
+    ids = np.ascontiguousarray(ids.reshape(steps, L, M * TK))
+    w = np.ascontiguousarray(w.reshape(steps, L, M * TK))
+    co = cache.CacheOracle(L, E, S, ring_cap=1 << 12, budget=120, age=4, qmax=32, latency=3, victim_ring=K)
+    orecs, olog = co.run(ids, w)
+    store, tier, blobs, ref_ptr = _setup(L, E, S, 128, 128, 3, 120, 32, 4, 3, 1 << 12, 13, pool=pool, wb_queue=48,
+                                         victim_ring=K)
+    store.X.moe_set_fused_ensure(fused)
+    try:
+        recs, bad = _run(store, tier, ids, w, 128, check_out_every=1, ref_ptr=ref_ptr, M=M)
+    finally:
+        store.X.moe_set_fused_ensure(1)
+    mism = np.nonzero((recs != orecs).any(axis=-1))
+    assert mism[0].size == 0, f"first mismatch at step/layer {mism[0][0]}/{mism[1][0]}"
+    for n, ((a1, e1), (a2, e2)) in enumerate(zip(tier.decisions, olog)):
+        assert a1.tolist() == a2.tolist() and e1.tolist() == e2.tolist(), n
+    assert bad == 0
+    ost = co.ring_stats()
+    meta = tier.vr_meta.cpu().numpy()
+    assert ost["error"] == 0 and ost["claims"] > 0
+    assert (ost["drops"] > 0) == (K == 4)
+    assert [int(meta[0]), int(meta[1]), int(meta[2])] == [ost["pos"], ost["claims"], ost["drops"]]
+    assert np.array_equal(meta[4:4 + K], co.vr_key) and np.array_equal(meta[4 + K:4 + 2 * K], co.vr_seq)
+    tier.ring_settle()
+    torch.cuda.synchronize()
+    assert not tier.policy.inflight[np.nonzero(tier.policy.res)[0]].any()
+    for key in np.nonzero(tier.policy.res)[0].tolist():
+        want = np.asarray(tier.src.blob_of(tier.rec_index(key)))
+        got = np.frombuffer(ctypes_bytes(store.addr(key), want.size), dtype=np.uint8)
+        assert np.array_equal(got, want), f"record of key {key}"
+    tier.close()
+
+
+def ctypes_bytes(addr: int, n: int) -> bytes:
+    import ctypes
+    return ctypes.string_at(addr, n)

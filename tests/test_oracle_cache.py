@@ -244,3 +244,59 @@ def test_cache_oracle_plan_hand_case():
     co2 = cache.CacheOracle(1, 64, 40, tier=False)
     r = co2.plan(0, np.arange(30, dtype=np.int32), max_fill=30)
     assert r[2 + 30] == 16 and int((co2.slot_last == 0x7FFFFFFF).sum()) == 16
+
+
+@pytest.mark.parametrize("K", [3, 96])
+def test_cache_oracle_victim_ring_claims_and_drains(K):
+    """The victim ring (co_set_ring) against a closed form of the reference's serial claim loop and the drain
+    protocol, call by call: the slots a call claims are the first min(write-backs, free) free slots in circular order
+    from the search position before it, taken by the call's written-back victims in victim order with consecutive
+    claim numbers; the rest are dropped; the position moves past the last slot claimed. Every key the host takes into
+    flight at step h is RAM-resident at step h + 1 with age h + 1, its slot free again before the next call; a ring
+    key is never RAM-resident and in flight at once."""
+    L, E, S, P, steps = 3, 48, 30, 6, 160
+    ids, w = synth.zipf_trace(77 + K, steps, L, E, P)
+    ids, w = ids[:, :, 0], w[:, :, 0]
+    co = cache.CacheOracle(L, E, S, budget=90, age=4, qmax=24, latency=2, victim_ring=K)
+    flying_prev = set()
+    total_claims = total_drops = 0
+    for n in range(steps):
+        for li in range(L):
+            key0, seq0, st0 = co.vr_key.copy(), co.vr_seq.copy(), co.ring_stats()
+            rec = co.ensure(li, ids[n, li].copy(), w[n, li].copy())
+            st1 = co.ring_stats()
+            nc, nd = st1["claims"] - st0["claims"], st1["drops"] - st0["drops"]
+            total_claims, total_drops = total_claims + nc, total_drops + nd
+            nm = int(rec[2 + P])
+            wbs = [int(rec[3 + 2 * P + 2 * mi]) for mi in range(nm)]
+            claimed_keys = [k for k in wbs if k >= 0]
+            assert len(claimed_keys) == nc
+            free = [(st0["pos"] + t) % K for t in range(K) if key0[(st0["pos"] + t) % K] < 0]
+            want = free[:nc]
+            assert nd == 0 or nc == len(free), "dropped while a slot was free"
+            got = [r for r in range(K) if co.vr_seq[r] != seq0[r]]
+            assert sorted(got) == sorted(want)
+            assert [int(co.vr_key[r]) for r in want] == claimed_keys
+            assert [int(co.vr_seq[r]) for r in want] == list(range(st0["claims"] + 1, st1["claims"] + 1))
+            if nc:
+                assert st1["pos"] == (want[-1] + 1) % K
+            else:
+                assert st1["pos"] == st0["pos"]
+            for k in claimed_keys:                     # the device never flags a ring victim RAM-resident
+                assert co.ram_res[k] == 0
+        infl0 = co.inflight.copy()
+        co.host_step()
+        t = co.host_tick
+        for k in flying_prev:                          # drains taken into flight last step have landed
+            assert co.res[k] == 1 and co.age[k] == t and co.inflight[k] == 0
+            assert k not in set(co.vr_key.tolist())      # and its slot is free again
+        # the ring keys taken into flight by this step (fills admitted now are not in the ring)
+        flying_prev = {int(k) for k in np.nonzero(co.inflight & ~infl0)[0]}
+        flying_prev &= {int(k) for k in co.vr_key.tolist() if k >= 0}
+        assert not (co.inflight.astype(bool) & (co.res == 1)).any()
+        assert co.ring_stats()["error"] == 0
+    assert total_claims > 0
+    if K == 3:
+        assert total_drops > 0                         # a small ring overflows on this trace
+    else:
+        assert total_drops == 0
