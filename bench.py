@@ -692,7 +692,8 @@ def main():
     capi.check(capi.lib().exl3_device_status(status, torch.cuda.current_stream().cuda_stream), "device status")
     tok_s = steps * bs / el if steps else 0.0
     d = {k: tier.stats.get(k, 0) - st0.get(k, 0) for k in ("masked", "evicts", "nvme_reads", "admit_dropped", "wait_ms",
-                                                          "wb_taken", "wb_dropped", "vr_claims", "vr_drops")}
+                                                          "wb_taken", "wb_dropped", "vr_claims", "vr_drops",
+                                                          "vr_ms", "vr_sync_ms")}
     ram_tier = {"mode": "fixed arena" if args.fixed_arena else "record pool",
                 "pinned_gib": round(tier.pinned_bytes() / 2**30, 3), "record_bytes": store.stride,
                 "budget_records": args.budget_records}
@@ -702,7 +703,9 @@ def main():
                         write_backs_dropped=int(tier.stats["wb_dropped"]))
     if tier.vr_K:                        # write-backs through the victim ring instead of the pool's queue
         ram_tier.update(victim_ring=tier.vr_K, write_backs_per_step=round(d["vr_claims"] / max(steps, 1), 3),
-                        write_backs_dropped=int(tier.stats["vr_drops"]))
+                        write_backs_dropped=int(tier.stats["vr_drops"]),
+                        ring_host_ms_per_step=round(d["vr_ms"] / max(steps, 1), 4),
+                        ring_drain_wait_ms_per_step=round(d["vr_sync_ms"] / max(steps, 1), 4))
     host_ms = {k: round(v / max(steps, 1) * 1e3, 4) for k, v in host_s.items()}
     host_ms["tier_wait"] = round(d.pop("wait_ms") / max(steps, 1), 4)     # of tier_step: waiting for the GPU
     sd = max(steps, 1)

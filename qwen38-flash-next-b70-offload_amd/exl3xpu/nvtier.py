@@ -955,11 +955,14 @@ class NvTierAsync(NvTierFast):
             t.fill_(-1)
         self._np_vr = [t.numpy() for t in self._h_vr]
         self._h_vfree = [X.host_alloc(8 * K).view(torch.int64) for _ in range(2)]
+        self._np_vfree = [t.numpy() for t in self._h_vfree]
+        self._d_vfree = torch.zeros(K, dtype=torch.int64, device=d)
+        self._vr_events = []                             # free events for the drains
         self._vr_seen = np.zeros(K, dtype=np.int64)      # claim number handled per slot (claims count from 1)
         self._vr_fly = []                                # [(event, due host step, [(slot, key), ...])]
         self._vr_cs = torch.cuda.Stream(d)
         self._vr_claims = self._vr_drops = 0
-        for key in ("vr_claims", "vr_drops", "vr_issued", "vr_landed"):
+        for key in ("vr_claims", "vr_drops", "vr_issued", "vr_landed", "vr_ms", "vr_sync_ms"):
             self.stats[key] = 0
         if not hasattr(self, "_vict_addr"):
             self._vict_addr = torch.zeros(self.E, dtype=torch.int64, device=d)
@@ -979,7 +982,10 @@ class NvTierAsync(NvTierFast):
         keys, slots, keep = [], [], []
         for ev, due, items in self._vr_fly:
             if wait_all or (due <= hs if self.completion == "steps" else ev.query()):
+                t = time.perf_counter()
                 ev.synchronize()
+                self.stats["vr_sync_ms"] += (time.perf_counter() - t) * 1e3
+                self._vr_events.append(ev)
                 for r, key in items:
                     slots.append(r)
                     keys.append(key)
@@ -1028,7 +1034,7 @@ class NvTierAsync(NvTierFast):
         for r, key in zip(new.tolist(), keys.tolist()):
             self._capi.check(L.exl3_memcpy_async(st.addr(key), base + r * self.vr_stride, self.vr_stride, h),
                              "victim ring drain")
-        ev = torch.cuda.Event()
+        ev = self._vr_events.pop() if self._vr_events else torch.cuda.Event()
         ev.record(cs)
         self._vr_fly.append((ev, hs + 1, list(zip(new.tolist(), keys.tolist()))))
         self.stats["vr_issued"] += int(new.size)
@@ -1038,9 +1044,10 @@ class NvTierAsync(NvTierFast):
         """Free ring slots on the compute stream (their copies have completed), before the next decode step."""
         if not slots:
             return
-        buf = self._h_vfree[k]
-        buf[:len(slots)] = torch.tensor(slots, dtype=torch.int64) + 4
-        idx = buf[:len(slots)].to(self.dev, non_blocking=True)
+        n = len(slots)
+        self._np_vfree[k][:n] = np.asarray(slots, dtype=np.int64) + 4
+        idx = self._d_vfree[:n]
+        idx.copy_(self._h_vfree[k][:n], non_blocking=True)
         self.vr_meta.index_fill_(0, idx, -1)
 
     def ring_settle(self) -> None:
@@ -1181,9 +1188,11 @@ class NvTierAsync(NvTierFast):
             if pool:
                 self._pool_collect(j, k)
                 self._start_fills()
+            tv = time.perf_counter()
             vr_keys, vr_slots = self._ring_landed(hs) if self.vr_K else ([], [])
             if self.vr_K:
                 vr_slots += self._ring_claims(self._np_vr[j], k, hs, self._snap_ev[j])
+                self.stats["vr_ms"] += (time.perf_counter() - tv) * 1e3
             view = self._view
             np.copyto(view, self._np_res[j])
             if self._last_diff is not None:         # the flags uploaded with that snapshot
@@ -1192,7 +1201,9 @@ class NvTierAsync(NvTierFast):
             done = self._completed(hs) + vr_keys
             adm, ev_keys, diff, vals = pol.decide(view, self._np_ring, self._np_slot[j], done)
             if self.vr_K:
+                tv = time.perf_counter()
                 self._ring_free(vr_slots, k)
+                self.stats["vr_ms"] += (time.perf_counter() - tv) * 1e3
             self._ring_from = int(self._np_ring[0]) & 0xFFFFFFFF
             self._queue_fills(adm, hs)
             if pool:
