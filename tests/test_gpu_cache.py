@@ -688,3 +688,57 @@ def test_tier_victim_ring(fused, pool, K):
 def ctypes_bytes(addr: int, n: int) -> bytes:
     import ctypes
     return ctypes.string_at(addr, n)
+
+
+def test_tier_victim_ring_wallclock_with_prefill(tmp_path):
+    """The victim ring (16 slots, drains landing by wall clock) over the record pool with fills from a packed expert
+    file, and every 12 steps a prefill layer whose experts ensure_for_prefill makes RAM-resident (it drains the
+    ring first, including the claims the host has not seen yet): every decode output equals the plain forward on the
+    true blobs, every prefill output (read zero-copy from the records and slots) equals the all-resident table's,
+    and after the last drain every RAM-resident key's record holds its own blob."""
+    from pool_checks import check_pool
+    from exl3xpu import nvtier
+    L, E, S, M, TK, steps, H, I, K = 4, 96, 90, 2, 8, 60, 128, 128, 3
+    ids, w = synth.zipf_trace(20261205, steps, L, E, TK, M=M)
+    src = nvtier.SyntheticExpertSource(H, I, K, 19, n_distinct=16)
+    path = str(tmp_path / "experts.bin")
+    nvtier.write_expert_file(path, src, L, E, H, I, K)
+    store = nvtier.TierStore(H, I, K, E, S, n_layers=L, pool=True)
+    keys = [f"model.layers.{li}.mlp" for li in range(L)]
+    for k in keys:
+        store.add_layer(k)
+    tier = nvtier.NvTierAsync(store, path, ring_cap=1 << 12, budget_records=120, latency=3, completion="wallclock",
+                              wb_queue=48, victim_ring=16)
+    tier.policy.admit_age, tier.policy.admit_qmax = 4, 32
+    print("case victim ring, wall-clock drains, prefill in between", flush=True)
+    X = store.X
+    blobs = torch.from_numpy(src.buf).cuda()
+    ref_ptr = torch.tensor([blobs[r % src.n].data_ptr() for r in range(L * E)], dtype=torch.int64, device="cuda")
+    x = torch.randn(M, H, generator=torch.Generator().manual_seed(2)).to(torch.bfloat16).cuda()
+    xp = torch.randn(40, H, generator=torch.Generator().manual_seed(3)).to(torch.bfloat16).cuda()
+    bad = prefills = 0
+    try:
+        for n in range(steps):
+            for li in range(L):
+                it = torch.from_numpy(np.ascontiguousarray(ids[n, li].reshape(M, TK))).cuda()
+                wt = torch.from_numpy(np.ascontiguousarray(w[n, li].reshape(M, TK))).cuda()
+                out = store.forward_cached(keys[li], x, it, wt)
+                ref = X.moe_forward(x, it, wt, ref_ptr[li * E:(li + 1) * E], I, K, E)
+                bad += int(not torch.equal(out, ref))
+            tier.step()
+            if n % 12 == 11:
+                li = (n // 12) % L
+                pid, pw = synth.softmax_topk(500 + n, 40, E, TK)
+                pit, pwt = torch.from_numpy(pid).cuda(), torch.from_numpy(pw).cuda()
+                tier.ensure_for_prefill(li, pit)
+                out = X.moe_forward(xp, pit, pwt, store.ptrs_all[li * E:(li + 1) * E].clone(), I, K, E)
+                ref = X.moe_forward(xp, pit, pwt, ref_ptr[li * E:(li + 1) * E], I, K, E)
+                torch.cuda.synchronize()
+                assert torch.equal(out, ref), n
+                prefills += 1
+        assert bad == 0 and prefills == steps // 12
+        assert tier.stats["vr_claims"] > 0 and tier.stats["vr_landed"] > 0
+        tier.ring_settle()
+        check_pool(store, tier, src, 120)
+    finally:
+        tier.close()
