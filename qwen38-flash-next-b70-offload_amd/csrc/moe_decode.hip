@@ -55,6 +55,14 @@ __device__ __forceinline__ void st_tag(uint64_t* p, unsigned tag, float v) {
 __device__ __forceinline__ uint64_t ld_tag(const uint64_t* p) {
     return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+// the same store for a consumer on this workgroup's XCD: workgroups are dispatched to the XCDs round-robin by
+// blockIdx (i % 8 with 8 XCDs, i % 4, % 2 or the one XCD in the partitioned modes), and a workgroup-scope store stops
+// in the XCD's L2, where the consumer's agent-scope load finds it about 0.35 us sooner than an agent-scope store
+// written through to memory. Used only where producer and consumer blockIdx differ by a multiple of 8; if that
+// assumption ever failed, the consumer's bounded poll would time out and count it in the status words.
+__device__ __forceinline__ void st_tag_xcd(uint64_t* p, unsigned tag, float v) {
+    __hip_atomic_store(p, ((uint64_t)tag << 32) | __float_as_uint(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
 __device__ __forceinline__ bool tag_is(uint64_t w, unsigned tag) { return (unsigned)(w >> 32) == tag; }
 __device__ __forceinline__ float tag_val(uint64_t w) { return __uint_as_float((uint32_t)w); }
 __device__ __forceinline__ unsigned call_tag() {
@@ -636,8 +644,15 @@ __device__ __forceinline__ void down_wg(const DecodeArgs& A, int blk, LayerShare
         v1 = v1 * sc * (float)sc_d.y;
         asm volatile("" : "+v"(v0), "+v"(v1));   // y rounded as stored (not fused into the combiner's sum)
         if (!comb) {                             // y of this pick for the row's combiner
-            st_tag(yb + (size_t)k * H, tag, v0);
-            st_tag(yb + (size_t)k * H + 1, tag, v1);
+            // the down workgroups of one column block nb, all picks, sit 16 a apart in blockIdx: with nbn a multiple
+            // of 8 they share an XCD with their combiner
+            if (nbn % 8 == 0) {
+                st_tag_xcd(yb + (size_t)k * H, tag, v0);
+                st_tag_xcd(yb + (size_t)k * H + 1, tag, v1);
+            } else {
+                st_tag(yb + (size_t)k * H, tag, v0);
+                st_tag(yb + (size_t)k * H + 1, tag, v1);
+            }
             return;
         }
         // combiner: wave 0 loads the other picks' y (lower workgroup ids) itself, up to kCombPicks per round, and sums
