@@ -38,8 +38,8 @@ HBM_PEAK = 8000.0   # GB/s, MI355X HBM3E
 # HBM counters of one resident moe_layer_kernel<3> call at this workload (KiB per dispatch, rocprofv3 --pmc FETCH_SIZE
 # and --pmc WRITE_SIZE over bench.py --roofline-only) and the factor that maps each counter to the bytes of a plain
 # 256 MiB device copy in the same runs; re-measured whenever the kernel changes.
-PMC_KIB = {"fetch": 7587.4, "write": 467.0}
-PMC_SCALE = {"fetch": 262144 / 131087.2, "write": 1.0}
+PMC_KIB = {"fetch": 7571.3, "write": 323.0}
+PMC_SCALE = {"fetch": 262144 / 131086.3, "write": 1.0}
 
 
 def log(*a):
