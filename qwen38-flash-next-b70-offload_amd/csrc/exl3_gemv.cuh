@@ -17,6 +17,23 @@ __device__ __forceinline__ void accum_period(const Period<K>& P, const half2_t (
     }
 }
 
+// accum_period split in two: the period's raw h pairs decoded ahead of its activations (h[u / 2] for values u, u + 1),
+// then the same v_dot2_f32_f16 chain over them once the activations are known
+template <int K, int u>
+__device__ __forceinline__ void decode_period(const Period<K>& P, half2_t* h) {
+    if constexpr (u < Geo<K>::V) {
+        h[u >> 1] = cb_h2(P.template state<u>(), P.template state<u + 1>());
+        decode_period<K, u + 2>(P, h);
+    }
+}
+template <int K, int NQ, int u>
+__device__ __forceinline__ void dot_period(const half2_t* h, const half2_t (&xv)[2][NQ], float (&acc)[2]) {
+    if constexpr (u < Geo<K>::V) {
+        acc[(u >> 2) & 1] = __builtin_amdgcn_fdot2(h[u >> 1], xv[(u >> 1) & 1][u >> 3], acc[(u >> 2) & 1], false);
+        dot_period<K, NQ, u + 2>(h, xv, acc);
+    }
+}
+
 // the same for MR activation rows at once: each pair of codebook values is decoded once and multiplied into every row
 // (codebook CB: mul1 as raw h, 3inst / mcg as the weights, see cb_dot_pair)
 template <int K, int NQ, int MR, int u, int CB = 2>

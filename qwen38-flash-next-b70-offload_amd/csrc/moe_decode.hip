@@ -167,6 +167,56 @@ struct Gemv8 {
         }
     }
 
+    // compute() in two parts: the raw h values of the chunk's first NR tile-rows decoded while its activations are
+    // still being produced (NR * 32 values, NR * 16 half2 registers per lane), then the chunk with only their dot
+    // products left
+    template <int NR>
+    using Decoded = half2_t[NCP][NR > 0 ? NR : 1][V / 2];
+    template <int NR>
+    __device__ __forceinline__ void decode(Decoded<NR>& h) const {
+        const int l = lane_id();
+        const int p = l % G, j = l / G;
+        const int src_lane = j * G + ((p + G - 1) % G);
+#pragma unroll
+        for (int cp = 0; cp < NCP; ++cp)
+#pragma unroll
+            for (int rr = 0; rr < NR; ++rr) {
+                const uint32_t prev = (uint32_t)__shfl((int)wd[cp][rr][D - 1], src_lane, 64);
+                Period<K> P;
+                P.set(wd[cp][rr], prev);
+                decode_period<K, 0>(P, h[cp][rr]);
+            }
+    }
+    template <int NR>
+    __device__ __forceinline__ void compute_pre(const Decoded<NR>& h, const half2_t* xh, float (&acc)[NCP][2]) const {
+        const int l = lane_id();
+        const int p = l % G, j = l / G;
+        const int src_lane = j * G + ((p + G - 1) % G);
+        const int qb = ((V * p) >> 3) & 3;
+#pragma unroll
+        for (int cp = 0; cp < NCP; ++cp) {
+            acc[cp][0] = 0.f;
+            acc[cp][1] = 0.f;
+#pragma unroll
+            for (int rr = 0; rr < 4; ++rr) {
+                const half2_t* xr = xh + rr * 8;
+                half2_t xv[2][NQ];
+#pragma unroll
+                for (int a = 0; a < 2; ++a)
+#pragma unroll
+                    for (int qq = 0; qq < NQ; ++qq) xv[a][qq] = xr[4 * a + ((qb + qq) & 3)];
+                if (rr < NR) {
+                    dot_period<K, NQ, 0>(h[cp][rr < NR ? rr : 0], xv, acc[cp]);
+                } else {
+                    const uint32_t prev = (uint32_t)__shfl((int)wd[cp][rr][D - 1], src_lane, 64);
+                    Period<K> P;
+                    P.set(wd[cp][rr], prev);
+                    accum_period<K, NQ, 0>(P, xv, acc[cp]);
+                }
+            }
+        }
+    }
+
     // sum lanes sharing a column (call exactly once per pass); returns true for the lane owning the column pair and
     // sets col0 (column of h = 0 within the 128-column block; h = 1 is col0 + 8)
     __device__ __forceinline__ static bool reduce(float (&acc)[2], int cp, int& col0) {
@@ -329,6 +379,9 @@ __device__ __forceinline__ const uint8_t* pair_lookup(const DecodeArgs& A, int a
 template <int K>
 __device__ __forceinline__ void gateup_wg(const DecodeArgs& A, int blk, LayerShared& S) {
     using GQ = Gemv4<K>;
+    // issue priority over the down waves that share the CU: their weights are decoded ahead of their input, in the
+    // cycles the gate/up waves (the critical path) leave free
+    __builtin_amdgcn_s_setprio(2);
     const int H = A.g.H, I = A.g.I;
     const int nhb = H / 128, ksn = gu_kslices(H), ncg = I / 64;
     const int per = 2 * ncg * ksn;               // gate/up workgroups per pair
@@ -448,7 +501,9 @@ __device__ __forceinline__ void gateup_wg(const DecodeArgs& A, int blk, LayerSha
 // down WG per (pair, 128-column block of H) over the full K = I: the 4-row chunks of the I/16 tile-rows go round-robin
 // to the eight waves, the per-wave column sums are reduced in LDS in wave order (no cross-WG exchange), then the output
 // Hadamard * w * svh_d -> y, and the combine.
-template <int K>
+// NR > 0: every wave has at most one 4-row chunk (I <= 512), whose first NR tile-rows are decoded ahead of the down
+// input, and no second chunk's words are held across the wait
+template <int K, int NR>
 __device__ __forceinline__ void down_wg(const DecodeArgs& A, int blk, LayerShared& S) {
     using GV = Gemv8<K>;
     const int H = A.g.H, I = A.g.I;
@@ -461,7 +516,8 @@ __device__ __forceinline__ void down_wg(const DecodeArgs& A, int blk, LayerShare
     const int m = a / A.topk;
     const int tiles_n = H / 16, ct0 = nb * 8;
     const uint32_t* tr = (const uint32_t*)(base + A.g.gu_bytes);
-    const int nch = (kt / 4 + kWaves - 1 - wv) / kWaves;      // 4-row chunks of this wave: q = wv + kWaves * c
+    const int nch0 = (kt / 4 + kWaves - 1 - wv) / kWaves;     // 4-row chunks of this wave: q = wv + kWaves * c
+    const int nch = NR > 0 ? min(nch0, 1) : nch0;
     {   // the down weights are needed only after the gate/up phase: let the gate/up loads (the critical path) take
         // HBM first, then issue these (constant 100 MHz clock)
         const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
@@ -524,6 +580,22 @@ __device__ __forceinline__ void down_wg(const DecodeArgs& A, int blk, LayerShare
         S.fwb = f && A.vict_inline ? inline_victim(A, f, wa) : -1;
         S.fwa = wa;
     }
+    // the first chunk's raw h values decoded now, while the gate/up sums are still being produced: only its dot
+    // products are left once the down input is known (the asm keeps the decode ahead of the wait)
+    typename GV::template Decoded<NR> hd;
+    if (NR > 0 && nch > 0) {
+        g0.template decode<NR>(hd);
+#pragma unroll
+        for (int cp = 0; cp < GV::NCP; ++cp)
+#pragma unroll
+            for (int rr = 0; rr < NR; ++rr)
+#pragma unroll
+                for (int i = 0; i < GV::V / 2; ++i) {
+                    uint32_t b = __builtin_bit_cast(uint32_t, hd[cp][rr][i]);
+                    asm volatile("" : "+v"(b));
+                    hd[cp][rr][i] = __builtin_bit_cast(half2_t, b);
+                }
+    }
     const int ksn = gu_kslices(H);
     half2_t* xs = S.u.dn.xd;                     // the pair's down input, [I/2] half2
     // gate/up epilogue of the pair, one 128-column block b of I per wave and round: wait for the sums of its 4 * ksn
@@ -583,7 +655,8 @@ __device__ __forceinline__ void down_wg(const DecodeArgs& A, int blk, LayerShare
     }
     __syncthreads();
     if (tid == 0) st_tag(A.xstart + A.n_gu + blk, tag, 0.f);     // ids, pointers, w and fill target consumed
-    uint32_t* trd = S.fdst ? (uint32_t*)((uint8_t*)S.fdst + A.g.gu_bytes) : nullptr;
+    // (no write-through target at all when the call has no fills: then the words are dead once decoded)
+    uint32_t* trd = (A.fused || A.fill) && S.fdst ? (uint32_t*)((uint8_t*)S.fdst + A.g.gu_bytes) : nullptr;
     if (trd && S.fwb >= 0) {                     // the victim's old down words at this wave's positions, first
         uint32_t* tro = (uint32_t*)((uint8_t*)S.fwa + A.g.gu_bytes);
         for (int c = 0; c < nch; ++c) g0.copy_old(trd, tro, tiles_n, (wv + kWaves * c) * 4, ct0);
@@ -598,7 +671,8 @@ __device__ __forceinline__ void down_wg(const DecodeArgs& A, int blk, LayerShare
     for (int c = 0; c < nch; ++c) {
         const int r0 = (wv + kWaves * c) * 4;
         if (trd) g0.write_through(trd, tiles_n, r0, ct0);
-        g0.compute(0, xs + r0 * 8, tacc);
+        if (NR > 0 && c == 0) g0.template compute_pre<NR>(hd, xs + r0 * 8, tacc);
+        else g0.compute(0, xs + r0 * 8, tacc);
         if (c + 1 < nch) {
             g0 = g1;
             if (c + 2 < nch) g1.load(tr, tiles_n, r0 + 8 * kWaves, ct0);
@@ -737,8 +811,12 @@ __device__ __forceinline__ void down_wg(const DecodeArgs& A, int blk, LayerShare
 // compiled without those paths (21.6 KB of code against 54.6 KB for K = 3, no SGPR spills); MODE 2: the tier's cached
 // call (ensure inside the launch, victims copied inline by the writers of each miss, no victim workgroups); MODE 0:
 // every other combination. Each instantiation carries only its own paths, so the hot code of a call stays small.
-template <int K, int MODE>
-__global__ void __launch_bounds__(kThreads) moe_layer_kernel(DecodeArgs A0) {
+// ONE: I <= 512, the down waves decode the weights of their one chunk ahead of their input (all four tile-rows in
+// the lean call, three where the words are also kept for a write-through), within 128 VGPRs: 4 waves per SIMD, so a
+// gate/up and a down workgroup share a CU.
+template <int K, int MODE, bool ONE>
+__global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(ONE ? 4 : 1)))
+moe_layer_kernel(DecodeArgs A0) {
     DecodeArgs A = A0;
     if constexpr (MODE == 1) {       // lean
         A.fused = 0;
@@ -768,7 +846,7 @@ __global__ void __launch_bounds__(kThreads) moe_layer_kernel(DecodeArgs A0) {
     }
     if (b < nv) victim_wg(A, b);
     else if (b < nv + n_gu) gateup_wg<K>(A, b - nv, S);
-    else down_wg<K>(A, b - nv - n_gu, S);
+    else down_wg<K, ONE ? (MODE == 1 ? 4 : 3) : 0>(A, b - nv - n_gu, S);
 }
 
 // bit-exact dequantization of one trellis matrix (PLANAR4 words [k_tiles][n_tiles][8K]) -> fp16 [16 k_tiles][16 n_tiles]
@@ -798,25 +876,23 @@ __global__ void __launch_bounds__(256) dequant_kernel(const uint32_t* __restrict
 
 // ---- host launchers ------------------------------------------------------------------------------------------------
 
+template <int K, bool ONE>
+static void launch_layer_k(int mode, dim3 grid, const DecodeArgs& a, hipStream_t s) {
+    if (mode == 1) hipLaunchKernelGGL((moe_layer_kernel<K, 1, ONE>), grid, dim3(kThreads), 0, s, a);
+    else if (mode == 2) hipLaunchKernelGGL((moe_layer_kernel<K, 2, ONE>), grid, dim3(kThreads), 0, s, a);
+    else hipLaunchKernelGGL((moe_layer_kernel<K, 0, ONE>), grid, dim3(kThreads), 0, s, a);
+}
+
 hipError_t launch_moe_layer(int K, const DecodeArgs& a, hipStream_t s) {
     const int n_gu = a.n_gu;
     const int n_dn = a.npairs * (a.g.H / 128);
     dim3 grid((unsigned)(a.fused + a.n_vict_wg + n_gu + n_dn));
     const bool lean = !a.fused && !a.fill && !a.pair_ptr && !a.commit_ptrs && !a.n_vict_wg && !a.vict_inline;
     const int mode = lean ? 1 : (a.fused && !a.pair_ptr && !a.n_vict_wg && a.vict_inline ? 2 : 0);
-    if (K == 2) {
-        if (mode == 1) hipLaunchKernelGGL((moe_layer_kernel<2, 1>), grid, dim3(kThreads), 0, s, a);
-        else if (mode == 2) hipLaunchKernelGGL((moe_layer_kernel<2, 2>), grid, dim3(kThreads), 0, s, a);
-        else hipLaunchKernelGGL((moe_layer_kernel<2, 0>), grid, dim3(kThreads), 0, s, a);
-    } else if (K == 3) {
-        if (mode == 1) hipLaunchKernelGGL((moe_layer_kernel<3, 1>), grid, dim3(kThreads), 0, s, a);
-        else if (mode == 2) hipLaunchKernelGGL((moe_layer_kernel<3, 2>), grid, dim3(kThreads), 0, s, a);
-        else hipLaunchKernelGGL((moe_layer_kernel<3, 0>), grid, dim3(kThreads), 0, s, a);
-    } else if (K == 4) {
-        if (mode == 1) hipLaunchKernelGGL((moe_layer_kernel<4, 1>), grid, dim3(kThreads), 0, s, a);
-        else if (mode == 2) hipLaunchKernelGGL((moe_layer_kernel<4, 2>), grid, dim3(kThreads), 0, s, a);
-        else hipLaunchKernelGGL((moe_layer_kernel<4, 0>), grid, dim3(kThreads), 0, s, a);
-    }
+    const bool one = a.g.I / 64 <= kWaves;       // at most one 4-row chunk per down wave
+    if (K == 2) one ? launch_layer_k<2, true>(mode, grid, a, s) : launch_layer_k<2, false>(mode, grid, a, s);
+    else if (K == 3) one ? launch_layer_k<3, true>(mode, grid, a, s) : launch_layer_k<3, false>(mode, grid, a, s);
+    else if (K == 4) one ? launch_layer_k<4, true>(mode, grid, a, s) : launch_layer_k<4, false>(mode, grid, a, s);
     else return hipErrorInvalidValue;
     return hipGetLastError();
 }
