@@ -38,7 +38,7 @@ HBM_PEAK = 8000.0   # GB/s, MI355X HBM3E
 # HBM counters of one resident moe_layer_kernel<3> call at this workload (KiB per dispatch, rocprofv3 --pmc FETCH_SIZE
 # and --pmc WRITE_SIZE over bench.py --roofline-only) and the factor that maps each counter to the bytes of a plain
 # 256 MiB device copy in the same runs; re-measured whenever the kernel changes.
-PMC_KIB = {"fetch": 7571.3, "write": 323.0}
+PMC_KIB = {"fetch": 7073.7, "write": 323.0}
 PMC_SCALE = {"fetch": 262144 / 131086.3, "write": 1.0}
 
 
@@ -796,7 +796,7 @@ def main():
                      "traffic_note": "FETCH_SIZE + WRITE_SIZE per call from rocprofv3 --pmc runs of --roofline-only, "
                                      "scaled by a 256 MiB copy (x%.2f / x%.2f): profiles/moe_layer_kernel_h2048_i512_top10_k3_resident_pmc.md"
                                      % (PMC_SCALE["fetch"], PMC_SCALE["write"]),
-                     "kernel": "moe_layer_kernel<3, 1> (the resident instantiation; one moe_forward call per layer, HBM-resident experts)",
+                     "kernel": "moe_layer_kernel<3, 1, true> (the resident instantiation; one moe_forward call per layer, HBM-resident experts)",
                      "bytes_per_call": per_call_bytes, "us_per_call": round(us_call, 2)},
         "launch": "eager" if graph is None else "hip graph of the 48 layer calls per step",
         "host_ms_per_step": host_ms,
