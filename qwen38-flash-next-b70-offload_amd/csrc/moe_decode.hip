@@ -813,9 +813,10 @@ __device__ __forceinline__ void down_wg(const DecodeArgs& A, int blk, LayerShare
 // every other combination. Each instantiation carries only its own paths, so the hot code of a call stays small.
 // ONE: I <= 512, the down waves decode the weights of their one chunk ahead of their input (all four tile-rows in
 // the lean call, three where the words are also kept for a write-through), within 128 VGPRs: 4 waves per SIMD, so a
-// gate/up and a down workgroup share a CU.
+// gate/up and a down workgroup share a CU. The lean call is held to 128 VGPRs for wider I too (K = 4 needs 148
+// otherwise, one workgroup per CU; at 128 it spills 5, and runs the H 4096 / I 1536 layer in 38.0 us against 48.2).
 template <int K, int MODE, bool ONE>
-__global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(ONE ? 4 : 1)))
+__global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(ONE || MODE == 1 ? 4 : 1)))
 moe_layer_kernel(DecodeArgs A0) {
     DecodeArgs A = A0;
     if constexpr (MODE == 1) {       // lean
