@@ -580,6 +580,20 @@ __device__ __forceinline__ void down_wg(const DecodeArgs& A, int blk, LayerShare
         S.fwb = f && A.vict_inline ? inline_victim(A, f, wa) : -1;
         S.fwa = wa;
     }
+    // with one chunk per wave, a call that can fill copies the victim's old words and writes its words through now
+    // (the target is the ensure's decision, taken before these loads return), so that they are dead once decoded
+    bool done_wt = false;
+    if constexpr (NR > 0) {
+        if (A.fused || A.fill) {
+            __syncthreads();                     // the target and the victim from thread 0
+            uint32_t* trd0 = S.fdst ? (uint32_t*)((uint8_t*)S.fdst + A.g.gu_bytes) : nullptr;
+            if (trd0 && nch > 0) {
+                if (S.fwb >= 0) g0.copy_old(trd0, (uint32_t*)((uint8_t*)S.fwa + A.g.gu_bytes), tiles_n, wv * 4, ct0);
+                g0.write_through(trd0, tiles_n, wv * 4, ct0);
+            }
+            done_wt = true;
+        }
+    }
     // the first chunk's raw h values decoded now, while the gate/up sums are still being produced: only its dot
     // products are left once the down input is known (the asm keeps the decode ahead of the wait)
     typename GV::template Decoded<NR> hd;
@@ -656,7 +670,7 @@ __device__ __forceinline__ void down_wg(const DecodeArgs& A, int blk, LayerShare
     __syncthreads();
     if (tid == 0) st_tag(A.xstart + A.n_gu + blk, tag, 0.f);     // ids, pointers, w and fill target consumed
     // (no write-through target at all when the call has no fills: then the words are dead once decoded)
-    uint32_t* trd = (A.fused || A.fill) && S.fdst ? (uint32_t*)((uint8_t*)S.fdst + A.g.gu_bytes) : nullptr;
+    uint32_t* trd = !done_wt && (A.fused || A.fill) && S.fdst ? (uint32_t*)((uint8_t*)S.fdst + A.g.gu_bytes) : nullptr;
     if (trd && S.fwb >= 0) {                     // the victim's old down words at this wave's positions, first
         uint32_t* tro = (uint32_t*)((uint8_t*)S.fwa + A.g.gu_bytes);
         for (int c = 0; c < nch; ++c) g0.copy_old(trd, tro, tiles_n, (wv + kWaves * c) * 4, ct0);
@@ -811,9 +825,8 @@ __device__ __forceinline__ void down_wg(const DecodeArgs& A, int blk, LayerShare
 // compiled without those paths (21.6 KB of code against 54.6 KB for K = 3, no SGPR spills); MODE 2: the tier's cached
 // call (ensure inside the launch, victims copied inline by the writers of each miss, no victim workgroups); MODE 0:
 // every other combination. Each instantiation carries only its own paths, so the hot code of a call stays small.
-// ONE: I <= 512, the down waves decode the weights of their one chunk ahead of their input (all four tile-rows in
-// the lean call, three where the words are also kept for a write-through), within 128 VGPRs: 4 waves per SIMD, so a
-// gate/up and a down workgroup share a CU. The lean call is held to 128 VGPRs for wider I too (K = 4 needs 148
+// ONE: I <= 512, the down waves decode the weights of their one chunk (all four tile-rows) ahead of their input,
+// within 128 VGPRs: 4 waves per SIMD, so a gate/up and a down workgroup share a CU. The lean call is held to 128 VGPRs for wider I too (K = 4 needs 148
 // otherwise, one workgroup per CU; at 128 it spills 5, and runs the H 4096 / I 1536 layer in 38.0 us against 48.2).
 template <int K, int MODE, bool ONE>
 __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(ONE || MODE == 1 ? 4 : 1)))
@@ -847,7 +860,7 @@ moe_layer_kernel(DecodeArgs A0) {
     }
     if (b < nv) victim_wg(A, b);
     else if (b < nv + n_gu) gateup_wg<K>(A, b - nv, S);
-    else down_wg<K, ONE ? (MODE == 1 ? 4 : 3) : 0>(A, b - nv - n_gu, S);
+    else down_wg<K, ONE ? 4 : 0>(A, b - nv - n_gu, S);
 }
 
 // bit-exact dequantization of one trellis matrix (PLANAR4 words [k_tiles][n_tiles][8K]) -> fp16 [16 k_tiles][16 n_tiles]
