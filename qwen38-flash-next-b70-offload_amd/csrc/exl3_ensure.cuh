@@ -101,13 +101,12 @@ __device__ void ensure_wg(const EnsureArgs& A, EnsureShared& Z, int* done) {
     const int kb = A.layer * E;
     const int nwords = (S + 31) >> 5;
 
-    // this thread's contiguous slot chunk [s0, s0 + n_own): loaded first, in flight during the tier mask
+    // this thread's contiguous slot chunk [s0, s0 + n_own) of the stamps, loaded only once the call is known to
+    // miss: a call without misses never reads them, and its done signal (after a store fence, which on this
+    // architecture also waits for outstanding loads) is not held up by S stamps read beside the layer's weights
     const int C = (S + NT - 1) / NT;
     const int s0 = min(S, tid * C);
     const int n_own = min(S, s0 + C) - s0;
-    int slr[kEnsRegSlots];
-#pragma unroll
-    for (int j = 0; j < kEnsRegSlots; ++j) slr[j] = j < n_own ? A.slot_last[s0 + j] : INT_MAX;
     for (int i = tid; i < nwords; i += NT) Z.stm[i] = 0u;
     for (int e = tid; e < E; e += NT) Z.need[e] = 0;
 
@@ -184,6 +183,9 @@ __device__ void ensure_wg(const EnsureArgs& A, EnsureShared& Z, int* done) {
         if (tid == 0) counter_add(done, 1);
         return;
     }
+    int slr[kEnsRegSlots];
+#pragma unroll
+    for (int j = 0; j < kEnsRegSlots; ++j) slr[j] = j < n_own ? A.slot_last[s0 + j] : INT_MAX;
     const int T = Z.sh[0];
     // need[e] = 1 hit / 2 miss; hits stamp slot_last = T unless pinned, and mark the slot in the bitmap
     if (tid < P) {
