@@ -360,13 +360,14 @@ __device__ __forceinline__ const uint8_t* pair_lookup(const DecodeArgs& A, int a
     masked = false;
     if (Q.ram_res) {
         const int safe = Q.safe[Q.layer];
-        const int64_t ps = A.ptrs[safe];
         const uint8_t rr = Q.ram_res[kb + id];
         const int so = Q.slot_of[kb + id];
         masked = !rr && so < 0;
-        if (masked) {
-            id = safe;
-            p = ps;
+        int sf = safe;
+        asm volatile("" : "+v"(sf));             // the safe id loaded beside the mask inputs, not after them
+        if (masked) {                            // (uniform) the safe expert's pointer only when it is needed: an
+            id = sf;                             // unmasked pair's lookup is two rounds of loads, not three
+            p = A.ptrs[sf];
         }
     }
     e = id;
